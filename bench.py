@@ -1,0 +1,507 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized-decode hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]      # one JSON line
+    python bench.py --table [--table-out FILE]               # every workload
+
+Default workload (one JSON line): Q4 dequant+GEMV over one Qwen2.5-7B MLP,
+i.e. the gate and up matrices [18944, 3584] and the down matrix
+[3584, 18944], per-row symmetric Q4 from N(0, 0.02) weights, times one fp16
+activation row ~N(0, 1) (M = 1).  One step = the three GEMVs (three launches
+of the Q4 GEMV kernel).  Weight copies are rotated over more than 1 GB so
+that the 256 MB Infinity Cache cannot serve them; inputs are resident in HBM
+before the timed region starts.
+
+Timing: the stream is held by a short sleep kernel while the timed launches
+are queued, with a HIP event between consecutive launches; the GPU then runs
+them back to back and each event pair brackets exactly one kernel.  ms/step
+and the per-launch durations come from those events.
+
+The ``cpu_baseline`` leg runs the CPU oracle's restatement of the reference
+Q4 row dot (OpenMP, all host threads) on a bounded sample of the same
+workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+PEAK_HBM_GBS = 8000.0
+MALL_BYTES = 1 << 30  # rotate at least this many distinct weight bytes
+
+
+def _args(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--table", action="store_true", help="measure every workload, print a markdown table")
+    ap.add_argument("--table-out", default=None, help="also write the table to this file")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample length")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args(argv)
+
+
+# --------------------------------------------------------------------------- timing
+
+class Timer:
+    """Per-launch GPU durations from HIP events, launches queued behind a sleep."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.cycles_per_ms = self._calibrate()
+
+    def _calibrate(self) -> float:
+        torch = self.torch
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        torch.cuda._sleep(2_000_000)
+        b.record()
+        torch.cuda.synchronize()
+        ms = max(a.elapsed_time(b), 1e-3)
+        return 2_000_000 / ms
+
+    def run(self, launches, hold_ms: float = 30.0):
+        """launches: list of zero-arg callables, each enqueuing one kernel.
+        Returns the per-launch durations in ms."""
+        torch = self.torch
+        events = [torch.cuda.Event(enable_timing=True) for _ in range(len(launches) + 1)]
+        torch.cuda.synchronize()
+        torch.cuda._sleep(int(self.cycles_per_ms * hold_ms))
+        events[0].record()
+        for i, fn in enumerate(launches):
+            fn()
+            events[i + 1].record()
+        torch.cuda.synchronize()
+        return [events[i].elapsed_time(events[i + 1]) for i in range(len(launches))]
+
+
+def _stream_ptr(torch):
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+# --------------------------------------------------------------------------- workloads
+
+def _q4_sets(torch, fmt, shapes, nsets, seed=20261201):
+    """nsets copies of Q4 matrices of the given [rows, cols] shapes (device)."""
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    sets = []
+    for _ in range(nsets):
+        mats = []
+        for rows, cols in shapes:
+            w = torch.randn((rows, cols), generator=gen, device="cuda", dtype=torch.float32).mul_(0.02).to(torch.float16)
+            packed, scales, _ = fmt.quantize_tensor_to_q4(w)
+            del w
+            mats.append((packed, scales, rows, cols))
+        sets.append(mats)
+    torch.cuda.synchronize()
+    return sets
+
+
+def q4_bytes(rows, cols):
+    # packed weights + fp16 scales + fp16 x + fp32 y
+    return rows * cols // 2 + 2 * rows + 2 * cols + 4 * rows
+
+
+def fp8_bytes(rows, cols, m):
+    return rows * cols + 4 * math.ceil(rows / 128) * math.ceil(cols / 128) + 2 * m * cols + 4 * m * rows
+
+
+def bench_q4_gemv(torch, lib, fmt, steps, warmup, timer):
+    shapes = [(18944, 3584), (18944, 3584), (3584, 18944)]
+    per_set = sum(r * c // 2 for r, c in shapes)
+    nsets = max(2, math.ceil(MALL_BYTES / per_set))
+    sets = _q4_sets(torch, fmt, shapes, nsets)
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    x_in = torch.randn((3584,), generator=gen, device="cuda").to(torch.float16)
+    x_down = torch.randn((18944,), generator=gen, device="cuda").to(torch.float16)
+    outs = [torch.empty((r,), device="cuda", dtype=torch.float32) for r, _ in shapes]
+    lib.pocketlm_set_stream(_stream_ptr(torch))
+    calls = []
+    for mats in sets:
+        step = []
+        for j, (packed, scales, rows, cols) in enumerate(mats):
+            x = x_in if cols == 3584 else x_down
+            args = (ctypes.c_void_p(packed.data_ptr()), ctypes.c_void_p(scales.data_ptr()),
+                    ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(outs[j].data_ptr()), rows, cols)
+            step.append((args, q4_bytes(rows, cols)))
+        calls.append(step)
+
+    def launch(args):
+        code = lib.q4_gemv_f16_f32(*args)
+        if code != 0:
+            raise RuntimeError(f"q4_gemv_f16_f32 failed with code {code}")
+
+    for i in range(warmup):
+        for args, _ in calls[i % nsets]:
+            launch(args)
+    torch.cuda.synchronize()
+    launches, nbytes = [], []
+    for i in range(steps):
+        for args, b in calls[i % nsets]:
+            launches.append(lambda a=args: launch(a))
+            nbytes.append(b)
+    t0 = time.perf_counter()
+    durs = timer.run(launches, hold_ms=max(30.0, 0.05 * len(launches)))
+    wall = time.perf_counter() - t0
+    total_ms = sum(durs)
+    step_bytes = sum(b for _, b in calls[0])
+    return {
+        "durations_ms": durs,
+        "bytes": nbytes,
+        "ms_per_step": total_ms / steps,
+        "step_bytes": step_bytes,
+        "wall_s": wall,
+        "nsets": nsets,
+        "host_set": sets[0],
+        "x_in": x_in,
+        "x_down": x_down,
+    }
+
+
+def cpu_q4_baseline(torch, sample, seconds):
+    import numpy as np
+
+    import oracle
+
+    mats = [(p.cpu().numpy(), s.cpu().view(torch.int16).numpy().view(np.uint16), r, c)
+            for p, s, r, c in sample["host_set"]]
+    x_in = sample["x_in"].float().cpu().numpy()
+    x_down = sample["x_down"].float().cpu().numpy()
+    step_bytes = sum(q4_bytes(r, c) for _, _, r, c in mats)
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        for p, s, r, c in mats:
+            oracle.q4_gemv(p, s, x_in if c == 3584 else x_down, r, c)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    gbs = step_bytes * steps / el / 1e9
+    return {
+        "value": round(gbs, 3),
+        "unit": "GB/s",
+        "cores": oracle.num_threads(),
+        "kind": "port",
+        "sample": f"{steps} steps (gate+up+down Q4 GEMV, M=1) of one weight copy, "
+                  f"{el:.1f} s, {el / steps * 1e6:.0f} us/step, weights warm in host RAM",
+    }
+
+
+def _traffic(workload):
+    f = REPO / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        data = json.loads(f.read_text())
+        return data.get(workload)
+    except (OSError, ValueError):
+        return None
+
+
+def main_line(args):
+    import torch
+
+    from pocketlm_amd import _lib, formats
+
+    torch.cuda.set_device(0)
+    lib = _lib.load()
+    if lib.pocketlm_device_available() != 1:
+        raise RuntimeError("libpocketlm_hip.so reports no gfx950 device")
+    timer = Timer(torch)
+    r = bench_q4_gemv(torch, lib, formats, args.steps, args.warmup, timer)
+    ms = r["ms_per_step"]
+    value = r["step_bytes"] / (ms / 1e3) / 1e9
+    achieved = sum(r["bytes"]) / (sum(r["durations_ms"]) / 1e3) / 1e9
+    roof = {
+        "bound": "hbm",
+        "kernel": "q4_rows_kernel<8,1,false,true> (q4_gemv_f16_f32)",
+        "achieved": round(achieved, 2),
+        "peak": PEAK_HBM_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / PEAK_HBM_GBS, 4),
+        "traffic": _traffic("q4_gemv"),
+        "avg_launch_us": round(1e3 * sum(r["durations_ms"]) / len(r["durations_ms"]), 3),
+        "bytes_per_launch": round(sum(r["bytes"]) / len(r["bytes"])),
+    }
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_q4_baseline(torch, r, args.cpu_seconds)
+    line = {
+        "metric": "dequant-GEMV µs & achieved HBM GB/s (% of peak) at M=1 and M=8",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_gemv": round(1e3 * ms / 3, 3),
+        "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4 weights, fp16 x, fp32 accumulate",
+        "data": "synthetic (N(0,0.02) weights quantized with the reference Q4 scheme, x ~ N(0,1) fp16)",
+        "config": {
+            "workload": "Q4 dequant+GEMV, Qwen2.5-7B MLP: gate/up [18944,3584] + down [3584,18944], M=1",
+            "bytes_per_step": r["step_bytes"],
+            "weight_copies_rotated": r["nsets"],
+        },
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+# --------------------------------------------------------------------------- table mode
+
+def table(args):
+    import numpy as np
+    import torch
+
+    from pocketlm_amd import _lib, formats, native
+
+    torch.cuda.set_device(0)
+    lib = _lib.load()
+    timer = Timer(torch)
+    rows_out = []
+
+    def measure(name, m, make_calls, nbytes, cpu_fn=None, cpu_kind="port"):
+        calls = make_calls()
+        for fn in calls[: min(len(calls), 8)]:
+            fn()
+        torch.cuda.synchronize()
+        reps = max(3, min(400, int(5e8 // max(nbytes, 1))))
+        launches = [calls[i % len(calls)] for i in range(reps)]
+        durs = sorted(timer.run(launches, hold_ms=max(30.0, 0.05 * len(launches))))
+        med = durs[len(durs) // 2]
+        gbs = nbytes / (med / 1e3) / 1e9
+        cpu_us = cpu_gbs = None
+        if cpu_fn is not None and not args.no_cpu:
+            t0 = time.perf_counter()
+            n = 0
+            while True:
+                cpu_fn()
+                n += 1
+                if time.perf_counter() - t0 > 1.5:
+                    break
+            cpu_us = (time.perf_counter() - t0) / n * 1e6
+            cpu_gbs = nbytes / (cpu_us / 1e6) / 1e9
+        rows_out.append((name, m, 1e3 * med, gbs, 100 * gbs / PEAK_HBM_GBS, cpu_us, cpu_gbs, cpu_kind))
+        print(f"{name:40s} M={m}  {1e3 * med:9.2f} us  {gbs:8.1f} GB/s  {100 * gbs / PEAK_HBM_GBS:5.1f}%"
+              + (f"   cpu {cpu_us:10.1f} us {cpu_gbs:7.2f} GB/s" if cpu_us else ""), flush=True)
+
+    import oracle
+
+    gen = torch.Generator(device="cuda").manual_seed(11)
+
+    def fp8_sets(rows, cols, count):
+        out = []
+        for _ in range(count):
+            w = torch.randn((rows, cols), generator=gen, device="cuda").mul_(0.02).to(torch.float8_e4m3fn)
+            w = w.view(torch.uint8)
+            s = torch.rand((math.ceil(rows / 128), math.ceil(cols / 128)), generator=gen, device="cuda") * 9e-3 + 1e-3
+            out.append((w, s))
+        return out
+
+    # ---- FP8 linear shapes (configs 1 and 5)
+    for name, rows, cols in (("fp8 linear 2048x7168", 2048, 7168), ("fp8 q_a 1536x7168", 1536, 7168),
+                             ("fp8 kv_a 576x7168", 576, 7168), ("fp8 o 7168x16384", 7168, 16384),
+                             ("fp8 expert gate/up 2048x7168", 2048, 7168), ("fp8 expert down 7168x2048", 7168, 2048)):
+        count = max(2, math.ceil(MALL_BYTES / (rows * cols)))
+        sets = fp8_sets(rows, cols, count)
+        host_w, host_s = sets[0][0].cpu().numpy(), sets[0][1].cpu().numpy()
+        for m in (1, 2, 4, 8):
+            if name.startswith("fp8 linear") and m > 1:
+                continue
+            x = torch.randn((m, cols), generator=gen, device="cuda").to(torch.bfloat16).float()
+            y = torch.empty((m, rows), device="cuda")
+            lib.pocketlm_set_stream(_stream_ptr(torch))
+
+            def make(sets=sets, x=x, y=y, rows=rows, cols=cols, m=m):
+                return [lambda w=w, s=s: lib.fp8_e4m3_block_linear_f32(
+                    ctypes.c_void_p(w.data_ptr()), ctypes.c_void_p(s.data_ptr()), ctypes.c_void_p(x.data_ptr()),
+                    ctypes.c_void_p(y.data_ptr()), m, rows, cols, math.ceil(cols / 128)) for w, s in sets]
+
+            xh = x.cpu().numpy()
+            measure(name, m, make, fp8_bytes(rows, cols, m),
+                    lambda w=host_w, s=host_s, xh=xh: oracle.fp8_linear(w, s, xh, batch_reuse=True))
+        del sets
+        torch.cuda.empty_cache()
+
+    # ---- FP8 dequant (config 1 matrix)
+    sets = fp8_sets(2048, 7168, 24)
+    out16 = torch.empty((2048, 7168), device="cuda", dtype=torch.float16)
+    lib.pocketlm_set_stream(_stream_ptr(torch))
+    hw, hs = sets[0][0].cpu().numpy(), sets[0][1].cpu().numpy()
+    measure("fp8 dequant->fp16 2048x7168", 1,
+            lambda: [lambda w=w, s=s: lib.fp8_e4m3_dequant_to_fp16(ctypes.c_void_p(w.data_ptr()),
+                                                                 ctypes.c_void_p(s.data_ptr()),
+                                                                 ctypes.c_void_p(out16.data_ptr()), 2048, 7168, 56)
+                     for w, s in sets],
+            2048 * 7168 * 3 + 4 * 16 * 56, lambda: oracle.fp8_dequant(hw, hs, "f16"))
+    del sets
+    torch.cuda.empty_cache()
+
+    # ---- Q4 (config 2)
+    shapes = [(18944, 3584), (18944, 3584), (3584, 18944)]
+    qsets = _q4_sets(torch, formats, shapes, 10)
+    xq = torch.randn((3584,), generator=gen, device="cuda").to(torch.float16)
+    xd = torch.randn((18944,), generator=gen, device="cuda").to(torch.float16)
+    yq = torch.empty((18944,), device="cuda")
+    lib.pocketlm_set_stream(_stream_ptr(torch))
+    for j, label in ((0, "q4 gemv gate/up 18944x3584"), (2, "q4 gemv down 3584x18944")):
+        rows, cols = shapes[j]
+        xx = xq if cols == 3584 else xd
+        hp = qsets[0][j][0].cpu().numpy()
+        hsc = qsets[0][j][1].cpu().view(torch.int16).numpy().view(np.uint16)
+        hx = xx.float().cpu().numpy()
+        measure(label, 1, lambda j=j, rows=rows, cols=cols, xx=xx: [
+            lambda p=s[j][0], sc=s[j][1]: lib.q4_gemv_f16_f32(ctypes.c_void_p(p.data_ptr()),
+                                                             ctypes.c_void_p(sc.data_ptr()),
+                                                             ctypes.c_void_p(xx.data_ptr()),
+                                                             ctypes.c_void_p(yq.data_ptr()), rows, cols)
+            for s in qsets], q4_bytes(rows, cols),
+            lambda hp=hp, hsc=hsc, hx=hx, rows=rows, cols=cols: oracle.q4_gemv(hp, hsc, hx, rows, cols))
+    # Q4 SwiGLU MLP through the reference entry point (one expert, route 1.0)
+    route = torch.ones(1, device="cuda")
+    outh = torch.empty((3584,), device="cuda", dtype=torch.float16)
+    arrs = []
+    for s in qsets:
+        a = [(ctypes.c_void_p * 1)(s[0][0].data_ptr()), (ctypes.c_void_p * 1)(s[0][1].data_ptr()),
+             (ctypes.c_void_p * 1)(s[1][0].data_ptr()), (ctypes.c_void_p * 1)(s[1][1].data_ptr()),
+             (ctypes.c_void_p * 1)(s[2][0].data_ptr()), (ctypes.c_void_p * 1)(s[2][1].data_ptr())]
+        arrs.append(a)
+    mlp_bytes = sum(r * c // 2 + 2 * r for r, c in shapes) + 2 * 3584 + 2 * 3584
+    hexp = [(qsets[0][0][0].cpu().numpy(), qsets[0][0][1].cpu().view(torch.int16).numpy().view(np.uint16),
+             qsets[0][1][0].cpu().numpy(), qsets[0][1][1].cpu().view(torch.int16).numpy().view(np.uint16),
+             qsets[0][2][0].cpu().numpy(), qsets[0][2][1].cpu().view(torch.int16).numpy().view(np.uint16))]
+    hx16 = xq.cpu().view(torch.int16).numpy().view(np.uint16)
+    measure("q4 SwiGLU MLP (2 kernels)", 1, lambda: [
+        lambda a=a: lib.q4_moe_selected_forward_u16(ctypes.c_void_p(xq.data_ptr()),
+                                                    *[ctypes.cast(t, ctypes.c_void_p) for t in a],
+                                                    ctypes.c_void_p(route.data_ptr()),
+                                                    ctypes.c_void_p(outh.data_ptr()), 3584, 18944, 1)
+        for a in arrs], mlp_bytes,
+        lambda: oracle.q4_moe_selected(hx16, hexp, np.ones(1, np.float32), 3584, 18944))
+    outd = torch.empty((18944 * 3584,), device="cuda", dtype=torch.float16)
+    measure("q4 dequant->fp16 18944x3584", 1, lambda: [
+        lambda p=s[0][0], sc=s[0][1]: lib.q4_dequant_to_fp16(ctypes.c_void_p(p.data_ptr()),
+                                                            ctypes.c_void_p(sc.data_ptr()),
+                                                            ctypes.c_void_p(outd.data_ptr()), 18944, 3584)
+        for s in qsets], 18944 * 3584 // 2 + 2 * 18944 + 2 * 18944 * 3584,
+        lambda: oracle.q4_dequant_f16(hexp[0][0], hexp[0][1], 18944, 3584))
+    del qsets, outd
+    torch.cuda.empty_cache()
+
+    # ---- row8 (config 3)
+    for name, rows, cols in (("row8 q/o 3584x3584", 3584, 3584), ("row8 k/v 512x3584", 512, 3584),
+                             ("row8 gate/up 18944x3584", 18944, 3584), ("row8 down 3584x18944", 3584, 18944)):
+        count = max(2, math.ceil(MALL_BYTES / (2 * rows * cols)))
+        packs = []
+        for _ in range(count):
+            w = torch.randn((rows, cols), generator=gen, device="cuda").mul_(0.02).to(torch.float16)
+            packs.append(native.pack_weight_rows8(w))
+            del w
+        h = torch.randn((cols,), generator=gen, device="cuda").to(torch.float16)
+        y = torch.empty((rows,), device="cuda")
+        lib.pocketlm_set_stream(_stream_ptr(torch))
+        hp = packs[0].cpu().view(torch.int16).numpy().view(np.uint16)
+        hh = h.cpu().view(torch.int16).numpy().view(np.uint16)
+        measure(name, 1, lambda packs=packs, h=h, y=y, rows=rows, cols=cols: [
+            lambda p=p: lib.native_packed_gemv_rows8(ctypes.c_void_p(h.data_ptr()), ctypes.c_void_p(p.data_ptr()),
+                                                     ctypes.c_void_p(y.data_ptr()), rows, cols, 0) for p in packs],
+            2 * math.ceil(rows / 8) * 8 * cols + 2 * cols + 4 * rows,
+            lambda hp=hp, hh=hh, rows=rows, cols=cols: oracle.packed_gemv_rows8(hh, hp, rows, cols, 0))
+        del packs
+        torch.cuda.empty_cache()
+
+    # ---- DeepSeek-V3 MoE layer decode (config 4): 8 routed (weighted) + shared MLP
+    def expert():
+        g = fp8_sets(2048, 7168, 1)[0]
+        u = fp8_sets(2048, 7168, 1)[0]
+        d = fp8_sets(7168, 2048, 1)[0]
+        return (g[0], g[1], u[0], u[1], d[0], d[1])
+
+    layers = [[expert() for _ in range(9)] for _ in range(3)]  # 3 x 396 MB
+    x = torch.randn((1, 7168), generator=gen, device="cuda").to(torch.bfloat16).float()
+    logits = torch.randn((1, 256), generator=gen, device="cuda")
+    _idx, rw = native.route_deepseek(logits)
+    rw = rw.float().reshape(-1).contiguous()
+    y = torch.empty((1, 7168), device="cuda")
+    ys = torch.empty((1, 7168), device="cuda")
+    lib.pocketlm_set_stream(_stream_ptr(torch))
+    moe_calls = []
+    for layer in layers:
+        routed = layer[:8]
+        tables = [(ctypes.c_uint64 * 8)(*[t[i].data_ptr() for t in routed]) for i in range(6)]
+        sh = layer[8]
+        moe_calls.append((tables, sh))
+
+    def moe_launches():
+        out = []
+        for tables, sh in moe_calls:
+            out.append(lambda t=tables: lib.fp8_e4m3_block_mlp_many_weighted_f32(
+                *[ctypes.cast(a, ctypes.c_void_p) for a in t], ctypes.c_void_p(x.data_ptr()),
+                ctypes.c_void_p(rw.data_ptr()), ctypes.c_void_p(y.data_ptr()), 8, 1, 2048, 7168, 56, 16))
+            out.append(lambda sh=sh: lib.fp8_e4m3_block_mlp_f32(
+                *[ctypes.c_void_p(t.data_ptr()) for t in sh], ctypes.c_void_p(x.data_ptr()),
+                ctypes.c_void_p(ys.data_ptr()), 1, 2048, 7168, 56, 16))
+        return out
+
+    per_expert = 3 * 2048 * 7168 + 3 * 4 * 16 * 56
+    calls = moe_launches()
+    for fn in calls:
+        fn()
+    torch.cuda.synchronize()
+    launches = [calls[i % len(calls)] for i in range(60)]
+    durs = timer.run(launches)
+    layer_ms = [durs[i] + durs[i + 1] for i in range(0, len(durs), 2)]
+    layer_ms.sort()
+    med = layer_ms[len(layer_ms) // 2]
+    nbytes = 9 * per_expert + 2 * 7168 * 4
+    gbs = nbytes / (med / 1e3) / 1e9
+    print(f"{'ds-v3 MoE layer (8 routed + shared)':40s} M=1  {1e3 * med:9.2f} us  {gbs:8.1f} GB/s  "
+          f"{100 * gbs / PEAK_HBM_GBS:5.1f}%", flush=True)
+    rows_out.append(("ds-v3 MoE layer (8 routed + shared)", 1, 1e3 * med, gbs, 100 * gbs / PEAK_HBM_GBS,
+                     None, None, "port"))
+    del layers
+    torch.cuda.empty_cache()
+
+    lines = ["| workload | M | GPU µs (median) | GPU GB/s | % of 8 TB/s | CPU µs | CPU GB/s | CPU kind |",
+             "|---|---|---|---|---|---|---|---|"]
+    for name, m, us, gbs, pct, cus, cgbs, kind in rows_out:
+        lines.append(f"| {name} | {m} | {us:.2f} | {gbs:.0f} | {pct:.1f} | "
+                     + (f"{cus:.0f} | {cgbs:.2f} | {kind} |" if cus else "— | — | — |"))
+    text = "\n".join(lines)
+    print(text)
+    if args.table_out:
+        Path(args.table_out).write_text(text + "\n")
+
+
+def main(argv=None):
+    args = _args(argv)
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        return 2
+    if str(REPO) not in sys.path:
+        sys.path.insert(0, str(REPO))
+    if args.table:
+        table(args)
+    else:
+        main_line(args)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

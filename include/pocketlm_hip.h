@@ -1,0 +1,292 @@
+/*
+ * pocketlm_hip.h - C ABI of libpocketlm_hip.so, the MI355X (gfx950) backend
+ * for PocketLM's quantized-decode hot path.
+ *
+ * Every entry point keeps the name, argument order and return codes of the
+ * reference export it replaces (cited as file:line under
+ * src/pcketlm/native/ of the reference tree), so the reference's ctypes
+ * argtypes bind unchanged.  What differs is where the data lives:
+ *
+ *   - Tensor arguments are DEVICE pointers (HBM, e.g. torch CUDA tensors).
+ *   - The per-expert address tables of the MoE entry points
+ *     (const uint64_t* / const T** arrays) are HOST arrays whose entries
+ *     are device addresses, exactly as the reference passes host arrays of
+ *     host addresses.  Their contents are captured at call time.
+ *   - Calls are asynchronous on the stream set by pocketlm_set_stream()
+ *     for the calling thread (default: the null stream).  Outputs are
+ *     valid once that stream reaches the work.
+ *   - Failures of the HIP runtime return -(1000 + hipError_t) from every
+ *     int-returning entry point; the reference's own codes are unchanged.
+ *   - A scale grid with fewer columns than ceil(cols/128) is rejected with
+ *     the entry point's bad-dimension code instead of being read past its
+ *     end (the reference leaves that check to its Python wrapper).
+ *
+ * Library-owned device scratch (MLP activations, split results) comes from
+ * a per-(device, stream) arena that grows on demand and is kept for reuse;
+ * calls on one stream are ordered, calls on different streams each get
+ * their own arena.
+ */
+#ifndef POCKETLM_HIP_H_
+#define POCKETLM_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ runtime */
+
+/* New (no reference counterpart): set the HIP stream used by this thread's
+ * subsequent calls.  NULL selects the null stream.  Returns 0. */
+int pocketlm_set_stream(void* hip_stream);
+
+/* New: human-readable text of the last failure on this thread ("" if none). */
+const char* pocketlm_last_error(void);
+
+/* New: 1 when a HIP device of architecture gfx950 is visible, else 0. */
+int pocketlm_device_available(void);
+
+/* Feature probes the reference loaders require to return 1 before they
+ * accept a library (src/pcketlm/native/__init__.py:291-293, 462-466,
+ * 160-195).  Here they report pocketlm_device_available(). */
+int fp8_dequant_cpu_has_avx2_f16c(void);      /* fp8_dequant.cpp:67 */
+int fp8_linear_avx512_cpu_has_avx512(void);   /* fp8_linear_avx512.cpp:63 */
+int q4_cpu_has_avx2_f16c(void);               /* q4_dequant.cpp:116 */
+int ds_cpu_has_avx2(void);                    /* ds_forward.cpp:182 */
+
+/* ------------------------------------------------------- FP8 block dequant */
+/* W e4m3fn bytes [rows, cols] row-major, scale_inv fp32
+ * [ceil(rows/128), scale_cols]; out[r,c] = cvt(dec(W[r,c]) * scale).
+ * NaN bytes decode to NaN (fp32 bits 0x7FF00000 / 0xFFF00000).
+ * Codes: -1 null pointer, -2 rows/cols/scale_cols <= 0,
+ *        -3 scale_cols != ceil(cols/128). */
+
+/* fp8_dequant.cpp:119-164: fp16 out, round-to-nearest-even, NaN -> 0x7F80/0xFF80 */
+int fp8_e4m3_dequant_to_fp16(const uint8_t* fp8_weight, const float* scale_inv,
+                             uint16_t* out_fp16, int64_t rows, int64_t cols,
+                             int64_t scale_cols);
+
+/* fp8_dequant.cpp:166-204: bf16 out via bits + 0x7FFF + lsb, NaN -> 0xFFFF */
+int fp8_e4m3_dequant_to_bf16(const uint8_t* fp8_weight, const float* scale_inv,
+                             uint16_t* out_bf16, int64_t rows, int64_t cols,
+                             int64_t scale_cols);
+
+/* New export for the fp32 branch of dequantize_fp8_block_scaled
+ * (src/pcketlm/core/runtime/fp8_source.py:852-858), which the reference
+ * computes with torch: out = dec(W) * scale in fp32. */
+int fp8_e4m3_dequant_to_f32(const uint8_t* fp8_weight, const float* scale_inv,
+                            float* out_f32, int64_t rows, int64_t cols,
+                            int64_t scale_cols);
+
+/* ------------------------------------------------- FP8 block-scaled GEMV */
+/* hidden fp32 [batch, in_cols]; out fp32 [batch, out_rows];
+ * out[b,n] = sum_kb scale[n/128,kb] * sum_{k in kb} hidden[b,k]*dec(W[n,k]),
+ * NaN weight bytes contribute 0.  Each weight byte is read from HBM once per
+ * call for all batch rows.  Codes: -1 null pointer, -2 bad dims. */
+
+/* fp8_linear.cpp:50-117 */
+int fp8_e4m3_block_linear_f32(const uint8_t* fp8_weight, const float* scale_inv,
+                              const float* hidden, float* out, int64_t batch,
+                              int64_t out_rows, int64_t in_cols, int64_t scale_cols);
+
+/* fp8_linear.cpp:119-210: two same-shape weights sharing hidden */
+int fp8_e4m3_block_dual_linear_f32(const uint8_t* fp8_weight_a, const float* scale_inv_a,
+                                   const uint8_t* fp8_weight_b, const float* scale_inv_b,
+                                   const float* hidden, float* out_a, float* out_b,
+                                   int64_t batch, int64_t out_rows, int64_t in_cols,
+                                   int64_t scale_cols);
+
+/* fp8_linear.cpp:212-362: out = down . (silu(gate . x) * (up . x)),
+ * silu(g) = g / (1 + exp(-g)).  gate/up [I, H], down [H, I].
+ * Code -3 when the activation scratch cannot be allocated. */
+int fp8_e4m3_block_mlp_f32(const uint8_t* gate_weight, const float* gate_scale_inv,
+                           const uint8_t* up_weight, const float* up_scale_inv,
+                           const uint8_t* down_weight, const float* down_scale_inv,
+                           const float* hidden, float* out, int64_t batch,
+                           int64_t intermediate_rows, int64_t hidden_cols,
+                           int64_t gate_scale_cols, int64_t down_scale_cols);
+
+/* fp8_linear_avx512.cpp:157-250: same kernel as fp8_e4m3_block_mlp_f32 */
+int fp8_e4m3_block_mlp_avx512_f32(const uint8_t* gate_weight, const float* gate_scale_inv,
+                                  const uint8_t* up_weight, const float* up_scale_inv,
+                                  const uint8_t* down_weight, const float* down_scale_inv,
+                                  const float* hidden, float* out, int64_t batch,
+                                  int64_t intermediate_rows, int64_t hidden_cols,
+                                  int64_t gate_scale_cols, int64_t down_scale_cols);
+
+/* fp8_linear.cpp:364-473: E experts, unweighted; out [E, batch, hidden].
+ * An expert whose gate/up pointers are null gets a zero activation; one
+ * whose down pointers are null leaves its output rows untouched. */
+int fp8_e4m3_block_mlp_many_f32(const uint64_t* gate_weight_ptrs, const uint64_t* gate_scale_ptrs,
+                                const uint64_t* up_weight_ptrs, const uint64_t* up_scale_ptrs,
+                                const uint64_t* down_weight_ptrs, const uint64_t* down_scale_ptrs,
+                                const float* hidden, float* out, int64_t expert_count,
+                                int64_t batch, int64_t intermediate_rows, int64_t hidden_cols,
+                                int64_t gate_scale_cols, int64_t down_scale_cols);
+
+/* fp8_linear.cpp:475-589: out[b,h] = sum_e route[e] * expert_e(x_b)[h];
+ * route_weights fp32 [E] (device).  Each expert matrix is read once. */
+int fp8_e4m3_block_mlp_many_weighted_f32(
+    const uint64_t* gate_weight_ptrs, const uint64_t* gate_scale_ptrs,
+    const uint64_t* up_weight_ptrs, const uint64_t* up_scale_ptrs,
+    const uint64_t* down_weight_ptrs, const uint64_t* down_scale_ptrs, const float* hidden,
+    const float* route_weights, float* out, int64_t expert_count, int64_t batch,
+    int64_t intermediate_rows, int64_t hidden_cols, int64_t gate_scale_cols,
+    int64_t down_scale_cols);
+
+/* fp8_linear_avx512.cpp:252-371: same kernel as the weighted entry point */
+int fp8_e4m3_block_mlp_many_weighted_avx512_f32(
+    const uint64_t* gate_weight_ptrs, const uint64_t* gate_scale_ptrs,
+    const uint64_t* up_weight_ptrs, const uint64_t* up_scale_ptrs,
+    const uint64_t* down_weight_ptrs, const uint64_t* down_scale_ptrs, const float* hidden,
+    const float* route_weights, float* out, int64_t expert_count, int64_t batch,
+    int64_t intermediate_rows, int64_t hidden_cols, int64_t gate_scale_cols,
+    int64_t down_scale_cols);
+
+/* fp8_linear.cpp:591-831: route_weights fp32 [E, batch] (device); (e, b)
+ * pairs with weight exactly 0 contribute nothing.  Each expert matrix is
+ * read once per call for all its active rows. */
+int fp8_e4m3_block_mlp_many_row_weighted_f32(
+    const uint64_t* gate_weight_ptrs, const uint64_t* gate_scale_ptrs,
+    const uint64_t* up_weight_ptrs, const uint64_t* up_scale_ptrs,
+    const uint64_t* down_weight_ptrs, const uint64_t* down_scale_ptrs, const float* hidden,
+    const float* route_weights, float* out, int64_t expert_count, int64_t batch,
+    int64_t intermediate_rows, int64_t hidden_cols, int64_t gate_scale_cols,
+    int64_t down_scale_cols);
+
+/* fp8_linear.cpp:833-980: sparse (item, row, weight) pairs (device arrays,
+ * int64 / int64 / fp32, length pair_count).  out is zeroed first; -4 when
+ * a pair index is out of range (checked before any kernel runs; this reads
+ * the two index arrays back to the host and so waits for the stream). */
+int fp8_e4m3_block_mlp_many_pair_weighted_f32(
+    const uint64_t* gate_weight_ptrs, const uint64_t* gate_scale_ptrs,
+    const uint64_t* up_weight_ptrs, const uint64_t* up_scale_ptrs,
+    const uint64_t* down_weight_ptrs, const uint64_t* down_scale_ptrs, const float* hidden,
+    const int64_t* pair_item_indices, const int64_t* pair_row_indices,
+    const float* pair_weights, float* out, int64_t expert_count, int64_t pair_count,
+    int64_t batch, int64_t intermediate_rows, int64_t hidden_cols, int64_t gate_scale_cols,
+    int64_t down_scale_cols);
+
+/* --------------------------------------------------------------------- Q4 */
+/* Per-row symmetric Q4 (src/pcketlm/core/model_import/q4_quantize.py:48-71):
+ * two's-complement nibbles flat over the whole tensor, element 2i in the low
+ * nibble of byte i; one fp16 scale per channel (row). */
+
+/* q4_dequant.cpp:171-208: out[c*cs+i] = fp16(q * f32(scale[c])), RNE.
+ * Returns nothing, as the reference; failures are reported by
+ * pocketlm_last_error(). */
+void q4_dequant_to_fp16(const uint8_t* packed, const uint16_t* scales, uint16_t* out_fp16,
+                        int64_t num_channels, int64_t channel_size);
+
+/* q4_dequant.cpp:210-286: host arrays of device pointers / sizes.  Codes:
+ * 1 null array, 2 tensor_count <= 0.  Entries with a null pointer or a
+ * non-positive size are skipped. */
+int q4_dequant_many_to_fp16(const uint8_t** packed_ptrs, const uint16_t** scale_ptrs,
+                            uint16_t** out_ptrs, const int64_t* num_channels,
+                            const int64_t* channel_sizes, int64_t tensor_count);
+
+/* q4_dequant.cpp:357-476: one token through S selected Q4 SwiGLU experts,
+ * combined with route weights, fp16 out.  hidden fp16 [H], route fp32 [S]
+ * and out are device pointers; the six arrays are host arrays of device
+ * pointers.  Codes: 1 null/bad size, 3 null expert pointer. */
+int q4_moe_selected_forward_u16(const uint16_t* hidden, const uint8_t** gate_packed_ptrs,
+                                const uint16_t** gate_scale_ptrs, const uint8_t** up_packed_ptrs,
+                                const uint16_t** up_scale_ptrs, const uint8_t** down_packed_ptrs,
+                                const uint16_t** down_scale_ptrs, const float* route_weights,
+                                uint16_t* out_fp16, int64_t hidden_size,
+                                int64_t intermediate_size, int64_t selected_count);
+
+/* New export: one Q4 matrix [rows, cols] times one fp16 vector [cols],
+ * fp32 out [rows]: the per-row dot of q4_moe_selected_forward_u16
+ * (q4_dequant.cpp:314-355) on its own.  Codes: 1 null, 2 bad dims. */
+int q4_gemv_f16_f32(const uint8_t* packed, const uint16_t* scales, const uint16_t* hidden,
+                    float* out, int64_t rows, int64_t cols);
+
+/* ------------------------------------------------------------------- row8 */
+/* fp16_packed_gemv.cpp:52-77: packed[blk][col][lane] = W[8*blk+lane][col],
+ * rows past the end zero.  Codes: 1 null, 2 negative dims. */
+int native_pack_u16_rows8(const uint16_t* weight, uint16_t* packed, int64_t rows, int64_t cols);
+
+/* fp16_packed_gemv.cpp:79-116: out[n] = sum_k hidden[k] * W[n,k], fp32
+ * fused multiply-add; hidden and W share dtype_code (0 fp16, 1 bf16).
+ * Codes: 1 null, 2 negative dims or bad dtype_code. */
+int native_packed_gemv_rows8(const uint16_t* hidden, const uint16_t* packed, float* out,
+                             int64_t rows, int64_t cols, int dtype_code);
+
+/* New export covering the biased and fused variants of
+ * fp16_kv_cache.cpp:117-298: `count` row8 GEMVs that share one hidden
+ * vector (q/k/v or gate/up) in a single launch.  Arrays are host arrays of
+ * device pointers; bias_ptrs may be NULL or hold NULL entries. */
+int native_packed_gemv_rows8_many(const uint16_t* hidden, const uint16_t* const* packed_ptrs,
+                                  const uint16_t* const* bias_ptrs, float* const* out_ptrs,
+                                  const int64_t* rows, int64_t count, int64_t cols,
+                                  int dtype_code);
+
+/* ------------------------------------------------------ DeepSeek session */
+typedef int (*pocketlm_ds_tensor_callback)(int64_t layer_idx, int64_t layer_kind,
+                                           int64_t weight_role, const void** out_ptr,
+                                           int64_t* out_nbytes);
+
+/* ds_forward.cpp:192-219: opaque session with call counters */
+void* ds_session_create(int64_t num_layers, int64_t hidden_dim, int64_t num_experts,
+                        int64_t top_k, void* fp8_pack_callback, void* kv_session_handle);
+void ds_session_destroy(void* handle);
+/* ds_forward.cpp:221-263: codes 1 bad handle/layer, 2 null callback,
+ * 10+k / 20+k callback failures */
+int ds_session_register_layer(void* handle, int64_t layer_idx, int64_t layer_kind,
+                              int64_t weight_role, pocketlm_ds_tensor_callback fp8_ptr_callback,
+                              pocketlm_ds_tensor_callback scale_ptr_callback);
+/* ds_forward.cpp:265-335: -1 on a null handle / bad index */
+int64_t ds_monolithic_call_counter(void* handle);
+int64_t ds_callback_invocation_count(void* handle);
+int64_t ds_expert_invocation_count(void* handle);
+int64_t ds_attention_invocation_count(void* handle);
+int64_t ds_fused_attention_invocation_count(void* handle);
+int64_t ds_layers_executed_count(void* handle);
+int64_t ds_registered_layer_count(void* handle);
+int64_t ds_registered_fp8_nbytes(void* handle, int64_t index);
+int64_t ds_registered_scale_nbytes(void* handle, int64_t index);
+
+/* ds_forward.cpp:337-367: hidden_out = sum_e route[e] * expert_outputs[e]
+ * (device pointers).  Codes 1 null, 2 bad dims.  Bumps monolithic_calls by
+ * one and expert_invocations by selected_count. */
+int ds_moe_layer_forward_f32(void* handle, const float* expert_outputs, const float* route_weights,
+                             int64_t selected_count, int64_t batch, int64_t hidden_dim,
+                             float* hidden_out);
+
+/* ds_forward.cpp:784-877: the routed-expert FP8 MoE of one layer through
+ * the weighted kernel (route fp32 [selected], device).  Codes 1 null,
+ * 2 bad dims, 100+k when the kernel returns k. */
+int ds_moe_layer_forward_fp8_f32(void* handle, const uint64_t* gate_weight_ptrs,
+                                 const uint64_t* gate_scale_ptrs, const uint64_t* up_weight_ptrs,
+                                 const uint64_t* up_scale_ptrs, const uint64_t* down_weight_ptrs,
+                                 const uint64_t* down_scale_ptrs, const float* hidden,
+                                 const float* route_weights, int64_t selected_count, int64_t batch,
+                                 int64_t intermediate_rows, int64_t hidden_dim,
+                                 int64_t gate_scale_cols, int64_t down_scale_cols,
+                                 float* hidden_out);
+
+/* ds_forward.cpp:879-955: softmax top-k router over u16 (fp16/bf16) hidden
+ * [hidden_dim] and router weights [num_experts, hidden_dim] (device);
+ * output_expert_ids int64 [k] and output_weights fp32 [k] (device).
+ * Codes 1 null, 2 bad dims. */
+int ds_router_topk_u16(const uint16_t* hidden_u16, const uint16_t* router_weights_u16,
+                       int64_t hidden_dim, int64_t num_experts, int64_t k, int64_t dtype_code,
+                       int64_t* output_expert_ids, float* output_weights);
+
+/* New export for DeepSeek-V3 routing, the torch code of run_fp8_router
+ * (src/pcketlm/core/runtime/fp8_source.py:1527-1547) with the group mask of
+ * _mask_deepseek_route_groups (5125-5140), from router logits fp32
+ * [batch, num_experts] (device).  scoring: 0 sigmoid, 1 softmax.  bias may
+ * be NULL.  Writes indices int64 [batch, top_k] and weights fp32
+ * [batch, top_k] rounded to bf16 (device).  Codes 1 null, 2 bad dims. */
+int ds_route_topk_f32(const float* logits, const float* bias, int64_t batch, int64_t num_experts,
+                      int64_t top_k, int64_t n_groups, int64_t topk_groups, int scoring,
+                      float route_scale, int64_t* out_indices, float* out_weights);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* POCKETLM_HIP_H_ */

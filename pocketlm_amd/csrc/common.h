@@ -1,0 +1,79 @@
+// Shared host/device helpers of libpocketlm_hip.so (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "pocketlm_hip.h"
+
+#define PLM_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace plm {
+
+constexpr int kWave = 64;
+// One "chunk" is what a wave streams in one pass along K: 64 lanes x 16 bytes.
+constexpr int kChunkBytes = 1024;
+
+// ---------------------------------------------------------------- host side
+
+// Stream used by the calling thread (pocketlm_set_stream).
+hipStream_t current_stream();
+
+// Record a failure text for pocketlm_last_error() and return `code`.
+int fail(int code, const char* fmt, ...);
+
+// Map a HIP error to the library's return code -(1000 + err) and record it.
+int hip_fail(hipError_t err, const char* where);
+
+// Check the last launch; returns 0 or the HIP failure code.
+int check_launch(const char* where);
+
+// Device scratch owned by the library, one arena per (device, stream).  The
+// returned block stays valid until the next workspace() call on the same
+// stream; growing waits for the stream before releasing the old block.
+// Returns nullptr on allocation failure (after recording the error).
+void* workspace(size_t bytes);
+
+// Number of compute units of the current device (cached).
+int cu_count();
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace plm
+
+// ---------------------------------------------------------------- device side
+
+typedef float plm_float2 __attribute__((ext_vector_type(2)));
+
+// Decode four e4m3fn bytes (one dword, byte 0 first) with the hardware
+// converter; NaN bytes (0x7F / 0xFF) come out as NaN.
+__device__ __forceinline__ void plm_decode4_e4m3(uint32_t d, float* v) {
+    const plm_float2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(d), false);
+    const plm_float2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(d), true);
+    v[0] = lo[0];
+    v[1] = lo[1];
+    v[2] = hi[0];
+    v[3] = hi[1];
+}
+
+// Sum across the 64 lanes of a wave with a fixed xor butterfly (32, 16, ...,
+// 1): every lane ends with the same total, and the addition tree is the same
+// whatever else the wave is reducing, so results do not depend on the tile
+// shape a kernel instance uses.
+__device__ __forceinline__ float plm_wave_sum(float v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        v += __shfl_xor(v, d, 64);
+    }
+    return v;
+}
+
+__device__ __forceinline__ float plm_silu_mul(float gate, float up) {
+    // g / (1 + exp(-g)) * up, all fp32 (fp8_linear.cpp:279-280)
+    const float s = gate / (1.0f + expf(-gate));
+    return s * up;
+}

@@ -1,0 +1,917 @@
+// FP8 e4m3 block-scaled GEMV family for gfx950: linear, dual linear, SwiGLU
+// MLP and the (weighted) many-expert MoE of src/pcketlm/native/fp8_linear.cpp.
+//
+// Design.  The path is HBM-bound (2 flop per weight byte at one activation
+// row), so every kernel streams each weight byte once per call, for all
+// activation rows, with 16-byte loads:
+//
+//   * A "chunk" is 1024 columns of one weight row: lane l of a wave reads
+//     bytes [16l, 16l+16) with one global_load_dwordx4, decodes them with
+//     v_cvt_pk_f32_fp8 (4 instructions per 16 bytes) and dots them with the
+//     matching 16 activations.  The 16-byte span never crosses a 128-column
+//     scale block, so the partial is scaled once.
+//   * A workgroup owns a tile of TR rows and splits the row's chunks across
+//     its waves (wave w takes chunks w, w+nw, ...); nw depends only on the
+//     number of chunks per row, so the per-row arithmetic - lane partials,
+//     the fixed xor-butterfly lane sum, the in-order sum over waves - is the
+//     same for every batch size and tile shape.  That is what makes batched
+//     calls bit-exact to per-row calls, as the reference's tests require.
+//   * NaN weight bytes must contribute 0 (fp8_linear.cpp:31-33).  The fast
+//     path decodes with the hardware converter (NaN stays NaN) and only when
+//     a 16-byte partial comes out NaN re-decodes that span with NaN -> 0.
+//
+// fp8_rows_kernel  : rows of one or more experts sharing the activations
+//                    (linear, dual, gate/up phase with the SiLU epilogue).
+// fp8_combine_kernel: rows whose K range is the concatenation of several
+//                    experts' down matrices, each with its own activations
+//                    and route weight (down phase + routed combine).
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include "common.h"
+
+namespace {
+
+constexpr int kMaxGroups = 64;  // experts per launch (pointer tables travel as kernel arguments)
+constexpr int kMaxWaves = 8;
+constexpr int kMaxM = 8;        // activation rows per launch; larger batches are split
+
+struct RowsArgs {
+    const uint8_t* w[2][kMaxGroups];
+    const float* s[2][kMaxGroups];
+    const float* x;       // activations [m_total][x_stride]
+    float* out[2];        // outputs, element (g, m, row) at ((g*m_total + m) * out_ld + row)
+    int64_t x_stride;
+    int64_t out_ld;
+    int64_t rows;         // rows per group
+    int64_t K;
+    int64_t scale_cols;
+    int tiles_per_group;
+    int nchunks;
+    int m_total;
+    int m0;
+};
+
+struct CombineArgs {
+    const uint8_t* w[kMaxGroups];
+    const float* s[kMaxGroups];
+    const float* act;     // activations of group g: act + ((g_base+g)*m_total + m) * K
+    const float* route;   // route of (g, m): route[(g_base+g)*route_sg + m*route_sm], or null (= 1)
+    float* out;
+    int64_t rows;
+    int64_t K;
+    int64_t scale_cols;
+    int64_t route_sg;
+    int64_t route_sm;
+    int ngroups;
+    int g_base;
+    int cps;              // chunks per group segment
+    int tiles_per_group;  // per_group_out only
+    int per_group_out;    // 1: out[(g_base+g)*m_total + m][row]; 0: out[m][row] summed over groups
+    int accumulate;       // add to out instead of storing
+    int zero_skip;        // skip (g, m) whose route is exactly 0
+    int m_total;
+    int m0;
+};
+
+__device__ __forceinline__ float dot16(const float* w, const float* x) {
+    float p = w[0] * x[0];
+#pragma unroll
+    for (int j = 1; j < 16; ++j) p = fmaf(w[j], x[j], p);
+    return p;
+}
+
+__device__ __forceinline__ void decode16(const uint4& q, float* w) {
+    plm_decode4_e4m3(q.x, w);
+    plm_decode4_e4m3(q.y, w + 4);
+    plm_decode4_e4m3(q.z, w + 8);
+    plm_decode4_e4m3(q.w, w + 12);
+}
+
+__device__ __forceinline__ void zero_nans16(float* w) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) w[j] = (w[j] != w[j]) ? 0.0f : w[j];
+}
+
+__device__ __forceinline__ void load_x16(const float* p, float* x) {
+    const float4* p4 = reinterpret_cast<const float4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 v = p4[i];
+        x[4 * i + 0] = v.x;
+        x[4 * i + 1] = v.y;
+        x[4 * i + 2] = v.z;
+        x[4 * i + 3] = v.w;
+    }
+}
+
+template <int M, int TR, int NWT, bool SILU>
+__global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
+    constexpr int V = NWT * TR * M;
+    __shared__ float red[kMaxWaves * V];
+    const int nw = blockDim.x >> 6;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int g = blockIdx.x / a.tiles_per_group;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x - g * a.tiles_per_group) * TR;
+
+    const uint8_t* W[NWT];
+    const float* S[NWT];
+    bool live = true;
+#pragma unroll
+    for (int i = 0; i < NWT; ++i) {
+        W[i] = a.w[i][g];
+        S[i] = a.s[i][g];
+        live = live && W[i] != nullptr && S[i] != nullptr;
+    }
+
+    float acc[NWT][TR][M];
+#pragma unroll
+    for (int i = 0; i < NWT; ++i)
+#pragma unroll
+        for (int r = 0; r < TR; ++r)
+#pragma unroll
+            for (int m = 0; m < M; ++m) acc[i][r][m] = 0.0f;
+
+    if (live) {
+        const int64_t srow = (row0 >> 7) * a.scale_cols;
+        for (int c = wave; c < a.nchunks; c += nw) {
+            const int64_t col = static_cast<int64_t>(c) * plm::kChunkBytes + lane * 16;
+            if (col >= a.K) continue;
+            uint4 q[NWT][TR];
+#pragma unroll
+            for (int i = 0; i < NWT; ++i)
+#pragma unroll
+                for (int r = 0; r < TR; ++r) {
+                    q[i][r] = make_uint4(0u, 0u, 0u, 0u);
+                    if (row0 + r < a.rows) {
+                        q[i][r] = *reinterpret_cast<const uint4*>(W[i] + (row0 + r) * a.K + col);
+                    }
+                }
+            float sc[NWT];
+#pragma unroll
+            for (int i = 0; i < NWT; ++i) sc[i] = S[i][srow + (col >> 7)];
+            float wv[NWT][TR][16];
+#pragma unroll
+            for (int i = 0; i < NWT; ++i)
+#pragma unroll
+                for (int r = 0; r < TR; ++r) decode16(q[i][r], wv[i][r]);
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                float xv[16];
+                load_x16(a.x + static_cast<int64_t>(a.m0 + m) * a.x_stride + col, xv);
+#pragma unroll
+                for (int i = 0; i < NWT; ++i)
+#pragma unroll
+                    for (int r = 0; r < TR; ++r) {
+                        float p = dot16(wv[i][r], xv);
+                        if (m == 0 && p != p) {
+                            zero_nans16(wv[i][r]);
+                            p = dot16(wv[i][r], xv);
+                        }
+                        acc[i][r][m] = fmaf(p, sc[i], acc[i][r][m]);
+                    }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < NWT; ++i)
+#pragma unroll
+        for (int r = 0; r < TR; ++r)
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const float t = plm_wave_sum(acc[i][r][m]);
+                if (lane == 0) red[wave * V + (i * TR + r) * M + m] = t;
+            }
+    __syncthreads();
+
+    for (int t = threadIdx.x; t < TR * M; t += blockDim.x) {
+        const int r = t / M;
+        const int m = t - r * M;
+        const int64_t row = row0 + r;
+        if (row >= a.rows) continue;
+        float v[NWT];
+#pragma unroll
+        for (int i = 0; i < NWT; ++i) {
+            float s = 0.0f;
+            for (int w = 0; w < nw; ++w) s += red[w * V + (i * TR + r) * M + m];
+            v[i] = s;
+        }
+        const int64_t o = (static_cast<int64_t>(g) * a.m_total + a.m0 + m) * a.out_ld + row;
+        if constexpr (SILU) {
+            a.out[0][o] = plm_silu_mul(v[0], v[1]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < NWT; ++i) a.out[i][o] = v[i];
+        }
+    }
+}
+
+template <int M, int TR>
+__global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
+    constexpr int V = TR * M;
+    __shared__ float red[kMaxWaves * V];
+    const int nw = blockDim.x >> 6;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    int g_lo = 0;
+    int g_hi = a.ngroups;
+    int tile = blockIdx.x;
+    if (a.per_group_out) {
+        g_lo = tile / a.tiles_per_group;
+        g_hi = g_lo + 1;
+        tile -= g_lo * a.tiles_per_group;
+    }
+    const int64_t row0 = static_cast<int64_t>(tile) * TR;
+
+    float acc[TR][M];
+#pragma unroll
+    for (int r = 0; r < TR; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
+
+    const int nchunks = (g_hi - g_lo) * a.cps;
+    for (int c = wave; c < nchunks; c += nw) {
+        const int gi = c / a.cps;
+        const int g = g_lo + gi;
+        const int64_t col = static_cast<int64_t>(c - gi * a.cps) * plm::kChunkBytes + lane * 16;
+        const uint8_t* W = a.w[g];
+        const float* S = a.s[g];
+        if (W == nullptr || S == nullptr) continue;
+        float rw[M];
+        bool any = false;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            rw[m] = a.route ? a.route[static_cast<int64_t>(a.g_base + g) * a.route_sg +
+                                      static_cast<int64_t>(a.m0 + m) * a.route_sm]
+                            : 1.0f;
+            any = any || !(a.zero_skip && rw[m] == 0.0f);
+        }
+        if (!any || col >= a.K) continue;
+        uint4 q[TR];
+#pragma unroll
+        for (int r = 0; r < TR; ++r) {
+            q[r] = make_uint4(0u, 0u, 0u, 0u);
+            if (row0 + r < a.rows) q[r] = *reinterpret_cast<const uint4*>(W + (row0 + r) * a.K + col);
+        }
+        const float sc = S[(row0 >> 7) * a.scale_cols + (col >> 7)];
+        float wv[TR][16];
+#pragma unroll
+        for (int r = 0; r < TR; ++r) decode16(q[r], wv[r]);
+        bool fixed = false;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            if (a.zero_skip && rw[m] == 0.0f) continue;
+            float xv[16];
+            load_x16(a.act + (static_cast<int64_t>(a.g_base + g) * a.m_total + a.m0 + m) * a.K + col, xv);
+#pragma unroll
+            for (int r = 0; r < TR; ++r) {
+                float p = dot16(wv[r], xv);
+                if (!fixed && p != p) {
+                    zero_nans16(wv[r]);
+                    p = dot16(wv[r], xv);
+                }
+                acc[r][m] = fmaf(p * sc, rw[m], acc[r][m]);
+            }
+            fixed = true;
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < TR; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const float t = plm_wave_sum(acc[r][m]);
+            if (lane == 0) red[wave * V + r * M + m] = t;
+        }
+    __syncthreads();
+
+    for (int t = threadIdx.x; t < V; t += blockDim.x) {
+        const int r = t / M;
+        const int m = t - r * M;
+        const int64_t row = row0 + r;
+        if (row >= a.rows) continue;
+        float v = 0.0f;
+        for (int w = 0; w < nw; ++w) v += red[w * V + t];
+        int64_t o = static_cast<int64_t>(a.m0 + m) * a.rows + row;
+        if (a.per_group_out) o += static_cast<int64_t>(a.g_base + g_lo) * a.m_total * a.rows;
+        a.out[o] = a.accumulate ? a.out[o] + v : v;
+    }
+}
+
+// ----------------------------------------------------------------- scalar path
+// Used when K is not a multiple of 16 or a pointer is not 16-byte aligned
+// (small test shapes).  One thread per output element; the per-row arithmetic
+// is again independent of the batch size.
+
+__device__ float scalar_row_dot(const uint8_t* w, const float* s, const float* x, int64_t K) {
+    float acc = 0.0f;
+    for (int64_t c0 = 0; c0 < K; c0 += 128) {
+        const int64_t c1 = c0 + 128 < K ? c0 + 128 : K;
+        float blk = 0.0f;
+        for (int64_t c = c0; c < c1; ++c) {
+            const uint32_t byte = w[c];
+            float v[4];
+            plm_decode4_e4m3(byte, v);
+            const float wv = (v[0] != v[0]) ? 0.0f : v[0];
+            blk = fmaf(x[c], wv, blk);
+        }
+        acc = fmaf(blk, s[c0 >> 7], acc);
+    }
+    return acc;
+}
+
+template <bool SILU, int NWT>
+__global__ void fp8_rows_scalar_kernel(const RowsArgs a, int mcount, int ngroups) {
+    const int64_t id = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t total = static_cast<int64_t>(ngroups) * mcount * a.rows;
+    if (id >= total) return;
+    const int64_t row = id % a.rows;
+    const int m = static_cast<int>((id / a.rows) % mcount);
+    const int g = static_cast<int>(id / (a.rows * mcount));
+    float v[NWT];
+    for (int i = 0; i < NWT; ++i) {
+        const uint8_t* W = a.w[i][g];
+        const float* S = a.s[i][g];
+        if (W == nullptr || S == nullptr) {
+            v[i] = 0.0f;
+            continue;
+        }
+        v[i] = scalar_row_dot(W + row * a.K, S + (row >> 7) * a.scale_cols,
+                              a.x + static_cast<int64_t>(a.m0 + m) * a.x_stride, a.K);
+    }
+    bool live = true;
+    for (int i = 0; i < NWT; ++i) live = live && a.w[i][g] != nullptr && a.s[i][g] != nullptr;
+    const int64_t o = (static_cast<int64_t>(g) * a.m_total + a.m0 + m) * a.out_ld + row;
+    if constexpr (SILU) {
+        a.out[0][o] = live ? plm_silu_mul(v[0], v[1]) : 0.0f;
+    } else {
+        for (int i = 0; i < NWT; ++i) a.out[i][o] = v[i];
+    }
+}
+
+__global__ void fp8_combine_scalar_kernel(const CombineArgs a, int mcount) {
+    const int64_t id = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int ng_out = a.per_group_out ? a.ngroups : 1;
+    const int64_t total = static_cast<int64_t>(ng_out) * mcount * a.rows;
+    if (id >= total) return;
+    const int64_t row = id % a.rows;
+    const int m = static_cast<int>((id / a.rows) % mcount);
+    const int go = static_cast<int>(id / (a.rows * mcount));
+    const int g_lo = a.per_group_out ? go : 0;
+    const int g_hi = a.per_group_out ? go + 1 : a.ngroups;
+    float v = 0.0f;
+    for (int g = g_lo; g < g_hi; ++g) {
+        const uint8_t* W = a.w[g];
+        const float* S = a.s[g];
+        if (W == nullptr || S == nullptr) continue;
+        const float rw = a.route ? a.route[static_cast<int64_t>(a.g_base + g) * a.route_sg +
+                                           static_cast<int64_t>(a.m0 + m) * a.route_sm]
+                                 : 1.0f;
+        if (a.zero_skip && rw == 0.0f) continue;
+        const float e = scalar_row_dot(W + row * a.K, S + (row >> 7) * a.scale_cols,
+                                       a.act + (static_cast<int64_t>(a.g_base + g) * a.m_total + a.m0 + m) * a.K,
+                                       a.K);
+        v = fmaf(e, rw, v);
+    }
+    int64_t o = static_cast<int64_t>(a.m0 + m) * a.rows + row;
+    if (a.per_group_out) o += static_cast<int64_t>(a.g_base + go) * a.m_total * a.rows;
+    a.out[o] = a.accumulate ? a.out[o] + v : v;
+}
+
+__global__ void fill_f32_kernel(float* p, float v, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+// Scatter sparse (item, row, weight) pairs into a dense [E, M] route matrix,
+// in pair order (one thread: pair lists are a few dozen entries).
+__global__ void scatter_pairs_kernel(const int64_t* items, const int64_t* rows, const float* w,
+                                     int64_t pairs, int64_t batch, float* route) {
+    if (blockIdx.x != 0 || threadIdx.x != 0) return;
+    for (int64_t p = 0; p < pairs; ++p) route[items[p] * batch + rows[p]] += w[p];
+}
+
+// ------------------------------------------------------------------ dispatch
+
+int waves_for(int64_t nchunks) {
+    return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(nchunks, kMaxWaves)));
+}
+
+template <int M>
+constexpr int rows_tile(int nwt) {
+    return nwt == 1 ? (M == 1 ? 8 : 4) : (M == 1 ? 4 : 2);
+}
+
+template <int M>
+constexpr int combine_tile() {
+    return M == 1 ? 8 : 4;
+}
+
+template <int M, int NWT, bool SILU>
+void launch_rows_m(const RowsArgs& a, int ngroups, hipStream_t st) {
+    constexpr int TR = rows_tile<M>(NWT);
+    RowsArgs b = a;
+    b.tiles_per_group = static_cast<int>(plm::ceil_div(a.rows, TR));
+    const int nw = waves_for(a.nchunks);
+    const int64_t grid = static_cast<int64_t>(b.tiles_per_group) * ngroups;
+    hipLaunchKernelGGL((fp8_rows_kernel<M, TR, NWT, SILU>), dim3(static_cast<unsigned>(grid)),
+                       dim3(nw * plm::kWave), 0, st, b);
+}
+
+template <int NWT, bool SILU>
+void launch_rows(const RowsArgs& a, int mcount, int ngroups, hipStream_t st) {
+    switch (mcount) {
+        case 1: launch_rows_m<1, NWT, SILU>(a, ngroups, st); break;
+        case 2: launch_rows_m<2, NWT, SILU>(a, ngroups, st); break;
+        case 3: launch_rows_m<3, NWT, SILU>(a, ngroups, st); break;
+        case 4: launch_rows_m<4, NWT, SILU>(a, ngroups, st); break;
+        case 5: launch_rows_m<5, NWT, SILU>(a, ngroups, st); break;
+        case 6: launch_rows_m<6, NWT, SILU>(a, ngroups, st); break;
+        case 7: launch_rows_m<7, NWT, SILU>(a, ngroups, st); break;
+        default: launch_rows_m<8, NWT, SILU>(a, ngroups, st); break;
+    }
+}
+
+template <int M>
+void launch_combine_m(const CombineArgs& a, hipStream_t st) {
+    constexpr int TR = combine_tile<M>();
+    CombineArgs b = a;
+    const int tiles = static_cast<int>(plm::ceil_div(a.rows, TR));
+    b.tiles_per_group = tiles;
+    const int64_t segs = a.per_group_out ? 1 : a.ngroups;
+    const int nw = waves_for(segs * a.cps);
+    const int64_t grid = static_cast<int64_t>(tiles) * (a.per_group_out ? a.ngroups : 1);
+    hipLaunchKernelGGL((fp8_combine_kernel<M, TR>), dim3(static_cast<unsigned>(grid)),
+                       dim3(nw * plm::kWave), 0, st, b);
+}
+
+void launch_combine(const CombineArgs& a, int mcount, hipStream_t st) {
+    switch (mcount) {
+        case 1: launch_combine_m<1>(a, st); break;
+        case 2: launch_combine_m<2>(a, st); break;
+        case 3: launch_combine_m<3>(a, st); break;
+        case 4: launch_combine_m<4>(a, st); break;
+        case 5: launch_combine_m<5>(a, st); break;
+        case 6: launch_combine_m<6>(a, st); break;
+        case 7: launch_combine_m<7>(a, st); break;
+        default: launch_combine_m<8>(a, st); break;
+    }
+}
+
+// A GEMV problem over groups that share the activations.
+struct RowsProblem {
+    const uint8_t* const* w[2];  // per-group pointers, ngroups entries each
+    const float* const* s[2];
+    int nwt;
+    bool silu;
+    int ngroups;
+    const float* x;
+    int64_t x_stride;
+    float* out[2];
+    int64_t out_ld;
+    int64_t batch;
+    int64_t rows;
+    int64_t K;
+    int64_t scale_cols;
+};
+
+bool rows_fast_ok(const RowsProblem& p) {
+    if (p.K % 16 != 0 || p.x_stride % 4 != 0 || !plm::aligned16(p.x)) return false;
+    for (int i = 0; i < p.nwt; ++i)
+        for (int g = 0; g < p.ngroups; ++g)
+            if (!plm::aligned16(p.w[i][g])) return false;
+    return true;
+}
+
+int run_rows(const RowsProblem& p, hipStream_t st) {
+    const bool fast = rows_fast_ok(p);
+    for (int g0 = 0; g0 < p.ngroups; g0 += kMaxGroups) {
+        const int ng = std::min(kMaxGroups, p.ngroups - g0);
+        RowsArgs a;
+        std::memset(&a, 0, sizeof(a));
+        for (int i = 0; i < p.nwt; ++i)
+            for (int g = 0; g < ng; ++g) {
+                a.w[i][g] = p.w[i][g0 + g];
+                a.s[i][g] = p.s[i][g0 + g];
+            }
+        a.x = p.x;
+        a.x_stride = p.x_stride;
+        // Output offsets of this group batch: element (g, m, row) lives at
+        // ((g0 + g) * batch + m) * out_ld + row.
+        for (int i = 0; i < p.nwt; ++i) {
+            a.out[i] = p.out[i] ? p.out[i] + static_cast<int64_t>(g0) * p.batch * p.out_ld : nullptr;
+        }
+        a.out_ld = p.out_ld;
+        a.rows = p.rows;
+        a.K = p.K;
+        a.scale_cols = p.scale_cols;
+        a.nchunks = static_cast<int>(plm::ceil_div(p.K, plm::kChunkBytes));
+        a.m_total = static_cast<int>(p.batch);
+        for (int64_t m0 = 0; m0 < p.batch; m0 += kMaxM) {
+            const int mc = static_cast<int>(std::min<int64_t>(kMaxM, p.batch - m0));
+            a.m0 = static_cast<int>(m0);
+            if (fast) {
+                if (p.nwt == 1) {
+                    launch_rows<1, false>(a, mc, ng, st);
+                } else if (p.silu) {
+                    launch_rows<2, true>(a, mc, ng, st);
+                } else {
+                    launch_rows<2, false>(a, mc, ng, st);
+                }
+            } else {
+                const int64_t total = static_cast<int64_t>(ng) * mc * p.rows;
+                const unsigned blocks = static_cast<unsigned>(plm::ceil_div(total, 256));
+                if (p.nwt == 1) {
+                    hipLaunchKernelGGL((fp8_rows_scalar_kernel<false, 1>), dim3(blocks), dim3(256), 0, st, a, mc, ng);
+                } else if (p.silu) {
+                    hipLaunchKernelGGL((fp8_rows_scalar_kernel<true, 2>), dim3(blocks), dim3(256), 0, st, a, mc, ng);
+                } else {
+                    hipLaunchKernelGGL((fp8_rows_scalar_kernel<false, 2>), dim3(blocks), dim3(256), 0, st, a, mc, ng);
+                }
+            }
+            const int code = plm::check_launch("fp8 rows kernel");
+            if (code != 0) return code;
+        }
+    }
+    return 0;
+}
+
+// Down phase: out[m][row] = sum_g route(g, m) * (D_g . act_g,m)[row], or one
+// output per group when per_group_out.
+struct CombineProblem {
+    const uint8_t* const* w;
+    const float* const* s;
+    int ngroups;
+    const float* act;     // [ngroups][batch][K]
+    const float* route;   // see route_sg / route_sm, or null
+    int64_t route_sg;
+    int64_t route_sm;
+    bool zero_skip;
+    bool per_group_out;
+    float* out;
+    int64_t batch;
+    int64_t rows;
+    int64_t K;
+    int64_t scale_cols;
+};
+
+int run_combine(const CombineProblem& p, hipStream_t st) {
+    bool fast = p.K % 16 == 0 && plm::aligned16(p.act);
+    for (int g = 0; g < p.ngroups && fast; ++g) fast = plm::aligned16(p.w[g]);
+    for (int g0 = 0; g0 < p.ngroups; g0 += kMaxGroups) {
+        const int ng = std::min(kMaxGroups, p.ngroups - g0);
+        CombineArgs a;
+        std::memset(&a, 0, sizeof(a));
+        for (int g = 0; g < ng; ++g) {
+            a.w[g] = p.w[g0 + g];
+            a.s[g] = p.s[g0 + g];
+        }
+        a.act = p.act;
+        a.route = p.route;
+        a.route_sg = p.route_sg;
+        a.route_sm = p.route_sm;
+        a.out = p.out;
+        a.rows = p.rows;
+        a.K = p.K;
+        a.scale_cols = p.scale_cols;
+        a.ngroups = ng;
+        a.g_base = g0;
+        a.cps = static_cast<int>(plm::ceil_div(p.K, plm::kChunkBytes));
+        a.per_group_out = p.per_group_out ? 1 : 0;
+        a.accumulate = (!p.per_group_out && g0 > 0) ? 1 : 0;
+        a.zero_skip = p.zero_skip ? 1 : 0;
+        a.m_total = static_cast<int>(p.batch);
+        for (int64_t m0 = 0; m0 < p.batch; m0 += kMaxM) {
+            const int mc = static_cast<int>(std::min<int64_t>(kMaxM, p.batch - m0));
+            a.m0 = static_cast<int>(m0);
+            if (fast) {
+                launch_combine(a, mc, st);
+            } else {
+                const int64_t total = static_cast<int64_t>(p.per_group_out ? ng : 1) * mc * p.rows;
+                const unsigned blocks = static_cast<unsigned>(plm::ceil_div(total, 256));
+                hipLaunchKernelGGL(fp8_combine_scalar_kernel, dim3(blocks), dim3(256), 0, st, a, mc);
+            }
+            const int code = plm::check_launch("fp8 combine kernel");
+            if (code != 0) return code;
+        }
+    }
+    return 0;
+}
+
+int fill_f32(float* p, float v, int64_t n, hipStream_t st) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(fill_f32_kernel, dim3(static_cast<unsigned>(plm::ceil_div(n, 256))), dim3(256), 0, st,
+                       p, v, n);
+    return plm::check_launch("fill kernel");
+}
+
+// Gather six host address tables into typed vectors.
+struct ExpertTables {
+    std::vector<const uint8_t*> g, u, d;
+    std::vector<const float*> gs, us, ds;
+    ExpertTables(const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp,
+                 const uint64_t* dp, const uint64_t* dsp, int64_t n) {
+        for (int64_t e = 0; e < n; ++e) {
+            g.push_back(reinterpret_cast<const uint8_t*>(static_cast<uintptr_t>(gp[e])));
+            gs.push_back(reinterpret_cast<const float*>(static_cast<uintptr_t>(gsp[e])));
+            u.push_back(reinterpret_cast<const uint8_t*>(static_cast<uintptr_t>(up[e])));
+            us.push_back(reinterpret_cast<const float*>(static_cast<uintptr_t>(usp[e])));
+            d.push_back(reinterpret_cast<const uint8_t*>(static_cast<uintptr_t>(dp[e])));
+            ds.push_back(reinterpret_cast<const float*>(static_cast<uintptr_t>(dsp[e])));
+        }
+    }
+};
+
+// Phase 1 of every SwiGLU path: act[e][m][row] = silu(gate_e . x_m) * (up_e . x_m).
+int gate_up_phase(const ExpertTables& t, int64_t experts, const float* hidden, float* act,
+                  int64_t batch, int64_t inter, int64_t hid, int64_t gsc, hipStream_t st) {
+    RowsProblem p;
+    std::memset(&p, 0, sizeof(p));
+    p.w[0] = t.g.data();
+    p.w[1] = t.u.data();
+    p.s[0] = t.gs.data();
+    p.s[1] = t.us.data();
+    p.nwt = 2;
+    p.silu = true;
+    p.ngroups = static_cast<int>(experts);
+    p.x = hidden;
+    p.x_stride = hid;
+    p.out[0] = act;
+    p.out[1] = nullptr;
+    p.out_ld = inter;
+    p.batch = batch;
+    p.rows = inter;
+    p.K = hid;
+    p.scale_cols = gsc;
+    return run_rows(p, st);
+}
+
+bool moe_dims_bad(int64_t experts, int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
+    return experts <= 0 || batch <= 0 || inter <= 0 || hid <= 0 || gsc < plm::ceil_div(hid, 128) ||
+           dsc < plm::ceil_div(inter, 128);
+}
+
+// Shared body of the weighted / row-weighted MoE entry points.
+int weighted_moe(const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp,
+                 const uint64_t* dp, const uint64_t* dsp, const float* hidden, const float* route,
+                 int64_t route_sg, int64_t route_sm, bool zero_skip, float* out, int64_t experts,
+                 int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
+    hipStream_t st = plm::current_stream();
+    float* act = static_cast<float*>(plm::workspace(static_cast<size_t>(experts * batch * inter) * sizeof(float)));
+    if (act == nullptr) return -3;
+    ExpertTables t(gp, gsp, up, usp, dp, dsp, experts);
+    int code = gate_up_phase(t, experts, hidden, act, batch, inter, hid, gsc, st);
+    if (code != 0) return code;
+    CombineProblem c;
+    std::memset(&c, 0, sizeof(c));
+    c.w = t.d.data();
+    c.s = t.ds.data();
+    c.ngroups = static_cast<int>(experts);
+    c.act = act;
+    c.route = route;
+    c.route_sg = route_sg;
+    c.route_sm = route_sm;
+    c.zero_skip = zero_skip;
+    c.per_group_out = false;
+    c.out = out;
+    c.batch = batch;
+    c.rows = hid;
+    c.K = inter;
+    c.scale_cols = dsc;
+    return run_combine(c, st);
+}
+
+}  // namespace
+
+// ====================================================================== C ABI
+
+PLM_EXPORT int fp8_e4m3_block_linear_f32(const uint8_t* fp8_weight, const float* scale_inv,
+                                         const float* hidden, float* out, int64_t batch,
+                                         int64_t out_rows, int64_t in_cols, int64_t scale_cols) {
+    if (!fp8_weight || !scale_inv || !hidden || !out) return plm::fail(-1, "null pointer");
+    if (batch <= 0 || out_rows <= 0 || in_cols <= 0 || scale_cols < plm::ceil_div(in_cols, 128))
+        return plm::fail(-2, "bad dimensions");
+    const uint8_t* w[1] = {fp8_weight};
+    const float* s[1] = {scale_inv};
+    RowsProblem p;
+    std::memset(&p, 0, sizeof(p));
+    p.w[0] = w;
+    p.s[0] = s;
+    p.nwt = 1;
+    p.ngroups = 1;
+    p.x = hidden;
+    p.x_stride = in_cols;
+    p.out[0] = out;
+    p.out_ld = out_rows;
+    p.batch = batch;
+    p.rows = out_rows;
+    p.K = in_cols;
+    p.scale_cols = scale_cols;
+    return run_rows(p, plm::current_stream());
+}
+
+PLM_EXPORT int fp8_e4m3_block_dual_linear_f32(const uint8_t* wa, const float* sa, const uint8_t* wb,
+                                              const float* sb, const float* hidden, float* out_a,
+                                              float* out_b, int64_t batch, int64_t out_rows,
+                                              int64_t in_cols, int64_t scale_cols) {
+    if (!wa || !sa || !wb || !sb || !hidden || !out_a || !out_b) return plm::fail(-1, "null pointer");
+    if (batch <= 0 || out_rows <= 0 || in_cols <= 0 || scale_cols < plm::ceil_div(in_cols, 128))
+        return plm::fail(-2, "bad dimensions");
+    const uint8_t* w0[1] = {wa};
+    const uint8_t* w1[1] = {wb};
+    const float* s0[1] = {sa};
+    const float* s1[1] = {sb};
+    RowsProblem p;
+    std::memset(&p, 0, sizeof(p));
+    p.w[0] = w0;
+    p.w[1] = w1;
+    p.s[0] = s0;
+    p.s[1] = s1;
+    p.nwt = 2;
+    p.silu = false;
+    p.ngroups = 1;
+    p.x = hidden;
+    p.x_stride = in_cols;
+    p.out[0] = out_a;
+    p.out[1] = out_b;
+    p.out_ld = out_rows;
+    p.batch = batch;
+    p.rows = out_rows;
+    p.K = in_cols;
+    p.scale_cols = scale_cols;
+    return run_rows(p, plm::current_stream());
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_f32(const uint8_t* gate_weight, const float* gate_scale_inv,
+                                      const uint8_t* up_weight, const float* up_scale_inv,
+                                      const uint8_t* down_weight, const float* down_scale_inv,
+                                      const float* hidden, float* out, int64_t batch,
+                                      int64_t intermediate_rows, int64_t hidden_cols,
+                                      int64_t gate_scale_cols, int64_t down_scale_cols) {
+    if (!gate_weight || !gate_scale_inv || !up_weight || !up_scale_inv || !down_weight || !down_scale_inv ||
+        !hidden || !out)
+        return plm::fail(-1, "null pointer");
+    if (moe_dims_bad(1, batch, intermediate_rows, hidden_cols, gate_scale_cols, down_scale_cols))
+        return plm::fail(-2, "bad dimensions");
+    const uint64_t gp = reinterpret_cast<uintptr_t>(gate_weight), gsp = reinterpret_cast<uintptr_t>(gate_scale_inv);
+    const uint64_t upp = reinterpret_cast<uintptr_t>(up_weight), usp = reinterpret_cast<uintptr_t>(up_scale_inv);
+    const uint64_t dp = reinterpret_cast<uintptr_t>(down_weight), dsp = reinterpret_cast<uintptr_t>(down_scale_inv);
+    hipStream_t st = plm::current_stream();
+    float* act = static_cast<float*>(plm::workspace(static_cast<size_t>(batch * intermediate_rows) * sizeof(float)));
+    if (act == nullptr) return -3;
+    ExpertTables t(&gp, &gsp, &upp, &usp, &dp, &dsp, 1);
+    int code = gate_up_phase(t, 1, hidden, act, batch, intermediate_rows, hidden_cols, gate_scale_cols, st);
+    if (code != 0) return code;
+    CombineProblem c;
+    std::memset(&c, 0, sizeof(c));
+    c.w = t.d.data();
+    c.s = t.ds.data();
+    c.ngroups = 1;
+    c.act = act;
+    c.out = out;
+    c.batch = batch;
+    c.rows = hidden_cols;
+    c.K = intermediate_rows;
+    c.scale_cols = down_scale_cols;
+    return run_combine(c, st);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_avx512_f32(const uint8_t* gate_weight, const float* gate_scale_inv,
+                                             const uint8_t* up_weight, const float* up_scale_inv,
+                                             const uint8_t* down_weight, const float* down_scale_inv,
+                                             const float* hidden, float* out, int64_t batch,
+                                             int64_t intermediate_rows, int64_t hidden_cols,
+                                             int64_t gate_scale_cols, int64_t down_scale_cols) {
+    return fp8_e4m3_block_mlp_f32(gate_weight, gate_scale_inv, up_weight, up_scale_inv, down_weight,
+                                  down_scale_inv, hidden, out, batch, intermediate_rows, hidden_cols,
+                                  gate_scale_cols, down_scale_cols);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_many_f32(const uint64_t* gp, const uint64_t* gsp, const uint64_t* up,
+                                           const uint64_t* usp, const uint64_t* dp, const uint64_t* dsp,
+                                           const float* hidden, float* out, int64_t expert_count,
+                                           int64_t batch, int64_t inter, int64_t hid, int64_t gsc,
+                                           int64_t dsc) {
+    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden || !out) return plm::fail(-1, "null pointer");
+    if (moe_dims_bad(expert_count, batch, inter, hid, gsc, dsc)) return plm::fail(-2, "bad dimensions");
+    hipStream_t st = plm::current_stream();
+    float* act = static_cast<float*>(plm::workspace(static_cast<size_t>(expert_count * batch * inter) * sizeof(float)));
+    if (act == nullptr) return -3;
+    ExpertTables t(gp, gsp, up, usp, dp, dsp, expert_count);
+    int code = gate_up_phase(t, expert_count, hidden, act, batch, inter, hid, gsc, st);
+    if (code != 0) return code;
+    CombineProblem c;
+    std::memset(&c, 0, sizeof(c));
+    c.w = t.d.data();
+    c.s = t.ds.data();
+    c.ngroups = static_cast<int>(expert_count);
+    c.act = act;
+    c.per_group_out = true;
+    c.out = out;
+    c.batch = batch;
+    c.rows = hid;
+    c.K = inter;
+    c.scale_cols = dsc;
+    return run_combine(c, st);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_many_weighted_f32(const uint64_t* gp, const uint64_t* gsp, const uint64_t* up,
+                                                    const uint64_t* usp, const uint64_t* dp, const uint64_t* dsp,
+                                                    const float* hidden, const float* route_weights, float* out,
+                                                    int64_t expert_count, int64_t batch, int64_t inter,
+                                                    int64_t hid, int64_t gsc, int64_t dsc) {
+    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden || !route_weights || !out)
+        return plm::fail(-1, "null pointer");
+    if (moe_dims_bad(expert_count, batch, inter, hid, gsc, dsc)) return plm::fail(-2, "bad dimensions");
+    return weighted_moe(gp, gsp, up, usp, dp, dsp, hidden, route_weights, 1, 0, false, out, expert_count,
+                        batch, inter, hid, gsc, dsc);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_many_weighted_avx512_f32(
+    const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp, const uint64_t* dp,
+    const uint64_t* dsp, const float* hidden, const float* route_weights, float* out, int64_t expert_count,
+    int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
+    return fp8_e4m3_block_mlp_many_weighted_f32(gp, gsp, up, usp, dp, dsp, hidden, route_weights, out,
+                                                expert_count, batch, inter, hid, gsc, dsc);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_many_row_weighted_f32(
+    const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp, const uint64_t* dp,
+    const uint64_t* dsp, const float* hidden, const float* route_weights, float* out, int64_t expert_count,
+    int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
+    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden || !route_weights || !out)
+        return plm::fail(-1, "null pointer");
+    if (moe_dims_bad(expert_count, batch, inter, hid, gsc, dsc)) return plm::fail(-2, "bad dimensions");
+    return weighted_moe(gp, gsp, up, usp, dp, dsp, hidden, route_weights, batch, 1, true, out, expert_count,
+                        batch, inter, hid, gsc, dsc);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_many_pair_weighted_f32(
+    const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp, const uint64_t* dp,
+    const uint64_t* dsp, const float* hidden, const int64_t* pair_item_indices, const int64_t* pair_row_indices,
+    const float* pair_weights, float* out, int64_t expert_count, int64_t pair_count, int64_t batch, int64_t inter,
+    int64_t hid, int64_t gsc, int64_t dsc) {
+    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden || !pair_item_indices || !pair_row_indices ||
+        !pair_weights || !out)
+        return plm::fail(-1, "null pointer");
+    if (pair_count < 0 || moe_dims_bad(expert_count, batch, inter, hid, gsc, dsc))
+        return plm::fail(-2, "bad dimensions");
+    hipStream_t st = plm::current_stream();
+    int code = fill_f32(out, 0.0f, batch * hid, st);
+    if (code != 0 || pair_count == 0) return code;
+    // The index check needs the values on the host: read them back.
+    std::vector<int64_t> items(static_cast<size_t>(pair_count)), rows(static_cast<size_t>(pair_count));
+    hipError_t err = hipMemcpyAsync(items.data(), pair_item_indices, sizeof(int64_t) * pair_count,
+                                    hipMemcpyDeviceToHost, st);
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(rows.data(), pair_row_indices, sizeof(int64_t) * pair_count, hipMemcpyDeviceToHost, st);
+    if (err == hipSuccess) err = hipStreamSynchronize(st);
+    if (err != hipSuccess) return plm::hip_fail(err, "pair index read-back");
+    for (int64_t p = 0; p < pair_count; ++p) {
+        if (items[p] < 0 || items[p] >= expert_count || rows[p] < 0 || rows[p] >= batch)
+            return plm::fail(-4, "pair %lld out of range", static_cast<long long>(p));
+    }
+    // Dense route matrix [E, batch] after the activations in the workspace.
+    const size_t act_elems = static_cast<size_t>(expert_count * batch * inter);
+    float* ws = static_cast<float*>(plm::workspace((act_elems + static_cast<size_t>(expert_count * batch)) * sizeof(float)));
+    if (ws == nullptr) return -3;
+    float* route = ws + act_elems;
+    code = fill_f32(route, 0.0f, expert_count * batch, st);
+    if (code != 0) return code;
+    hipLaunchKernelGGL(scatter_pairs_kernel, dim3(1), dim3(1), 0, st, pair_item_indices, pair_row_indices,
+                       pair_weights, pair_count, batch, route);
+    code = plm::check_launch("scatter pairs");
+    if (code != 0) return code;
+    // weighted_moe asks for the same workspace size prefix, so act stays at ws.
+    ExpertTables t(gp, gsp, up, usp, dp, dsp, expert_count);
+    code = gate_up_phase(t, expert_count, hidden, ws, batch, inter, hid, gsc, st);
+    if (code != 0) return code;
+    CombineProblem c;
+    std::memset(&c, 0, sizeof(c));
+    c.w = t.d.data();
+    c.s = t.ds.data();
+    c.ngroups = static_cast<int>(expert_count);
+    c.act = ws;
+    c.route = route;
+    c.route_sg = batch;
+    c.route_sm = 1;
+    c.zero_skip = true;
+    c.out = out;
+    c.batch = batch;
+    c.rows = hid;
+    c.K = inter;
+    c.scale_cols = dsc;
+    return run_combine(c, st);
+}
+
+// Used by the DeepSeek session entry points (ds_session.hip).
+int plm_weighted_moe_fp8(const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp,
+                         const uint64_t* dp, const uint64_t* dsp, const float* hidden, const float* route,
+                         float* out, int64_t experts, int64_t batch, int64_t inter, int64_t hid, int64_t gsc,
+                         int64_t dsc) {
+    return fp8_e4m3_block_mlp_many_weighted_f32(gp, gsp, up, usp, dp, dsp, hidden, route, out, experts, batch,
+                                                inter, hid, gsc, dsc);
+}

@@ -1,0 +1,887 @@
+"""Drop-in for the hot-path functions of ``pcketlm.native`` on an MI355X.
+
+Same function names, argument meaning, validation messages and exception
+types as the reference's ctypes wrappers (src/pcketlm/native/__init__.py,
+cited per function), backed by libpocketlm_hip.so.  Differences, all on
+purpose:
+
+* Tensors stay on the GPU.  Inputs already on a CUDA device are used in
+  place (no ``.cpu()``); results are returned on that device.  CPU inputs are
+  copied to the current CUDA device and the result is copied back, so a
+  caller written for the CPU reference keeps working (at PCIe cost).
+* Calls run on torch's current stream and return without synchronising.
+* ``PCKETLM_DISABLE_NATIVE_*`` kill switches make the ``native_*_available``
+  predicates return False and the wrappers raise
+  ``RuntimeError("... unavailable: disabled")``, as the reference wrappers
+  do when their DLL is not loaded.  There is no CPU or torch fallback in this
+  package: a missing library raises.
+* FP8 weights may be given as ``torch.uint8`` or ``torch.float8_e4m3fn``;
+  both are read as raw e4m3 bytes.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from collections import OrderedDict
+from contextlib import contextmanager
+
+import torch
+
+from . import _lib
+
+_TRUE = {"1", "true", "yes", "on"}
+
+
+def _flag(name: str) -> bool:
+    return os.environ.get(name, "").strip().lower() in _TRUE
+
+
+# --------------------------------------------------------------------------- availability
+# Kill switches: src/pcketlm/native/__init__.py:64-138.
+
+def _lib_or_none():
+    try:
+        return _lib.load()
+    except OSError:
+        return None
+
+
+def _available(kill_switch: str) -> bool:
+    if _flag(kill_switch):
+        return False
+    lib = _lib_or_none()
+    return bool(lib is not None and torch.cuda.is_available() and lib.pocketlm_device_available() == 1)
+
+
+def native_fp8_dequant_available() -> bool:
+    return _available("PCKETLM_DISABLE_NATIVE_FP8_DEQUANT")
+
+
+def native_fp8_linear_available() -> bool:
+    return _available("PCKETLM_DISABLE_NATIVE_FP8_LINEAR")
+
+
+native_fp8_dual_linear_available = native_fp8_linear_available
+native_fp8_mlp_available = native_fp8_linear_available
+native_fp8_mlp_many_available = native_fp8_linear_available
+native_fp8_mlp_many_weighted_available = native_fp8_linear_available
+native_fp8_mlp_many_row_weighted_available = native_fp8_linear_available
+native_fp8_mlp_many_pair_weighted_available = native_fp8_linear_available
+
+
+def native_fp8_mlp_avx512_available() -> bool:
+    return _available("PCKETLM_DISABLE_NATIVE_FP8_AVX512")
+
+
+native_fp8_mlp_many_weighted_avx512_available = native_fp8_mlp_avx512_available
+
+
+def native_q4_available() -> bool:
+    return _available("PCKETLM_DISABLE_NATIVE_Q4")
+
+
+def native_fp16_packed_gemv_available() -> bool:
+    return _available("PCKETLM_DISABLE_NATIVE_PACKED_GEMV")
+
+
+def native_ds_moe_available() -> bool:
+    return _available("PCKETLM_DISABLE_NATIVE_DS_MOE")
+
+
+def native_ds_router_available() -> bool:
+    return _available("PCKETLM_DISABLE_NATIVE_DS_ROUTER")
+
+
+def _require(kill_switch: str, what: str):
+    if _flag(kill_switch):
+        raise RuntimeError(f"{what} is unavailable: disabled")
+    try:
+        lib = _lib.load()
+    except OSError as exc:
+        raise RuntimeError(f"{what} is unavailable: {exc}") from exc
+    if not torch.cuda.is_available():
+        raise RuntimeError(f"{what} is unavailable: no HIP device")
+    return lib
+
+
+# --------------------------------------------------------------------------- plumbing
+
+def _target_device(*tensors: torch.Tensor) -> torch.device:
+    for t in tensors:
+        if isinstance(t, torch.Tensor) and t.device.type == "cuda":
+            return t.device
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _on(t: torch.Tensor, device: torch.device, dtype: torch.dtype | None = None) -> torch.Tensor:
+    t = t.detach()
+    if dtype is not None and t.dtype != dtype:
+        if dtype == torch.uint8 and t.dtype == torch.float8_e4m3fn:
+            t = t.view(torch.uint8)
+        else:
+            t = t.to(dtype)
+    return t.to(device, non_blocking=False).contiguous()
+
+
+def _fp8_bytes(t: torch.Tensor, device: torch.device) -> torch.Tensor:
+    if t.dtype == torch.float8_e4m3fn:
+        t = t.view(torch.uint8)
+    if t.dtype != torch.uint8:
+        raise TypeError("FP8 weights must be torch.uint8 raw e4m3 bytes or torch.float8_e4m3fn")
+    return t.detach().to(device).contiguous()
+
+
+def _p(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else int(t.data_ptr()))
+
+
+@contextmanager
+def _launch(lib, device: torch.device):
+    with torch.cuda.device(device):
+        lib.pocketlm_set_stream(ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream))
+        yield
+
+
+def _check(name: str, code: int) -> None:
+    if code != 0:
+        detail = _lib.last_error()
+        raise RuntimeError(f"{name} failed with code {code}" + (f" ({detail})" if detail else ""))
+
+
+def _home(result: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
+    """Return the result where the caller's main input lives."""
+    if like.device.type == "cuda":
+        return result
+    return result.to(like.device)
+
+
+# --------------------------------------------------------------------------- FP8 dequant
+
+def _fp8_dequant(fp8_weight, scale_inv, out_dtype: torch.dtype, symbol: str, what: str) -> torch.Tensor:
+    lib = _require("PCKETLM_DISABLE_NATIVE_FP8_DEQUANT", what)
+    if fp8_weight.ndim != 2:
+        raise ValueError("fp8_weight must have shape [rows, cols]")
+    if scale_inv.ndim != 2:
+        raise ValueError("scale_inv must have shape [scale_rows, scale_cols]")
+    dev = _target_device(fp8_weight, scale_inv)
+    w = _fp8_bytes(fp8_weight, dev)
+    s = _on(scale_inv, dev, torch.float32)
+    rows, cols = int(w.shape[0]), int(w.shape[1])
+    if tuple(s.shape) != ((rows + 127) // 128, (cols + 127) // 128):
+        raise ValueError("scale_inv shape does not match FP8 128x128 block layout")
+    out = torch.empty((rows, cols), dtype=out_dtype, device=dev)
+    if rows and cols:
+        with _launch(lib, dev):
+            code = getattr(lib, symbol)(_p(w), _p(s), _p(out), rows, cols, (cols + 127) // 128)
+        _check(symbol, code)
+    return _home(out, fp8_weight)
+
+
+def fp8_e4m3_dequant_to_fp16(fp8_weight: torch.Tensor, scale_inv: torch.Tensor) -> torch.Tensor:
+    """src/pcketlm/native/__init__.py:3378-3407 -> fp8_dequant.cpp:119-164."""
+    return _fp8_dequant(fp8_weight, scale_inv, torch.float16, "fp8_e4m3_dequant_to_fp16", "Native FP8 dequant")
+
+
+def fp8_e4m3_dequant_to_bf16(fp8_weight: torch.Tensor, scale_inv: torch.Tensor) -> torch.Tensor:
+    """src/pcketlm/native/__init__.py:3410-3439 -> fp8_dequant.cpp:166-204."""
+    return _fp8_dequant(fp8_weight, scale_inv, torch.bfloat16, "fp8_e4m3_dequant_to_bf16", "Native FP8 BF16 dequant")
+
+
+def fp8_e4m3_dequant_to_f32(fp8_weight: torch.Tensor, scale_inv: torch.Tensor) -> torch.Tensor:
+    """The fp32 branch of dequantize_fp8_block_scaled (fp8_source.py:852-858)."""
+    return _fp8_dequant(fp8_weight, scale_inv, torch.float32, "fp8_e4m3_dequant_to_f32", "Native FP8 F32 dequant")
+
+
+def dequantize_fp8_block_scaled(
+    fp8_bytes: torch.Tensor,
+    scale_inv: torch.Tensor,
+    *,
+    block_size: int = 128,
+    dtype: torch.dtype = torch.bfloat16,
+) -> torch.Tensor:
+    """src/pcketlm/core/runtime/fp8_source.py:812-858 on the device.
+
+    fp16 / bf16 / fp32 come straight from the dequant kernels; any other
+    dtype is the fp32 result cast with torch, as the reference's torch branch
+    does.  Only the 128x128 block layout exists on this path.
+    """
+    if fp8_bytes.dtype not in (torch.uint8, torch.float8_e4m3fn):
+        raise TypeError("fp8_bytes must be a uint8 tensor containing raw E4M3 bytes.")
+    if fp8_bytes.ndim != 2:
+        raise ValueError("FP8 block dequant currently supports 2D weight tensors only.")
+    if scale_inv.ndim != 2:
+        raise ValueError("scale_inv must be a 2D block-scale tensor.")
+    if int(block_size) != 128:
+        raise ValueError("only block_size=128 is supported by the device dequant kernels")
+    rows, cols = int(fp8_bytes.shape[0]), int(fp8_bytes.shape[1])
+    expected = [(rows + 127) // 128, (cols + 127) // 128]
+    if [int(scale_inv.shape[0]), int(scale_inv.shape[1])] != expected:
+        raise ValueError(
+            "scale_inv shape "
+            f"{list(scale_inv.shape)} does not match FP8 weight shape {list(fp8_bytes.shape)} "
+            f"with block_size={block_size}; expected {expected}."
+        )
+    if dtype == torch.float16:
+        return fp8_e4m3_dequant_to_fp16(fp8_bytes, scale_inv)
+    if dtype == torch.bfloat16:
+        return fp8_e4m3_dequant_to_bf16(fp8_bytes, scale_inv)
+    out = fp8_e4m3_dequant_to_f32(fp8_bytes, scale_inv)
+    return out if dtype == torch.float32 else out.to(dtype).contiguous()
+
+
+# --------------------------------------------------------------------------- FP8 GEMV family
+
+def _hidden_f32(hidden: torch.Tensor, dev: torch.device) -> torch.Tensor:
+    return _on(hidden, dev).reshape(-1, int(hidden.shape[-1])).to(torch.float32).contiguous()
+
+
+def fp8_e4m3_block_linear_f32(fp8_weight: torch.Tensor, scale_inv: torch.Tensor, hidden: torch.Tensor) -> torch.Tensor:
+    """src/pcketlm/native/__init__.py:3442-3476 -> fp8_linear.cpp:50-117."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_FP8_LINEAR", "Native FP8 linear")
+    if fp8_weight.ndim != 2:
+        raise ValueError("fp8_weight must have shape [out_rows, in_cols]")
+    if scale_inv.ndim != 2:
+        raise ValueError("scale_inv must have shape [scale_rows, scale_cols]")
+    dev = _target_device(fp8_weight, scale_inv, hidden)
+    x = _hidden_f32(hidden, dev)
+    w = _fp8_bytes(fp8_weight, dev)
+    s = _on(scale_inv, dev, torch.float32)
+    out_rows, in_cols = int(w.shape[0]), int(w.shape[1])
+    if int(x.shape[1]) != in_cols:
+        raise ValueError("hidden input size does not match FP8 weight columns")
+    if int(s.shape[0]) != (out_rows + 127) // 128 or int(s.shape[1]) != (in_cols + 127) // 128:
+        raise ValueError("scale_inv shape does not match FP8 128x128 block layout")
+    out = torch.empty((int(x.shape[0]), out_rows), dtype=torch.float32, device=dev)
+    with _launch(lib, dev):
+        code = lib.fp8_e4m3_block_linear_f32(_p(w), _p(s), _p(x), _p(out), int(x.shape[0]), out_rows, in_cols,
+                                             (in_cols + 127) // 128)
+    _check("fp8_e4m3_block_linear_f32", code)
+    return _home(out, hidden)
+
+
+def fp8_e4m3_block_dual_linear_f32(
+    fp8_weight_a: torch.Tensor,
+    scale_inv_a: torch.Tensor,
+    fp8_weight_b: torch.Tensor,
+    scale_inv_b: torch.Tensor,
+    hidden: torch.Tensor,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """src/pcketlm/native/__init__.py:3479-3530 -> fp8_linear.cpp:119-210."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_FP8_LINEAR", "Native FP8 dual linear")
+    if fp8_weight_a.ndim != 2 or fp8_weight_b.ndim != 2:
+        raise ValueError("fp8 weights must have shape [out_rows, in_cols]")
+    dev = _target_device(fp8_weight_a, fp8_weight_b, hidden)
+    wa, wb = _fp8_bytes(fp8_weight_a, dev), _fp8_bytes(fp8_weight_b, dev)
+    if tuple(wa.shape) != tuple(wb.shape):
+        raise ValueError("dual FP8 weights must have matching shapes")
+    sa, sb = _on(scale_inv_a, dev, torch.float32), _on(scale_inv_b, dev, torch.float32)
+    if tuple(sa.shape) != tuple(sb.shape):
+        raise ValueError("dual FP8 scales must have matching shapes")
+    x = _hidden_f32(hidden, dev)
+    out_rows, in_cols = int(wa.shape[0]), int(wa.shape[1])
+    if int(x.shape[1]) != in_cols:
+        raise ValueError("hidden input size does not match FP8 weight columns")
+    if int(sa.shape[0]) != (out_rows + 127) // 128 or int(sa.shape[1]) != (in_cols + 127) // 128:
+        raise ValueError("scale_inv shape does not match FP8 128x128 block layout")
+    out_a = torch.empty((int(x.shape[0]), out_rows), dtype=torch.float32, device=dev)
+    out_b = torch.empty_like(out_a)
+    with _launch(lib, dev):
+        code = lib.fp8_e4m3_block_dual_linear_f32(_p(wa), _p(sa), _p(wb), _p(sb), _p(x), _p(out_a), _p(out_b),
+                                                  int(x.shape[0]), out_rows, in_cols, (in_cols + 127) // 128)
+    _check("fp8_e4m3_block_dual_linear_f32", code)
+    return _home(out_a, hidden), _home(out_b, hidden)
+
+
+def _mlp_common(gate_weight, gate_scale_inv, up_weight, up_scale_inv, down_weight, down_scale_inv, hidden, dev):
+    if gate_weight.ndim != 2 or up_weight.ndim != 2 or down_weight.ndim != 2:
+        raise ValueError("FP8 MLP weights must be 2D")
+    g, u, d = _fp8_bytes(gate_weight, dev), _fp8_bytes(up_weight, dev), _fp8_bytes(down_weight, dev)
+    if tuple(g.shape) != tuple(u.shape):
+        raise ValueError("FP8 MLP gate and up weights must have matching shapes")
+    inter, hid = int(g.shape[0]), int(g.shape[1])
+    if tuple(d.shape) != (hid, inter):
+        raise ValueError("FP8 MLP down weight must have shape [hidden, intermediate]")
+    gs, us, ds = (_on(t, dev, torch.float32) for t in (gate_scale_inv, up_scale_inv, down_scale_inv))
+    if tuple(gs.shape) != tuple(us.shape):
+        raise ValueError("FP8 MLP gate and up scales must have matching shapes")
+    egs = ((inter + 127) // 128, (hid + 127) // 128)
+    eds = ((hid + 127) // 128, (inter + 127) // 128)
+    if tuple(gs.shape) != egs:
+        raise ValueError("FP8 MLP gate scale shape does not match 128x128 block layout")
+    if tuple(ds.shape) != eds:
+        raise ValueError("FP8 MLP down scale shape does not match 128x128 block layout")
+    x = _hidden_f32(hidden, dev)
+    if int(x.shape[1]) != hid:
+        raise ValueError("hidden input size does not match FP8 MLP input size")
+    return g, gs, u, us, d, ds, x, inter, hid, egs[1], eds[1]
+
+
+def _run_mlp(symbol: str, kill: str, what: str, gate_weight, gate_scale_inv, up_weight, up_scale_inv, down_weight,
+             down_scale_inv, hidden) -> torch.Tensor:
+    lib = _require(kill, what)
+    dev = _target_device(gate_weight, up_weight, down_weight, hidden)
+    g, gs, u, us, d, ds, x, inter, hid, gsc, dsc = _mlp_common(
+        gate_weight, gate_scale_inv, up_weight, up_scale_inv, down_weight, down_scale_inv, hidden, dev)
+    out = torch.empty((int(x.shape[0]), hid), dtype=torch.float32, device=dev)
+    with _launch(lib, dev):
+        code = getattr(lib, symbol)(_p(g), _p(gs), _p(u), _p(us), _p(d), _p(ds), _p(x), _p(out), int(x.shape[0]),
+                                    inter, hid, gsc, dsc)
+    _check(symbol, code)
+    return _home(out, hidden)
+
+
+def fp8_e4m3_block_mlp_f32(gate_weight, gate_scale_inv, up_weight, up_scale_inv, down_weight, down_scale_inv,
+                           hidden) -> torch.Tensor:
+    """src/pcketlm/native/__init__.py:3533-3590 -> fp8_linear.cpp:212-362."""
+    return _run_mlp("fp8_e4m3_block_mlp_f32", "PCKETLM_DISABLE_NATIVE_FP8_LINEAR", "Native FP8 MLP", gate_weight,
+                    gate_scale_inv, up_weight, up_scale_inv, down_weight, down_scale_inv, hidden)
+
+
+def fp8_e4m3_block_mlp_avx512_f32(gate_weight, gate_scale_inv, up_weight, up_scale_inv, down_weight,
+                                  down_scale_inv, hidden) -> torch.Tensor:
+    """src/pcketlm/native/__init__.py:3593-3650 (same device kernel as the scalar name)."""
+    return _run_mlp("fp8_e4m3_block_mlp_avx512_f32", "PCKETLM_DISABLE_NATIVE_FP8_AVX512", "Native FP8 AVX-512 MLP",
+                    gate_weight, gate_scale_inv, up_weight, up_scale_inv, down_weight, down_scale_inv, hidden)
+
+
+class _Experts:
+    """Validated expert weights on one device plus the six host address tables."""
+
+    def __init__(self, items, hidden, dev: torch.device):
+        if not items:
+            raise ValueError("items must not be empty")
+        first = _fp8_bytes(items[0][0], dev)
+        self.inter, self.hid = int(first.shape[0]), int(first.shape[1])
+        prepared = []
+        for gate, gate_scale, up, up_scale, down, down_scale in items:
+            g, u, d = _fp8_bytes(gate, dev), _fp8_bytes(up, dev), _fp8_bytes(down, dev)
+            gs, us, ds = (_on(t, dev, torch.float32) for t in (gate_scale, up_scale, down_scale))
+            if tuple(g.shape) != (self.inter, self.hid):
+                raise ValueError("all gate weights must have matching shape")
+            if tuple(u.shape) != (self.inter, self.hid):
+                raise ValueError("all up weights must have matching shape")
+            if tuple(d.shape) != (self.hid, self.inter):
+                raise ValueError("all down weights must have matching shape")
+            prepared.append((g, gs, u, us, d, ds))
+        egs = ((self.inter + 127) // 128, (self.hid + 127) // 128)
+        eds = ((self.hid + 127) // 128, (self.inter + 127) // 128)
+        for g, gs, u, us, d, ds in prepared:
+            if tuple(gs.shape) != egs or tuple(us.shape) != egs:
+                raise ValueError("gate/up scale shapes do not match 128x128 block layout")
+            if tuple(ds.shape) != eds:
+                raise ValueError("down scale shape does not match 128x128 block layout")
+        self.gsc, self.dsc = egs[1], eds[1]
+        self.prepared = prepared
+        self.count = len(prepared)
+        self.tables = [(ctypes.c_uint64 * self.count)(*[int(p[i].data_ptr()) for p in prepared]) for i in range(6)]
+        self.x = _hidden_f32(hidden, dev)
+        if int(self.x.shape[1]) != self.hid:
+            raise ValueError("hidden input size does not match FP8 MLP input size")
+
+    def table_args(self):
+        return [ctypes.cast(t, ctypes.c_void_p) for t in self.tables]
+
+
+def fp8_e4m3_block_mlp_many_f32(items, hidden: torch.Tensor) -> torch.Tensor:
+    """src/pcketlm/native/__init__.py:3653-3719 -> fp8_linear.cpp:364-473; out [E, M, H]."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_FP8_LINEAR", "Native FP8 many-MLP")
+    dev = _target_device(hidden, *(items[0] if items else ()))
+    ex = _Experts(items, hidden, dev)
+    out = torch.empty((ex.count, int(ex.x.shape[0]), ex.hid), dtype=torch.float32, device=dev)
+    with _launch(lib, dev):
+        code = lib.fp8_e4m3_block_mlp_many_f32(*ex.table_args(), _p(ex.x), _p(out), ex.count, int(ex.x.shape[0]),
+                                               ex.inter, ex.hid, ex.gsc, ex.dsc)
+    _check("fp8_e4m3_block_mlp_many_f32", code)
+    return _home(out, hidden)
+
+
+def _weighted(symbol: str, kill: str, what: str, items, hidden, route_weights, *, per_row: bool) -> torch.Tensor:
+    lib = _require(kill, what)
+    dev = _target_device(hidden, *(items[0] if items else ()))
+    ex = _Experts(items, hidden, dev)
+    batch = int(ex.x.shape[0])
+    if per_row:
+        route = _on(route_weights, dev, torch.float32)
+        if tuple(route.shape) != (ex.count, batch):
+            raise ValueError("route_weights must have shape [expert_count, batch]")
+    else:
+        route = _on(route_weights, dev, torch.float32).reshape(-1)
+        if int(route.numel()) != ex.count:
+            raise ValueError("route_weights length must match item count")
+    out = torch.empty((batch, ex.hid), dtype=torch.float32, device=dev)
+    with _launch(lib, dev):
+        code = getattr(lib, symbol)(*ex.table_args(), _p(ex.x), _p(route), _p(out), ex.count, batch, ex.inter,
+                                    ex.hid, ex.gsc, ex.dsc)
+    _check(symbol, code)
+    return _home(out, hidden)
+
+
+def fp8_e4m3_block_mlp_many_weighted_f32(items, hidden, route_weights) -> torch.Tensor:
+    """src/pcketlm/native/__init__.py:3722-3793 -> fp8_linear.cpp:475-589."""
+    return _weighted("fp8_e4m3_block_mlp_many_weighted_f32", "PCKETLM_DISABLE_NATIVE_FP8_LINEAR",
+                     "Native FP8 weighted many-MLP", items, hidden, route_weights, per_row=False)
+
+
+def fp8_e4m3_block_mlp_many_weighted_avx512_f32(items, hidden, route_weights) -> torch.Tensor:
+    """src/pcketlm/native/__init__.py:3951-4022 (same device kernel as the scalar name)."""
+    return _weighted("fp8_e4m3_block_mlp_many_weighted_avx512_f32", "PCKETLM_DISABLE_NATIVE_FP8_AVX512",
+                     "Native FP8 AVX-512 weighted many-MLP", items, hidden, route_weights, per_row=False)
+
+
+def fp8_e4m3_block_mlp_many_row_weighted_f32(items, hidden, route_weights) -> torch.Tensor:
+    """src/pcketlm/native/__init__.py:3796-3867 -> fp8_linear.cpp:591-831; route [E, M]."""
+    return _weighted("fp8_e4m3_block_mlp_many_row_weighted_f32", "PCKETLM_DISABLE_NATIVE_FP8_LINEAR",
+                     "Native FP8 row-weighted many-MLP", items, hidden, route_weights, per_row=True)
+
+
+def fp8_e4m3_block_mlp_many_pair_weighted_f32(items, hidden, pair_item_indices, pair_row_indices,
+                                              pair_weights) -> torch.Tensor:
+    """src/pcketlm/native/__init__.py:3870-3948 -> fp8_linear.cpp:833-980."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_FP8_LINEAR", "Native FP8 pair-weighted many-MLP")
+    dev = _target_device(hidden, *(items[0] if items else ()))
+    ex = _Experts(items, hidden, dev)
+    pi = _on(pair_item_indices, dev, torch.int64).reshape(-1)
+    pr = _on(pair_row_indices, dev, torch.int64).reshape(-1)
+    pw = _on(pair_weights, dev, torch.float32).reshape(-1)
+    if int(pi.numel()) != int(pr.numel()) or int(pi.numel()) != int(pw.numel()):
+        raise ValueError("pair index and weight tensors must have matching length")
+    batch = int(ex.x.shape[0])
+    out = torch.empty((batch, ex.hid), dtype=torch.float32, device=dev)
+    with _launch(lib, dev):
+        code = lib.fp8_e4m3_block_mlp_many_pair_weighted_f32(*ex.table_args(), _p(ex.x), _p(pi), _p(pr), _p(pw),
+                                                             _p(out), ex.count, int(pi.numel()), batch, ex.inter,
+                                                             ex.hid, ex.gsc, ex.dsc)
+    _check("fp8_e4m3_block_mlp_many_pair_weighted_f32", code)
+    return _home(out, hidden)
+
+
+# --------------------------------------------------------------------------- Q4
+
+def q4_dequant_to_fp16(packed: torch.Tensor, scales: torch.Tensor, num_channels: int, channel_size: int) -> torch.Tensor:
+    """src/pcketlm/native/__init__.py:4025-4045 -> q4_dequant.cpp:171-208; flat fp16 out."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_Q4", "Native Q4 dequant")
+    dev = _target_device(packed, scales)
+    p = _on(packed, dev, torch.uint8)
+    s = _on(scales, dev, torch.float16)
+    count = int(num_channels) * int(channel_size)
+    if int(p.numel()) < (count + 1) // 2 or int(s.numel()) < int(num_channels):
+        raise ValueError("packed / scales are smaller than num_channels * channel_size requires")
+    out = torch.empty((count,), dtype=torch.float16, device=dev)
+    if count:
+        with _launch(lib, dev):
+            lib.q4_dequant_to_fp16(_p(p), _p(s), _p(out), int(num_channels), int(channel_size))
+        err = _lib.last_error()
+        if err:
+            raise RuntimeError(f"q4_dequant_to_fp16 failed ({err})")
+    return _home(out, packed)
+
+
+def q4_dequant_many_to_fp16(items) -> list[torch.Tensor]:
+    """src/pcketlm/native/__init__.py:4048-4089 -> q4_dequant.cpp:210-286."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_Q4", "Native Q4 batch dequant")
+    if not items:
+        return []
+    dev = _target_device(*(t for item in items for t in item[:2]))
+    keep, outs = [], []
+    n = len(items)
+    pp, sp, op = (ctypes.c_void_p * n)(), (ctypes.c_void_p * n)(), (ctypes.c_void_p * n)()
+    ch, cs = (ctypes.c_longlong * n)(), (ctypes.c_longlong * n)()
+    for i, (packed, scales, num_channels, channel_size) in enumerate(items):
+        p = _on(packed, dev, torch.uint8)
+        s = _on(scales, dev, torch.float16)
+        count = int(num_channels) * int(channel_size)
+        if int(p.numel()) < (count + 1) // 2 or int(s.numel()) < int(num_channels):
+            raise ValueError("packed / scales are smaller than num_channels * channel_size requires")
+        out = torch.empty((count,), dtype=torch.float16, device=dev)
+        keep += [p, s]
+        outs.append(out)
+        pp[i], sp[i], op[i] = p.data_ptr(), s.data_ptr(), out.data_ptr() if count else 0
+        ch[i], cs[i] = int(num_channels), int(channel_size)
+    with _launch(lib, dev):
+        code = lib.q4_dequant_many_to_fp16(ctypes.cast(pp, ctypes.c_void_p), ctypes.cast(sp, ctypes.c_void_p),
+                                           ctypes.cast(op, ctypes.c_void_p), ctypes.cast(ch, ctypes.c_void_p),
+                                           ctypes.cast(cs, ctypes.c_void_p), n)
+    if code != 0:
+        raise RuntimeError(f"Native Q4 batch dequant failed with code {code}")
+    like = items[0][0]
+    return [_home(o, like) for o in outs]
+
+
+def q4_gemv_f16_f32(packed: torch.Tensor, scales: torch.Tensor, hidden: torch.Tensor, *, rows: int, cols: int) -> torch.Tensor:
+    """One Q4 matrix [rows, cols] times an fp16 vector: the row dot of
+    q4_moe_selected_forward_u16 (q4_dequant.cpp:314-355) on its own."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_Q4", "Native Q4 GEMV")
+    dev = _target_device(packed, hidden)
+    p = _on(packed, dev, torch.uint8)
+    s = _on(scales, dev, torch.float16)
+    h = _on(hidden, dev, torch.float16).reshape(-1)
+    if int(h.numel()) != int(cols):
+        raise ValueError("hidden size mismatch")
+    if int(p.numel()) < (int(rows) * int(cols) + 1) // 2 or int(s.numel()) < int(rows):
+        raise ValueError("packed / scales are smaller than rows * cols requires")
+    out = torch.empty((int(rows),), dtype=torch.float32, device=dev)
+    with _launch(lib, dev):
+        code = lib.q4_gemv_f16_f32(_p(p), _p(s), _p(h), _p(out), int(rows), int(cols))
+    _check("q4_gemv_f16_f32", code)
+    return _home(out, hidden)
+
+
+def q4_moe_selected_forward_u16(hidden: torch.Tensor, experts, route_weights: torch.Tensor, *, hidden_size: int,
+                                intermediate_size: int) -> torch.Tensor:
+    """src/pcketlm/native/__init__.py:4092-4155 -> q4_dequant.cpp:357-476; fp16 [H] out."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_Q4", "Native Q4 MoE selected forward")
+    if not experts:
+        raise ValueError("experts must not be empty")
+    dev = _target_device(hidden, *experts[0])
+    h = _on(hidden, dev, torch.float16).reshape(-1)
+    if h.numel() != int(hidden_size):
+        raise ValueError("hidden size mismatch")
+    route = _on(route_weights, dev, torch.float32).reshape(-1)
+    if route.numel() != len(experts):
+        raise ValueError("route weight count must match selected experts")
+    n = len(experts)
+    arrays = [(ctypes.c_void_p * n)() for _ in range(6)]
+    keep = [h, route]
+    H, I = int(hidden_size), int(intermediate_size)
+    need = [(I * H + 1) // 2, I, (I * H + 1) // 2, I, (H * I + 1) // 2, H]
+    for e, tensors in enumerate(experts):
+        for slot, t in enumerate(tensors):
+            dt = torch.uint8 if slot % 2 == 0 else torch.float16
+            d = _on(t, dev, dt)
+            if int(d.numel()) < need[slot]:
+                raise ValueError("expert tensor is smaller than hidden_size / intermediate_size require")
+            keep.append(d)
+            arrays[slot][e] = d.data_ptr()
+    out = torch.empty((H,), dtype=torch.float16, device=dev)
+    with _launch(lib, dev):
+        code = lib.q4_moe_selected_forward_u16(_p(h), *[ctypes.cast(a, ctypes.c_void_p) for a in arrays], _p(route),
+                                               _p(out), H, I, n)
+    if code != 0:
+        raise RuntimeError(f"Native Q4 MoE selected forward failed with code {code}")
+    return _home(out, hidden)
+
+
+# --------------------------------------------------------------------------- row8
+# Pack cache: src/pcketlm/native/__init__.py:2108-2193.
+
+_PACKED_GEMV_CACHE: "OrderedDict[str, torch.Tensor]" = OrderedDict()
+_PACKED_GEMV_CACHE_BYTES = 0
+_PACKED_GEMV_CACHE_STATS = {"hits": 0, "misses": 0, "stores": 0, "evictions": 0}
+
+
+def _u16_storage_dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float16:
+        return 0
+    if dtype == torch.bfloat16:
+        return 1
+    raise TypeError("native KV kernels require torch.float16 or torch.bfloat16 tensors")
+
+
+def _packed_gemv_cache_disabled() -> bool:
+    return _flag("PCKETLM_DISABLE_PACKED_GEMV_CACHE")
+
+
+def _packed_gemv_cache_budget_bytes() -> int:
+    raw = os.environ.get("PCKETLM_PACKED_GEMV_CACHE_MB", "").strip()
+    if not raw:
+        return 0
+    try:
+        mb = int(raw)
+    except ValueError:
+        return 0
+    return max(0, mb) * 1024 * 1024
+
+
+def reset_packed_gemv_cache() -> None:
+    global _PACKED_GEMV_CACHE_BYTES
+    _PACKED_GEMV_CACHE.clear()
+    _PACKED_GEMV_CACHE_BYTES = 0
+    for key in _PACKED_GEMV_CACHE_STATS:
+        _PACKED_GEMV_CACHE_STATS[key] = 0
+
+
+def packed_gemv_cache_stats() -> dict[str, int | float]:
+    return {
+        **_PACKED_GEMV_CACHE_STATS,
+        "resident_count": len(_PACKED_GEMV_CACHE),
+        "resident_bytes": _PACKED_GEMV_CACHE_BYTES,
+        "resident_mb": round(_PACKED_GEMV_CACHE_BYTES / 1024 / 1024, 4),
+        "budget_bytes": _packed_gemv_cache_budget_bytes(),
+    }
+
+
+def pack_weight_rows8(weight: torch.Tensor) -> torch.Tensor:
+    """src/pcketlm/native/__init__.py:2141-2163 -> fp16_packed_gemv.cpp:52-77 (device pack)."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_PACKED_GEMV", "Native packed GEMV")
+    if weight.dtype not in {torch.float16, torch.bfloat16}:
+        raise TypeError("pack_weight_rows8 requires torch.float16 or torch.bfloat16 weight")
+    if weight.ndim != 2:
+        raise ValueError("weight must have shape [rows, cols]")
+    dev = _target_device(weight)
+    w = _on(weight, dev)
+    rows, cols = int(w.shape[0]), int(w.shape[1])
+    packed = torch.empty((((rows + 7) // 8) * cols * 8,), dtype=torch.uint16, device=dev)
+    if packed.numel():
+        with _launch(lib, dev):
+            code = lib.native_pack_u16_rows8(_p(w), _p(packed), rows, cols)
+        _check("native_pack_u16_rows8", code)
+    return _home(packed, weight)
+
+
+def cached_pack_weight_rows8(cache_key: str, weight: torch.Tensor) -> torch.Tensor:
+    """src/pcketlm/native/__init__.py:2166-2193 (LRU bounded by PCKETLM_PACKED_GEMV_CACHE_MB)."""
+    global _PACKED_GEMV_CACHE_BYTES
+    if _packed_gemv_cache_disabled():
+        _PACKED_GEMV_CACHE_STATS["misses"] += 1
+        return pack_weight_rows8(weight)
+    budget = _packed_gemv_cache_budget_bytes()
+    if budget <= 0:
+        _PACKED_GEMV_CACHE_STATS["misses"] += 1
+        return pack_weight_rows8(weight)
+    key = str(cache_key)
+    cached = _PACKED_GEMV_CACHE.get(key)
+    if cached is not None:
+        _PACKED_GEMV_CACHE.move_to_end(key)
+        _PACKED_GEMV_CACHE_STATS["hits"] += 1
+        return cached
+    _PACKED_GEMV_CACHE_STATS["misses"] += 1
+    packed = pack_weight_rows8(weight)
+    nbytes = int(packed.numel() * packed.element_size())
+    if nbytes > budget:
+        return packed
+    while _PACKED_GEMV_CACHE and _PACKED_GEMV_CACHE_BYTES + nbytes > budget:
+        _old, old = _PACKED_GEMV_CACHE.popitem(last=False)
+        _PACKED_GEMV_CACHE_BYTES -= int(old.numel() * old.element_size())
+        _PACKED_GEMV_CACHE_STATS["evictions"] += 1
+    _PACKED_GEMV_CACHE[key] = packed
+    _PACKED_GEMV_CACHE_BYTES += nbytes
+    _PACKED_GEMV_CACHE_STATS["stores"] += 1
+    return packed
+
+
+def packed_gemv_rows8(hidden: torch.Tensor, packed_weight: torch.Tensor, *, rows: int, cols: int) -> torch.Tensor:
+    """src/pcketlm/native/__init__.py:2196-2223 -> fp16_packed_gemv.cpp:79-116."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_PACKED_GEMV", "Native packed GEMV")
+    if hidden.dtype not in {torch.float16, torch.bfloat16}:
+        raise TypeError("packed_gemv_rows8 requires torch.float16 or torch.bfloat16 hidden")
+    if packed_weight.dtype != torch.uint16:
+        raise TypeError("packed_weight must be a torch.uint16 tensor from pack_weight_rows8")
+    dev = _target_device(hidden, packed_weight)
+    h = _on(hidden, dev).reshape(-1)
+    if h.numel() != int(cols):
+        raise ValueError("hidden length does not match packed weight column count")
+    pw = _on(packed_weight, dev)
+    if pw.numel() != ((int(rows) + 7) // 8) * int(cols) * 8:
+        raise ValueError("packed weight length does not match rows/cols")
+    out = torch.empty((int(rows),), dtype=torch.float32, device=dev)
+    if int(rows):
+        with _launch(lib, dev):
+            code = lib.native_packed_gemv_rows8(_p(h), _p(pw), _p(out), int(rows), int(cols),
+                                                _u16_storage_dtype_code(h.dtype))
+        _check("native_packed_gemv_rows8", code)
+    return _home(out, hidden)
+
+
+def packed_gemv_rows8_many(hidden: torch.Tensor, packed_weights, rows, *, cols: int, biases=None) -> list[torch.Tensor]:
+    """Several row8 GEMVs sharing one hidden vector in one launch (the q/k/v and
+    gate/up fusions of fp16_kv_cache.cpp:239-298), with optional biases."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_PACKED_GEMV", "Native packed GEMV")
+    if hidden.dtype not in {torch.float16, torch.bfloat16}:
+        raise TypeError("packed_gemv_rows8 requires torch.float16 or torch.bfloat16 hidden")
+    n = len(packed_weights)
+    if n == 0 or n != len(rows) or n > 8:
+        raise ValueError("packed_weights and rows must have the same length (1..8)")
+    dev = _target_device(hidden, *packed_weights)
+    h = _on(hidden, dev).reshape(-1)
+    if h.numel() != int(cols):
+        raise ValueError("hidden length does not match packed weight column count")
+    keep, outs = [], []
+    pp, bp, op = (ctypes.c_void_p * n)(), (ctypes.c_void_p * n)(), (ctypes.c_void_p * n)()
+    rr = (ctypes.c_longlong * n)()
+    for i, (pwt, r) in enumerate(zip(packed_weights, rows)):
+        if pwt.dtype != torch.uint16:
+            raise TypeError("packed_weight must be a torch.uint16 tensor from pack_weight_rows8")
+        pw = _on(pwt, dev)
+        if pw.numel() != ((int(r) + 7) // 8) * int(cols) * 8:
+            raise ValueError("packed weight length does not match rows/cols")
+        out = torch.empty((int(r),), dtype=torch.float32, device=dev)
+        keep.append(pw)
+        outs.append(out)
+        pp[i], op[i], rr[i] = pw.data_ptr(), out.data_ptr(), int(r)
+        if biases is not None and biases[i] is not None:
+            b = _on(biases[i], dev, h.dtype).reshape(-1)
+            if b.numel() != int(r):
+                raise ValueError("bias length must match rows")
+            keep.append(b)
+            bp[i] = b.data_ptr()
+    with _launch(lib, dev):
+        code = lib.native_packed_gemv_rows8_many(_p(h), ctypes.cast(pp, ctypes.c_void_p),
+                                                 ctypes.cast(bp, ctypes.c_void_p), ctypes.cast(op, ctypes.c_void_p),
+                                                 ctypes.cast(rr, ctypes.c_void_p), n, int(cols),
+                                                 _u16_storage_dtype_code(h.dtype))
+    _check("native_packed_gemv_rows8_many", code)
+    return [_home(o, hidden) for o in outs]
+
+
+# --------------------------------------------------------------------------- DeepSeek session / MoE
+
+class DeepSeekNativeSession:
+    """src/pcketlm/native/__init__.py:1411-1519: C-side session with call counters."""
+
+    def __init__(self, *, num_layers: int, hidden_dim: int, num_experts: int, top_k: int,
+                 fp8_pack_callback: object | None = None, kv_session_handle: int | None = None):
+        lib = _require("PCKETLM_DISABLE_DS_MONOLITHIC", "DeepSeek native session")
+        self._lib = lib
+        self._callback_keepalive: list[object] = []
+        self._tensor_keepalive: list[object] = []
+        pack_ptr = 0 if fp8_pack_callback is None else int(ctypes.cast(fp8_pack_callback, ctypes.c_void_p).value or 0)
+        kv_ptr = 0 if kv_session_handle is None else int(kv_session_handle)
+        handle = lib.ds_session_create(int(num_layers), int(hidden_dim), int(num_experts), int(top_k),
+                                       ctypes.c_void_p(pack_ptr), ctypes.c_void_p(kv_ptr))
+        if not handle:
+            raise RuntimeError("ds_session_create returned a null handle")
+        self._handle = ctypes.c_void_p(handle)
+
+    def close(self) -> None:
+        if getattr(self, "_handle", None):
+            self._lib.ds_session_destroy(self._handle)
+            self._handle = None
+            self._callback_keepalive.clear()
+            self._tensor_keepalive.clear()
+
+    def __enter__(self) -> "DeepSeekNativeSession":
+        return self
+
+    def __exit__(self, *_exc: object) -> None:
+        self.close()
+
+    @staticmethod
+    def tensor_callback(fn):
+        return _lib.DS_TENSOR_CALLBACK(fn)
+
+    def register_layer(self, *, layer_idx: int, layer_kind: int, weight_role: int, fp8_callback,
+                       scale_callback) -> None:
+        cb = _lib.DS_TENSOR_CALLBACK
+        fp8_cb = fp8_callback if isinstance(fp8_callback, cb) else cb(fp8_callback)
+        scale_cb = scale_callback if isinstance(scale_callback, cb) else cb(scale_callback)
+        self._callback_keepalive.extend([fp8_cb, scale_cb])
+        code = self._lib.ds_session_register_layer(self._handle, int(layer_idx), int(layer_kind), int(weight_role),
+                                                   fp8_cb, scale_cb)
+        if code != 0:
+            raise RuntimeError(f"ds_session_register_layer failed with code {code}")
+
+    def keep_tensor_alive(self, tensor: object) -> None:
+        self._tensor_keepalive.append(tensor)
+
+    def monolithic_call_count(self) -> int:
+        return int(self._lib.ds_monolithic_call_counter(self._handle))
+
+    def callback_invocation_count(self) -> int:
+        return int(self._lib.ds_callback_invocation_count(self._handle))
+
+    def expert_invocation_count(self) -> int:
+        return int(self._lib.ds_expert_invocation_count(self._handle))
+
+    def attention_invocation_count(self) -> int:
+        return int(self._lib.ds_attention_invocation_count(self._handle))
+
+    def fused_attention_invocation_count(self) -> int:
+        return int(self._lib.ds_fused_attention_invocation_count(self._handle))
+
+    def layers_executed_count(self) -> int:
+        return int(self._lib.ds_layers_executed_count(self._handle))
+
+    def registered_layer_count(self) -> int:
+        return int(self._lib.ds_registered_layer_count(self._handle))
+
+    def registered_fp8_nbytes(self, index: int) -> int:
+        return int(self._lib.ds_registered_fp8_nbytes(self._handle, int(index)))
+
+    def registered_scale_nbytes(self, index: int) -> int:
+        return int(self._lib.ds_registered_scale_nbytes(self._handle, int(index)))
+
+
+def ds_moe_layer_forward(session: DeepSeekNativeSession, expert_outputs: torch.Tensor,
+                         route_weights: torch.Tensor) -> torch.Tensor:
+    """src/pcketlm/native/__init__.py:1300-1328 -> ds_forward.cpp:337-367."""
+    if not native_ds_moe_available():
+        raise RuntimeError("Native DeepSeek MoE combine is unavailable: disabled")
+    dev = _target_device(expert_outputs, route_weights)
+    outs = _on(expert_outputs, dev, torch.float32)
+    if outs.ndim == 2:
+        outs = outs.unsqueeze(1)
+    if outs.ndim != 3:
+        raise ValueError("expert_outputs must be [selected, batch, hidden]")
+    w = _on(route_weights, dev, torch.float32).reshape(-1)
+    if int(w.numel()) != int(outs.shape[0]):
+        raise ValueError("route weight count must match selected expert count")
+    out = torch.empty((int(outs.shape[1]), int(outs.shape[2])), dtype=torch.float32, device=dev)
+    with _launch(session._lib, dev):
+        code = session._lib.ds_moe_layer_forward_f32(session._handle, _p(outs), _p(w), int(outs.shape[0]),
+                                                     int(outs.shape[1]), int(outs.shape[2]), _p(out))
+    _check("ds_moe_layer_forward_f32", code)
+    return _home(out, expert_outputs)
+
+
+def ds_moe_layer_forward_fp8(session: DeepSeekNativeSession, items, hidden: torch.Tensor,
+                             route_weights: torch.Tensor) -> torch.Tensor:
+    """src/pcketlm/native/__init__.py:1331-1400 -> ds_forward.cpp:784-877."""
+    if not native_ds_moe_available():
+        raise RuntimeError("Native DeepSeek MoE is unavailable: disabled")
+    dev = _target_device(hidden, *(items[0] if items else ()))
+    ex = _Experts(items, hidden, dev)
+    route = _on(route_weights, dev, torch.float32).reshape(-1)
+    if int(route.numel()) != ex.count:
+        raise ValueError("route weight count must match selected experts")
+    batch = int(ex.x.shape[0])
+    out = torch.empty((batch, ex.hid), dtype=torch.float32, device=dev)
+    with _launch(session._lib, dev):
+        code = session._lib.ds_moe_layer_forward_fp8_f32(session._handle, *ex.table_args(), _p(ex.x), _p(route),
+                                                         ex.count, batch, ex.inter, ex.hid, ex.gsc, ex.dsc, _p(out))
+    _check("ds_moe_layer_forward_fp8_f32", code)
+    return _home(out, hidden)
+
+
+def ds_router_topk(hidden: torch.Tensor, router_weights: torch.Tensor, *, k: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """src/pcketlm/native/__init__.py:765-801 -> ds_forward.cpp:879-955 (softmax top-k)."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_DS_ROUTER", "Native DeepSeek router")
+    dtype_code = _u16_storage_dtype_code(router_weights.dtype)
+    dev = _target_device(hidden, router_weights)
+    r = _on(router_weights, dev)
+    h = _on(hidden, dev, r.dtype).reshape(-1)
+    if r.ndim != 2 or int(r.shape[1]) != int(h.numel()):
+        raise ValueError("router weights must be [num_experts, hidden_dim] matching hidden")
+    ids = torch.empty((int(k),), dtype=torch.int64, device=dev)
+    weights = torch.empty((int(k),), dtype=torch.float32, device=dev)
+    with _launch(lib, dev):
+        code = lib.ds_router_topk_u16(_p(h), _p(r), int(r.shape[1]), int(r.shape[0]), int(k), dtype_code, _p(ids),
+                                      _p(weights))
+    _check("ds_router_topk_u16", code)
+    return _home(ids, hidden), _home(weights, hidden)
+
+
+def route_deepseek(logits: torch.Tensor, *, top_k: int = 8, n_groups: int = 8, topk_groups: int = 4,
+                   scoring_func: str = "sigmoid", route_scale: float = 2.5,
+                   bias: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """DeepSeek-V3 routing (src/pcketlm/core/runtime/fp8_source.py:1527-1547 with
+    _mask_deepseek_route_groups 5125-5140) from router logits [M, E].
+
+    Returns (indices int64 [M, top_k], weights bfloat16 [M, top_k]).
+    """
+    lib = _require("PCKETLM_DISABLE_NATIVE_DS_ROUTER", "Native DeepSeek router")
+    if scoring_func not in ("sigmoid", "softmax"):
+        raise ValueError("scoring_func must be 'sigmoid' or 'softmax'")
+    dev = _target_device(logits)
+    lg = _on(logits, dev, torch.float32)
+    lg = lg.reshape(-1, int(lg.shape[-1]))
+    m, e = int(lg.shape[0]), int(lg.shape[1])
+    k = max(1, min(int(top_k), e))
+    b = None if bias is None else _on(bias, dev, torch.float32).reshape(-1)
+    idx = torch.empty((m, k), dtype=torch.int64, device=dev)
+    w = torch.empty((m, k), dtype=torch.float32, device=dev)
+    with _launch(lib, dev):
+        code = lib.ds_route_topk_f32(_p(lg), _p(b), m, e, k, int(n_groups), int(topk_groups),
+                                     0 if scoring_func == "sigmoid" else 1, float(route_scale), _p(idx), _p(w))
+    _check("ds_route_topk_f32", code)
+    return _home(idx, logits), _home(w.to(torch.bfloat16), logits)

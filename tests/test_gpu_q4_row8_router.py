@@ -1,0 +1,192 @@
+"""Q4, row8 and router kernels on the GPU against the oracle and the golden
+vectors.  Dequant and pack are bit-exact; dot products within rel-L2 1e-5
+(fp32 outputs) or one fp16 ulp (fp16 outputs)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def nat():
+    from pocketlm_amd import native
+
+    assert native.native_q4_available(), "libpocketlm_hip.so must load on the GPU box"
+    return native
+
+
+def dev(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return t if dtype is None else t.to(dtype)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def q4_matrix(oracle_mod, rows, cols, seed, std=0.02):
+    w = (np.random.default_rng(seed).standard_normal((rows, cols)) * std).astype(np.float16).astype(np.float32)
+    packed, scales, _ = oracle_mod.q4_quantize(w)
+    return packed, scales
+
+
+def f16_bits(x: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(x.astype(np.float16)).view(np.uint16)
+
+
+# --------------------------------------------------------------------------- Q4
+
+def test_q4_dequant_golden_bit_exact(nat, golden, oracle_mod):
+    g = golden("q4")
+    for i in range(int(g["count"])):
+        ch, cs = oracle_mod.q4_shape_params(list(g[f"t{i}_shape"]))
+        got = host(nat.q4_dequant_to_fp16(dev(g[f"t{i}_packed"]), dev(g[f"t{i}_scales"]).view(torch.float16), ch, cs))
+        assert np.array_equal(got.view(np.uint16), g[f"t{i}_deq"]), i
+
+
+def test_q4_dequant_full_size_and_many(nat, oracle_mod):
+    packed, scales = q4_matrix(oracle_mod, 18944, 3584, 1)
+    got = host(nat.q4_dequant_to_fp16(dev(packed), dev(scales).view(torch.float16), 18944, 3584))
+    assert np.array_equal(got.view(np.uint16), oracle_mod.q4_dequant_f16(packed, scales, 18944, 3584))
+    items, wants = [], []
+    for j, (r, c) in enumerate(((64, 3584), (7, 33), (5, 17), (3, 1))):
+        p, s = q4_matrix(oracle_mod, r, c, 10 + j, std=1.0)
+        items.append((dev(p), dev(s).view(torch.float16), r, c))
+        wants.append(oracle_mod.q4_dequant_f16(p, s, r, c))
+    outs = nat.q4_dequant_many_to_fp16(items)
+    for o, w in zip(outs, wants):
+        assert np.array_equal(host(o).view(np.uint16), w)
+
+
+@pytest.mark.parametrize("shape", [(18944, 3584), (3584, 18944), (64, 96), (33, 1001)])
+def test_q4_gemv_vs_oracle(nat, oracle_mod, shape):
+    rows, cols = shape
+    packed, scales = q4_matrix(oracle_mod, rows, cols, rows + cols)
+    x16 = np.random.default_rng(cols).standard_normal(cols).astype(np.float16)
+    y = host(nat.q4_gemv_f16_f32(dev(packed), dev(scales).view(torch.float16), dev(x16), rows=rows, cols=cols))
+    want = oracle_mod.q4_gemv(packed, scales, x16.astype(np.float32), rows, cols)
+    assert rel_l2(y, want) < 1e-5
+
+
+def _moe_experts(g):
+    out = []
+    for e in range(2):
+        out.append(tuple(g[f"moe_{n}{e}_{k}"] for n in ("g", "u", "d") for k in ("packed", "scales")))
+    return out
+
+
+def test_q4_moe_kat(nat, golden, oracle_mod):
+    g = golden("q4")
+    experts = _moe_experts(g)
+    dexp = [tuple(dev(a) if i % 2 == 0 else dev(a).view(torch.float16) for i, a in enumerate(e)) for e in experts]
+    out = nat.q4_moe_selected_forward_u16(dev(g["moe_hidden"]).view(torch.float16), dexp, dev(g["moe_route"]),
+                                          hidden_size=16, intermediate_size=12)
+    got = host(out).astype(np.float32)
+    want = g["moe_expected_f32"].reshape(-1)
+    assert np.allclose(got, want.astype(np.float16).astype(np.float32), atol=1e-2, rtol=1e-2)
+    orc = oracle_mod.q4_moe_selected(g["moe_hidden"], experts, g["moe_route"], 16, 12).view(np.float16)
+    assert np.allclose(got, orc.astype(np.float32), rtol=2e-3, atol=1e-3)
+
+
+def test_q4_mlp_qwen_shape_vs_oracle(nat, oracle_mod):
+    H, I = 3584, 18944
+    g = q4_matrix(oracle_mod, I, H, 41)
+    u = q4_matrix(oracle_mod, I, H, 42)
+    d = q4_matrix(oracle_mod, H, I, 43)
+    x16 = np.random.default_rng(44).standard_normal(H).astype(np.float16)
+    expert = (g[0], g[1], u[0], u[1], d[0], d[1])
+    dexp = [tuple(dev(a) if i % 2 == 0 else dev(a).view(torch.float16) for i, a in enumerate(expert))]
+    out = nat.q4_moe_selected_forward_u16(dev(x16), dexp, torch.ones(1, device="cuda"), hidden_size=H,
+                                          intermediate_size=I)
+    want = oracle_mod.q4_moe_selected(x16.view(np.uint16), [expert], np.ones(1, np.float32), H, I)
+    assert rel_l2(host(out).astype(np.float32), want.view(np.float16).astype(np.float32)) < 1e-3
+
+
+# --------------------------------------------------------------------------- row8
+
+def test_row8_pack_golden_and_full(nat, golden, oracle_mod):
+    g = golden("row8")
+    for dt, tdt in (("f16", torch.float16), ("bf16", torch.bfloat16)):
+        w = dev(g[f"pack_{dt}_w"]).view(tdt)
+        assert np.array_equal(host(nat.pack_weight_rows8(w)).view(np.uint16), g[f"pack_{dt}_packed"])
+    w = np.random.default_rng(5).standard_normal((3589, 515)).astype(np.float16)
+    got = host(nat.pack_weight_rows8(dev(w))).view(np.uint16)
+    assert np.array_equal(got, oracle_mod.pack_rows8(w.view(np.uint16)))
+
+
+def test_row8_gemv_golden(nat, golden):
+    g = golden("row8")
+    for key in g["cases"]:
+        code = int(g[f"{key}_code"])
+        tdt = torch.float16 if code == 0 else torch.bfloat16
+        w = dev(g[f"{key}_w"]).view(tdt)
+        h = dev(g[f"{key}_h"]).view(tdt)
+        rows, cols = g[f"{key}_w"].shape
+        y = host(nat.packed_gemv_rows8(h, nat.pack_weight_rows8(w), rows=rows, cols=cols))
+        assert np.allclose(y, g[f"{key}_mv"], atol=1e-5, rtol=1e-5), key
+        assert rel_l2(y, g[f"{key}_y"]) < 1e-6, key
+
+
+@pytest.mark.parametrize("shape", [(3584, 3584), (512, 3584), (18944, 3584), (3584, 18944)])
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_row8_qwen_shapes_vs_oracle(nat, oracle_mod, shape, dt):
+    rows, cols = shape
+    tdt = torch.float16 if dt == "f16" else torch.bfloat16
+    rng = np.random.default_rng(rows + cols)
+    w = torch.from_numpy((rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)).to(tdt)
+    h = torch.from_numpy(rng.standard_normal(cols).astype(np.float32)).to(tdt)
+    packed = nat.pack_weight_rows8(w.cuda())
+    y = host(nat.packed_gemv_rows8(h.cuda(), packed, rows=rows, cols=cols))
+    want = oracle_mod.packed_gemv_rows8(h.view(torch.int16).numpy().view(np.uint16),
+                                        host(packed).view(np.uint16), rows, cols, 0 if dt == "f16" else 1)
+    assert rel_l2(y, want) < 1e-5
+
+
+def test_row8_many_with_bias(nat, oracle_mod):
+    cols = 3584
+    rng = np.random.default_rng(8)
+    h = rng.standard_normal(cols).astype(np.float16)
+    mats, packs, biases, rows = [], [], [], (3584, 512, 512)
+    for r in rows:
+        w = (rng.standard_normal((r, cols)) * 0.02).astype(np.float16)
+        mats.append(w)
+        packs.append(nat.pack_weight_rows8(dev(w)))
+        biases.append(dev(rng.standard_normal(r).astype(np.float16)))
+    outs = nat.packed_gemv_rows8_many(dev(h), packs, rows, cols=cols, biases=biases)
+    for w, p, b, o, r in zip(mats, packs, biases, outs, rows):
+        want = oracle_mod.packed_gemv_rows8(h.view(np.uint16), host(p).view(np.uint16), r, cols, 0,
+                                            host(b).view(np.uint16))
+        assert rel_l2(host(o), want) < 1e-5
+
+
+# --------------------------------------------------------------------------- routers
+
+def test_softmax_router_golden(nat, golden):
+    g = golden("router")
+    router = dev(g["softmax_router"]).view(torch.float16)
+    for i, h in enumerate(g["softmax_hidden"]):
+        ids, w = nat.ds_router_topk(dev(h).view(torch.float16), router, k=4)
+        assert host(ids).tolist() == g["softmax_ids"][i].tolist()
+        assert np.allclose(host(w), g["softmax_weights"][i], atol=1e-6, rtol=1e-6)
+
+
+def test_deepseek_route_kat_and_random(nat, golden, oracle_mod):
+    g = golden("router")
+    idx, w = nat.route_deepseek(dev(g["ds_kat_logits"]), top_k=1, n_groups=1, topk_groups=1, route_scale=2.5,
+                                bias=dev(g["ds_kat_bias"]))
+    assert host(idx).tolist() == [[1]] and host(w.float()).tolist() == [[2.5]]
+    rng = np.random.default_rng(12)
+    logits = rng.standard_normal((8, 256)).astype(np.float32)
+    bias = (rng.standard_normal(256) * 0.1).astype(np.float32)
+    for b in (bias, None):
+        idx, w = nat.route_deepseek(dev(logits), bias=None if b is None else dev(b))
+        oi, ow = oracle_mod.deepseek_route(logits, bias=b)
+        assert host(idx).tolist() == oi.tolist()
+        assert np.allclose(host(w.float()), ow, rtol=8e-3)
