@@ -24,6 +24,9 @@ hipStream_t current_stream();
 // Record a failure text for pocketlm_last_error() and return `code`.
 int fail(int code, const char* fmt, ...);
 
+// Forget the previous failure text (entry points without a return code).
+void clear_error();
+
 // Map a HIP error to the library's return code -(1000 + err) and record it.
 int hip_fail(hipError_t err, const char* where);
 

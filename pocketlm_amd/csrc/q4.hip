@@ -85,8 +85,9 @@ __global__ __launch_bounds__(256) void q4_dequant_kernel(const uint8_t* __restri
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
         for (int k = 0; k < 8; k += 2) {
-            const float q0 = static_cast<float>(__builtin_amdgcn_sbfe(static_cast<int>(d[i]), 4 * k, 4));
-            const float q1 = static_cast<float>(__builtin_amdgcn_sbfe(static_cast<int>(d[i]), 4 * k + 4, 4));
+            // sign-extend nibble k / k+1 (compiles to v_bfe_i32)
+            const float q0 = static_cast<float>(static_cast<int>(d[i] << (28 - 4 * k)) >> 28);
+            const float q1 = static_cast<float>(static_cast<int>(d[i] << (24 - 4 * k)) >> 28);
             uint32_t lo, hi;
             if (finite) {
                 lo = f16_rne_hw(q0 * sc);
@@ -387,6 +388,7 @@ bool q4_fast_ok(int64_t K, const void* x, const uint8_t* const* w, int n) {
 
 PLM_EXPORT void q4_dequant_to_fp16(const uint8_t* packed, const uint16_t* scales, uint16_t* out_fp16,
                                    int64_t num_channels, int64_t channel_size) {
+    plm::clear_error();
     if (!packed || !scales || !out_fp16 || num_channels <= 0 || channel_size <= 0) {
         plm::fail(1, "q4_dequant_to_fp16: null pointer or empty tensor");
         return;

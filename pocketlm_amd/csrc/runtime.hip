@@ -36,6 +36,8 @@ int fail(int code, const char* fmt, ...) {
     return code;
 }
 
+void clear_error() { t_error[0] = 0; }
+
 int hip_fail(hipError_t err, const char* where) {
     return fail(-(1000 + static_cast<int>(err)), "%s: %s", where, hipGetErrorString(err));
 }

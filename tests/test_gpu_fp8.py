@@ -33,8 +33,12 @@ def dev(a, dtype=None):
 
 
 def host(t):
+    """Device tensor -> numpy; bf16 / uint16 come back as their 16-bit patterns."""
     torch.cuda.synchronize()
-    return t.detach().cpu().numpy()
+    t = t.detach().cpu()
+    if t.dtype in (torch.bfloat16, torch.uint16):
+        t = t.view(torch.int16)
+    return t.numpy()
 
 
 def cuda_items(items):
@@ -76,7 +80,8 @@ def test_dequant_full_size_bit_exact(nat, oracle_mod):
                     ("bf16", nat.fp8_e4m3_dequant_to_bf16)):
         got = host(fn(dw, ds))
         want = oracle_mod.fp8_dequant(w, s, out)
-        assert np.array_equal(got.view(want.dtype), want), out
+        width = np.uint32 if out == "f32" else np.uint16
+        assert np.array_equal(got.view(width), want.view(width)), out
 
 
 def test_dequant_dispatcher_and_errors(nat):
