@@ -7,19 +7,19 @@
 Default workload (one JSON line): Q4 dequant+GEMV over one Qwen2.5-7B MLP,
 i.e. the gate and up matrices [18944, 3584] and the down matrix
 [3584, 18944], per-row symmetric Q4 from N(0, 0.02) weights, times one fp16
-activation row ~N(0, 1) (M = 1).  One step = the three GEMVs (three launches
-of the Q4 GEMV kernel).  Weight copies are rotated over more than 1 GB so
+activation row ~N(0, 1) (M = 1).  One step = one call of the reference's Q4
+MLP entry point q4_moe_selected_forward_u16 (one selected expert, route
+weight 1.0): a fused gate/up + SiLU launch and a down launch.  Weight copies are rotated over more than 1 GB so
 that the 256 MB Infinity Cache cannot serve them; inputs are resident in HBM
 before the timed region starts.
 
 Timing: the stream is held by a short sleep kernel while the timed launches
-are queued, with a HIP event between consecutive launches; the GPU then runs
-them back to back and each event pair brackets exactly one kernel.  ms/step
-and the per-launch durations come from those events.
+are queued; one HIP event pair on the launch stream brackets all of them, and
+the GPU runs them back to back.  ms/step and the average launch duration come
+from that pair.
 
-The ``cpu_baseline`` leg runs the CPU oracle's restatement of the reference
-Q4 row dot (OpenMP, all host threads) on a bounded sample of the same
-workload.
+The ``cpu_baseline`` leg runs the CPU oracle's restatement of the same
+entry point (OpenMP, all host threads) on a bounded sample of the workload.
 """
 
 from __future__ import annotations
@@ -53,7 +53,10 @@ def _args(argv=None):
 # --------------------------------------------------------------------------- timing
 
 class Timer:
-    """Per-launch GPU durations from HIP events, launches queued behind a sleep."""
+    """GPU time of a batch of launches from one pair of HIP events on the
+    launch stream.  The launches are queued behind a sleep kernel first, so
+    the host's enqueue cost stays out of the timed region and the kernels run
+    back to back."""
 
     def __init__(self, torch):
         self.torch = torch
@@ -70,19 +73,19 @@ class Timer:
         ms = max(a.elapsed_time(b), 1e-3)
         return 2_000_000 / ms
 
-    def run(self, launches, hold_ms: float = 30.0):
-        """launches: list of zero-arg callables, each enqueuing one kernel.
-        Returns the per-launch durations in ms."""
+    def run(self, launches, hold_ms: float = 30.0) -> float:
+        """launches: zero-arg callables, each enqueuing kernels on the current
+        stream.  Returns the total GPU time of all of them in ms."""
         torch = self.torch
-        events = [torch.cuda.Event(enable_timing=True) for _ in range(len(launches) + 1)]
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         torch.cuda._sleep(int(self.cycles_per_ms * hold_ms))
-        events[0].record()
-        for i, fn in enumerate(launches):
+        start.record()
+        for fn in launches:
             fn()
-            events[i + 1].record()
+        end.record()
         torch.cuda.synchronize()
-        return [events[i].elapsed_time(events[i + 1]) for i in range(len(launches))]
+        return start.elapsed_time(end)
 
 
 def _stream_ptr(torch):
@@ -116,55 +119,58 @@ def fp8_bytes(rows, cols, m):
     return rows * cols + 4 * math.ceil(rows / 128) * math.ceil(cols / 128) + 2 * m * cols + 4 * m * rows
 
 
-def bench_q4_gemv(torch, lib, fmt, steps, warmup, timer):
-    shapes = [(18944, 3584), (18944, 3584), (3584, 18944)]
+def mlp_bytes(hidden, inter):
+    """Algorithmic HBM bytes of one Q4 SwiGLU MLP call: the three packed
+    matrices and their fp16 row scales, the fp16 input and output, and the
+    fp32 intermediate written by the gate/up kernel and read by the down
+    kernel."""
+    weights = 3 * hidden * inter // 2
+    scales = 2 * (2 * inter + hidden)
+    return weights + scales + 2 * hidden + 2 * hidden + 2 * 4 * inter
+
+
+def bench_q4_mlp(torch, lib, fmt, steps, warmup, timer, hidden=3584, inter=18944):
+    """One step = one call of the reference's Q4 MLP entry point
+    (q4_moe_selected_forward_u16 with one selected expert, route weight 1.0):
+    gate/up [inter, hidden] + SiLU, then down [hidden, inter]."""
+    shapes = [(inter, hidden), (inter, hidden), (hidden, inter)]
     per_set = sum(r * c // 2 for r, c in shapes)
     nsets = max(2, math.ceil(MALL_BYTES / per_set))
     sets = _q4_sets(torch, fmt, shapes, nsets)
     gen = torch.Generator(device="cuda").manual_seed(7)
-    x_in = torch.randn((3584,), generator=gen, device="cuda").to(torch.float16)
-    x_down = torch.randn((18944,), generator=gen, device="cuda").to(torch.float16)
-    outs = [torch.empty((r,), device="cuda", dtype=torch.float32) for r, _ in shapes]
+    x = torch.randn((hidden,), generator=gen, device="cuda").to(torch.float16)
+    route = torch.ones(1, device="cuda")
+    out = torch.empty((hidden,), device="cuda", dtype=torch.float16)
     lib.pocketlm_set_stream(_stream_ptr(torch))
     calls = []
     for mats in sets:
-        step = []
-        for j, (packed, scales, rows, cols) in enumerate(mats):
-            x = x_in if cols == 3584 else x_down
-            args = (ctypes.c_void_p(packed.data_ptr()), ctypes.c_void_p(scales.data_ptr()),
-                    ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(outs[j].data_ptr()), rows, cols)
-            step.append((args, q4_bytes(rows, cols)))
-        calls.append(step)
+        tables = [(ctypes.c_void_p * 1)(t.data_ptr()) for m in mats for t in m[:2]]
+        calls.append(tuple(ctypes.cast(t, ctypes.c_void_p) for t in tables))
 
-    def launch(args):
-        code = lib.q4_gemv_f16_f32(*args)
+    def launch(tabs):
+        code = lib.q4_moe_selected_forward_u16(ctypes.c_void_p(x.data_ptr()), *tabs,
+                                               ctypes.c_void_p(route.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                                               hidden, inter, 1)
         if code != 0:
-            raise RuntimeError(f"q4_gemv_f16_f32 failed with code {code}")
+            raise RuntimeError(f"q4_moe_selected_forward_u16 failed with code {code}")
 
     for i in range(warmup):
-        for args, _ in calls[i % nsets]:
-            launch(args)
+        launch(calls[i % nsets])
     torch.cuda.synchronize()
-    launches, nbytes = [], []
-    for i in range(steps):
-        for args, b in calls[i % nsets]:
-            launches.append(lambda a=args: launch(a))
-            nbytes.append(b)
+    launches = [lambda t=calls[i % nsets]: launch(t) for i in range(steps)]
     t0 = time.perf_counter()
-    durs = timer.run(launches, hold_ms=max(30.0, 0.05 * len(launches)))
+    total_ms = timer.run(launches, hold_ms=max(30.0, 0.05 * len(launches)))
     wall = time.perf_counter() - t0
-    total_ms = sum(durs)
-    step_bytes = sum(b for _, b in calls[0])
     return {
-        "durations_ms": durs,
-        "bytes": nbytes,
+        "total_ms": total_ms,
         "ms_per_step": total_ms / steps,
-        "step_bytes": step_bytes,
+        "step_bytes": mlp_bytes(hidden, inter),
         "wall_s": wall,
         "nsets": nsets,
         "host_set": sets[0],
-        "x_in": x_in,
-        "x_down": x_down,
+        "x": x,
+        "hidden": hidden,
+        "inter": inter,
     }
 
 
@@ -173,28 +179,33 @@ def cpu_q4_baseline(torch, sample, seconds):
 
     import oracle
 
-    mats = [(p.cpu().numpy(), s.cpu().view(torch.int16).numpy().view(np.uint16), r, c)
-            for p, s, r, c in sample["host_set"]]
-    x_in = sample["x_in"].float().cpu().numpy()
-    x_down = sample["x_down"].float().cpu().numpy()
-    step_bytes = sum(q4_bytes(r, c) for _, _, r, c in mats)
+    def u16(t):
+        return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+    mats = sample["host_set"]
+    expert = []
+    for p, s, _r, _c in mats:
+        expert += [p.cpu().numpy(), u16(s)]
+    x16 = u16(sample["x"])
+    hidden, inter = sample["hidden"], sample["inter"]
+    route = np.ones(1, np.float32)
     steps = 0
     t0 = time.perf_counter()
     while True:
-        for p, s, r, c in mats:
-            oracle.q4_gemv(p, s, x_in if c == 3584 else x_down, r, c)
+        oracle.q4_moe_selected(x16, [tuple(expert)], route, hidden, inter)
         steps += 1
         el = time.perf_counter() - t0
         if el >= seconds:
             break
-    gbs = step_bytes * steps / el / 1e9
+    gbs = sample["step_bytes"] * steps / el / 1e9
     return {
         "value": round(gbs, 3),
         "unit": "GB/s",
         "cores": oracle.num_threads(),
         "kind": "port",
-        "sample": f"{steps} steps (gate+up+down Q4 GEMV, M=1) of one weight copy, "
-                  f"{el:.1f} s, {el / steps * 1e6:.0f} us/step, weights warm in host RAM",
+        "sample": f"{steps} calls of the oracle's restatement of q4_moe_selected_forward_u16 (Qwen2.5-7B MLP, "
+                  f"one expert, M=1) on one weight copy, {el:.1f} s, {el / steps * 1e6:.0f} us/call, "
+                  f"weights warm in host RAM",
     }
 
 
@@ -219,20 +230,21 @@ def main_line(args):
     if lib.pocketlm_device_available() != 1:
         raise RuntimeError("libpocketlm_hip.so reports no gfx950 device")
     timer = Timer(torch)
-    r = bench_q4_gemv(torch, lib, formats, args.steps, args.warmup, timer)
+    r = bench_q4_mlp(torch, lib, formats, args.steps, args.warmup, timer)
     ms = r["ms_per_step"]
     value = r["step_bytes"] / (ms / 1e3) / 1e9
-    achieved = sum(r["bytes"]) / (sum(r["durations_ms"]) / 1e3) / 1e9
+    # The step is two launches of the Q4 row-dot kernels (gate/up + SiLU,
+    # then down); the roofline is taken over both, from the same events.
     roof = {
         "bound": "hbm",
-        "kernel": "q4_rows_kernel<8,1,false,true> (q4_gemv_f16_f32)",
-        "achieved": round(achieved, 2),
+        "kernel": "q4_rows_kernel (gate/up + SiLU) + q4_combine_kernel (down), one MLP call",
+        "achieved": round(value, 2),
         "peak": PEAK_HBM_GBS,
         "unit": "GB/s",
-        "frac": round(achieved / PEAK_HBM_GBS, 4),
-        "traffic": _traffic("q4_gemv"),
-        "avg_launch_us": round(1e3 * sum(r["durations_ms"]) / len(r["durations_ms"]), 3),
-        "bytes_per_launch": round(sum(r["bytes"]) / len(r["bytes"])),
+        "frac": round(value / PEAK_HBM_GBS, 4),
+        "traffic": _traffic("q4_mlp"),
+        "launches_per_step": 2,
+        "bytes_per_step": r["step_bytes"],
     }
     cpu = None
     if not args.no_cpu:
@@ -245,7 +257,7 @@ def main_line(args):
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
-        "us_per_gemv": round(1e3 * ms / 3, 3),
+        "us_per_step": round(1e3 * ms, 3),
         "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
         "higher_is_better": True,
         "scaling": "weak",
@@ -253,7 +265,8 @@ def main_line(args):
         "dtype": "q4 weights, fp16 x, fp32 accumulate",
         "data": "synthetic (N(0,0.02) weights quantized with the reference Q4 scheme, x ~ N(0,1) fp16)",
         "config": {
-            "workload": "Q4 dequant+GEMV, Qwen2.5-7B MLP: gate/up [18944,3584] + down [3584,18944], M=1",
+            "workload": "Q4 dequant+GEMV, Qwen2.5-7B MLP: gate/up [18944,3584] + down [3584,18944], M=1, "
+                        "through q4_moe_selected_forward_u16 (one expert, route 1.0)",
             "bytes_per_step": r["step_bytes"],
             "weight_copies_rotated": r["nsets"],
         },
@@ -281,10 +294,9 @@ def table(args):
         for fn in calls[: min(len(calls), 8)]:
             fn()
         torch.cuda.synchronize()
-        reps = max(3, min(400, int(5e8 // max(nbytes, 1))))
+        reps = max(20, min(400, int(5e9 // max(nbytes, 1))))
         launches = [calls[i % len(calls)] for i in range(reps)]
-        durs = sorted(timer.run(launches, hold_ms=max(30.0, 0.05 * len(launches))))
-        med = durs[len(durs) // 2]
+        med = timer.run(launches, hold_ms=max(30.0, 0.05 * len(launches))) / reps
         gbs = nbytes / (med / 1e3) / 1e9
         cpu_us = cpu_gbs = None
         if cpu_fn is not None and not args.no_cpu:
@@ -465,10 +477,7 @@ def table(args):
         fn()
     torch.cuda.synchronize()
     launches = [calls[i % len(calls)] for i in range(60)]
-    durs = timer.run(launches)
-    layer_ms = [durs[i] + durs[i + 1] for i in range(0, len(durs), 2)]
-    layer_ms.sort()
-    med = layer_ms[len(layer_ms) // 2]
+    med = timer.run(launches) / (len(launches) // 2)
     nbytes = 9 * per_expert + 2 * 7168 * 4
     gbs = nbytes / (med / 1e3) / 1e9
     print(f"{'ds-v3 MoE layer (8 routed + shared)':40s} M=1  {1e3 * med:9.2f} us  {gbs:8.1f} GB/s  "
@@ -478,7 +487,7 @@ def table(args):
     del layers
     torch.cuda.empty_cache()
 
-    lines = ["| workload | M | GPU µs (median) | GPU GB/s | % of 8 TB/s | CPU µs | CPU GB/s | CPU kind |",
+    lines = ["| workload | M | GPU µs (mean) | GPU GB/s | % of 8 TB/s | CPU µs | CPU GB/s | CPU kind |",
              "|---|---|---|---|---|---|---|---|"]
     for name, m, us, gbs, pct, cus, cgbs, kind in rows_out:
         lines.append(f"| {name} | {m} | {us:.2f} | {gbs:.0f} | {pct:.1f} | "

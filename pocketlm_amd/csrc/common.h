@@ -63,17 +63,25 @@ __device__ __forceinline__ void plm_decode4_e4m3(uint32_t d, float* v) {
     v[3] = hi[1];
 }
 
-// Sum across the 64 lanes of a wave with a fixed xor butterfly (32, 16, ...,
-// 1): every lane ends with the same total, and the addition tree is the same
-// whatever else the wave is reducing, so results do not depend on the tile
-// shape a kernel instance uses.
+// Sum across the 64 lanes of a wave with DPP row operations (no LDS
+// traffic); the total is valid in lane 63 only.  The addition tree is fixed,
+// so a value's sum does not depend on what else the wave reduces or on the
+// tile shape a kernel instance uses.
+#define PLM_DPP_ADD(v, ctrl, row_mask)                                                                   \
+    ((v) + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), (ctrl), \
+                                                                 (row_mask), 0xF, false)))
+
 __device__ __forceinline__ float plm_wave_sum(float v) {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-        v += __shfl_xor(v, d, 64);
-    }
-    return v;
+    v = PLM_DPP_ADD(v, 0xB1, 0xF);   // quad_perm [1,0,3,2]: pairs
+    v = PLM_DPP_ADD(v, 0x4E, 0xF);   // quad_perm [2,3,0,1]: quads
+    v = PLM_DPP_ADD(v, 0x141, 0xF);  // row_half_mirror: groups of 8
+    v = PLM_DPP_ADD(v, 0x140, 0xF);  // row_mirror: rows of 16
+    v = PLM_DPP_ADD(v, 0x142, 0xA);  // row_bcast:15 into rows 1 and 3
+    v = PLM_DPP_ADD(v, 0x143, 0xC);  // row_bcast:31 into rows 2 and 3
+    return v;                        // lane 63 holds the wave total
 }
+
+constexpr int kSumLane = 63;
 
 __device__ __forceinline__ float plm_silu_mul(float gate, float up) {
     // g / (1 + exp(-g)) * up, all fp32 (fp8_linear.cpp:279-280)

@@ -10,8 +10,8 @@
 // (RNE, NaN -> sign|0x7E00|payload>>13); bf16 is bits + 0x7FFF + lsb with
 // every NaN -> 0xFFFF (fp8_dequant.cpp:108-117).
 //
-// Streaming kernel: one thread reads 16 weight bytes (one 16-byte load) and
-// writes 16 outputs; HBM-bound on the writes (2 or 4 bytes per weight byte).
+// Streaming kernel, HBM-bound on the writes (2 or 4 bytes per weight byte):
+// every wave-wide store is 1 KB contiguous.
 #include "common.h"
 
 namespace {
@@ -54,48 +54,68 @@ __device__ __forceinline__ void decode4_dequant(uint32_t d, float* v) {
     }
 }
 
+// True when one of the four bytes of d is an e4m3 NaN (0x7F / 0xFF).
+__device__ __forceinline__ bool has_nan_byte(uint32_t d) {
+    return (((d & 0x7F7F7F7Fu) + 0x01010101u) & 0x80808080u) != 0u;
+}
+
 template <int OUT>
-__device__ __forceinline__ void store16(void* out, int64_t idx, const uint32_t* bits) {
-    if constexpr (OUT == 2) {
-        float4* o = reinterpret_cast<float4*>(static_cast<float*>(out) + idx);
+__device__ __forceinline__ uint32_t out_bits16(uint32_t bits) {
+    return OUT == 0 ? f16_bits_f16c(bits) : bf16_bits(bits);
+}
+
+// Dequantize the 4 bytes of d with scale sc into 4 fp32 bit patterns.
+__device__ __forceinline__ void deq4(uint32_t d, float sc, bool exact, uint32_t* bits) {
+    float v[4];
+    if (exact) {
+        decode4_dequant(d, v);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            o[i] = make_float4(u2f(bits[4 * i]), u2f(bits[4 * i + 1]), u2f(bits[4 * i + 2]), u2f(bits[4 * i + 3]));
+        for (int j = 0; j < 4; ++j) bits[j] = x86_mul_bits(v[j], sc);
     } else {
-        uint32_t h[8];
+        plm_decode4_e4m3(d, v);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t lo = OUT == 0 ? f16_bits_f16c(bits[2 * i]) : bf16_bits(bits[2 * i]);
-            const uint32_t hi = OUT == 0 ? f16_bits_f16c(bits[2 * i + 1]) : bf16_bits(bits[2 * i + 1]);
-            h[i] = lo | (hi << 16);
-        }
-        uint4* o = reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + idx);
-        o[0] = make_uint4(h[0], h[1], h[2], h[3]);
-        o[1] = make_uint4(h[4], h[5], h[6], h[7]);
+        for (int j = 0; j < 4; ++j) bits[j] = f2u(v[j] * sc);
     }
 }
 
-// One workgroup covers 256 x 16 = 4096 columns of one row.
+// One workgroup covers 4096 columns of one row.  For 16-bit outputs a lane
+// reads 8 bytes and writes 16, for fp32 it reads 4 and writes 16, so every
+// wave-wide store is 1 KB contiguous.  Finite spans take the plain
+// multiply; spans holding a NaN byte (or a non-finite scale) take the exact
+// x86 emulation.
 template <int OUT>
 __global__ __launch_bounds__(256) void fp8_dequant_kernel(const uint8_t* __restrict__ w, const float* __restrict__ s,
                                                           void* __restrict__ out, int64_t cols, int64_t scale_cols,
                                                           int segs_per_row) {
+    constexpr int BPL = OUT == 2 ? 4 : 8;        // input bytes per lane per pass
+    constexpr int PASSES = 4096 / (256 * BPL);   // 4 (fp32) or 2 (16-bit)
     const int64_t row = blockIdx.x / segs_per_row;
     const int seg = blockIdx.x - static_cast<int>(row) * segs_per_row;
-    const int64_t col = static_cast<int64_t>(seg) * 4096 + threadIdx.x * 16;
-    if (col >= cols) return;
-    const int64_t idx = row * cols + col;
-    const uint4 q = *reinterpret_cast<const uint4*>(w + idx);
-    const float sc = s[(row >> 7) * scale_cols + (col >> 7)];
-    float v[16];
-    decode4_dequant(q.x, v);
-    decode4_dequant(q.y, v + 4);
-    decode4_dequant(q.z, v + 8);
-    decode4_dequant(q.w, v + 12);
-    uint32_t bits[16];
+    const float* srow = s + (row >> 7) * scale_cols;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) bits[j] = x86_mul_bits(v[j], sc);
-    store16<OUT>(out, idx, bits);
+    for (int p = 0; p < PASSES; ++p) {
+        const int64_t col = static_cast<int64_t>(seg) * 4096 + (p * 256 + threadIdx.x) * BPL;
+        if (col >= cols) break;
+        const int64_t idx = row * cols + col;
+        const float sc = srow[col >> 7];
+        const bool sc_finite = (f2u(sc) & 0x7F800000u) != 0x7F800000u;
+        if constexpr (OUT == 2) {
+            const uint32_t d = *reinterpret_cast<const uint32_t*>(w + idx);
+            uint32_t b[4];
+            deq4(d, sc, !sc_finite || has_nan_byte(d), b);
+            *reinterpret_cast<uint4*>(static_cast<float*>(out) + idx) = make_uint4(b[0], b[1], b[2], b[3]);
+        } else {
+            const uint2 d = *reinterpret_cast<const uint2*>(w + idx);
+            const bool exact = !sc_finite || has_nan_byte(d.x) || has_nan_byte(d.y);
+            uint32_t b[8];
+            deq4(d.x, sc, exact, b);
+            deq4(d.y, sc, exact, b + 4);
+            uint32_t h[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) h[i] = out_bits16<OUT>(b[2 * i]) | (out_bits16<OUT>(b[2 * i + 1]) << 16);
+            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + idx) = make_uint4(h[0], h[1], h[2], h[3]);
+        }
+    }
 }
 
 template <int OUT>

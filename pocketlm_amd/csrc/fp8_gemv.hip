@@ -139,15 +139,16 @@ __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
         for (int c = wave; c < a.nchunks; c += nw) {
             const int64_t col = static_cast<int64_t>(c) * plm::kChunkBytes + lane * 16;
             if (col >= a.K) continue;
+            // Loads are unconditional (rows past the end are clamped to the last
+            // row and their results dropped) so that all of them issue before
+            // the first wait.
             uint4 q[NWT][TR];
 #pragma unroll
             for (int i = 0; i < NWT; ++i)
 #pragma unroll
                 for (int r = 0; r < TR; ++r) {
-                    q[i][r] = make_uint4(0u, 0u, 0u, 0u);
-                    if (row0 + r < a.rows) {
-                        q[i][r] = *reinterpret_cast<const uint4*>(W[i] + (row0 + r) * a.K + col);
-                    }
+                    const int64_t rr = row0 + r < a.rows ? row0 + r : a.rows - 1;
+                    q[i][r] = *reinterpret_cast<const uint4*>(W[i] + rr * a.K + col);
                 }
             float sc[NWT];
 #pragma unroll
@@ -183,7 +184,7 @@ __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 const float t = plm_wave_sum(acc[i][r][m]);
-                if (lane == 0) red[wave * V + (i * TR + r) * M + m] = t;
+                if (lane == kSumLane) red[wave * V + (i * TR + r) * M + m] = t;
             }
     __syncthreads();
 
@@ -253,8 +254,8 @@ __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
         uint4 q[TR];
 #pragma unroll
         for (int r = 0; r < TR; ++r) {
-            q[r] = make_uint4(0u, 0u, 0u, 0u);
-            if (row0 + r < a.rows) q[r] = *reinterpret_cast<const uint4*>(W + (row0 + r) * a.K + col);
+            const int64_t rr = row0 + r < a.rows ? row0 + r : a.rows - 1;
+            q[r] = *reinterpret_cast<const uint4*>(W + rr * a.K + col);
         }
         const float sc = S[(row0 >> 7) * a.scale_cols + (col >> 7)];
         float wv[TR][16];
@@ -284,7 +285,7 @@ __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             const float t = plm_wave_sum(acc[r][m]);
-            if (lane == 0) red[wave * V + r * M + m] = t;
+            if (lane == kSumLane) red[wave * V + r * M + m] = t;
         }
     __syncthreads();
 
@@ -400,14 +401,17 @@ int waves_for(int64_t nchunks) {
     return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(nchunks, kMaxWaves)));
 }
 
+// Rows per tile: 4 for one weight, fewer when two weights or many activation
+// rows would need too many accumulators (the per-row arithmetic does not
+// depend on this choice).
 template <int M>
 constexpr int rows_tile(int nwt) {
-    return nwt == 1 ? (M == 1 ? 8 : 4) : (M == 1 ? 4 : 2);
+    return nwt == 1 ? 4 : (M == 1 ? 4 : 2);
 }
 
 template <int M>
 constexpr int combine_tile() {
-    return M == 1 ? 8 : 4;
+    return 4;
 }
 
 template <int M, int NWT, bool SILU>

@@ -7,11 +7,12 @@
 //
 // Dot products.  A lane reads 16 packed bytes (32 values) per load.  Each
 // dword d holds 8 nibbles; u = d ^ 0x88888888 turns every signed nibble q
-// into the unsigned u = q + 8, so (u & 0x0F0F0F0F) and ((u >> 4) & ...) give
-// the even / odd elements as bytes, which v_cvt_f32_ubyte{0..3} turn into
-// floats with no per-element extract.  The +8 bias is removed once per
-// 32-value span: sum(q*x) = sum(u*x) - 8*sum(x), where sum(x) over the span
-// is shared by every row of the tile.  The row scale multiplies the span sum.
+// into the unsigned u = q + 8, which is unpacked without per-element
+// extracts (as fp16 subnormal pairs for v_dot2_f32_f16 when x is fp16, as
+// bytes for v_cvt_f32_ubyte when x is fp32).  The +8 bias is removed once
+// per 32-value span: sum(q*x) = sum(u*x) - 8*sum(x), where sum(x) over the
+// span is shared by every row of the tile.  The row scale multiplies the
+// row's sum.
 #include <algorithm>
 #include <cstring>
 #include <vector>
@@ -21,7 +22,6 @@
 namespace {
 
 constexpr int kMaxGroups = 64;
-constexpr int kMaxWaves = 8;
 
 __device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
 __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
@@ -68,26 +68,30 @@ __device__ __forceinline__ int q4_at(const uint8_t* p, int64_t idx) {
 
 // ------------------------------------------------------------------ dequant
 
-// Fast path: channel_size % 32 == 0; one thread = 16 packed bytes = 32 values.
-__global__ __launch_bounds__(256) void q4_dequant_kernel(const uint8_t* __restrict__ packed,
+// Fast path: channel_size % 32 == 0 (a channel is whole dwords of packed
+// data).  A lane converts one packed dword (8 values) into one 16-byte store,
+// so each wave-wide store is 1 KB contiguous; a thread handles 4 dwords
+// 256 apart, loading all four before converting.
+__global__ __launch_bounds__(256) void q4_dequant_kernel(const uint32_t* __restrict__ packed,
                                                          const uint16_t* __restrict__ scales,
-                                                         uint16_t* __restrict__ out, int64_t nvec,
-                                                         uint32_t vec_per_channel) {
-    const int64_t v = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (v >= nvec) return;
-    const int64_t c = static_cast<uint64_t>(v) / vec_per_channel;
-    const float sc = h2f_ref(scales[c]);
-    const uint4 q = *reinterpret_cast<const uint4*>(packed + v * 16);
-    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
-    uint32_t h[16];
-    const bool finite = (f2u(sc) & 0x7F800000u) != 0x7F800000u;
+                                                         uint4* __restrict__ out, uint32_t ndw,
+                                                         uint32_t dw_per_channel) {
+    const uint32_t base = blockIdx.x * 1024u + threadIdx.x;
+    uint32_t d[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int p = 0; p < 4; ++p) d[p] = packed[min(base + p * 256u, ndw - 1u)];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const uint32_t idx = base + p * 256u;
+        if (idx >= ndw) break;
+        const float sc = h2f_ref(scales[idx / dw_per_channel]);
+        const bool finite = (f2u(sc) & 0x7F800000u) != 0x7F800000u;
+        uint32_t h[4];
 #pragma unroll
         for (int k = 0; k < 8; k += 2) {
-            // sign-extend nibble k / k+1 (compiles to v_bfe_i32)
-            const float q0 = static_cast<float>(static_cast<int>(d[i] << (28 - 4 * k)) >> 28);
-            const float q1 = static_cast<float>(static_cast<int>(d[i] << (24 - 4 * k)) >> 28);
+            // sign-extend nibbles k and k+1
+            const float q0 = static_cast<float>(static_cast<int>(d[p] << (28 - 4 * k)) >> 28);
+            const float q1 = static_cast<float>(static_cast<int>(d[p] << (24 - 4 * k)) >> 28);
             uint32_t lo, hi;
             if (finite) {
                 lo = f16_rne_hw(q0 * sc);
@@ -96,14 +100,10 @@ __global__ __launch_bounds__(256) void q4_dequant_kernel(const uint8_t* __restri
                 lo = f16_from_bits(q_mul_bits(q0, sc), true);
                 hi = f16_from_bits(q_mul_bits(q1, sc), true);
             }
-            h[i * 4 + k / 2] = lo | (hi << 16);
+            h[k / 2] = lo | (hi << 16);
         }
+        out[idx] = make_uint4(h[0], h[1], h[2], h[3]);
     }
-    uint4* o = reinterpret_cast<uint4*>(out + v * 32);
-    o[0] = make_uint4(h[0], h[1], h[2], h[3]);
-    o[1] = make_uint4(h[4], h[5], h[6], h[7]);
-    o[2] = make_uint4(h[8], h[9], h[10], h[11]);
-    o[3] = make_uint4(h[12], h[13], h[14], h[15]);
 }
 
 // Any shape: one thread per value, choosing the reference's converter per
@@ -124,10 +124,11 @@ int q4_dequant_launch(const uint8_t* packed, const uint16_t* scales, uint16_t* o
                       hipStream_t st) {
     const int64_t total = channels * cs;
     if (total <= 0) return 0;
-    if (cs % 32 == 0 && plm::aligned16(packed) && plm::aligned16(out) && cs / 32 <= 0xFFFFFFFFll) {
-        const int64_t nvec = total / 32;
-        hipLaunchKernelGGL(q4_dequant_kernel, dim3(static_cast<unsigned>(plm::ceil_div(nvec, 256))), dim3(256), 0, st,
-                           packed, scales, out, nvec, static_cast<uint32_t>(cs / 32));
+    if (cs % 32 == 0 && plm::aligned16(packed) && plm::aligned16(out) && total / 8 < (int64_t{1} << 31)) {
+        const int64_t ndw = total / 8;
+        hipLaunchKernelGGL(q4_dequant_kernel, dim3(static_cast<unsigned>(plm::ceil_div(ndw, 1024))), dim3(256), 0, st,
+                           reinterpret_cast<const uint32_t*>(packed), scales, reinterpret_cast<uint4*>(out),
+                           static_cast<uint32_t>(ndw), static_cast<uint32_t>(cs / 8));
     } else {
         hipLaunchKernelGGL(q4_dequant_scalar_kernel, dim3(static_cast<unsigned>(plm::ceil_div(total, 256))),
                            dim3(256), 0, st, packed, scales, out, channels, cs);
@@ -136,9 +137,67 @@ int q4_dequant_launch(const uint8_t* packed, const uint16_t* scales, uint16_t* o
 }
 
 // ------------------------------------------------------------------ dot products
+//
+// Layout of the dot-product kernels.  A wave is four groups of 16 lanes; a
+// group owns TR rows and reads them in steps of 256 packed bytes (512 values),
+// lane li taking bytes [16*li, 16*li + 16) of the step, so one wave-wide load
+// instruction fetches 4 x 256 contiguous bytes.  The NWS waves of a workgroup
+// split a row's steps, UNR steps of a wave are loaded before any is used, and
+// every load is unconditional: rows and steps past the end read a clamped
+// address and their contribution is dropped.  Row sums are four DPP adds
+// inside the 16-lane row, then an in-order sum over the waves in LDS.
 
-// sum over the 32 values of one 16-byte span of (u * x), with u = q + 8.
-__device__ __forceinline__ float span_dot_u(const uint4& q, const float* x) {
+typedef _Float16 plm_half2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float half_lo(uint32_t v) { return static_cast<float>(__builtin_bit_cast(plm_half2, v)[0]); }
+__device__ __forceinline__ float half_hi(uint32_t v) { return static_cast<float>(__builtin_bit_cast(plm_half2, v)[1]); }
+
+// fp16 activations of one 16-byte span: xr[m] holds values 2m (low half) and
+// 2m + 1 (high half); *xsum is their fp32 sum.
+__device__ __forceinline__ void q4_load_x_f16(const uint4* xp4, uint32_t* xr, float* xsum) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint4 v = xp4[i];
+        xr[4 * i] = v.x;
+        xr[4 * i + 1] = v.y;
+        xr[4 * i + 2] = v.z;
+        xr[4 * i + 3] = v.w;
+    }
+    float xs = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+        xs += half_lo(xr[m]);
+        xs += half_hi(xr[m]);
+    }
+    *xsum = xs;
+}
+
+// sum over the span of q * x for fp16 x.  Dword i of the span holds nibbles
+// k = 0..7 (values 8i + k).  With u = d ^ 0x88888888 (u = q + 8),
+// (u >> 4j) & 0x000F000F is the pair (u_{8i+j}, u_{8i+j+4}) as fp16
+// subnormals u * 2^-24.  Each product is one fp32 fma (v_fma_mix_f32 reads
+// the fp16 halves directly, so every product is exact and every add is
+// round-to-nearest fp32); 2^24 * sum(u * 2^-24 * x) - 8 * sum(x) is then
+// sum(q * x).
+__device__ __forceinline__ float q4_span_dot_f16(const uint4& q, const uint32_t* xr, float xs8) {
+    const uint32_t d[4] = {q.x ^ 0x88888888u, q.y ^ 0x88888888u, q.z ^ 0x88888888u, q.w ^ 0x88888888u};
+    float p = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t pr = (d[i] >> (4 * j)) & 0x000F000Fu;
+            const uint32_t xa = xr[4 * i + (j >> 1)], xb = xr[4 * i + 2 + (j >> 1)];
+            p = fmaf(half_lo(pr), (j & 1) ? half_hi(xa) : half_lo(xa), p);
+            p = fmaf(half_hi(pr), (j & 1) ? half_hi(xb) : half_lo(xb), p);
+        }
+    }
+    return p * 16777216.0f - xs8;
+}
+
+// fp32 activations: (u & 0x0F0F0F0F) and ((u >> 4) & ...) give the even / odd
+// values as bytes, which v_cvt_f32_ubyte{0..3} turn into floats.
+__device__ __forceinline__ float q4_span_dot_f32(const uint4& q, const float* x, float xs8) {
     const uint32_t d[4] = {q.x ^ 0x88888888u, q.y ^ 0x88888888u, q.z ^ 0x88888888u, q.w ^ 0x88888888u};
     float p = 0.0f;
 #pragma unroll
@@ -147,48 +206,38 @@ __device__ __forceinline__ float span_dot_u(const uint4& q, const float* x) {
         const uint32_t hi = (d[i] >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-            const float ue = static_cast<float>((lo >> (8 * b)) & 0xFFu);
-            const float uo = static_cast<float>((hi >> (8 * b)) & 0xFFu);
-            p = fmaf(ue, x[i * 8 + 2 * b], p);
-            p = fmaf(uo, x[i * 8 + 2 * b + 1], p);
+            p = fmaf(static_cast<float>((lo >> (8 * b)) & 0xFFu), x[i * 8 + 2 * b], p);
+            p = fmaf(static_cast<float>((hi >> (8 * b)) & 0xFFu), x[i * 8 + 2 * b + 1], p);
         }
     }
-    return p;
+    return p - xs8;
 }
 
-template <bool XF16>
-__device__ __forceinline__ void load_x32(const void* xbase, int64_t col, float* x) {
-    if constexpr (XF16) {
-        const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(xbase) + col);
+__device__ __forceinline__ void q4_load_x_f32(const float* xb, float* x, float* xsum) {
+    const float4* p = reinterpret_cast<const float4*>(xb);
+    float xs = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint4 v = p[i];
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                x[i * 8 + 2 * j] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[j] & 0xFFFFu)));
-                x[i * 8 + 2 * j + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[j] >> 16)));
-            }
-        }
-    } else {
-        const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(xbase) + col);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float4 v = p[i];
-            x[4 * i] = v.x;
-            x[4 * i + 1] = v.y;
-            x[4 * i + 2] = v.z;
-            x[4 * i + 3] = v.w;
-        }
+    for (int i = 0; i < 8; ++i) {
+        const float4 v = p[i];
+        x[4 * i] = v.x;
+        x[4 * i + 1] = v.y;
+        x[4 * i + 2] = v.z;
+        x[4 * i + 3] = v.w;
+        xs += v.x + v.y + v.z + v.w;
     }
+    *xsum = xs;
 }
 
-__device__ __forceinline__ float sum32(const float* x) {
-    float s = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) s += x[j];
-    return s;
+// Sum over the 16 lanes of a row group; every lane of the group ends with it.
+__device__ __forceinline__ float row16_sum(float v) {
+    v = PLM_DPP_ADD(v, 0xB1, 0xF);
+    v = PLM_DPP_ADD(v, 0x4E, 0xF);
+    v = PLM_DPP_ADD(v, 0x141, 0xF);
+    v = PLM_DPP_ADD(v, 0x140, 0xF);
+    return v;
 }
+
+constexpr int kStepBytes = 256;
 
 struct Q4RowsArgs {
     const uint8_t* w[2][kMaxGroups];
@@ -198,67 +247,95 @@ struct Q4RowsArgs {
     int64_t rows;
     int64_t K;            // values per row (multiple of 32 on this path)
     int tiles_per_group;
-    int nchunks;          // ceil(K/2 / 1024)
 };
 
 // Rows of one or more experts against one shared activation vector.  NWT=2
 // with SILU computes silu(gate) * up (the gate/up phase of the MoE).
-template <int TR, int NWT, bool SILU, bool XF16>
-__global__ __launch_bounds__(512) void q4_rows_kernel(const Q4RowsArgs a) {
-    constexpr int V = NWT * TR;
-    __shared__ float red[kMaxWaves * V];
-    const int nw = blockDim.x >> 6;
+template <int TR, int NWT, int NWS, int UNR, bool SILU, bool XF16>
+__global__ __launch_bounds__(NWS * 64) void q4_rows_kernel(const Q4RowsArgs a) {
+    constexpr int T = 4 * TR;  // rows per workgroup
+    __shared__ float red[NWS][NWT][T];
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
+    const int grp = lane >> 4, li = lane & 15;
     const int g = blockIdx.x / a.tiles_per_group;
-    const int64_t row0 = static_cast<int64_t>(blockIdx.x - g * a.tiles_per_group) * TR;
+    const int64_t tile0 = static_cast<int64_t>(blockIdx.x - g * a.tiles_per_group) * T;
+    const int64_t row0 = tile0 + grp * TR;
     const int64_t row_bytes = a.K >> 1;
+    const int steps = static_cast<int>((row_bytes + kStepBytes - 1) / kStepBytes);
+    const uint8_t* wp[NWT];
+    int64_t roff[TR];
+#pragma unroll
+    for (int i = 0; i < NWT; ++i) wp[i] = a.w[i][g];
+#pragma unroll
+    for (int t = 0; t < TR; ++t) roff[t] = (row0 + t < a.rows ? row0 + t : a.rows - 1) * row_bytes;
 
     float acc[NWT][TR];
 #pragma unroll
     for (int i = 0; i < NWT; ++i)
 #pragma unroll
-        for (int r = 0; r < TR; ++r) acc[i][r] = 0.0f;
+        for (int t = 0; t < TR; ++t) acc[i][t] = 0.0f;
 
-    for (int c = wave; c < a.nchunks; c += nw) {
-        const int64_t byte = static_cast<int64_t>(c) * plm::kChunkBytes + lane * 16;
-        if (byte >= row_bytes) continue;
-        uint4 q[NWT][TR];
+    for (int s0 = wave; s0 < steps; s0 += NWS * UNR) {
+        uint4 q[UNR][NWT][TR];
 #pragma unroll
-        for (int i = 0; i < NWT; ++i)
+        for (int u = 0; u < UNR; ++u) {
+            const int64_t byte = static_cast<int64_t>(s0 + u * NWS) * kStepBytes + li * 16;
+            const int64_t bc = byte < row_bytes ? byte : row_bytes - 16;
 #pragma unroll
-            for (int r = 0; r < TR; ++r) {
-                q[i][r] = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
-                if (row0 + r < a.rows)
-                    q[i][r] = *reinterpret_cast<const uint4*>(a.w[i][g] + (row0 + r) * row_bytes + byte);
+            for (int i = 0; i < NWT; ++i)
+#pragma unroll
+                for (int t = 0; t < TR; ++t) q[u][i][t] = *reinterpret_cast<const uint4*>(wp[i] + roff[t] + bc);
+        }
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            if (s0 + u * NWS >= steps) break;
+            const int64_t byte = static_cast<int64_t>(s0 + u * NWS) * kStepBytes + li * 16;
+            const bool ok = byte < row_bytes;
+            const int64_t bc = ok ? byte : row_bytes - 16;
+            if constexpr (XF16) {
+                uint32_t xr[16];
+                float xs;
+                q4_load_x_f16(reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + 2 * bc), xr, &xs);
+#pragma unroll
+                for (int i = 0; i < NWT; ++i)
+#pragma unroll
+                    for (int t = 0; t < TR; ++t) {
+                        const float p = q4_span_dot_f16(q[u][i][t], xr, 8.0f * xs);
+                        acc[i][t] += ok ? p : 0.0f;
+                    }
+            } else {
+                float x[32], xs;
+                q4_load_x_f32(static_cast<const float*>(a.x) + 2 * bc, x, &xs);
+#pragma unroll
+                for (int i = 0; i < NWT; ++i)
+#pragma unroll
+                    for (int t = 0; t < TR; ++t) {
+                        const float p = q4_span_dot_f32(q[u][i][t], x, 8.0f * xs);
+                        acc[i][t] += ok ? p : 0.0f;
+                    }
             }
-        float x[32];
-        load_x32<XF16>(a.x, byte * 2, x);
-        const float xs8 = 8.0f * sum32(x);
-#pragma unroll
-        for (int i = 0; i < NWT; ++i)
-#pragma unroll
-            for (int r = 0; r < TR; ++r) acc[i][r] += span_dot_u(q[i][r], x) - xs8;
+        }
     }
 
 #pragma unroll
     for (int i = 0; i < NWT; ++i)
 #pragma unroll
-        for (int r = 0; r < TR; ++r) {
-            const float t = plm_wave_sum(acc[i][r]);
-            if (lane == 0) red[wave * V + i * TR + r] = t;
+        for (int t = 0; t < TR; ++t) {
+            const float v = row16_sum(acc[i][t]);
+            if (li == 0) red[wave][i][grp * TR + t] = v;
         }
     __syncthreads();
-    if (threadIdx.x < TR) {
-        const int r = threadIdx.x;
-        const int64_t row = row0 + r;
+    if (threadIdx.x < T) {
+        const int64_t row = tile0 + threadIdx.x;
         if (row < a.rows) {
             float v[NWT];
 #pragma unroll
             for (int i = 0; i < NWT; ++i) {
-                float s = 0.0f;
-                for (int w = 0; w < nw; ++w) s += red[w * V + i * TR + r];
-                v[i] = s * h2f_ref(a.s[i][g][row]);
+                float sum = 0.0f;
+#pragma unroll
+                for (int w = 0; w < NWS; ++w) sum += red[w][i][threadIdx.x];
+                v[i] = sum * h2f_ref(a.s[i][g][row]);
             }
             if constexpr (SILU) {
                 a.out[static_cast<int64_t>(g) * a.rows + row] = plm_silu_mul(v[0], v[1]);
@@ -278,53 +355,72 @@ struct Q4CombineArgs {
     int64_t rows;
     int64_t K;
     int ngroups;
-    int cps;
 };
 
-// Down phase + routed combine of the Q4 MoE, fp16 out (software RNE).
-template <int TR>
-__global__ __launch_bounds__(512) void q4_combine_kernel(const Q4CombineArgs a) {
-    __shared__ float red[kMaxWaves * TR];
-    const int nw = blockDim.x >> 6;
+// Down phase + routed combine of the Q4 MoE, fp16 out (software RNE).  The
+// (expert, step) items are split over the waves; each span's sum is scaled by
+// the expert's row scale and route weight as it is added.
+template <int TR, int NWS, int UNR>
+__global__ __launch_bounds__(NWS * 64) void q4_combine_kernel(const Q4CombineArgs a) {
+    constexpr int T = 4 * TR;
+    __shared__ float red[NWS][T];
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * TR;
+    const int grp = lane >> 4, li = lane & 15;
+    const int64_t tile0 = static_cast<int64_t>(blockIdx.x) * T;
+    const int64_t row0 = tile0 + grp * TR;
     const int64_t row_bytes = a.K >> 1;
+    const int steps = static_cast<int>((row_bytes + kStepBytes - 1) / kStepBytes);
+    const int items = steps * a.ngroups;
+    int64_t rc[TR];
+#pragma unroll
+    for (int t = 0; t < TR; ++t) rc[t] = row0 + t < a.rows ? row0 + t : a.rows - 1;
     float acc[TR];
 #pragma unroll
-    for (int r = 0; r < TR; ++r) acc[r] = 0.0f;
-    const int nchunks = a.ngroups * a.cps;
-    for (int c = wave; c < nchunks; c += nw) {
-        const int g = c / a.cps;
-        const int64_t byte = static_cast<int64_t>(c - g * a.cps) * plm::kChunkBytes + lane * 16;
-        if (byte >= row_bytes) continue;
-        uint4 q[TR];
+    for (int t = 0; t < TR; ++t) acc[t] = 0.0f;
+
+    for (int i0 = wave; i0 < items; i0 += NWS * UNR) {
+        uint4 q[UNR][TR];
 #pragma unroll
-        for (int r = 0; r < TR; ++r) {
-            q[r] = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
-            if (row0 + r < a.rows) q[r] = *reinterpret_cast<const uint4*>(a.w[g] + (row0 + r) * row_bytes + byte);
+        for (int u = 0; u < UNR; ++u) {
+            const int it = min(i0 + u * NWS, items - 1);
+            const int g = it / steps;
+            const int64_t byte = static_cast<int64_t>(it - g * steps) * kStepBytes + li * 16;
+            const int64_t bc = byte < row_bytes ? byte : row_bytes - 16;
+#pragma unroll
+            for (int t = 0; t < TR; ++t) q[u][t] = *reinterpret_cast<const uint4*>(a.w[g] + rc[t] * row_bytes + bc);
         }
-        float x[32];
-        load_x32<false>(a.act + static_cast<int64_t>(g) * a.K, byte * 2, x);
-        const float xs8 = 8.0f * sum32(x);
-        const float rw = a.route[g];
 #pragma unroll
-        for (int r = 0; r < TR; ++r) {
-            const float sc = (row0 + r < a.rows) ? h2f_ref(a.s[g][row0 + r]) : 0.0f;
-            acc[r] = fmaf((span_dot_u(q[r], x) - xs8) * sc, rw, acc[r]);
+        for (int u = 0; u < UNR; ++u) {
+            const int it = i0 + u * NWS;
+            if (it >= items) break;
+            const int g = it / steps;
+            const int64_t byte = static_cast<int64_t>(it - g * steps) * kStepBytes + li * 16;
+            const bool ok = byte < row_bytes;
+            const int64_t bc = ok ? byte : row_bytes - 16;
+            float x[32], xs;
+            q4_load_x_f32(a.act + static_cast<int64_t>(g) * a.K + 2 * bc, x, &xs);
+            const float rw = a.route[g];
+#pragma unroll
+            for (int t = 0; t < TR; ++t) {
+                const float sc = h2f_ref(a.s[g][rc[t]]);
+                const float p = q4_span_dot_f32(q[u][t], x, 8.0f * xs);
+                acc[t] = ok ? fmaf(p * sc, rw, acc[t]) : acc[t];
+            }
         }
     }
 #pragma unroll
-    for (int r = 0; r < TR; ++r) {
-        const float t = plm_wave_sum(acc[r]);
-        if (lane == 0) red[wave * TR + r] = t;
+    for (int t = 0; t < TR; ++t) {
+        const float v = row16_sum(acc[t]);
+        if (li == 0) red[wave][grp * TR + t] = v;
     }
     __syncthreads();
-    if (threadIdx.x < TR) {
-        const int64_t row = row0 + threadIdx.x;
+    if (threadIdx.x < T) {
+        const int64_t row = tile0 + threadIdx.x;
         if (row < a.rows) {
             float v = 0.0f;
-            for (int w = 0; w < nw; ++w) v += red[w * TR + threadIdx.x];
+#pragma unroll
+            for (int w = 0; w < NWS; ++w) v += red[w][threadIdx.x];
             a.out_f16[row] = f16_from_bits(f2u(v), false);
         }
     }
@@ -363,16 +459,22 @@ __global__ void q4_combine_scalar_kernel(const Q4CombineArgs a) {
     a.out_f16[row] = f16_from_bits(f2u(acc), false);
 }
 
-int waves_for(int64_t nchunks) { return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(nchunks, kMaxWaves))); }
-
-template <int TR, int NWT, bool SILU, bool XF16>
+template <int TR, int NWT, int NWS, int UNR, bool SILU, bool XF16>
 void launch_q4_rows(Q4RowsArgs a, int ngroups, hipStream_t st) {
-    a.tiles_per_group = static_cast<int>(plm::ceil_div(a.rows, TR));
-    a.nchunks = static_cast<int>(plm::ceil_div(a.K / 2, plm::kChunkBytes));
-    const int nw = waves_for(a.nchunks);
-    hipLaunchKernelGGL((q4_rows_kernel<TR, NWT, SILU, XF16>),
+    a.tiles_per_group = static_cast<int>(plm::ceil_div(a.rows, 4 * TR));
+    hipLaunchKernelGGL((q4_rows_kernel<TR, NWT, NWS, UNR, SILU, XF16>),
                        dim3(static_cast<unsigned>(static_cast<int64_t>(a.tiles_per_group) * ngroups)),
-                       dim3(nw * plm::kWave), 0, st, a);
+                       dim3(NWS * plm::kWave), 0, st, a);
+}
+
+// Long rows (many 256-byte steps) favour fewer rows per group and more
+// waves splitting each row; short rows the opposite.
+void launch_q4_gemv(const Q4RowsArgs& a, hipStream_t st) {
+    if (a.K / 2 >= 16 * kStepBytes) {
+        launch_q4_rows<2, 1, 16, 1, false, true>(a, 1, st);
+    } else {
+        launch_q4_rows<4, 1, 4, 2, false, true>(a, 1, st);
+    }
 }
 
 bool q4_fast_ok(int64_t K, const void* x, const uint8_t* const* w, int n) {
@@ -427,7 +529,7 @@ PLM_EXPORT int q4_gemv_f16_f32(const uint8_t* packed, const uint16_t* scales, co
     a.K = cols;
     const uint8_t* wl[1] = {packed};
     if (q4_fast_ok(cols, hidden, wl, 1)) {
-        launch_q4_rows<8, 1, false, true>(a, 1, st);
+        launch_q4_gemv(a, st);
     } else {
         hipLaunchKernelGGL(q4_rows_scalar_kernel<true>, dim3(static_cast<unsigned>(plm::ceil_div(rows, 256))),
                            dim3(256), 0, st, a, 1, 1, 0);
@@ -477,7 +579,7 @@ PLM_EXPORT int q4_moe_selected_forward_u16(const uint16_t* hidden, const uint8_t
         a.rows = I;
         a.K = H;
         if (fast1) {
-            launch_q4_rows<4, 2, true, true>(a, ng, st);
+            launch_q4_rows<2, 2, 4, 2, true, true>(a, ng, st);
         } else {
             hipLaunchKernelGGL(q4_rows_scalar_kernel<true>,
                                dim3(static_cast<unsigned>(plm::ceil_div(static_cast<int64_t>(ng) * I, 256))), dim3(256),
@@ -501,12 +603,9 @@ PLM_EXPORT int q4_moe_selected_forward_u16(const uint16_t* hidden, const uint8_t
     c.rows = H;
     c.K = I;
     c.ngroups = static_cast<int>(S);
-    c.cps = static_cast<int>(plm::ceil_div(I / 2, plm::kChunkBytes));
     if (fast2) {
-        constexpr int TR = 8;
-        const int nw = waves_for(static_cast<int64_t>(c.cps) * S);
-        hipLaunchKernelGGL(q4_combine_kernel<TR>, dim3(static_cast<unsigned>(plm::ceil_div(H, TR))),
-                           dim3(nw * plm::kWave), 0, st, c);
+        hipLaunchKernelGGL((q4_combine_kernel<2, 16, 1>), dim3(static_cast<unsigned>(plm::ceil_div(H, 8))),
+                           dim3(16 * plm::kWave), 0, st, c);
     } else {
         hipLaunchKernelGGL(q4_combine_scalar_kernel, dim3(static_cast<unsigned>(plm::ceil_div(H, 256))), dim3(256), 0,
                            st, c);

@@ -14,7 +14,7 @@
 namespace {
 
 constexpr int kMaxWaves = 8;
-constexpr int kUnroll = 4;       // chunks whose loads are issued together
+constexpr int kUnroll = 8;       // chunks whose loads are issued together
 constexpr int kMaxMats = 8;      // matrices per fused launch
 
 __device__ __forceinline__ float u16_to_f32(uint32_t v, int bf16) {
@@ -77,13 +77,14 @@ __global__ __launch_bounds__(512) void row8_gemv_kernel(const Row8Args a) {
         float xv[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
+            // Unconditional loads from a clamped column (its x is zeroed) so
+            // that every load of the group issues before the first wait.
             const int64_t col = static_cast<int64_t>(c0 + u * nw) * 64 + lane;
-            q[u] = make_uint4(0u, 0u, 0u, 0u);
-            xv[u] = 0.0f;
-            if (c0 + u * nw < a.nchunks && col < a.K) {
-                q[u] = *reinterpret_cast<const uint4*>(base + col * 8);
-                xv[u] = u16_to_f32(a.hidden[col], BF16);
-            }
+            const bool ok = c0 + u * nw < a.nchunks && col < a.K;
+            const int64_t cc = ok ? col : a.K - 1;
+            q[u] = *reinterpret_cast<const uint4*>(base + cc * 8);
+            const float xh = u16_to_f32(a.hidden[cc], BF16);
+            xv[u] = ok ? xh : 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
@@ -96,7 +97,7 @@ __global__ __launch_bounds__(512) void row8_gemv_kernel(const Row8Args a) {
 #pragma unroll
     for (int l = 0; l < 8; ++l) {
         const float t = plm_wave_sum(acc[l]);
-        if (lane == 0) red[wave * 8 + l] = t;
+        if (lane == kSumLane) red[wave * 8 + l] = t;
     }
     __syncthreads();
     if (threadIdx.x < 8) {
