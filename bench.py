@@ -47,6 +47,9 @@ def _args(argv=None):
     ap.add_argument("--table-out", default=None, help="also write the table to this file")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample length")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="run a few default steps, then a plain 256 MiB device copy, for counter runs "
+                         "(rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE); prints nothing else")
     return ap.parse_args(argv)
 
 
@@ -210,13 +213,16 @@ def cpu_q4_baseline(torch, sample, seconds):
 
 
 def _traffic(workload):
+    """HBM bytes per step from the committed counter runs (FETCH_SIZE and
+    WRITE_SIZE scaled by a plain copy's reading; profiles/traffic.json), or
+    None when they are absent."""
     f = REPO / "profiles" / "traffic.json"
     if not f.exists():
         return None
     try:
-        data = json.loads(f.read_text())
-        return data.get(workload)
-    except (OSError, ValueError):
+        entry = json.loads(f.read_text()).get(workload) or {}
+        return entry.get("bytes_per_step")
+    except (OSError, ValueError, AttributeError):
         return None
 
 
@@ -243,6 +249,7 @@ def main_line(args):
         "unit": "GB/s",
         "frac": round(value / PEAK_HBM_GBS, 4),
         "traffic": _traffic("q4_mlp"),
+        "traffic_unit": "bytes per step (both launches)",
         "launches_per_step": 2,
         "bytes_per_step": r["step_bytes"],
     }
@@ -498,6 +505,27 @@ def table(args):
         Path(args.table_out).write_text(text + "\n")
 
 
+def pmc_probe(args):
+    """Counter calibration workload: 5 default steps, then 3 copies of a
+    256 MiB fp32 buffer (256 MiB read + 256 MiB written per copy).  The
+    copy's FETCH_SIZE / WRITE_SIZE readings give the factor that turns the
+    counters into bytes."""
+    import torch
+
+    from pocketlm_amd import _lib, formats
+
+    torch.cuda.set_device(0)
+    lib = _lib.load()
+    timer = Timer(torch)
+    bench_q4_mlp(torch, lib, formats, 5, 2, timer)
+    src = torch.ones(64 << 20, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("pmc probe done: 7 MLP calls, 3 copies of 268435456 bytes", flush=True)
+
+
 def main(argv=None):
     args = _args(argv)
     if args.gpus != 1:
@@ -507,6 +535,8 @@ def main(argv=None):
         sys.path.insert(0, str(REPO))
     if args.table:
         table(args)
+    elif args.pmc_probe:
+        pmc_probe(args)
     else:
         main_line(args)
     return 0

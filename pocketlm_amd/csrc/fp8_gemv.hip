@@ -111,7 +111,7 @@ __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
     constexpr int V = NWT * TR * M;
     __shared__ float red[kMaxWaves * V];
     const int nw = blockDim.x >> 6;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63;
     const int g = blockIdx.x / a.tiles_per_group;
     const int64_t row0 = static_cast<int64_t>(blockIdx.x - g * a.tiles_per_group) * TR;
@@ -215,7 +215,7 @@ __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
     constexpr int V = TR * M;
     __shared__ float red[kMaxWaves * V];
     const int nw = blockDim.x >> 6;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63;
     int g_lo = 0;
     int g_hi = a.ngroups;

@@ -152,16 +152,15 @@ typedef _Float16 plm_half2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float half_lo(uint32_t v) { return static_cast<float>(__builtin_bit_cast(plm_half2, v)[0]); }
 __device__ __forceinline__ float half_hi(uint32_t v) { return static_cast<float>(__builtin_bit_cast(plm_half2, v)[1]); }
 
-// fp16 activations of one 16-byte span: xr[m] holds values 2m (low half) and
-// 2m + 1 (high half); *xsum is their fp32 sum.
-__device__ __forceinline__ void q4_load_x_f16(const uint4* xp4, uint32_t* xr, float* xsum) {
+// fp16 activations of one 16-byte span (four 16-byte pieces): xr[m] holds
+// values 2m (low half) and 2m + 1 (high half); *xsum is their fp32 sum.
+__device__ __forceinline__ void q4_unpack_x_f16(const uint4* xv, uint32_t* xr, float* xsum) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint4 v = xp4[i];
-        xr[4 * i] = v.x;
-        xr[4 * i + 1] = v.y;
-        xr[4 * i + 2] = v.z;
-        xr[4 * i + 3] = v.w;
+        xr[4 * i] = xv[i].x;
+        xr[4 * i + 1] = xv[i].y;
+        xr[4 * i + 2] = xv[i].z;
+        xr[4 * i + 3] = xv[i].w;
     }
     float xs = 0.0f;
 #pragma unroll
@@ -195,37 +194,21 @@ __device__ __forceinline__ float q4_span_dot_f16(const uint4& q, const uint32_t*
     return p * 16777216.0f - xs8;
 }
 
-// fp32 activations: (u & 0x0F0F0F0F) and ((u >> 4) & ...) give the even / odd
-// values as bytes, which v_cvt_f32_ubyte{0..3} turn into floats.
+// fp32 activations: the same fp16-subnormal pairs, each product one fp32
+// fma of the pair's half (read as fp16) and the fp32 x value.
 __device__ __forceinline__ float q4_span_dot_f32(const uint4& q, const float* x, float xs8) {
     const uint32_t d[4] = {q.x ^ 0x88888888u, q.y ^ 0x88888888u, q.z ^ 0x88888888u, q.w ^ 0x88888888u};
     float p = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t lo = d[i] & 0x0F0F0F0Fu;
-        const uint32_t hi = (d[i] >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            p = fmaf(static_cast<float>((lo >> (8 * b)) & 0xFFu), x[i * 8 + 2 * b], p);
-            p = fmaf(static_cast<float>((hi >> (8 * b)) & 0xFFu), x[i * 8 + 2 * b + 1], p);
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t pr = (d[i] >> (4 * j)) & 0x000F000Fu;
+            p = fmaf(half_lo(pr), x[8 * i + j], p);
+            p = fmaf(half_hi(pr), x[8 * i + j + 4], p);
         }
     }
-    return p - xs8;
-}
-
-__device__ __forceinline__ void q4_load_x_f32(const float* xb, float* x, float* xsum) {
-    const float4* p = reinterpret_cast<const float4*>(xb);
-    float xs = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float4 v = p[i];
-        x[4 * i] = v.x;
-        x[4 * i + 1] = v.y;
-        x[4 * i + 2] = v.z;
-        x[4 * i + 3] = v.w;
-        xs += v.x + v.y + v.z + v.w;
-    }
-    *xsum = xs;
+    return p * 16777216.0f - xs8;
 }
 
 // Sum over the 16 lanes of a row group; every lane of the group ends with it.
@@ -243,19 +226,32 @@ struct Q4RowsArgs {
     const uint8_t* w[2][kMaxGroups];
     const uint16_t* s[2][kMaxGroups];
     const void* x;        // fp16 or fp32 activations [K]
-    float* out;           // (g, row) at g * rows + row
+    float* out;           // (g, row) at g * out_stride + row, or the step order below
     int64_t rows;
     int64_t K;            // values per row (multiple of 32 on this path)
+    int64_t out_stride;
+    int out_steps;        // write the output in step order (see act_pos)
     int tiles_per_group;
 };
 
-// Rows of one or more experts against one shared activation vector.  NWT=2
-// with SILU computes silu(gate) * up (the gate/up phase of the MoE).
-template <int TR, int NWT, int NWS, int UNR, bool SILU, bool XF16>
+// Position of value k of an fp32 activation vector stored in "step order":
+// within each 512-value step, value li * 32 + e (the e-th value of lane li's
+// 16-byte weight span) sits at (e / 4) * 64 + li * 4 + e % 4, so that the
+// i-th float4 load of the 16 lanes of a row group reads 256 contiguous
+// bytes.  The buffer is padded to whole steps.
+__device__ __forceinline__ int64_t act_pos(int64_t k) {
+    return (k & ~int64_t{511}) | (((k & 31) >> 2) << 6) | (((k & 511) >> 5) << 2) | (k & 3);
+}
+
+// Rows of one or more experts against one shared fp16 activation vector.
+// NWT=2 with SILU computes silu(gate) * up (the gate/up phase of the MoE).
+// (Staging x in LDS was measured slower: the workgroup barrier holds every
+// wave until the slowest wave's first weights arrive.)
+template <int TR, int NWT, int NWS, int UNR, bool SILU>
 __global__ __launch_bounds__(NWS * 64) void q4_rows_kernel(const Q4RowsArgs a) {
     constexpr int T = 4 * TR;  // rows per workgroup
     __shared__ float red[NWS][NWT][T];
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63;
     const int grp = lane >> 4, li = lane & 15;
     const int g = blockIdx.x / a.tiles_per_group;
@@ -276,8 +272,8 @@ __global__ __launch_bounds__(NWS * 64) void q4_rows_kernel(const Q4RowsArgs a) {
 #pragma unroll
         for (int t = 0; t < TR; ++t) acc[i][t] = 0.0f;
 
-    for (int s0 = wave; s0 < steps; s0 += NWS * UNR) {
-        uint4 q[UNR][NWT][TR];
+    uint4 q[UNR][NWT][TR];
+    auto load_w = [&](int s0) {
 #pragma unroll
         for (int u = 0; u < UNR; ++u) {
             const int64_t byte = static_cast<int64_t>(s0 + u * NWS) * kStepBytes + li * 16;
@@ -287,34 +283,30 @@ __global__ __launch_bounds__(NWS * 64) void q4_rows_kernel(const Q4RowsArgs a) {
 #pragma unroll
                 for (int t = 0; t < TR; ++t) q[u][i][t] = *reinterpret_cast<const uint4*>(wp[i] + roff[t] + bc);
         }
+    };
+    for (int s0 = wave; s0 < steps; s0 += NWS * UNR) {
+        load_w(s0);
 #pragma unroll
         for (int u = 0; u < UNR; ++u) {
-            if (s0 + u * NWS >= steps) break;
-            const int64_t byte = static_cast<int64_t>(s0 + u * NWS) * kStepBytes + li * 16;
+            const int s = s0 + u * NWS;
+            if (s >= steps) break;
+            const int64_t byte = static_cast<int64_t>(s) * kStepBytes + li * 16;
             const bool ok = byte < row_bytes;
             const int64_t bc = ok ? byte : row_bytes - 16;
-            if constexpr (XF16) {
-                uint32_t xr[16];
-                float xs;
-                q4_load_x_f16(reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + 2 * bc), xr, &xs);
+            const uint4* xp = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + 2 * bc);
+            uint4 xv[4];
 #pragma unroll
-                for (int i = 0; i < NWT; ++i)
+            for (int i = 0; i < 4; ++i) xv[i] = xp[i];
+            uint32_t xr[16];
+            float xs;
+            q4_unpack_x_f16(xv, xr, &xs);
 #pragma unroll
-                    for (int t = 0; t < TR; ++t) {
-                        const float p = q4_span_dot_f16(q[u][i][t], xr, 8.0f * xs);
-                        acc[i][t] += ok ? p : 0.0f;
-                    }
-            } else {
-                float x[32], xs;
-                q4_load_x_f32(static_cast<const float*>(a.x) + 2 * bc, x, &xs);
+            for (int i = 0; i < NWT; ++i)
 #pragma unroll
-                for (int i = 0; i < NWT; ++i)
-#pragma unroll
-                    for (int t = 0; t < TR; ++t) {
-                        const float p = q4_span_dot_f32(q[u][i][t], x, 8.0f * xs);
-                        acc[i][t] += ok ? p : 0.0f;
-                    }
-            }
+                for (int t = 0; t < TR; ++t) {
+                    const float p = q4_span_dot_f16(q[u][i][t], xr, 8.0f * xs);
+                    acc[i][t] += ok ? p : 0.0f;
+                }
         }
     }
 
@@ -337,10 +329,11 @@ __global__ __launch_bounds__(NWS * 64) void q4_rows_kernel(const Q4RowsArgs a) {
                 for (int w = 0; w < NWS; ++w) sum += red[w][i][threadIdx.x];
                 v[i] = sum * h2f_ref(a.s[i][g][row]);
             }
+            const int64_t o = static_cast<int64_t>(g) * a.out_stride + (a.out_steps ? act_pos(row) : row);
             if constexpr (SILU) {
-                a.out[static_cast<int64_t>(g) * a.rows + row] = plm_silu_mul(v[0], v[1]);
+                a.out[o] = plm_silu_mul(v[0], v[1]);
             } else {
-                a.out[static_cast<int64_t>(g) * a.rows + row] = v[0];
+                a.out[o] = v[0];
             }
         }
     }
@@ -349,7 +342,8 @@ __global__ __launch_bounds__(NWS * 64) void q4_rows_kernel(const Q4RowsArgs a) {
 struct Q4CombineArgs {
     const uint8_t* w[kMaxGroups];
     const uint16_t* s[kMaxGroups];
-    const float* act;     // [ngroups][K] fp32
+    const float* act;     // [ngroups][act_stride] fp32, step order (act_pos) on the fast path
+    int64_t act_stride;
     const float* route;   // [ngroups]
     uint16_t* out_f16;    // [rows]
     int64_t rows;
@@ -358,13 +352,14 @@ struct Q4CombineArgs {
 };
 
 // Down phase + routed combine of the Q4 MoE, fp16 out (software RNE).  The
-// (expert, step) items are split over the waves; each span's sum is scaled by
-// the expert's row scale and route weight as it is added.
+// (expert, step) items are split over the waves in expert order; a wave sums
+// the spans of one expert raw and folds that sum into the output with the
+// expert's row scale and route weight when its expert changes.
 template <int TR, int NWS, int UNR>
 __global__ __launch_bounds__(NWS * 64) void q4_combine_kernel(const Q4CombineArgs a) {
     constexpr int T = 4 * TR;
     __shared__ float red[NWS][T];
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63;
     const int grp = lane >> 4, li = lane & 15;
     const int64_t tile0 = static_cast<int64_t>(blockIdx.x) * T;
@@ -375,9 +370,18 @@ __global__ __launch_bounds__(NWS * 64) void q4_combine_kernel(const Q4CombineArg
     int64_t rc[TR];
 #pragma unroll
     for (int t = 0; t < TR; ++t) rc[t] = row0 + t < a.rows ? row0 + t : a.rows - 1;
-    float acc[TR];
+    float acc[TR], part[TR];
 #pragma unroll
-    for (int t = 0; t < TR; ++t) acc[t] = 0.0f;
+    for (int t = 0; t < TR; ++t) acc[t] = part[t] = 0.0f;
+    int gcur = -1;
+    auto fold = [&](int g) {
+        const float rw = a.route[g];
+#pragma unroll
+        for (int t = 0; t < TR; ++t) {
+            acc[t] = fmaf(part[t] * h2f_ref(a.s[g][rc[t]]), rw, acc[t]);
+            part[t] = 0.0f;
+        }
+    };
 
     for (int i0 = wave; i0 < items; i0 += NWS * UNR) {
         uint4 q[UNR][TR];
@@ -395,20 +399,33 @@ __global__ __launch_bounds__(NWS * 64) void q4_combine_kernel(const Q4CombineArg
             const int it = i0 + u * NWS;
             if (it >= items) break;
             const int g = it / steps;
+            if (g != gcur) {
+                if (gcur >= 0) fold(gcur);
+                gcur = g;
+            }
             const int64_t byte = static_cast<int64_t>(it - g * steps) * kStepBytes + li * 16;
             const bool ok = byte < row_bytes;
-            const int64_t bc = ok ? byte : row_bytes - 16;
-            float x[32], xs;
-            q4_load_x_f32(a.act + static_cast<int64_t>(g) * a.K + 2 * bc, x, &xs);
-            const float rw = a.route[g];
+            // step order: the i-th float4 of lane li is at step * 512 + i * 64 + li * 4
+            const float4* xp = reinterpret_cast<const float4*>(a.act + static_cast<int64_t>(g) * a.act_stride +
+                                                               static_cast<int64_t>(it - g * steps) * 512 + li * 4);
+            float x[32], xs = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4 v = xp[i * 16];
+                x[4 * i] = v.x;
+                x[4 * i + 1] = v.y;
+                x[4 * i + 2] = v.z;
+                x[4 * i + 3] = v.w;
+                xs += v.x + v.y + v.z + v.w;
+            }
 #pragma unroll
             for (int t = 0; t < TR; ++t) {
-                const float sc = h2f_ref(a.s[g][rc[t]]);
                 const float p = q4_span_dot_f32(q[u][t], x, 8.0f * xs);
-                acc[t] = ok ? fmaf(p * sc, rw, acc[t]) : acc[t];
+                part[t] += ok ? p : 0.0f;
             }
         }
     }
+    if (gcur >= 0) fold(gcur);
 #pragma unroll
     for (int t = 0; t < TR; ++t) {
         const float v = row16_sum(acc[t]);
@@ -443,7 +460,8 @@ __global__ void q4_rows_scalar_kernel(const Q4RowsArgs a, int ngroups, int nwt, 
         }
         v[i] = s * h2f_ref(a.s[i][g][row]);
     }
-    a.out[id] = silu ? plm_silu_mul(v[0], v[1]) : v[0];
+    a.out[static_cast<int64_t>(g) * a.out_stride + (a.out_steps ? act_pos(row) : row)] =
+        silu ? plm_silu_mul(v[0], v[1]) : v[0];
 }
 
 __global__ void q4_combine_scalar_kernel(const Q4CombineArgs a) {
@@ -453,16 +471,16 @@ __global__ void q4_combine_scalar_kernel(const Q4CombineArgs a) {
     for (int g = 0; g < a.ngroups; ++g) {
         float s = 0.0f;
         for (int64_t k = 0; k < a.K; ++k)
-            s = fmaf(static_cast<float>(q4_at(a.w[g], row * a.K + k)), a.act[static_cast<int64_t>(g) * a.K + k], s);
+            s = fmaf(static_cast<float>(q4_at(a.w[g], row * a.K + k)), a.act[static_cast<int64_t>(g) * a.act_stride + k], s);
         acc = fmaf(s * h2f_ref(a.s[g][row]), a.route[g], acc);
     }
     a.out_f16[row] = f16_from_bits(f2u(acc), false);
 }
 
-template <int TR, int NWT, int NWS, int UNR, bool SILU, bool XF16>
+template <int TR, int NWT, int NWS, int UNR, bool SILU>
 void launch_q4_rows(Q4RowsArgs a, int ngroups, hipStream_t st) {
     a.tiles_per_group = static_cast<int>(plm::ceil_div(a.rows, 4 * TR));
-    hipLaunchKernelGGL((q4_rows_kernel<TR, NWT, NWS, UNR, SILU, XF16>),
+    hipLaunchKernelGGL((q4_rows_kernel<TR, NWT, NWS, UNR, SILU>),
                        dim3(static_cast<unsigned>(static_cast<int64_t>(a.tiles_per_group) * ngroups)),
                        dim3(NWS * plm::kWave), 0, st, a);
 }
@@ -471,17 +489,23 @@ void launch_q4_rows(Q4RowsArgs a, int ngroups, hipStream_t st) {
 // waves splitting each row; short rows the opposite.
 void launch_q4_gemv(const Q4RowsArgs& a, hipStream_t st) {
     if (a.K / 2 >= 16 * kStepBytes) {
-        launch_q4_rows<2, 1, 16, 1, false, true>(a, 1, st);
+        launch_q4_rows<2, 1, 16, 1, false>(a, 1, st);
     } else {
-        launch_q4_rows<4, 1, 4, 2, false, true>(a, 1, st);
+        launch_q4_rows<4, 1, 4, 2, false>(a, 1, st);
     }
 }
 
-bool q4_fast_ok(int64_t K, const void* x, const uint8_t* const* w, int n) {
-    if (K % 32 != 0 || !plm::aligned16(x)) return false;
+// The vector kernels need whole 16-byte spans: K % 32 == 0 and 16-byte
+// aligned weight (and activation) pointers.
+bool q4_weights_ok(int64_t K, const uint8_t* const* w, int n) {
+    if (K % 32 != 0) return false;
     for (int i = 0; i < n; ++i)
         if (!plm::aligned16(w[i])) return false;
     return true;
+}
+
+bool q4_fast_ok(int64_t K, const void* x, const uint8_t* const* w, int n) {
+    return plm::aligned16(x) && q4_weights_ok(K, w, n);
 }
 
 }  // namespace
@@ -527,6 +551,7 @@ PLM_EXPORT int q4_gemv_f16_f32(const uint8_t* packed, const uint16_t* scales, co
     a.out = out;
     a.rows = rows;
     a.K = cols;
+    a.out_stride = rows;
     const uint8_t* wl[1] = {packed};
     if (q4_fast_ok(cols, hidden, wl, 1)) {
         launch_q4_gemv(a, st);
@@ -555,7 +580,13 @@ PLM_EXPORT int q4_moe_selected_forward_u16(const uint16_t* hidden, const uint8_t
     if (selected_count > kMaxGroups) return plm::fail(1, "more than %d selected experts", kMaxGroups);
     hipStream_t st = plm::current_stream();
     const int64_t S = selected_count, H = hidden_size, I = intermediate_size;
-    float* act = static_cast<float*>(plm::workspace(static_cast<size_t>(S * I) * sizeof(float)));
+    std::vector<const uint8_t*> dl(down_packed_ptrs, down_packed_ptrs + S);
+    // The down kernel's fast path reads the activations in step order, padded
+    // to whole 512-value steps; the plain layout otherwise.  The workspace is
+    // 256-byte aligned, so only the down weights and I decide.
+    const bool fast2 = q4_weights_ok(I, dl.data(), static_cast<int>(S));
+    const int64_t stride = fast2 ? plm::ceil_div(I, 512) * 512 : I;
+    float* act = static_cast<float*>(plm::workspace(static_cast<size_t>(S * stride) * sizeof(float)));
     if (act == nullptr) return 2;
     // Phase 1, groups of up to kMaxGroups experts.
     std::vector<const uint8_t*> wl;
@@ -575,11 +606,13 @@ PLM_EXPORT int q4_moe_selected_forward_u16(const uint16_t* hidden, const uint8_t
             a.s[1][g] = up_scale_ptrs[g0 + g];
         }
         a.x = hidden;
-        a.out = act + g0 * I;
+        a.out = act + g0 * stride;
         a.rows = I;
         a.K = H;
+        a.out_stride = stride;
+        a.out_steps = fast2 ? 1 : 0;
         if (fast1) {
-            launch_q4_rows<2, 2, 4, 2, true, true>(a, ng, st);
+            launch_q4_rows<2, 2, 4, 2, true>(a, ng, st);
         } else {
             hipLaunchKernelGGL(q4_rows_scalar_kernel<true>,
                                dim3(static_cast<unsigned>(plm::ceil_div(static_cast<int64_t>(ng) * I, 256))), dim3(256),
@@ -588,9 +621,7 @@ PLM_EXPORT int q4_moe_selected_forward_u16(const uint16_t* hidden, const uint8_t
         const int code = plm::check_launch("q4 gate/up kernel");
         if (code != 0) return code;
     }
-    // Phase 2: all selected experts in one pass when they fit.
-    std::vector<const uint8_t*> dl(down_packed_ptrs, down_packed_ptrs + S);
-    const bool fast2 = q4_fast_ok(I, act, dl.data(), static_cast<int>(S));
+    // Phase 2: all selected experts in one pass.
     Q4CombineArgs c;
     std::memset(&c, 0, sizeof(c));
     for (int64_t g = 0; g < S; ++g) {
@@ -598,14 +629,17 @@ PLM_EXPORT int q4_moe_selected_forward_u16(const uint16_t* hidden, const uint8_t
         c.s[g] = down_scale_ptrs[g];
     }
     c.act = act;
+    c.act_stride = stride;
     c.route = route_weights;
     c.out_f16 = out_fp16;
     c.rows = H;
     c.K = I;
     c.ngroups = static_cast<int>(S);
     if (fast2) {
-        hipLaunchKernelGGL((q4_combine_kernel<2, 16, 1>), dim3(static_cast<unsigned>(plm::ceil_div(H, 8))),
-                           dim3(16 * plm::kWave), 0, st, c);
+        // 8-wave groups: the kernel needs more than 64 VGPRs, so 16-wave
+        // groups would fit only once per CU.
+        hipLaunchKernelGGL((q4_combine_kernel<2, 8, 2>), dim3(static_cast<unsigned>(plm::ceil_div(H, 8))),
+                           dim3(8 * plm::kWave), 0, st, c);
     } else {
         hipLaunchKernelGGL(q4_combine_scalar_kernel, dim3(static_cast<unsigned>(plm::ceil_div(H, 256))), dim3(256), 0,
                            st, c);

@@ -58,7 +58,7 @@ template <bool BF16>
 __global__ __launch_bounds__(512) void row8_gemv_kernel(const Row8Args a) {
     __shared__ float red[kMaxWaves * 8];
     const int nw = blockDim.x >> 6;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63;
     int mi = 0;
 #pragma unroll 1
