@@ -636,9 +636,10 @@ PLM_EXPORT int q4_moe_selected_forward_u16(const uint16_t* hidden, const uint8_t
     c.K = I;
     c.ngroups = static_cast<int>(S);
     if (fast2) {
-        // 8-wave groups: the kernel needs more than 64 VGPRs, so 16-wave
-        // groups would fit only once per CU.
-        hipLaunchKernelGGL((q4_combine_kernel<2, 8, 2>), dim3(static_cast<unsigned>(plm::ceil_div(H, 8))),
+        // 4 rows per lane group: each lane's 128-byte read of the fp32
+        // activations feeds four rows.  8-wave groups keep two groups per CU
+        // (the kernel needs more than 64 VGPRs).
+        hipLaunchKernelGGL((q4_combine_kernel<4, 8, 1>), dim3(static_cast<unsigned>(plm::ceil_div(H, 16))),
                            dim3(8 * plm::kWave), 0, st, c);
     } else {
         hipLaunchKernelGGL(q4_combine_scalar_kernel, dim3(static_cast<unsigned>(plm::ceil_div(H, 256))), dim3(256), 0,
