@@ -442,6 +442,16 @@ def table(args):
                                                      ctypes.c_void_p(y.data_ptr()), rows, cols, 0) for p in packs],
             2 * math.ceil(rows / 8) * 8 * cols + 2 * cols + 4 * rows,
             lambda hp=hp, hh=hh, rows=rows, cols=cols: oracle.packed_gemv_rows8(hh, hp, rows, cols, 0))
+        if rows == 3584:  # o-proj and down-proj also run on fp32 activations
+            hf = h.float()
+            hhf = hf.cpu().numpy()
+            measure(name.replace("row8", "row8 f32-x"), 1, lambda packs=packs, hf=hf, y=y, rows=rows, cols=cols: [
+                lambda p=p: lib.native_packed_gemv_rows8_f32_hidden(ctypes.c_void_p(hf.data_ptr()),
+                                                                    ctypes.c_void_p(p.data_ptr()),
+                                                                    ctypes.c_void_p(y.data_ptr()), rows, cols, 0)
+                for p in packs],
+                2 * math.ceil(rows / 8) * 8 * cols + 4 * cols + 4 * rows,
+                lambda hp=hp, hhf=hhf, rows=rows, cols=cols: oracle.packed_gemv_rows8_f32_hidden(hhf, hp, rows, cols, 0))
         del packs
         torch.cuda.empty_cache()
 

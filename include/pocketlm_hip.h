@@ -223,6 +223,15 @@ int native_packed_gemv_rows8_many(const uint16_t* hidden, const uint16_t* const*
                                   const int64_t* rows, int64_t count, int64_t cols,
                                   int dtype_code);
 
+/* The fp32-activation row8 GEMV of the dense decode's o and down projections
+ * (packed_rows8_gemv_float_hidden, fp16_kv_cache.cpp:146-174; a static helper
+ * there, called at 1045 and 1515): y[r] = sum_k hidden[k] * W[r, k] as one fma
+ * chain per row, no bias.  hidden is fp32 [cols]; packed as
+ * native_packed_gemv_rows8 (dtype_code 0 fp16, 1 bf16).  Codes 1 null, 2 bad
+ * dimensions or dtype. */
+int native_packed_gemv_rows8_f32_hidden(const float* hidden, const uint16_t* packed, float* out, int64_t rows,
+                                        int64_t cols, int dtype_code);
+
 /* ------------------------------------------------------ DeepSeek session */
 typedef int (*pocketlm_ds_tensor_callback)(int64_t layer_idx, int64_t layer_kind,
                                            int64_t weight_role, const void** out_ptr,

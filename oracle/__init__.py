@@ -299,6 +299,17 @@ def packed_gemv_rows8(hidden_bits, packed, rows, cols, dtype_code, bias_bits=Non
     return out
 
 
+def packed_gemv_rows8_f32_hidden(hidden, packed, rows, cols, dtype_code) -> np.ndarray:
+    """fp16_kv_cache.cpp:146-174 (fp32 activations, no bias)."""
+    h = _c(hidden, np.float32).reshape(-1)
+    p = _c(packed, np.uint16).reshape(-1)
+    out = np.empty((int(rows),), dtype=np.float32)
+    code = lib().orc_packed_gemv_rows8_f32_hidden(_ptr(h), _ptr(p), _ptr(out), _c_i64(rows), _c_i64(cols),
+                                                  ctypes.c_int(dtype_code))
+    _check("orc_packed_gemv_rows8_f32_hidden", code)
+    return out
+
+
 def router_topk_u16(hidden_bits, router_bits, k: int, dtype_code: int):
     h = _c(hidden_bits, np.uint16).reshape(-1)
     r = _c(router_bits, np.uint16)
@@ -417,3 +428,69 @@ def deepseek_route(logits: np.ndarray, *, top_k: int = 8, n_groups: int = 8, top
     w = (w * np.float32(route_scale)).astype(np.float32)
     w_bf16 = f32_to_bf16(w)
     return idx, (w_bf16.astype(np.uint32) << 16).view(np.float32)
+
+
+# --------------------------------------------------------------------------- MoE layer orchestration
+
+def _bf16_values(f32: np.ndarray) -> np.ndarray:
+    """fp32 -> nearest bf16 (ties to even), returned widened to fp32."""
+    return (f32_to_bf16(np.asarray(f32, np.float32)).astype(np.uint32) << 16).view(np.float32)
+
+
+def run_fp8_moe(x_bf16: np.ndarray, route_idx: np.ndarray, route_w: np.ndarray, experts: dict, shared,
+                *, mode: str = "auto") -> tuple[np.ndarray, list[int], str]:
+    """DeepSeek MoE layer orchestration of run_fp8_moe
+    (src/pcketlm/core/runtime/fp8_source.py:1569-1884) on the oracle's kernels.
+
+    x_bf16: [M, H] activations as bf16 values (fp32 array); route_idx [M, k]
+    int64; route_w [M, k] fp32 holding bf16 values (the router's output);
+    experts: {expert id: (gate, gate_s, up, up_s, down, down_s)}; shared: the
+    shared expert's six arrays or None.  mode "auto" picks the path the
+    reference picks with its default flags: the route-weighted many-expert
+    kernel at M == 1 (1643-1646, 1736-1764), per-expert MLPs on each expert's
+    rows otherwise (1806-1836); "row" and "pair" force the row- and
+    pair-weighted kernels (1647-1734).  Every add into the output is a bf16
+    add (torch bf16 arithmetic: fp32 operation, round to nearest even).
+    Returns (output bf16 values [M, H] as fp32, selected experts, path).
+    """
+    x = np.asarray(x_bf16, np.float32)
+    m = x.shape[0]
+    selected = sorted({int(v) for v in np.asarray(route_idx).reshape(-1)})
+    jobs = []
+    for e in selected:
+        rows, tops = np.nonzero(np.asarray(route_idx) == e)
+        jobs.append((e, rows, tops))
+    out = np.zeros_like(x)
+    items = [experts[e] for e, _r, _t in jobs]
+    if mode == "pair" and m > 1:
+        pi, pr, pw = [], [], []
+        for item, (_e, rows, tops) in enumerate(jobs):
+            for r, t in zip(rows.tolist(), tops.tolist()):
+                pi.append(item)
+                pr.append(r)
+                pw.append(float(route_w[r, t]))
+        y = fp8_mlp_many_pair_weighted(items, x, np.array(pi, np.int64), np.array(pr, np.int64),
+                                       np.array(pw, np.float32))
+        out = _bf16_values(out + _bf16_values(y))
+        path = "pair_weighted"
+    elif mode == "row" and m > 1:
+        route = np.zeros((len(jobs), m), np.float32)
+        for item, (_e, rows, tops) in enumerate(jobs):
+            route[item, rows] = route_w[rows, tops]
+        y = fp8_mlp_many_row_weighted(items, x, route)
+        out = _bf16_values(out + _bf16_values(y))
+        path = "row_weighted"
+    elif m == 1:
+        route = np.array([route_w[rows[0], tops[0]] for _e, rows, tops in jobs], np.float32)
+        y = fp8_mlp_many_weighted(items, x, route)
+        out = _bf16_values(out + _bf16_values(y))
+        path = "weighted"
+    else:
+        for e, rows, tops in jobs:
+            y = _bf16_values(fp8_mlp(*experts[e], x[rows]))
+            r = route_w[rows, tops].astype(np.float32).reshape(-1, 1)
+            out[rows] = _bf16_values(out[rows] + _bf16_values(y * r))
+        path = "per_expert"
+    if shared is not None:
+        out = _bf16_values(out + _bf16_values(fp8_mlp(*shared, x)))
+    return out, selected, path

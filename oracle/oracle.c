@@ -713,6 +713,36 @@ ORC_API int orc_packed_gemv_rows8(const uint16_t* hidden, const uint16_t* packed
     return 0;
 }
 
+/*
+ * fp32-activation row8 GEMV of the dense decode's o and down projections
+ * (packed_rows8_gemv_float_hidden, src/pcketlm/native/fp16_kv_cache.cpp:146-174):
+ * per 8-row block one fused multiply-add chain over the columns in order,
+ * hidden[c] broadcast, no bias.
+ */
+ORC_API int orc_packed_gemv_rows8_f32_hidden(const float* hidden, const uint16_t* packed, float* out,
+                                             int64_t rows, int64_t cols, int dtype_code) {
+    if (!hidden || !packed || !out) return 1;
+    if (rows < 0 || cols < 0 || (dtype_code != 0 && dtype_code != 1)) return 2;
+    const int64_t blocks = (rows + 7) / 8;
+#pragma omp parallel for schedule(static)
+    for (int64_t blk = 0; blk < blocks; ++blk) {
+        float acc[8] = {0};
+        const uint16_t* wb = packed + blk * cols * 8;
+        for (int64_t c = 0; c < cols; ++c) {
+            const float h = hidden[c];
+            for (int l = 0; l < 8; ++l) {
+                const uint16_t wv = wb[c * 8 + l];
+                acc[l] = fmaf(h, dtype_code ? bf16_to_f32(wv) : orc_f16_to_f32(wv), acc[l]);
+            }
+        }
+        for (int l = 0; l < 8; ++l) {
+            const int64_t r = blk * 8 + l;
+            if (r < rows) out[r] = acc[l];
+        }
+    }
+    return 0;
+}
+
 /* ------------------------------------------------------------------------- */
 /* Softmax top-k router (src/pcketlm/native/ds_forward.cpp:879-955)          */
 /* ------------------------------------------------------------------------- */

@@ -57,6 +57,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "native_pack_u16_rows8": (_i32, [_vp, _vp, _i64, _i64]),
     "native_packed_gemv_rows8": (_i32, [_vp, _vp, _vp, _i64, _i64, _i32]),
     "native_packed_gemv_rows8_many": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32]),
+    "native_packed_gemv_rows8_f32_hidden": (_i32, [_vp, _vp, _vp, _i64, _i64, _i32]),
     "ds_session_create": (_vp, [_i64, _i64, _i64, _i64, _vp, _vp]),
     "ds_session_destroy": (None, [_vp]),
     "ds_session_register_layer": (_i32, [_vp, _i64, _i64, _i64, DS_TENSOR_CALLBACK, DS_TENSOR_CALLBACK]),

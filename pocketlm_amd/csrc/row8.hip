@@ -1,5 +1,6 @@
 // row8-packed fp16/bf16 GEMV for gfx950 (src/pcketlm/native/fp16_packed_gemv.cpp
-// and the fused variants of fp16_kv_cache.cpp:117-298).
+// and the fused variants of fp16_kv_cache.cpp:117-298, including the fp32
+// activation variant used for the o and down projections, 146-174).
 //
 // Layout: packed[blk][k][lane] = W[8*blk + lane][k], so one 8-row block is a
 // contiguous K x 16-byte run.  A lane loads one 16-byte column slice (the 8
@@ -46,7 +47,8 @@ struct Row8Mat {
 
 struct Row8Args {
     Row8Mat mat[kMaxMats];
-    const uint16_t* hidden;
+    const uint16_t* hidden;      // fp16 / bf16 activations (same type as the weights), or
+    const float* hidden_f32;     // fp32 activations
     int64_t K;
     int nmats;
     int nchunks;           // ceil(K / 64)
@@ -54,7 +56,7 @@ struct Row8Args {
 };
 
 // One workgroup = one 8-row block of one matrix; its waves split the columns.
-template <bool BF16>
+template <bool BF16, bool XF32>
 __global__ __launch_bounds__(512) void row8_gemv_kernel(const Row8Args a) {
     __shared__ float red[kMaxWaves * 8];
     const int nw = blockDim.x >> 6;
@@ -83,7 +85,7 @@ __global__ __launch_bounds__(512) void row8_gemv_kernel(const Row8Args a) {
             const bool ok = c0 + u * nw < a.nchunks && col < a.K;
             const int64_t cc = ok ? col : a.K - 1;
             q[u] = *reinterpret_cast<const uint4*>(base + cc * 8);
-            const float xh = u16_to_f32(a.hidden[cc], BF16);
+            const float xh = XF32 ? a.hidden_f32[cc] : u16_to_f32(a.hidden[cc], BF16);
             xv[u] = ok ? xh : 0.0f;
         }
 #pragma unroll
@@ -139,7 +141,8 @@ __global__ void pack_rows8_kernel(const uint16_t* __restrict__ w, uint16_t* __re
     }
 }
 
-int run_row8(const uint16_t* hidden, const Row8Mat* mats, int n, int64_t K, int dtype_code, hipStream_t st) {
+int run_row8(const uint16_t* hidden, const float* hidden_f32, const Row8Mat* mats, int n, int64_t K, int dtype_code,
+             hipStream_t st) {
     Row8Args a;
     std::memset(&a, 0, sizeof(a));
     int64_t tiles = 0;
@@ -154,16 +157,24 @@ int run_row8(const uint16_t* hidden, const Row8Mat* mats, int n, int64_t K, int 
     }
     if (used == 0) return 0;  // nothing to write
     a.hidden = hidden;
+    a.hidden_f32 = hidden_f32;
     a.K = K;
     a.nmats = used;
     a.nchunks = static_cast<int>(plm::ceil_div(K, 64));
     a.bf16 = dtype_code;
     const int nw = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(a.nchunks, kMaxWaves)));
     if (tiles > 0x7FFFFFFF) return plm::fail(2, "too many row blocks");
-    if (dtype_code == 1) {
-        hipLaunchKernelGGL(row8_gemv_kernel<true>, dim3(static_cast<unsigned>(tiles)), dim3(nw * plm::kWave), 0, st, a);
+    const dim3 grid(static_cast<unsigned>(tiles)), block(nw * plm::kWave);
+    if (hidden_f32 != nullptr) {
+        if (dtype_code == 1) {
+            hipLaunchKernelGGL((row8_gemv_kernel<true, true>), grid, block, 0, st, a);
+        } else {
+            hipLaunchKernelGGL((row8_gemv_kernel<false, true>), grid, block, 0, st, a);
+        }
+    } else if (dtype_code == 1) {
+        hipLaunchKernelGGL((row8_gemv_kernel<true, false>), grid, block, 0, st, a);
     } else {
-        hipLaunchKernelGGL(row8_gemv_kernel<false>, dim3(static_cast<unsigned>(tiles)), dim3(nw * plm::kWave), 0, st, a);
+        hipLaunchKernelGGL((row8_gemv_kernel<false, false>), grid, block, 0, st, a);
     }
     return plm::check_launch("row8 gemv kernel");
 }
@@ -190,7 +201,7 @@ PLM_EXPORT int native_packed_gemv_rows8(const uint16_t* hidden, const uint16_t* 
     m.out = out;
     m.rows = rows;
     m.first_tile = 0;
-    return run_row8(hidden, &m, 1, cols, dtype_code, plm::current_stream());
+    return run_row8(hidden, nullptr, &m, 1, cols, dtype_code, plm::current_stream());
 }
 
 PLM_EXPORT int native_packed_gemv_rows8_many(const uint16_t* hidden, const uint16_t* const* packed_ptrs,
@@ -208,5 +219,18 @@ PLM_EXPORT int native_packed_gemv_rows8_many(const uint16_t* hidden, const uint1
         mats[i].rows = rows[i];
         mats[i].first_tile = 0;
     }
-    return run_row8(hidden, mats, static_cast<int>(count), cols, dtype_code, plm::current_stream());
+    return run_row8(hidden, nullptr, mats, static_cast<int>(count), cols, dtype_code, plm::current_stream());
+}
+
+PLM_EXPORT int native_packed_gemv_rows8_f32_hidden(const float* hidden, const uint16_t* packed, float* out, int64_t rows,
+                                                   int64_t cols, int dtype_code) {
+    if (!hidden || !packed || !out) return plm::fail(1, "null pointer");
+    if (rows < 0 || cols < 0 || (dtype_code != 0 && dtype_code != 1)) return plm::fail(2, "bad dimensions or dtype");
+    Row8Mat m;
+    m.packed = packed;
+    m.bias = nullptr;
+    m.out = out;
+    m.rows = rows;
+    m.first_tile = 0;
+    return run_row8(nullptr, hidden, &m, 1, cols, dtype_code, plm::current_stream());
 }

@@ -724,6 +724,35 @@ def packed_gemv_rows8_many(hidden: torch.Tensor, packed_weights, rows, *, cols: 
     return [_home(o, hidden) for o in outs]
 
 
+def packed_gemv_rows8_f32_hidden(hidden: torch.Tensor, packed_weight: torch.Tensor, *, rows: int, cols: int,
+                                 weight_dtype: torch.dtype) -> torch.Tensor:
+    """fp32-activation row8 GEMV of the dense decode's o and down projections
+    (packed_rows8_gemv_float_hidden, src/pcketlm/native/fp16_kv_cache.cpp:146-174):
+    y = W x with an fp32 x, one fma chain per row, no bias.  weight_dtype is
+    the storage type of the packed weight (torch.float16 or torch.bfloat16)."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_PACKED_GEMV", "Native packed GEMV")
+    if hidden.dtype != torch.float32:
+        raise TypeError("packed_gemv_rows8_f32_hidden requires torch.float32 hidden")
+    if weight_dtype not in {torch.float16, torch.bfloat16}:
+        raise TypeError("weight_dtype must be torch.float16 or torch.bfloat16")
+    if packed_weight.dtype != torch.uint16:
+        raise TypeError("packed_weight must be a torch.uint16 tensor from pack_weight_rows8")
+    dev = _target_device(hidden, packed_weight)
+    h = _on(hidden, dev).reshape(-1)
+    if h.numel() != int(cols):
+        raise ValueError("hidden length does not match packed weight column count")
+    pw = _on(packed_weight, dev)
+    if pw.numel() != ((int(rows) + 7) // 8) * int(cols) * 8:
+        raise ValueError("packed weight length does not match rows/cols")
+    out = torch.empty((int(rows),), dtype=torch.float32, device=dev)
+    if int(rows):
+        with _launch(lib, dev):
+            code = lib.native_packed_gemv_rows8_f32_hidden(_p(h), _p(pw), _p(out), int(rows), int(cols),
+                                                           _u16_storage_dtype_code(weight_dtype))
+        _check("native_packed_gemv_rows8_f32_hidden", code)
+    return _home(out, hidden)
+
+
 # --------------------------------------------------------------------------- DeepSeek session / MoE
 
 class DeepSeekNativeSession:

@@ -170,6 +170,20 @@ def test_row8_many_with_bias(nat, oracle_mod):
         assert rel_l2(host(o), want) < 1e-5
 
 
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_row8_f32_hidden_vs_oracle(nat, oracle_mod, dt):
+    tdt = torch.float16 if dt == "f16" else torch.bfloat16
+    rng = np.random.default_rng(77)
+    for rows, cols in ((3584, 3584), (3584, 18944), (13, 40)):
+        w = torch.from_numpy((rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)).to(tdt)
+        x = rng.standard_normal(cols).astype(np.float32)
+        packed = nat.pack_weight_rows8(w.cuda())
+        y = host(nat.packed_gemv_rows8_f32_hidden(dev(x), packed, rows=rows, cols=cols, weight_dtype=tdt))
+        want = oracle_mod.packed_gemv_rows8_f32_hidden(x, host(packed).view(np.uint16), rows, cols,
+                                                       0 if dt == "f16" else 1)
+        assert rel_l2(y, want) < 1e-5, (rows, cols)
+
+
 # --------------------------------------------------------------------------- routers
 
 def test_softmax_router_golden(nat, golden):

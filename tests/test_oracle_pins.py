@@ -260,6 +260,30 @@ def test_row8_gemv_matches_reference_build_and_torch_mv(oracle_mod, golden):
         assert np.allclose(y, g[f"{key}_mv"], atol=1e-4, rtol=1e-4), key
 
 
+def test_row8_f32_hidden_pinned_to_reference_build_and_fp64(oracle_mod, golden):
+    # With x holding exactly the fp16 / bf16 values of the reference build's
+    # cases, the fp32-activation chain is the same fma chain: bit-exact to
+    # the reference's outputs.
+    g = golden("row8")
+    for key in g["cases"]:
+        w, h, code = g[f"{key}_w"], g[f"{key}_h"], int(g[f"{key}_code"])
+        rows, cols = w.shape
+        hf = (h.astype(np.uint32) << 16).view(np.float32) if code else h.view(np.float16).astype(np.float32)
+        y = oracle_mod.packed_gemv_rows8_f32_hidden(hf, oracle_mod.pack_rows8(w), rows, cols, code)
+        assert np.array_equal(y, g[f"{key}_y"]), key
+    # Arbitrary fp32 activations against the fp64 product.
+    rng = np.random.default_rng(31)
+    w = (rng.standard_normal((37, 300)) * 0.05).astype(np.float16)
+    x = rng.standard_normal(300).astype(np.float32)
+    y = oracle_mod.packed_gemv_rows8_f32_hidden(x, oracle_mod.pack_rows8(w.view(np.uint16)), 37, 300, 0)
+    want = w.astype(np.float64) @ x.astype(np.float64)
+    assert np.abs(y - want).max() < 1e-5 * np.abs(want).max()
+    # A planted transposed block order must fail the closed form.
+    bad = oracle_mod.pack_rows8(w.view(np.uint16)).reshape(-1, 300, 8)[::-1].reshape(-1)
+    y_bad = oracle_mod.packed_gemv_rows8_f32_hidden(x, bad, 37, 300, 0)
+    assert np.abs(y_bad - want).max() > 1e-2 * np.abs(want).max()
+
+
 # --------------------------------------------------------------------------- routers
 
 def test_softmax_router_matches_fp64_closed_form(oracle_mod, golden):
