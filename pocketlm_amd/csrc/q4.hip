@@ -8,11 +8,10 @@
 // Dot products.  A lane reads 16 packed bytes (32 values) per load.  Each
 // dword d holds 8 nibbles; u = d ^ 0x88888888 turns every signed nibble q
 // into the unsigned u = q + 8, which is unpacked without per-element
-// extracts (as fp16 subnormal pairs for v_dot2_f32_f16 when x is fp16, as
-// bytes for v_cvt_f32_ubyte when x is fp32).  The +8 bias is removed once
-// per 32-value span: sum(q*x) = sum(u*x) - 8*sum(x), where sum(x) over the
-// span is shared by every row of the tile.  The row scale multiplies the
-// row's sum.
+// extracts into exact fp16 subnormal pairs: matrix-core operands when x is
+// fp16 (gate/up and the plain GEMV), v_fma_mix operands when x is fp32 (the
+// down phase).  The +8 bias is removed with sum(q*x) = sum(u*x) - 8*sum(x).
+// The row scale multiplies the row's sum.
 #include <algorithm>
 #include <cstring>
 #include <vector>
@@ -140,62 +139,26 @@ int q4_dequant_launch(const uint8_t* packed, const uint16_t* scales, uint16_t* o
 //
 // Layout of the dot-product kernels.  A wave is four groups of 16 lanes; a
 // group owns TR rows and reads them in steps of 256 packed bytes (512 values),
-// lane li taking bytes [16*li, 16*li + 16) of the step, so one wave-wide load
-// instruction fetches 4 x 256 contiguous bytes.  The NWS waves of a workgroup
-// split a row's steps, UNR steps of a wave are loaded before any is used, and
+// 16 bytes per lane, so one wave-wide load instruction fetches 4 x 256
+// contiguous bytes.  The NWS waves of a workgroup split a row's steps, and
 // every load is unconditional: rows and steps past the end read a clamped
-// address and their contribution is dropped.  Row sums are four DPP adds
-// inside the 16-lane row, then an in-order sum over the waves in LDS.
+// address and their contribution is dropped.
 
 typedef _Float16 plm_half2 __attribute__((ext_vector_type(2)));
+typedef _Float16 plm_half8 __attribute__((ext_vector_type(8)));
+typedef float plm_f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t plm_u4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float half_lo(uint32_t v) { return static_cast<float>(__builtin_bit_cast(plm_half2, v)[0]); }
 __device__ __forceinline__ float half_hi(uint32_t v) { return static_cast<float>(__builtin_bit_cast(plm_half2, v)[1]); }
 
-// fp16 activations of one 16-byte span (four 16-byte pieces): xr[m] holds
-// values 2m (low half) and 2m + 1 (high half); *xsum is their fp32 sum.
-__device__ __forceinline__ void q4_unpack_x_f16(const uint4* xv, uint32_t* xr, float* xsum) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        xr[4 * i] = xv[i].x;
-        xr[4 * i + 1] = xv[i].y;
-        xr[4 * i + 2] = xv[i].z;
-        xr[4 * i + 3] = xv[i].w;
-    }
-    float xs = 0.0f;
-#pragma unroll
-    for (int m = 0; m < 16; ++m) {
-        xs += half_lo(xr[m]);
-        xs += half_hi(xr[m]);
-    }
-    *xsum = xs;
-}
-
-// sum over the span of q * x for fp16 x.  Dword i of the span holds nibbles
-// k = 0..7 (values 8i + k).  With u = d ^ 0x88888888 (u = q + 8),
+// sum over a 32-value span of q * x for fp32 x.  Dword i of the span holds
+// nibbles k = 0..7 (values 8i + k).  With u = d ^ 0x88888888 (u = q + 8),
 // (u >> 4j) & 0x000F000F is the pair (u_{8i+j}, u_{8i+j+4}) as fp16
 // subnormals u * 2^-24.  Each product is one fp32 fma (v_fma_mix_f32 reads
-// the fp16 halves directly, so every product is exact and every add is
+// the fp16 half in place, so every product is exact and every add is
 // round-to-nearest fp32); 2^24 * sum(u * 2^-24 * x) - 8 * sum(x) is then
 // sum(q * x).
-__device__ __forceinline__ float q4_span_dot_f16(const uint4& q, const uint32_t* xr, float xs8) {
-    const uint32_t d[4] = {q.x ^ 0x88888888u, q.y ^ 0x88888888u, q.z ^ 0x88888888u, q.w ^ 0x88888888u};
-    float p = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t pr = (d[i] >> (4 * j)) & 0x000F000Fu;
-            const uint32_t xa = xr[4 * i + (j >> 1)], xb = xr[4 * i + 2 + (j >> 1)];
-            p = fmaf(half_lo(pr), (j & 1) ? half_hi(xa) : half_lo(xa), p);
-            p = fmaf(half_hi(pr), (j & 1) ? half_hi(xb) : half_lo(xb), p);
-        }
-    }
-    return p * 16777216.0f - xs8;
-}
-
-// fp32 activations: the same fp16-subnormal pairs, each product one fp32
-// fma of the pair's half (read as fp16) and the fp32 x value.
 __device__ __forceinline__ float q4_span_dot_f32(const uint4& q, const float* x, float xs8) {
     const uint32_t d[4] = {q.x ^ 0x88888888u, q.y ^ 0x88888888u, q.z ^ 0x88888888u, q.w ^ 0x88888888u};
     float p = 0.0f;
@@ -222,6 +185,47 @@ __device__ __forceinline__ float row16_sum(float v) {
 
 constexpr int kStepBytes = 256;
 
+// Matrix-core dot products for fp16 activations.
+//
+// v_mfma_f32_16x16x32_f16 is used as a per-lane dot product: lane l supplies
+// 8 weights as row l % 16 of A and the 8 matching activations as column l % 16
+// of B, so the diagonal D[i][i] is the sum of the own-dot products of the four
+// lanes with l % 16 == i (the 240 off-diagonal outputs are cross terms and are
+// never read).  Any assignment of k positions to lanes is then valid as long
+// as those four lanes share a row: rows are given by (l % 16) / 4 and the 16
+// lanes of a row take the 16 pieces of a 256-byte step, the load layout above.
+//
+// Weights become exact fp16 subnormals with five bit operations per packed
+// dword.  With u = d ^ 0x88888888 (u = q + 8 per nibble):
+//   u & 0x000F000F        = (u0, u4) * 2^-24
+//   u & 0x00F000F0        = (u1, u5) * 2^-20
+//   (u >> 8) & 0x000F000F = (u2, u6) * 2^-24
+//   (u >> 8) & 0x00F000F0 = (u3, u7) * 2^-20
+// and the B halves paired with the 2^-20 values are the activations / 16.
+// A second accumulator with the constant 8 in the same encoding collects
+// 8 * sum(x) on its diagonal, so sum(q * x) = 2^24 * (D - C).  Products are
+// exact; the matrix core rounds its internal sums, which leaves results
+// within about 1e-5 relative of an fp32 FMA chain.
+__device__ __forceinline__ plm_half8 q4_mfma_a(uint32_t d) {
+    const uint32_t u = d ^ 0x88888888u;
+    const uint32_t t = u >> 8;
+    const plm_u4 r = {u & 0x000F000Fu, u & 0x00F000F0u, t & 0x000F000Fu, t & 0x00F000F0u};
+    return __builtin_bit_cast(plm_half8, r);
+}
+
+// B for 8 consecutive fp16 activations (x0, x1), (x2, x3), (x4, x5), (x6, x7):
+// the pairs (x0, x4), (x1, x5) / 16, (x2, x6), (x3, x7) / 16.
+__device__ __forceinline__ plm_half8 q4_mfma_b(const uint4& v) {
+    const plm_half2 s16 = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+    const uint32_t p1 = __builtin_bit_cast(
+        uint32_t, __builtin_bit_cast(plm_half2, __builtin_amdgcn_perm(v.z, v.x, 0x07060302u)) * s16);
+    const uint32_t p3 = __builtin_bit_cast(
+        uint32_t, __builtin_bit_cast(plm_half2, __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)) * s16);
+    const plm_u4 r = {__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), p1, __builtin_amdgcn_perm(v.w, v.y, 0x05040100u),
+                      p3};
+    return __builtin_bit_cast(plm_half8, r);
+}
+
 struct Q4RowsArgs {
     const uint8_t* w[2][kMaxGroups];
     const uint16_t* s[2][kMaxGroups];
@@ -243,20 +247,19 @@ __device__ __forceinline__ int64_t act_pos(int64_t k) {
     return (k & ~int64_t{511}) | (((k & 31) >> 2) << 6) | (((k & 511) >> 5) << 2) | (k & 3);
 }
 
-// Rows of one or more experts against one shared fp16 activation vector.
-// NWT=2 with SILU computes silu(gate) * up (the gate/up phase of the MoE).
-// (Staging x in LDS was measured slower: the workgroup barrier holds every
-// wave until the slowest wave's first weights arrive.)
-template <int TR, int NWT, int NWS, int UNR, bool SILU>
+// Rows of one or more experts against one shared fp16 activation vector, on
+// the matrix cores.  NWT=2 with SILU computes silu(gate) * up (the gate/up
+// phase of the MoE).
+template <int TR, int NWT, int NWS, bool SILU>
 __global__ __launch_bounds__(NWS * 64) void q4_rows_kernel(const Q4RowsArgs a) {
     constexpr int T = 4 * TR;  // rows per workgroup
     __shared__ float red[NWS][NWT][T];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63;
-    const int grp = lane >> 4, li = lane & 15;
+    const int i16 = lane & 15, c = i16 >> 2;
+    const int piece = (i16 & 3) + 4 * (lane >> 4);  // 16-byte piece of the step
     const int g = blockIdx.x / a.tiles_per_group;
     const int64_t tile0 = static_cast<int64_t>(blockIdx.x - g * a.tiles_per_group) * T;
-    const int64_t row0 = tile0 + grp * TR;
     const int64_t row_bytes = a.K >> 1;
     const int steps = static_cast<int>((row_bytes + kStepBytes - 1) / kStepBytes);
     const uint8_t* wp[NWT];
@@ -264,58 +267,62 @@ __global__ __launch_bounds__(NWS * 64) void q4_rows_kernel(const Q4RowsArgs a) {
 #pragma unroll
     for (int i = 0; i < NWT; ++i) wp[i] = a.w[i][g];
 #pragma unroll
-    for (int t = 0; t < TR; ++t) roff[t] = (row0 + t < a.rows ? row0 + t : a.rows - 1) * row_bytes;
-
-    float acc[NWT][TR];
+    for (int t = 0; t < TR; ++t) {
+        const int64_t row = tile0 + c * TR + t;
+        roff[t] = (row < a.rows ? row : a.rows - 1) * row_bytes;
+    }
+    plm_f4 acc[NWT][TR], corr = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < NWT; ++i)
 #pragma unroll
-        for (int t = 0; t < TR; ++t) acc[i][t] = 0.0f;
+        for (int t = 0; t < TR; ++t) acc[i][t] = plm_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    const plm_half8 c8 = __builtin_bit_cast(plm_half8, plm_u4{0x00080008u, 0x00800080u, 0x00080008u, 0x00800080u});
 
-    uint4 q[UNR][NWT][TR];
-    auto load_w = [&](int s0) {
+    for (int s = wave; s < steps; s += NWS) {
+        const int64_t byte = static_cast<int64_t>(s) * kStepBytes + piece * 16;
+        const bool ok = byte < row_bytes;
+        const int64_t bc = ok ? byte : row_bytes - 16;
+        uint4 q[NWT][TR];
 #pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            const int64_t byte = static_cast<int64_t>(s0 + u * NWS) * kStepBytes + li * 16;
-            const int64_t bc = byte < row_bytes ? byte : row_bytes - 16;
+        for (int i = 0; i < NWT; ++i)
 #pragma unroll
-            for (int i = 0; i < NWT; ++i)
+            for (int t = 0; t < TR; ++t) q[i][t] = *reinterpret_cast<const uint4*>(wp[i] + roff[t] + bc);
+        const uint4* xp = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + 2 * bc);
+        uint4 xv[4];
 #pragma unroll
-                for (int t = 0; t < TR; ++t) q[u][i][t] = *reinterpret_cast<const uint4*>(wp[i] + roff[t] + bc);
+        for (int k = 0; k < 4; ++k) xv[k] = xp[k];
+        if (!ok) {
+            // a piece past the end of the row contributes nothing
+#pragma unroll
+            for (int k = 0; k < 4; ++k) xv[k] = make_uint4(0u, 0u, 0u, 0u);
         }
-    };
-    for (int s0 = wave; s0 < steps; s0 += NWS * UNR) {
-        load_w(s0);
 #pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            const int s = s0 + u * NWS;
-            if (s >= steps) break;
-            const int64_t byte = static_cast<int64_t>(s) * kStepBytes + li * 16;
-            const bool ok = byte < row_bytes;
-            const int64_t bc = ok ? byte : row_bytes - 16;
-            const uint4* xp = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + 2 * bc);
-            uint4 xv[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) xv[i] = xp[i];
-            uint32_t xr[16];
-            float xs;
-            q4_unpack_x_f16(xv, xr, &xs);
+        for (int j = 0; j < 4; ++j) {
+            const plm_half8 b = q4_mfma_b(xv[j]);
+            corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(c8, b, corr, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < NWT; ++i)
 #pragma unroll
                 for (int t = 0; t < TR; ++t) {
-                    const float p = q4_span_dot_f16(q[u][i][t], xr, 8.0f * xs);
-                    acc[i][t] += ok ? p : 0.0f;
+                    const uint32_t d = j == 0 ? q[i][t].x : j == 1 ? q[i][t].y : j == 2 ? q[i][t].z : q[i][t].w;
+                    acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(q4_mfma_a(d), b, acc[i][t], 0, 0, 0);
                 }
         }
     }
 
+    // D[i][i] sits in lane 16 * (i / 4) + i, element i % 4; row group c owns
+    // i = 4c .. 4c + 3, i.e. the aligned quad of lanes 20c .. 20c + 3, each
+    // contributing its element lane % 4.
+    const int e = lane & 3;
+    const float cr = corr[e];
 #pragma unroll
     for (int i = 0; i < NWT; ++i)
 #pragma unroll
         for (int t = 0; t < TR; ++t) {
-            const float v = row16_sum(acc[i][t]);
-            if (li == 0) red[wave][i][grp * TR + t] = v;
+            float v = acc[i][t][e] - cr;
+            v = PLM_DPP_ADD(v, 0xB1, 0xF);
+            v = PLM_DPP_ADD(v, 0x4E, 0xF);
+            if (lane == 20 * c) red[wave][i][c * TR + t] = v;
         }
     __syncthreads();
     if (threadIdx.x < T) {
@@ -327,7 +334,7 @@ __global__ __launch_bounds__(NWS * 64) void q4_rows_kernel(const Q4RowsArgs a) {
                 float sum = 0.0f;
 #pragma unroll
                 for (int w = 0; w < NWS; ++w) sum += red[w][i][threadIdx.x];
-                v[i] = sum * h2f_ref(a.s[i][g][row]);
+                v[i] = sum * 16777216.0f * h2f_ref(a.s[i][g][row]);
             }
             const int64_t o = static_cast<int64_t>(g) * a.out_stride + (a.out_steps ? act_pos(row) : row);
             if constexpr (SILU) {
@@ -477,10 +484,10 @@ __global__ void q4_combine_scalar_kernel(const Q4CombineArgs a) {
     a.out_f16[row] = f16_from_bits(f2u(acc), false);
 }
 
-template <int TR, int NWT, int NWS, int UNR, bool SILU>
+template <int TR, int NWT, int NWS, bool SILU>
 void launch_q4_rows(Q4RowsArgs a, int ngroups, hipStream_t st) {
     a.tiles_per_group = static_cast<int>(plm::ceil_div(a.rows, 4 * TR));
-    hipLaunchKernelGGL((q4_rows_kernel<TR, NWT, NWS, UNR, SILU>),
+    hipLaunchKernelGGL((q4_rows_kernel<TR, NWT, NWS, SILU>),
                        dim3(static_cast<unsigned>(static_cast<int64_t>(a.tiles_per_group) * ngroups)),
                        dim3(NWS * plm::kWave), 0, st, a);
 }
@@ -489,9 +496,9 @@ void launch_q4_rows(Q4RowsArgs a, int ngroups, hipStream_t st) {
 // waves splitting each row; short rows the opposite.
 void launch_q4_gemv(const Q4RowsArgs& a, hipStream_t st) {
     if (a.K / 2 >= 16 * kStepBytes) {
-        launch_q4_rows<2, 1, 16, 1, false>(a, 1, st);
+        launch_q4_rows<2, 1, 16, false>(a, 1, st);
     } else {
-        launch_q4_rows<4, 1, 4, 2, false>(a, 1, st);
+        launch_q4_rows<4, 1, 4, false>(a, 1, st);
     }
 }
 
@@ -612,7 +619,7 @@ PLM_EXPORT int q4_moe_selected_forward_u16(const uint16_t* hidden, const uint8_t
         a.out_stride = stride;
         a.out_steps = fast2 ? 1 : 0;
         if (fast1) {
-            launch_q4_rows<2, 2, 4, 2, true>(a, ng, st);
+            launch_q4_rows<2, 2, 4, true>(a, ng, st);
         } else {
             hipLaunchKernelGGL(q4_rows_scalar_kernel<true>,
                                dim3(static_cast<unsigned>(plm::ceil_div(static_cast<int64_t>(ng) * I, 256))), dim3(256),

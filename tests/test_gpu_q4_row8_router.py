@@ -76,7 +76,10 @@ def test_q4_gemv_vs_oracle(nat, oracle_mod, shape):
     x16 = np.random.default_rng(cols).standard_normal(cols).astype(np.float16)
     y = host(nat.q4_gemv_f16_f32(dev(packed), dev(scales).view(torch.float16), dev(x16), rows=rows, cols=cols))
     want = oracle_mod.q4_gemv(packed, scales, x16.astype(np.float32), rows, cols)
-    assert rel_l2(y, want) < 1e-5
+    # fp16 activations run on the matrix cores: exact products, sums rounded
+    # inside the MFMA (about 1e-5 relative at K = 18944); the bar for the
+    # path is 1e-3.
+    assert rel_l2(y, want) < 1e-4
 
 
 def _moe_experts(g):
