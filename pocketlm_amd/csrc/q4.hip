@@ -13,6 +13,7 @@
 // down phase).  The +8 bias is removed with sum(q*x) = sum(u*x) - 8*sum(x).
 // The row scale multiplies the row's sum.
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <vector>
 
@@ -174,15 +175,6 @@ __device__ __forceinline__ float q4_span_dot_f32(const uint4& q, const float* x,
     return p * 16777216.0f - xs8;
 }
 
-// Sum over the 16 lanes of a row group; every lane of the group ends with it.
-__device__ __forceinline__ float row16_sum(float v) {
-    v = PLM_DPP_ADD(v, 0xB1, 0xF);
-    v = PLM_DPP_ADD(v, 0x4E, 0xF);
-    v = PLM_DPP_ADD(v, 0x141, 0xF);
-    v = PLM_DPP_ADD(v, 0x140, 0xF);
-    return v;
-}
-
 constexpr int kStepBytes = 256;
 
 // Matrix-core dot products for fp16 activations.
@@ -195,35 +187,69 @@ constexpr int kStepBytes = 256;
 // as those four lanes share a row: rows are given by (l % 16) / 4 and the 16
 // lanes of a row take the 16 pieces of a 256-byte step, the load layout above.
 //
-// Weights become exact fp16 subnormals with five bit operations per packed
-// dword.  With u = d ^ 0x88888888 (u = q + 8 per nibble):
-//   u & 0x000F000F        = (u0, u4) * 2^-24
-//   u & 0x00F000F0        = (u1, u5) * 2^-20
-//   (u >> 8) & 0x000F000F = (u2, u6) * 2^-24
-//   (u >> 8) & 0x00F000F0 = (u3, u7) * 2^-20
-// and the B halves paired with the 2^-20 values are the activations / 16.
-// A second accumulator with the constant 8 in the same encoding collects
-// 8 * sum(x) on its diagonal, so sum(q * x) = 2^24 * (D - C).  Products are
-// exact; the matrix core rounds its internal sums, which leaves results
-// within about 1e-5 relative of an fp32 FMA chain.
+// Weights become exact fp16 subnormals: with u = d ^ 0x88888888 (u = q + 8
+// per nibble), (u >> 4j) & 0x000F000F is the pair (u_j, u_{j+4}) * 2^-24.  The
+// matching B pairs are (x_j, x_{j+4}).  A second accumulator with the
+// constant 8 * 2^-24 as A collects 8 * sum(x) on its diagonal, so
+// sum(q * x) = 2^24 * (D - C).  Products are exact for every finite fp16 x;
+// the matrix core rounds its internal sums, which leaves results within about
+// 1e-5 relative of an fp32 FMA chain.
 __device__ __forceinline__ plm_half8 q4_mfma_a(uint32_t d) {
+    const uint32_t u = d ^ 0x88888888u;
+    const plm_u4 r = {u & 0x000F000Fu, (u >> 4) & 0x000F000Fu, (u >> 8) & 0x000F000Fu, (u >> 12) & 0x000F000Fu};
+    return __builtin_bit_cast(plm_half8, r);
+}
+
+// B for 8 consecutive fp16 activations (x0, x1), (x2, x3), (x4, x5), (x6, x7):
+// the pairs (x0, x4), (x1, x5), (x2, x6), (x3, x7).
+__device__ __forceinline__ plm_half8 q4_mfma_b(const uint4& v) {
+    const plm_u4 r = {__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                      __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
+    return __builtin_bit_cast(plm_half8, r);
+}
+
+__device__ __forceinline__ plm_half8 q4_mfma_c8() {
+    return __builtin_bit_cast(plm_half8, plm_u4{0x00080008u, 0x00080008u, 0x00080008u, 0x00080008u});
+}
+
+// Shorter encoding for B values prepared in advance (the down phase): the
+// pairs (u1, u5) and (u3, u7) stay in place at bits 4-7 of each half, i.e.
+// u * 2^-20, and their B values are stored divided by 16.  Five operations per
+// dword: u & 0x000F000F, u & 0x00F000F0, and the same on u >> 8.
+__device__ __forceinline__ plm_half8 q4_mfma_a_inplace(uint32_t d) {
     const uint32_t u = d ^ 0x88888888u;
     const uint32_t t = u >> 8;
     const plm_u4 r = {u & 0x000F000Fu, u & 0x00F000F0u, t & 0x000F000Fu, t & 0x00F000F0u};
     return __builtin_bit_cast(plm_half8, r);
 }
 
-// B for 8 consecutive fp16 activations (x0, x1), (x2, x3), (x4, x5), (x6, x7):
-// the pairs (x0, x4), (x1, x5) / 16, (x2, x6), (x3, x7) / 16.
-__device__ __forceinline__ plm_half8 q4_mfma_b(const uint4& v) {
-    const plm_half2 s16 = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
-    const uint32_t p1 = __builtin_bit_cast(
-        uint32_t, __builtin_bit_cast(plm_half2, __builtin_amdgcn_perm(v.z, v.x, 0x07060302u)) * s16);
-    const uint32_t p3 = __builtin_bit_cast(
-        uint32_t, __builtin_bit_cast(plm_half2, __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)) * s16);
-    const plm_u4 r = {__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), p1, __builtin_amdgcn_perm(v.w, v.y, 0x05040100u),
-                      p3};
-    return __builtin_bit_cast(plm_half8, r);
+__device__ __forceinline__ plm_half8 q4_mfma_c8_inplace() {
+    return __builtin_bit_cast(plm_half8, plm_u4{0x00080008u, 0x00800080u, 0x00080008u, 0x00800080u});
+}
+
+// The down phase reads its fp32 activations as two fp16 planes already in
+// the B operand order: for value k, step s = k / 512, piece p = (k / 32) % 16,
+// dword j = (k / 8) % 4 and n = k % 8, the uint4 ((s * 4 + j) * 2 + plane) * 16
+// + p holds it in half (n % 4) * 2 + n / 4.  Values with n % 4 odd are stored
+// divided by 16: the down kernel's weights use the shorter encoding below,
+// which leaves those nibbles 16 times too large.  With v' the stored value,
+// plane 0 is hi = fp16(v') and plane 1 is lo = fp16((v' - hi) * 2^11), so
+// hi + lo * 2^-11 carries 22 significant bits (the split follows the /16, so
+// no bits are lost to it).  A value that fp16 cannot hold (|v| >= 65504, inf,
+// NaN) records the call's sequence number here, and that call's down phase
+// reads the fp32 activations instead.
+__device__ unsigned g_q4_planes_overflow_seq = 0;
+
+__device__ __forceinline__ void q4_store_planes(uint4* base, int64_t k, float v, unsigned seq) {
+    if (!(fabsf(v) < 65504.0f)) atomicExch(&g_q4_planes_overflow_seq, seq);
+    const int64_t s = k >> 9;
+    const int p = static_cast<int>((k >> 5) & 15), j = static_cast<int>((k >> 3) & 3), n = static_cast<int>(k & 7);
+    const float vs = (n & 1) ? v * 0.0625f : v;
+    const _Float16 hi = static_cast<_Float16>(vs);
+    const _Float16 lo = static_cast<_Float16>((vs - static_cast<float>(hi)) * 2048.0f);
+    uint16_t* h = reinterpret_cast<uint16_t*>(base + ((s * 4 + j) * 2) * 16 + p) + (n & 3) * 2 + (n >> 2);
+    h[0] = __builtin_bit_cast(uint16_t, hi);
+    h[16 * 8] = __builtin_bit_cast(uint16_t, lo);  // plane 1: 16 uint4 further
 }
 
 struct Q4RowsArgs {
@@ -236,6 +262,9 @@ struct Q4RowsArgs {
     int64_t out_stride;
     int out_steps;        // write the output in step order (see act_pos)
     int tiles_per_group;
+    uint4* planes;        // SILU only: also write the fp16 B planes (nullptr: no)
+    int64_t planes_stride;  // uint4 per group
+    unsigned seq;         // call sequence number for the overflow record
 };
 
 // Position of value k of an fp32 activation vector stored in "step order":
@@ -276,7 +305,7 @@ __global__ __launch_bounds__(NWS * 64) void q4_rows_kernel(const Q4RowsArgs a) {
     for (int i = 0; i < NWT; ++i)
 #pragma unroll
         for (int t = 0; t < TR; ++t) acc[i][t] = plm_f4{0.0f, 0.0f, 0.0f, 0.0f};
-    const plm_half8 c8 = __builtin_bit_cast(plm_half8, plm_u4{0x00080008u, 0x00800080u, 0x00080008u, 0x00800080u});
+    const plm_half8 c8 = q4_mfma_c8();
 
     for (int s = wave; s < steps; s += NWS) {
         const int64_t byte = static_cast<int64_t>(s) * kStepBytes + piece * 16;
@@ -338,7 +367,9 @@ __global__ __launch_bounds__(NWS * 64) void q4_rows_kernel(const Q4RowsArgs a) {
             }
             const int64_t o = static_cast<int64_t>(g) * a.out_stride + (a.out_steps ? act_pos(row) : row);
             if constexpr (SILU) {
-                a.out[o] = plm_silu_mul(v[0], v[1]);
+                const float act = plm_silu_mul(v[0], v[1]);
+                a.out[o] = act;
+                if (a.planes != nullptr) q4_store_planes(a.planes + g * a.planes_stride, row, act, a.seq);
             } else {
                 a.out[o] = v[0];
             }
@@ -351,6 +382,9 @@ struct Q4CombineArgs {
     const uint16_t* s[kMaxGroups];
     const float* act;     // [ngroups][act_stride] fp32, step order (act_pos) on the fast path
     int64_t act_stride;
+    const uint4* planes;  // [ngroups][planes_stride] fp16 B planes, or nullptr
+    int64_t planes_stride;
+    unsigned seq;
     const float* route;   // [ngroups]
     uint16_t* out_f16;    // [rows]
     int64_t rows;
@@ -360,83 +394,195 @@ struct Q4CombineArgs {
 
 // Down phase + routed combine of the Q4 MoE, fp16 out (software RNE).  The
 // (expert, step) items are split over the waves in expert order; a wave sums
-// the spans of one expert raw and folds that sum into the output with the
-// expert's row scale and route weight when its expert changes.
-template <int TR, int NWS, int UNR>
-__global__ __launch_bounds__(NWS * 64) void q4_combine_kernel(const Q4CombineArgs a) {
+// the steps of one expert raw and folds that sum into the output with the
+// expert's row scale and route weight when its expert changes.  Lanes are
+// laid out as in q4_rows_kernel.  The activations come from the fp16 planes
+// on the matrix cores, or from the fp32 vector with v_fma_mix when the planes
+// are absent or could not hold this call's values.
+template <int TR, int NWS>
+__global__ __launch_bounds__(NWS * 64) void q4_down_kernel(const Q4CombineArgs a) {
     constexpr int T = 4 * TR;
     __shared__ float red[NWS][T];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63;
-    const int grp = lane >> 4, li = lane & 15;
+    const int i16 = lane & 15, c = i16 >> 2;
+    const int piece = (i16 & 3) + 4 * (lane >> 4);
     const int64_t tile0 = static_cast<int64_t>(blockIdx.x) * T;
-    const int64_t row0 = tile0 + grp * TR;
     const int64_t row_bytes = a.K >> 1;
     const int steps = static_cast<int>((row_bytes + kStepBytes - 1) / kStepBytes);
-    const int items = steps * a.ngroups;
-    int64_t rc[TR];
+    const int ng = a.ngroups;
+    int64_t rc[TR], roff[TR];
 #pragma unroll
-    for (int t = 0; t < TR; ++t) rc[t] = row0 + t < a.rows ? row0 + t : a.rows - 1;
-    float acc[TR], part[TR];
+    for (int t = 0; t < TR; ++t) {
+        const int64_t row = tile0 + c * TR + t;
+        rc[t] = row < a.rows ? row : a.rows - 1;
+        roff[t] = rc[t] * row_bytes;
+    }
+    float tot[TR];
 #pragma unroll
-    for (int t = 0; t < TR; ++t) acc[t] = part[t] = 0.0f;
-    int gcur = -1;
-    auto fold = [&](int g) {
-        const float rw = a.route[g];
-#pragma unroll
-        for (int t = 0; t < TR; ++t) {
-            acc[t] = fmaf(part[t] * h2f_ref(a.s[g][rc[t]]), rw, acc[t]);
-            part[t] = 0.0f;
+    for (int t = 0; t < TR; ++t) tot[t] = 0.0f;
+
+    // The wave's items are (expert g, step s) = wave, wave + NWS, ... in the
+    // order g * steps + s; the walk advances (g, s) without a division and
+    // reloads an expert's pointers only when the expert changes.
+    int g = 0, s = wave;
+    while (g < ng && s >= steps) {
+        s -= steps;
+        ++g;
+    }
+    auto advance = [&]() {
+        s += NWS;
+        while (s >= steps) {
+            s -= steps;
+            ++g;
         }
     };
+    const int gl = g < ng ? g : ng - 1;  // a wave without items reads a valid address and stops below
+    const uint8_t* wg = a.w[gl];
+    uint4 q[TR];
+    auto load_w = [&](int step) {
+        const int64_t byte = static_cast<int64_t>(step) * kStepBytes + piece * 16;
+        const int64_t bc = byte < row_bytes ? byte : row_bytes - 16;
+#pragma unroll
+        for (int t = 0; t < TR; ++t) q[t] = *reinterpret_cast<const uint4*>(wg + roff[t] + bc);
+    };
+    // Keeps each path's weight arithmetic inside its branch (otherwise the
+    // compiler hoists the shared part above the branch and waits for the
+    // weights before the record is read).  Placed after each path's
+    // activation loads, so it never delays them.
+    auto pin_w = [&]() {
+#pragma unroll
+        for (int t = 0; t < TR; ++t) asm volatile("" : "+v"(q[t].x), "+v"(q[t].y), "+v"(q[t].z), "+v"(q[t].w));
+    };
+    // Both paths read the same weights: the first item's go out right after
+    // the overflow record's read, which hides that read's latency.
+    const unsigned flagged =
+        __hip_atomic_load(&g_q4_planes_overflow_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    load_w(g < ng ? s : steps - 1);
+    const bool use_planes = a.planes != nullptr && __builtin_amdgcn_readfirstlane(flagged) != a.seq;
 
-    for (int i0 = wave; i0 < items; i0 += NWS * UNR) {
-        uint4 q[UNR][TR];
+    if (use_planes) {
+        plm_f4 ah[TR], al[TR], ch = {0.0f, 0.0f, 0.0f, 0.0f}, cl = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            const int it = min(i0 + u * NWS, items - 1);
-            const int g = it / steps;
-            const int64_t byte = static_cast<int64_t>(it - g * steps) * kStepBytes + li * 16;
-            const int64_t bc = byte < row_bytes ? byte : row_bytes - 16;
+        for (int t = 0; t < TR; ++t) ah[t] = al[t] = plm_f4{0.0f, 0.0f, 0.0f, 0.0f};
+        const plm_half8 c8 = q4_mfma_c8_inplace();
+        const int e = lane & 3;
+        auto fold = [&](int ge) {
+            const float rw = a.route[ge] * 16777216.0f;
 #pragma unroll
-            for (int t = 0; t < TR; ++t) q[u][t] = *reinterpret_cast<const uint4*>(a.w[g] + rc[t] * row_bytes + bc);
-        }
-#pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            const int it = i0 + u * NWS;
-            if (it >= items) break;
-            const int g = it / steps;
-            if (g != gcur) {
-                if (gcur >= 0) fold(gcur);
-                gcur = g;
+            for (int t = 0; t < TR; ++t) {
+                const float v = (ah[t][e] - ch[e]) + (al[t][e] - cl[e]) * (1.0f / 2048.0f);
+                tot[t] = fmaf(v * h2f_ref(a.s[ge][rc[t]]), rw, tot[t]);
+                ah[t] = al[t] = plm_f4{0.0f, 0.0f, 0.0f, 0.0f};
             }
-            const int64_t byte = static_cast<int64_t>(it - g * steps) * kStepBytes + li * 16;
-            const bool ok = byte < row_bytes;
-            // step order: the i-th float4 of lane li is at step * 512 + i * 64 + li * 4
-            const float4* xp = reinterpret_cast<const float4*>(a.act + static_cast<int64_t>(g) * a.act_stride +
-                                                               static_cast<int64_t>(it - g * steps) * 512 + li * 4);
+            ch = cl = plm_f4{0.0f, 0.0f, 0.0f, 0.0f};
+        };
+        const uint4* pg = a.planes + static_cast<int64_t>(gl) * a.planes_stride;
+        bool first = true;
+        while (g < ng) {
+            if (!first) load_w(s);
+            first = false;
+            const bool ok = static_cast<int64_t>(s) * kStepBytes + piece * 16 < row_bytes;
+            const uint4* bp = pg + static_cast<int64_t>(s) * 128 + piece;
+            uint4 bv[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) bv[k] = bp[k * 16];
+            pin_w();
+            if (!ok) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) bv[k] = make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const plm_half8 bh = __builtin_bit_cast(plm_half8, bv[2 * j]);
+                const plm_half8 bl = __builtin_bit_cast(plm_half8, bv[2 * j + 1]);
+                ch = __builtin_amdgcn_mfma_f32_16x16x32_f16(c8, bh, ch, 0, 0, 0);
+                cl = __builtin_amdgcn_mfma_f32_16x16x32_f16(c8, bl, cl, 0, 0, 0);
+#pragma unroll
+                for (int t = 0; t < TR; ++t) {
+                    const uint32_t d = j == 0 ? q[t].x : j == 1 ? q[t].y : j == 2 ? q[t].z : q[t].w;
+                    const plm_half8 av = q4_mfma_a_inplace(d);
+                    ah[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bh, ah[t], 0, 0, 0);
+                    al[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bl, al[t], 0, 0, 0);
+                }
+            }
+            const int gprev = g;
+            advance();
+            if (g != gprev) {
+                fold(gprev);
+                if (g < ng) {
+                    wg = a.w[g];
+                    pg = a.planes + static_cast<int64_t>(g) * a.planes_stride;
+                }
+            }
+        }
+        // the diagonal elements of row group c sit in the quad 20c .. 20c + 3
+#pragma unroll
+        for (int t = 0; t < TR; ++t) {
+            tot[t] = PLM_DPP_ADD(tot[t], 0xB1, 0xF);
+            tot[t] = PLM_DPP_ADD(tot[t], 0x4E, 0xF);
+        }
+    } else {
+        float part[TR];
+#pragma unroll
+        for (int t = 0; t < TR; ++t) part[t] = 0.0f;
+        auto fold = [&](int ge) {
+            const float rw = a.route[ge];
+#pragma unroll
+            for (int t = 0; t < TR; ++t) {
+                tot[t] = fmaf(part[t] * h2f_ref(a.s[ge][rc[t]]), rw, tot[t]);
+                part[t] = 0.0f;
+            }
+        };
+        const float* ag = a.act + static_cast<int64_t>(gl) * a.act_stride;
+        bool first = true;
+        while (g < ng) {
+            if (!first) load_w(s);
+            first = false;
+            const bool ok = static_cast<int64_t>(s) * kStepBytes + piece * 16 < row_bytes;
+            // step order: the i-th float4 of piece p is at step * 512 + i * 64 + p * 4
+            const float4* xp = reinterpret_cast<const float4*>(ag + static_cast<int64_t>(s) * 512 + piece * 4);
+            float4 xv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xv[i] = xp[i * 16];
+            pin_w();
             float x[32], xs = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const float4 v = xp[i * 16];
-                x[4 * i] = v.x;
-                x[4 * i + 1] = v.y;
-                x[4 * i + 2] = v.z;
-                x[4 * i + 3] = v.w;
-                xs += v.x + v.y + v.z + v.w;
+                x[4 * i] = xv[i].x;
+                x[4 * i + 1] = xv[i].y;
+                x[4 * i + 2] = xv[i].z;
+                x[4 * i + 3] = xv[i].w;
+                xs += xv[i].x + xv[i].y + xv[i].z + xv[i].w;
             }
 #pragma unroll
             for (int t = 0; t < TR; ++t) {
-                const float p = q4_span_dot_f32(q[u][t], x, 8.0f * xs);
+                const float p = q4_span_dot_f32(q[t], x, 8.0f * xs);
                 part[t] += ok ? p : 0.0f;
             }
+            const int gprev = g;
+            advance();
+            if (g != gprev) {
+                fold(gprev);
+                if (g < ng) {
+                    wg = a.w[g];
+                    ag = a.act + static_cast<int64_t>(g) * a.act_stride;
+                }
+            }
+        }
+        // row group c is the 16 lanes with (lane % 16) / 4 == c
+#pragma unroll
+        for (int t = 0; t < TR; ++t) {
+            float v = tot[t];
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            v = PLM_DPP_ADD(v, 0xB1, 0xF);
+            tot[t] = PLM_DPP_ADD(v, 0x4E, 0xF);
         }
     }
-    if (gcur >= 0) fold(gcur);
+    if (lane == 20 * c) {
 #pragma unroll
-    for (int t = 0; t < TR; ++t) {
-        const float v = row16_sum(acc[t]);
-        if (li == 0) red[wave][grp * TR + t] = v;
+        for (int t = 0; t < TR; ++t) red[wave][c * TR + t] = tot[t];
     }
     __syncthreads();
     if (threadIdx.x < T) {
@@ -593,15 +739,24 @@ PLM_EXPORT int q4_moe_selected_forward_u16(const uint16_t* hidden, const uint8_t
     // 256-byte aligned, so only the down weights and I decide.
     const bool fast2 = q4_weights_ok(I, dl.data(), static_cast<int>(S));
     const int64_t stride = fast2 ? plm::ceil_div(I, 512) * 512 : I;
-    float* act = static_cast<float*>(plm::workspace(static_cast<size_t>(S * stride) * sizeof(float)));
-    if (act == nullptr) return 2;
-    // Phase 1, groups of up to kMaxGroups experts.
     std::vector<const uint8_t*> wl;
     for (int64_t e = 0; e < S; ++e) {
         wl.push_back(gate_packed_ptrs[e]);
         wl.push_back(up_packed_ptrs[e]);
     }
     const bool fast1 = q4_fast_ok(H, hidden, wl.data(), static_cast<int>(wl.size()));
+    // With both fast paths the gate/up kernel also writes the activations as
+    // fp16 B planes for the matrix-core down phase (same size as the fp32
+    // vector, after it in the workspace).
+    const bool planes = fast1 && fast2;
+    const int64_t planes_stride = stride / 4;  // uint4 per expert
+    float* act = static_cast<float*>(plm::workspace(static_cast<size_t>(S * stride) * sizeof(float) * (planes ? 2 : 1)));
+    if (act == nullptr) return 2;
+    uint4* bplanes = planes ? reinterpret_cast<uint4*>(act + S * stride) : nullptr;
+    static std::atomic<unsigned> call_seq{0};
+    unsigned seq = ++call_seq;
+    if (seq == 0) seq = ++call_seq;  // 0 is the record's initial value
+    // Phase 1, groups of up to kMaxGroups experts.
     for (int64_t g0 = 0; g0 < S; g0 += kMaxGroups) {
         const int ng = static_cast<int>(std::min<int64_t>(kMaxGroups, S - g0));
         Q4RowsArgs a;
@@ -618,6 +773,9 @@ PLM_EXPORT int q4_moe_selected_forward_u16(const uint16_t* hidden, const uint8_t
         a.K = H;
         a.out_stride = stride;
         a.out_steps = fast2 ? 1 : 0;
+        a.planes = planes ? bplanes + g0 * planes_stride : nullptr;
+        a.planes_stride = planes_stride;
+        a.seq = seq;
         if (fast1) {
             launch_q4_rows<2, 2, 4, true>(a, ng, st);
         } else {
@@ -637,16 +795,17 @@ PLM_EXPORT int q4_moe_selected_forward_u16(const uint16_t* hidden, const uint8_t
     }
     c.act = act;
     c.act_stride = stride;
+    c.planes = bplanes;
+    c.planes_stride = planes_stride;
+    c.seq = seq;
     c.route = route_weights;
     c.out_f16 = out_fp16;
     c.rows = H;
     c.K = I;
     c.ngroups = static_cast<int>(S);
     if (fast2) {
-        // 4 rows per lane group: each lane's 128-byte read of the fp32
-        // activations feeds four rows.  8-wave groups keep two groups per CU
-        // (the kernel needs more than 64 VGPRs).
-        hipLaunchKernelGGL((q4_combine_kernel<4, 8, 1>), dim3(static_cast<unsigned>(plm::ceil_div(H, 16))),
+        // 4 rows per lane group: each lane's activation read feeds four rows.
+        hipLaunchKernelGGL((q4_down_kernel<4, 8>), dim3(static_cast<unsigned>(plm::ceil_div(H, 16))),
                            dim3(8 * plm::kWave), 0, st, c);
     } else {
         hipLaunchKernelGGL(q4_combine_scalar_kernel, dim3(static_cast<unsigned>(plm::ceil_div(H, 256))), dim3(256), 0,

@@ -116,6 +116,58 @@ def test_q4_mlp_qwen_shape_vs_oracle(nat, oracle_mod):
     assert rel_l2(host(out).astype(np.float32), want.view(np.float16).astype(np.float32)) < 1e-3
 
 
+def _q4_moe_case(oracle_mod, H, I, S, seed, gate_std=0.02, down_std=0.02):
+    experts = []
+    for e in range(S):
+        g = q4_matrix(oracle_mod, I, H, seed + 3 * e, std=gate_std)
+        u = q4_matrix(oracle_mod, I, H, seed + 3 * e + 1, std=gate_std)
+        d = q4_matrix(oracle_mod, H, I, seed + 3 * e + 2, std=down_std)
+        experts.append((g[0], g[1], u[0], u[1], d[0], d[1]))
+    x16 = np.random.default_rng(seed).standard_normal(H).astype(np.float16)
+    route = np.random.default_rng(seed + 1).random(S).astype(np.float32) + 0.1
+    return experts, x16, route
+
+
+def _run_q4_moe(nat, experts, x16, route, H, I):
+    dexp = [tuple(dev(a) if i % 2 == 0 else dev(a).view(torch.float16) for i, a in enumerate(e)) for e in experts]
+    out = nat.q4_moe_selected_forward_u16(dev(x16), dexp, dev(route), hidden_size=H, intermediate_size=I)
+    return host(out).astype(np.float32)
+
+
+def test_q4_moe_multi_expert_partial_step(nat, oracle_mod):
+    # three experts (the down phase folds each expert's sum with its scale and
+    # route weight) and I = 1568, whose last 512-value step is one 32-value piece
+    H, I, S = 1024, 1568, 3
+    experts, x16, route = _q4_moe_case(oracle_mod, H, I, S, 61)
+    got = _run_q4_moe(nat, experts, x16, route, H, I)
+    want = oracle_mod.q4_moe_selected(x16.view(np.uint16), experts, route, H, I).view(np.float16).astype(np.float32)
+    assert rel_l2(got, want) < 1e-3
+
+
+def test_q4_moe_intermediate_beyond_fp16_takes_exact_path(nat, oracle_mod):
+    # Large gate/up weights push silu(gate) * up past the fp16 range (the
+    # matrix-core down phase reads the intermediate as fp16 planes); tiny down
+    # weights keep the fp16 output finite.  The call must fall back to the fp32
+    # intermediate, and the next ordinary call must still be right.
+    H, I, S = 512, 1024, 2
+    experts, x16, route = _q4_moe_case(oracle_mod, H, I, S, 71, gate_std=50.0, down_std=1e-5)
+    acts = []
+    for g_p, g_s, u_p, u_s, _d, _ds in experts:
+        gate = oracle_mod.q4_gemv(g_p, g_s, x16.astype(np.float32), I, H)
+        up = oracle_mod.q4_gemv(u_p, u_s, x16.astype(np.float32), I, H)
+        with np.errstate(over="ignore"):
+            acts.append(gate / (1.0 + np.exp(-gate.astype(np.float64))) * up)
+    assert max(np.abs(a).max() for a in acts) > 65504.0
+    want = oracle_mod.q4_moe_selected(x16.view(np.uint16), experts, route, H, I).view(np.float16).astype(np.float32)
+    assert np.isfinite(want).all()
+    got = _run_q4_moe(nat, experts, x16, route, H, I)
+    assert rel_l2(got, want) < 1e-3
+    experts2, x2, route2 = _q4_moe_case(oracle_mod, H, I, S, 81)
+    got2 = _run_q4_moe(nat, experts2, x2, route2, H, I)
+    want2 = oracle_mod.q4_moe_selected(x2.view(np.uint16), experts2, route2, H, I).view(np.float16).astype(np.float32)
+    assert rel_l2(got2, want2) < 1e-3
+
+
 # --------------------------------------------------------------------------- row8
 
 def test_row8_pack_golden_and_full(nat, golden, oracle_mod):
