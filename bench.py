@@ -125,8 +125,10 @@ def fp8_bytes(rows, cols, m):
 def mlp_bytes(hidden, inter):
     """Algorithmic HBM bytes of one Q4 SwiGLU MLP call: the three packed
     matrices and their fp16 row scales, the fp16 input and output, and the
-    fp32 intermediate written by the gate/up kernel and read by the down
-    kernel."""
+    intermediate written once by the gate/up kernel and read once by the down
+    kernel (4 bytes per value each way).  The implementation also keeps an
+    fp32 copy of the intermediate for its exact fallback; those bytes show up
+    in the measured traffic, not here."""
     weights = 3 * hidden * inter // 2
     scales = 2 * (2 * inter + hidden)
     return weights + scales + 2 * hidden + 2 * hidden + 2 * 4 * inter
@@ -243,7 +245,7 @@ def main_line(args):
     # then down); the roofline is taken over both, from the same events.
     roof = {
         "bound": "hbm",
-        "kernel": "q4_rows_kernel (gate/up + SiLU) + q4_combine_kernel (down), one MLP call",
+        "kernel": "q4_rows_kernel (gate/up + SiLU) + q4_down_kernel (down + combine), one MLP call",
         "achieved": round(value, 2),
         "peak": PEAK_HBM_GBS,
         "unit": "GB/s",
