@@ -153,6 +153,26 @@ __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
             float sc[NWT];
 #pragma unroll
             for (int i = 0; i < NWT; ++i) sc[i] = S[i][srow + (col >> 7)];
+            if constexpr (M == 1) {
+                // one activation row: decode each weight row right before its
+                // dot, so a larger tile needs no more registers (same arithmetic)
+                float xv[16];
+                load_x16(a.x + static_cast<int64_t>(a.m0) * a.x_stride + col, xv);
+#pragma unroll
+                for (int i = 0; i < NWT; ++i)
+#pragma unroll
+                    for (int r = 0; r < TR; ++r) {
+                        float w16[16];
+                        decode16(q[i][r], w16);
+                        float p = dot16(w16, xv);
+                        if (p != p) {
+                            zero_nans16(w16);
+                            p = dot16(w16, xv);
+                        }
+                        acc[i][r][0] = fmaf(p, sc[i], acc[i][r][0]);
+                    }
+                continue;
+            }
             float wv[NWT][TR][16];
 #pragma unroll
             for (int i = 0; i < NWT; ++i)
@@ -258,6 +278,25 @@ __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
             q[r] = *reinterpret_cast<const uint4*>(W + rr * a.K + col);
         }
         const float sc = S[(row0 >> 7) * a.scale_cols + (col >> 7)];
+        if constexpr (M == 1) {
+            // one activation row: decode each weight row right before its dot,
+            // so a larger tile needs no more registers (same arithmetic)
+            if (a.zero_skip && rw[0] == 0.0f) continue;
+            float xv[16];
+            load_x16(a.act + (static_cast<int64_t>(a.g_base + g) * a.m_total + a.m0) * a.K + col, xv);
+#pragma unroll
+            for (int r = 0; r < TR; ++r) {
+                float w16[16];
+                decode16(q[r], w16);
+                float p = dot16(w16, xv);
+                if (p != p) {
+                    zero_nans16(w16);
+                    p = dot16(w16, xv);
+                }
+                acc[r][0] = fmaf(p * sc, rw[0], acc[r][0]);
+            }
+            continue;
+        }
         float wv[TR][16];
 #pragma unroll
         for (int r = 0; r < TR; ++r) decode16(q[r], wv[r]);
@@ -401,9 +440,14 @@ int waves_for(int64_t nchunks) {
     return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(nchunks, kMaxWaves)));
 }
 
-// Rows per tile: 4 for one weight, fewer when two weights or many activation
-// rows would need too many accumulators (the per-row arithmetic does not
-// depend on this choice).
+// Rows per tile.  The per-row arithmetic does not depend on it, so it is
+// chosen per launch: at one activation row (where each weight row is decoded
+// right before its dot) 8 rows halve the activation reads per weight byte,
+// used when the grid still has at least kTileWaves waves; otherwise 4 for one
+// weight, fewer when two weights or many activation rows would need too many
+// accumulators.
+constexpr int64_t kTileWaves = 4096;
+
 template <int M>
 constexpr int rows_tile(int nwt) {
     return nwt == 1 ? 4 : (M == 1 ? 4 : 2);
@@ -414,15 +458,29 @@ constexpr int combine_tile() {
     return 4;
 }
 
-template <int M, int NWT, bool SILU>
-void launch_rows_m(const RowsArgs& a, int ngroups, hipStream_t st) {
-    constexpr int TR = rows_tile<M>(NWT);
+bool wide_tile_fits(int64_t rows, int64_t groups, int nw) {
+    return plm::ceil_div(rows, 8) * groups * nw >= kTileWaves;
+}
+
+template <int M, int TR, int NWT, bool SILU>
+void launch_rows_tr(const RowsArgs& a, int ngroups, hipStream_t st) {
     RowsArgs b = a;
     b.tiles_per_group = static_cast<int>(plm::ceil_div(a.rows, TR));
     const int nw = waves_for(a.nchunks);
     const int64_t grid = static_cast<int64_t>(b.tiles_per_group) * ngroups;
     hipLaunchKernelGGL((fp8_rows_kernel<M, TR, NWT, SILU>), dim3(static_cast<unsigned>(grid)),
                        dim3(nw * plm::kWave), 0, st, b);
+}
+
+template <int M, int NWT, bool SILU>
+void launch_rows_m(const RowsArgs& a, int ngroups, hipStream_t st) {
+    if constexpr (M == 1 && NWT == 1) {
+        if (wide_tile_fits(a.rows, ngroups, waves_for(a.nchunks))) {
+            launch_rows_tr<1, 8, 1, SILU>(a, ngroups, st);
+            return;
+        }
+    }
+    launch_rows_tr<M, rows_tile<M>(NWT), NWT, SILU>(a, ngroups, st);
 }
 
 template <int NWT, bool SILU>
@@ -439,9 +497,8 @@ void launch_rows(const RowsArgs& a, int mcount, int ngroups, hipStream_t st) {
     }
 }
 
-template <int M>
-void launch_combine_m(const CombineArgs& a, hipStream_t st) {
-    constexpr int TR = combine_tile<M>();
+template <int M, int TR>
+void launch_combine_tr(const CombineArgs& a, hipStream_t st) {
     CombineArgs b = a;
     const int tiles = static_cast<int>(plm::ceil_div(a.rows, TR));
     b.tiles_per_group = tiles;
@@ -450,6 +507,18 @@ void launch_combine_m(const CombineArgs& a, hipStream_t st) {
     const int64_t grid = static_cast<int64_t>(tiles) * (a.per_group_out ? a.ngroups : 1);
     hipLaunchKernelGGL((fp8_combine_kernel<M, TR>), dim3(static_cast<unsigned>(grid)),
                        dim3(nw * plm::kWave), 0, st, b);
+}
+
+template <int M>
+void launch_combine_m(const CombineArgs& a, hipStream_t st) {
+    if constexpr (M == 1) {
+        const int64_t segs = a.per_group_out ? 1 : a.ngroups;
+        if (wide_tile_fits(a.rows, a.per_group_out ? a.ngroups : 1, waves_for(segs * a.cps))) {
+            launch_combine_tr<1, 8>(a, st);
+            return;
+        }
+    }
+    launch_combine_tr<M, combine_tile<M>()>(a, st);
 }
 
 void launch_combine(const CombineArgs& a, int mcount, hipStream_t st) {
