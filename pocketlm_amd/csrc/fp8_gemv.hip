@@ -173,6 +173,36 @@ __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
                     }
                 continue;
             }
+            if constexpr (TR >= 8) {
+                // wide tiles with several activation rows: each weight row is
+                // decoded again for every activation row (registers for one
+                // decoded row only), halving the activation reads per weight
+                // byte; a NaN span is redone with NaN bytes as 0, which equals
+                // using the sanitised row for every activation row.
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    float xv[16];
+                    load_x16(a.x + static_cast<int64_t>(a.m0 + m) * a.x_stride + col, xv);
+#pragma unroll
+                    for (int i = 0; i < NWT; ++i)
+#pragma unroll
+                        for (int r = 0; r < TR; ++r) {
+                            // opaque copy: the compiler would otherwise keep
+                            // every decoded row live across the activation rows
+                            uint4 qq = q[i][r];
+                            asm volatile("" : "+v"(qq.x), "+v"(qq.y), "+v"(qq.z), "+v"(qq.w));
+                            float w16[16];
+                            decode16(qq, w16);
+                            float p = dot16(w16, xv);
+                            if (p != p) {
+                                zero_nans16(w16);
+                                p = dot16(w16, xv);
+                            }
+                            acc[i][r][m] = fmaf(p, sc[i], acc[i][r][m]);
+                        }
+                }
+                continue;
+            }
             float wv[NWT][TR][16];
 #pragma unroll
             for (int i = 0; i < NWT; ++i)
@@ -441,11 +471,11 @@ int waves_for(int64_t nchunks) {
 }
 
 // Rows per tile.  The per-row arithmetic does not depend on it, so it is
-// chosen per launch: at one activation row (where each weight row is decoded
-// right before its dot) 8 rows halve the activation reads per weight byte,
-// used when the grid still has at least kTileWaves waves; otherwise 4 for one
-// weight, fewer when two weights or many activation rows would need too many
-// accumulators.
+// chosen per launch: at one or two activation rows (where each weight row is
+// decoded right before its dot) 8 rows halve the activation reads per weight
+// byte, used when the grid still has at least kTileWaves waves; otherwise 4
+// for one weight, fewer when two weights or many activation rows would need
+// too many accumulators.
 constexpr int64_t kTileWaves = 4096;
 
 template <int M>
@@ -474,9 +504,11 @@ void launch_rows_tr(const RowsArgs& a, int ngroups, hipStream_t st) {
 
 template <int M, int NWT, bool SILU>
 void launch_rows_m(const RowsArgs& a, int ngroups, hipStream_t st) {
-    if constexpr (M == 1 && NWT == 1) {
+    // (at three or more activation rows the wide tile's re-decoding and
+    // registers cost more than the activation reads it saves)
+    if constexpr (NWT == 1 && M <= 2) {
         if (wide_tile_fits(a.rows, ngroups, waves_for(a.nchunks))) {
-            launch_rows_tr<1, 8, 1, SILU>(a, ngroups, st);
+            launch_rows_tr<M, 8, 1, SILU>(a, ngroups, st);
             return;
         }
     }
