@@ -236,12 +236,13 @@ __device__ __forceinline__ plm_half8 q4_mfma_c8_inplace() {
 // plane 0 is hi = fp16(v') and plane 1 is lo = fp16((v' - hi) * 2^11), so
 // hi + lo * 2^-11 carries 22 significant bits (the split follows the /16, so
 // no bits are lost to it).  A value that fp16 cannot hold (|v| >= 65504, inf,
-// NaN) records the call's sequence number here, and that call's down phase
-// reads the fp32 activations instead.
-__device__ unsigned g_q4_planes_overflow_seq = 0;
-
-__device__ __forceinline__ void q4_store_planes(uint4* base, int64_t k, float v, unsigned seq) {
-    if (!(fabsf(v) < 65504.0f)) atomicExch(&g_q4_planes_overflow_seq, seq);
+// NaN) records the call's sequence number in a word of the stream's
+// workspace, and that call's down phase reads the fp32 activations instead.
+// Calls on one stream are ordered, and each stream has its own workspace, so
+// concurrent calls cannot overwrite each other's record; a stale word can
+// only equal a later call's number by chance, which selects the exact path.
+__device__ __forceinline__ void q4_store_planes(uint4* base, int64_t k, float v, unsigned seq, unsigned* record) {
+    if (!(fabsf(v) < 65504.0f)) atomicExch(record, seq);
     const int64_t s = k >> 9;
     const int p = static_cast<int>((k >> 5) & 15), j = static_cast<int>((k >> 3) & 3), n = static_cast<int>(k & 7);
     const float vs = (n & 1) ? v * 0.0625f : v;
@@ -265,6 +266,7 @@ struct Q4RowsArgs {
     uint4* planes;        // SILU only: also write the fp16 B planes (nullptr: no)
     int64_t planes_stride;  // uint4 per group
     unsigned seq;         // call sequence number for the overflow record
+    unsigned* overflow;   // the overflow record (with planes)
 };
 
 // Position of value k of an fp32 activation vector stored in "step order":
@@ -369,7 +371,7 @@ __global__ __launch_bounds__(NWS * 64) void q4_rows_kernel(const Q4RowsArgs a) {
             if constexpr (SILU) {
                 const float act = plm_silu_mul(v[0], v[1]);
                 a.out[o] = act;
-                if (a.planes != nullptr) q4_store_planes(a.planes + g * a.planes_stride, row, act, a.seq);
+                if (a.planes != nullptr) q4_store_planes(a.planes + g * a.planes_stride, row, act, a.seq, a.overflow);
             } else {
                 a.out[o] = v[0];
             }
@@ -385,6 +387,7 @@ struct Q4CombineArgs {
     const uint4* planes;  // [ngroups][planes_stride] fp16 B planes, or nullptr
     int64_t planes_stride;
     unsigned seq;
+    unsigned* overflow;   // the overflow record (with planes)
     const float* route;   // [ngroups]
     uint16_t* out_f16;    // [rows]
     int64_t rows;
@@ -457,7 +460,7 @@ __global__ __launch_bounds__(NWS * 64) void q4_down_kernel(const Q4CombineArgs a
     // Both paths read the same weights: the first item's go out right after
     // the overflow record's read, which hides that read's latency.
     const unsigned flagged =
-        __hip_atomic_load(&g_q4_planes_overflow_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        a.planes != nullptr ? __hip_atomic_load(a.overflow, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
     load_w(g < ng ? s : steps - 1);
     const bool use_planes = a.planes != nullptr && __builtin_amdgcn_readfirstlane(flagged) != a.seq;
 
@@ -750,8 +753,12 @@ PLM_EXPORT int q4_moe_selected_forward_u16(const uint16_t* hidden, const uint8_t
     // vector, after it in the workspace).
     const bool planes = fast1 && fast2;
     const int64_t planes_stride = stride / 4;  // uint4 per expert
-    float* act = static_cast<float*>(plm::workspace(static_cast<size_t>(S * stride) * sizeof(float) * (planes ? 2 : 1)));
-    if (act == nullptr) return 2;
+    // workspace: [256-byte header holding the overflow record][fp32 act][planes]
+    char* ws = static_cast<char*>(
+        plm::workspace(256 + static_cast<size_t>(S * stride) * sizeof(float) * (planes ? 2 : 1)));
+    if (ws == nullptr) return 2;
+    unsigned* overflow = reinterpret_cast<unsigned*>(ws);
+    float* act = reinterpret_cast<float*>(ws + 256);
     uint4* bplanes = planes ? reinterpret_cast<uint4*>(act + S * stride) : nullptr;
     static std::atomic<unsigned> call_seq{0};
     unsigned seq = ++call_seq;
@@ -776,6 +783,7 @@ PLM_EXPORT int q4_moe_selected_forward_u16(const uint16_t* hidden, const uint8_t
         a.planes = planes ? bplanes + g0 * planes_stride : nullptr;
         a.planes_stride = planes_stride;
         a.seq = seq;
+        a.overflow = overflow;
         if (fast1) {
             launch_q4_rows<2, 2, 4, true>(a, ng, st);
         } else {
@@ -798,6 +806,7 @@ PLM_EXPORT int q4_moe_selected_forward_u16(const uint16_t* hidden, const uint8_t
     c.planes = bplanes;
     c.planes_stride = planes_stride;
     c.seq = seq;
+    c.overflow = overflow;
     c.route = route_weights;
     c.out_f16 = out_fp16;
     c.rows = H;
