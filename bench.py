@@ -457,6 +457,94 @@ def table(args):
         del packs
         torch.cuda.empty_cache()
 
+    # ---- row8 dense decode layer (config 3) as the decode calls it: q/k/v in one
+    # launch, o on the fp32 attention output, gate/up in one launch, down on the
+    # fp32 intermediate (Qwen2.5-7B: 466 MB of packed weights per layer)
+    H, I, KV = 3584, 18944, 512
+    shapes = {"q": (H, H), "k": (KV, H), "v": (KV, H), "o": (H, H), "gate": (I, H), "up": (I, H), "down": (H, I)}
+
+    def packed(rows, cols):
+        w = torch.randn((rows, cols), generator=gen, device="cuda").mul_(0.02).to(torch.float16)
+        p = native.pack_weight_rows8(w)
+        del w
+        return p
+
+    dense = [{k: packed(*v) for k, v in shapes.items()} for _ in range(3)]  # 3 x 466 MB
+    h16 = torch.randn((H,), generator=gen, device="cuda").to(torch.float16)
+    attn = torch.randn((H,), generator=gen, device="cuda")
+    act = torch.randn((I,), generator=gen, device="cuda")
+    outs = {k: torch.empty((v[0],), device="cuda") for k, v in shapes.items()}
+    lib.pocketlm_set_stream(_stream_ptr(torch))
+
+    def many(layer, names):
+        pp = (ctypes.c_void_p * len(names))(*[layer[n].data_ptr() for n in names])
+        bp = (ctypes.c_void_p * len(names))()
+        op = (ctypes.c_void_p * len(names))(*[outs[n].data_ptr() for n in names])
+        rr = (ctypes.c_longlong * len(names))(*[shapes[n][0] for n in names])
+        keep = (pp, bp, op, rr)
+        return lambda keep=keep: lib.native_packed_gemv_rows8_many(
+            ctypes.c_void_p(h16.data_ptr()), ctypes.cast(keep[0], ctypes.c_void_p), ctypes.cast(keep[1], ctypes.c_void_p),
+            ctypes.cast(keep[2], ctypes.c_void_p), ctypes.cast(keep[3], ctypes.c_void_p), len(names), H, 0)
+
+    def f32x(layer, name, x):
+        rows, cols = shapes[name]
+        return lambda: lib.native_packed_gemv_rows8_f32_hidden(ctypes.c_void_p(x.data_ptr()),
+                                                               ctypes.c_void_p(layer[name].data_ptr()),
+                                                               ctypes.c_void_p(outs[name].data_ptr()), rows, cols, 0)
+
+    def wbytes(names):
+        return sum(2 * math.ceil(shapes[n][0] / 8) * 8 * shapes[n][1] + 4 * shapes[n][0] for n in names)
+
+    host = {k: dense[0][k].cpu().view(torch.int16).numpy().view(np.uint16) for k in shapes}
+    hh16 = h16.cpu().view(torch.int16).numpy().view(np.uint16)
+    hattn, hact = attn.cpu().numpy(), act.cpu().numpy()
+
+    def cpu_many(names):
+        return lambda: [oracle.packed_gemv_rows8(hh16, host[n], shapes[n][0], shapes[n][1], 0) for n in names]
+
+    measure("row8 q/k/v (one launch)", 1, lambda: [many(l, ["q", "k", "v"]) for l in dense],
+            wbytes(["q", "k", "v"]) + 2 * H, cpu_many(["q", "k", "v"]))
+    measure("row8 gate/up (one launch)", 1, lambda: [many(l, ["gate", "up"]) for l in dense],
+            wbytes(["gate", "up"]) + 2 * H, cpu_many(["gate", "up"]))
+
+    def layer_calls():
+        out = []
+        for l in dense:
+            out += [many(l, ["q", "k", "v"]), f32x(l, "o", attn), many(l, ["gate", "up"]), f32x(l, "down", act)]
+        return out
+
+    def cpu_layer():
+        cpu_many(["q", "k", "v"])()
+        oracle.packed_gemv_rows8_f32_hidden(hattn, host["o"], H, H, 0)
+        cpu_many(["gate", "up"])()
+        oracle.packed_gemv_rows8_f32_hidden(hact, host["down"], H, I, 0)
+
+    layer_bytes = wbytes(list(shapes)) + 2 * H * 2 + 4 * H + 4 * I
+    calls = layer_calls()
+    for fn in calls:
+        fn()
+    torch.cuda.synchronize()
+    launches = [calls[i % len(calls)] for i in range(4 * 30)]
+    med = timer.run(launches) / 30
+    gbs = layer_bytes / (med / 1e3) / 1e9
+    cpu_us = cpu_gbs = None
+    if not args.no_cpu:
+        t0 = time.perf_counter()
+        n = 0
+        while True:
+            cpu_layer()
+            n += 1
+            if time.perf_counter() - t0 > 1.5:
+                break
+        cpu_us = (time.perf_counter() - t0) / n * 1e6
+        cpu_gbs = layer_bytes / (cpu_us / 1e6) / 1e9
+    print(f"{'row8 dense layer (4 launches)':40s} M=1  {1e3 * med:9.2f} us  {gbs:8.1f} GB/s  "
+          f"{100 * gbs / PEAK_HBM_GBS:5.1f}%", flush=True)
+    rows_out.append(("row8 dense layer (4 launches)", 1, 1e3 * med, gbs, 100 * gbs / PEAK_HBM_GBS, cpu_us, cpu_gbs,
+                     "port"))
+    del dense, host
+    torch.cuda.empty_cache()
+
     # ---- DeepSeek-V3 MoE layer decode (config 4): 8 routed (weighted) + shared MLP
     def expert():
         g = fp8_sets(2048, 7168, 1)[0]
