@@ -16,6 +16,8 @@
 
 namespace {
 
+constexpr int kSegCols = 8192;  // columns of one row per workgroup
+
 __device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
 __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 
@@ -78,38 +80,50 @@ __device__ __forceinline__ void deq4(uint32_t d, float sc, bool exact, uint32_t*
     }
 }
 
-// One workgroup covers 4096 columns of one row.  For 16-bit outputs a lane
-// reads 8 bytes and writes 16, for fp32 it reads 4 and writes 16, so every
-// wave-wide store is 1 KB contiguous.  Finite spans take the plain
+// One workgroup covers kSegCols columns of one row.  For 16-bit outputs a lane
+// reads 8 bytes and writes 16 per pass, for fp32 it reads 4 and writes 16,
+// so every wave-wide store is 1 KB contiguous.  All passes' loads are issued
+// first (addresses past the row end are clamped and their results dropped),
+// so a workgroup waits for memory once.  Finite spans take the plain
 // multiply; spans holding a NaN byte (or a non-finite scale) take the exact
 // x86 emulation.
 template <int OUT>
 __global__ __launch_bounds__(256) void fp8_dequant_kernel(const uint8_t* __restrict__ w, const float* __restrict__ s,
                                                           void* __restrict__ out, int64_t cols, int64_t scale_cols,
                                                           int segs_per_row) {
-    constexpr int BPL = OUT == 2 ? 4 : 8;        // input bytes per lane per pass
-    constexpr int PASSES = 4096 / (256 * BPL);   // 4 (fp32) or 2 (16-bit)
+    constexpr int BPL = OUT == 2 ? 4 : 8;          // input bytes per lane per pass
+    constexpr int PASSES = kSegCols / (256 * BPL);  // 8 (fp32) or 4 (16-bit)
     const int64_t row = blockIdx.x / segs_per_row;
     const int seg = blockIdx.x - static_cast<int>(row) * segs_per_row;
     const float* srow = s + (row >> 7) * scale_cols;
+    int64_t col[PASSES];
+    uint2 d[PASSES];
+    float sc[PASSES];
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
-        const int64_t col = static_cast<int64_t>(seg) * 4096 + (p * 256 + threadIdx.x) * BPL;
-        if (col >= cols) break;
-        const int64_t idx = row * cols + col;
-        const float sc = srow[col >> 7];
-        const bool sc_finite = (f2u(sc) & 0x7F800000u) != 0x7F800000u;
+        col[p] = static_cast<int64_t>(seg) * kSegCols + (p * 256 + threadIdx.x) * BPL;
+        const int64_t cc = col[p] < cols ? col[p] : cols - BPL;
         if constexpr (OUT == 2) {
-            const uint32_t d = *reinterpret_cast<const uint32_t*>(w + idx);
+            d[p].x = *reinterpret_cast<const uint32_t*>(w + row * cols + cc);
+        } else {
+            d[p] = *reinterpret_cast<const uint2*>(w + row * cols + cc);
+        }
+        sc[p] = srow[cc >> 7];
+    }
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+        if (col[p] >= cols) break;
+        const int64_t idx = row * cols + col[p];
+        const bool sc_finite = (f2u(sc[p]) & 0x7F800000u) != 0x7F800000u;
+        if constexpr (OUT == 2) {
             uint32_t b[4];
-            deq4(d, sc, !sc_finite || has_nan_byte(d), b);
+            deq4(d[p].x, sc[p], !sc_finite || has_nan_byte(d[p].x), b);
             *reinterpret_cast<uint4*>(static_cast<float*>(out) + idx) = make_uint4(b[0], b[1], b[2], b[3]);
         } else {
-            const uint2 d = *reinterpret_cast<const uint2*>(w + idx);
-            const bool exact = !sc_finite || has_nan_byte(d.x) || has_nan_byte(d.y);
+            const bool exact = !sc_finite || has_nan_byte(d[p].x) || has_nan_byte(d[p].y);
             uint32_t b[8];
-            deq4(d.x, sc, exact, b);
-            deq4(d.y, sc, exact, b + 4);
+            deq4(d[p].x, sc[p], exact, b);
+            deq4(d[p].y, sc[p], exact, b + 4);
             uint32_t h[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) h[i] = out_bits16<OUT>(b[2 * i]) | (out_bits16<OUT>(b[2 * i + 1]) << 16);
@@ -142,7 +156,7 @@ int dequant(const uint8_t* w, const float* s, void* out, int64_t rows, int64_t c
     if (scale_cols != plm::ceil_div(cols, 128)) return plm::fail(-3, "scale_cols != ceil(cols/128)");
     hipStream_t st = plm::current_stream();
     if (cols % 16 == 0 && plm::aligned16(w) && plm::aligned16(out)) {
-        const int64_t segs = plm::ceil_div(cols, 4096);
+        const int64_t segs = plm::ceil_div(cols, kSegCols);
         const int64_t grid = rows * segs;
         if (grid > 0x7FFFFFFF) return plm::fail(-2, "tensor too large");
         hipLaunchKernelGGL((fp8_dequant_kernel<OUT>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, st, w, s, out,
