@@ -560,31 +560,21 @@ def table(args):
     y = torch.empty((1, 7168), device="cuda")
     ys = torch.empty((1, 7168), device="cuda")
     lib.pocketlm_set_stream(_stream_ptr(torch))
-    moe_calls = []
-    for layer in layers:
-        routed = layer[:8]
-        tables = [(ctypes.c_uint64 * 8)(*[t[i].data_ptr() for t in routed]) for i in range(6)]
-        sh = layer[8]
-        moe_calls.append((tables, sh))
-
-    def moe_launches():
-        out = []
-        for tables, sh in moe_calls:
-            out.append(lambda t=tables: lib.fp8_e4m3_block_mlp_many_weighted_f32(
-                *[ctypes.cast(a, ctypes.c_void_p) for a in t], ctypes.c_void_p(x.data_ptr()),
-                ctypes.c_void_p(rw.data_ptr()), ctypes.c_void_p(y.data_ptr()), 8, 1, 2048, 7168, 56, 16))
-            out.append(lambda sh=sh: lib.fp8_e4m3_block_mlp_f32(
-                *[ctypes.c_void_p(t.data_ptr()) for t in sh], ctypes.c_void_p(x.data_ptr()),
-                ctypes.c_void_p(ys.data_ptr()), 1, 2048, 7168, 56, 16))
-        return out
+    # one call per layer: the 8 routed experts (route-weighted sum) and the
+    # shared expert (its own output) in one gate/up and one down launch
+    moe_tables = [[(ctypes.c_uint64 * 9)(*[t[i].data_ptr() for t in layer]) for i in range(6)] for layer in layers]
+    calls = [lambda t=tables: lib.fp8_e4m3_block_mlp_many_weighted_shared_f32(
+        *[ctypes.cast(a, ctypes.c_void_p) for a in t], ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(rw.data_ptr()),
+        ctypes.c_void_p(y.data_ptr()), ctypes.c_void_p(ys.data_ptr()), 8, 1, 2048, 7168, 56, 16)
+        for tables in moe_tables]
 
     per_expert = 3 * 2048 * 7168 + 3 * 4 * 16 * 56
-    calls = moe_launches()
     for fn in calls:
-        fn()
+        if fn() != 0:
+            raise RuntimeError("fp8_e4m3_block_mlp_many_weighted_shared_f32 failed")
     torch.cuda.synchronize()
-    launches = [calls[i % len(calls)] for i in range(60)]
-    med = timer.run(launches) / (len(launches) // 2)
+    launches = [calls[i % len(calls)] for i in range(30)]
+    med = timer.run(launches) / len(launches)
     nbytes = 9 * per_expert + 2 * 7168 * 4
     gbs = nbytes / (med / 1e3) / 1e9
     print(f"{'ds-v3 MoE layer (8 routed + shared)':40s} M=1  {1e3 * med:9.2f} us  {gbs:8.1f} GB/s  "

@@ -135,6 +135,23 @@ int fp8_e4m3_block_mlp_many_weighted_f32(
     int64_t intermediate_rows, int64_t hidden_cols, int64_t gate_scale_cols,
     int64_t down_scale_cols);
 
+/* No single reference counterpart: the pair of calls run_fp8_moe makes at
+ * one token (fp8_source.py:1643-1646 -> fp8_linear.cpp:475-589 for the
+ * routed experts, fp8_source.py:1849-1859 -> fp8_linear.cpp:212-362 for the
+ * shared expert) in two launches instead of four.  The six tables hold
+ * expert_count routed experts followed by the shared expert (same shapes);
+ * out gets the routed sum as fp8_e4m3_block_mlp_many_weighted_f32 computes
+ * it, out_shared the shared expert's MLP as fp8_e4m3_block_mlp_f32 computes
+ * it (the same per-row arithmetic, so the same values).  Returns -2 for more
+ * than 63 routed experts. */
+int fp8_e4m3_block_mlp_many_weighted_shared_f32(
+    const uint64_t* gate_weight_ptrs, const uint64_t* gate_scale_ptrs,
+    const uint64_t* up_weight_ptrs, const uint64_t* up_scale_ptrs,
+    const uint64_t* down_weight_ptrs, const uint64_t* down_scale_ptrs, const float* hidden,
+    const float* route_weights, float* out, float* out_shared, int64_t expert_count, int64_t batch,
+    int64_t intermediate_rows, int64_t hidden_cols, int64_t gate_scale_cols,
+    int64_t down_scale_cols);
+
 /* fp8_linear_avx512.cpp:252-371: same kernel as the weighted entry point */
 int fp8_e4m3_block_mlp_many_weighted_avx512_f32(
     const uint64_t* gate_weight_ptrs, const uint64_t* gate_scale_ptrs,

@@ -69,6 +69,9 @@ struct CombineArgs {
     int cps;              // chunks per group segment
     int tiles_per_group;  // per_group_out only
     int per_group_out;    // 1: out[(g_base+g)*m_total + m][row]; 0: out[m][row] summed over groups
+    int split_last;       // (summed mode) the last group is not summed: its own tiles write it, with
+                          // route 1, to out_last[m][row]
+    float* out_last;
     int accumulate;       // add to out instead of storing
     int zero_skip;        // skip (g, m) whose route is exactly 0
     int m_total;
@@ -270,10 +273,19 @@ __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
     int g_lo = 0;
     int g_hi = a.ngroups;
     int tile = blockIdx.x;
+    bool last = false;  // this workgroup computes the split-off last group
     if (a.per_group_out) {
         g_lo = tile / a.tiles_per_group;
         g_hi = g_lo + 1;
         tile -= g_lo * a.tiles_per_group;
+    } else if (a.split_last) {
+        g_hi = a.ngroups - 1;
+        if (tile >= a.tiles_per_group) {
+            tile -= a.tiles_per_group;
+            g_lo = g_hi;
+            g_hi = a.ngroups;
+            last = true;
+        }
     }
     const int64_t row0 = static_cast<int64_t>(tile) * TR;
 
@@ -295,9 +307,9 @@ __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
         bool any = false;
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-            rw[m] = a.route ? a.route[static_cast<int64_t>(a.g_base + g) * a.route_sg +
-                                      static_cast<int64_t>(a.m0 + m) * a.route_sm]
-                            : 1.0f;
+            rw[m] = a.route && !last ? a.route[static_cast<int64_t>(a.g_base + g) * a.route_sg +
+                                               static_cast<int64_t>(a.m0 + m) * a.route_sm]
+                                     : 1.0f;
             any = any || !(a.zero_skip && rw[m] == 0.0f);
         }
         if (!any || col >= a.K) continue;
@@ -367,7 +379,8 @@ __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
         for (int w = 0; w < nw; ++w) v += red[w * V + t];
         int64_t o = static_cast<int64_t>(a.m0 + m) * a.rows + row;
         if (a.per_group_out) o += static_cast<int64_t>(a.g_base + g_lo) * a.m_total * a.rows;
-        a.out[o] = a.accumulate ? a.out[o] + v : v;
+        float* dst = last ? a.out_last : a.out;
+        dst[o] = a.accumulate ? dst[o] + v : v;
     }
 }
 
@@ -424,22 +437,23 @@ __global__ void fp8_rows_scalar_kernel(const RowsArgs a, int mcount, int ngroups
 
 __global__ void fp8_combine_scalar_kernel(const CombineArgs a, int mcount) {
     const int64_t id = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int ng_out = a.per_group_out ? a.ngroups : 1;
+    const int ng_out = a.per_group_out ? a.ngroups : (a.split_last ? 2 : 1);
     const int64_t total = static_cast<int64_t>(ng_out) * mcount * a.rows;
     if (id >= total) return;
     const int64_t row = id % a.rows;
     const int m = static_cast<int>((id / a.rows) % mcount);
     const int go = static_cast<int>(id / (a.rows * mcount));
-    const int g_lo = a.per_group_out ? go : 0;
-    const int g_hi = a.per_group_out ? go + 1 : a.ngroups;
+    const bool last = !a.per_group_out && a.split_last && go == 1;
+    const int g_lo = a.per_group_out ? go : (last ? a.ngroups - 1 : 0);
+    const int g_hi = a.per_group_out ? go + 1 : (a.split_last && !last ? a.ngroups - 1 : a.ngroups);
     float v = 0.0f;
     for (int g = g_lo; g < g_hi; ++g) {
         const uint8_t* W = a.w[g];
         const float* S = a.s[g];
         if (W == nullptr || S == nullptr) continue;
-        const float rw = a.route ? a.route[static_cast<int64_t>(a.g_base + g) * a.route_sg +
-                                           static_cast<int64_t>(a.m0 + m) * a.route_sm]
-                                 : 1.0f;
+        const float rw = a.route && !last ? a.route[static_cast<int64_t>(a.g_base + g) * a.route_sg +
+                                                    static_cast<int64_t>(a.m0 + m) * a.route_sm]
+                                          : 1.0f;
         if (a.zero_skip && rw == 0.0f) continue;
         const float e = scalar_row_dot(W + row * a.K, S + (row >> 7) * a.scale_cols,
                                        a.act + (static_cast<int64_t>(a.g_base + g) * a.m_total + a.m0 + m) * a.K,
@@ -448,7 +462,8 @@ __global__ void fp8_combine_scalar_kernel(const CombineArgs a, int mcount) {
     }
     int64_t o = static_cast<int64_t>(a.m0 + m) * a.rows + row;
     if (a.per_group_out) o += static_cast<int64_t>(a.g_base + go) * a.m_total * a.rows;
-    a.out[o] = a.accumulate ? a.out[o] + v : v;
+    float* dst = last ? a.out_last : a.out;
+    dst[o] = a.accumulate ? dst[o] + v : v;
 }
 
 __global__ void fill_f32_kernel(float* p, float v, int64_t n) {
@@ -529,14 +544,24 @@ void launch_rows(const RowsArgs& a, int mcount, int ngroups, hipStream_t st) {
     }
 }
 
+// Groups summed by one output tile: every group in summed mode, except a
+// split-off last group, whose own tiles (one group each) read it on the same
+// wave split.  Tiles of one output per group in per_group_out mode.
+int combine_segments(const CombineArgs& a) {
+    return a.per_group_out ? 1 : (a.split_last ? a.ngroups - 1 : a.ngroups);
+}
+
+int combine_outputs(const CombineArgs& a) {
+    return a.per_group_out ? a.ngroups : (a.split_last ? 2 : 1);
+}
+
 template <int M, int TR>
 void launch_combine_tr(const CombineArgs& a, hipStream_t st) {
     CombineArgs b = a;
     const int tiles = static_cast<int>(plm::ceil_div(a.rows, TR));
     b.tiles_per_group = tiles;
-    const int64_t segs = a.per_group_out ? 1 : a.ngroups;
-    const int nw = waves_for(segs * a.cps);
-    const int64_t grid = static_cast<int64_t>(tiles) * (a.per_group_out ? a.ngroups : 1);
+    const int nw = waves_for(combine_segments(a) * a.cps);
+    const int64_t grid = static_cast<int64_t>(tiles) * combine_outputs(a);
     hipLaunchKernelGGL((fp8_combine_kernel<M, TR>), dim3(static_cast<unsigned>(grid)),
                        dim3(nw * plm::kWave), 0, st, b);
 }
@@ -544,8 +569,7 @@ void launch_combine_tr(const CombineArgs& a, hipStream_t st) {
 template <int M>
 void launch_combine_m(const CombineArgs& a, hipStream_t st) {
     if constexpr (M == 1) {
-        const int64_t segs = a.per_group_out ? 1 : a.ngroups;
-        if (wide_tile_fits(a.rows, a.per_group_out ? a.ngroups : 1, waves_for(segs * a.cps))) {
+        if (wide_tile_fits(a.rows, combine_outputs(a), waves_for(combine_segments(a) * a.cps))) {
             launch_combine_tr<1, 8>(a, st);
             return;
         }
@@ -657,6 +681,7 @@ struct CombineProblem {
     bool zero_skip;
     bool per_group_out;
     float* out;
+    float* out_last;      // summed mode: the last group is left out of the sum and written here, route 1
     int64_t batch;
     int64_t rows;
     int64_t K;
@@ -664,6 +689,8 @@ struct CombineProblem {
 };
 
 int run_combine(const CombineProblem& p, hipStream_t st) {
+    if (p.out_last != nullptr && (p.per_group_out || p.ngroups < 2 || p.ngroups > kMaxGroups))
+        return plm::fail(-2, "a split-off last group needs 2..%d summed groups", kMaxGroups);
     bool fast = p.K % 16 == 0 && plm::aligned16(p.act);
     for (int g = 0; g < p.ngroups && fast; ++g) fast = plm::aligned16(p.w[g]);
     for (int g0 = 0; g0 < p.ngroups; g0 += kMaxGroups) {
@@ -686,6 +713,8 @@ int run_combine(const CombineProblem& p, hipStream_t st) {
         a.g_base = g0;
         a.cps = static_cast<int>(plm::ceil_div(p.K, plm::kChunkBytes));
         a.per_group_out = p.per_group_out ? 1 : 0;
+        a.split_last = p.out_last != nullptr ? 1 : 0;
+        a.out_last = p.out_last;
         a.accumulate = (!p.per_group_out && g0 > 0) ? 1 : 0;
         a.zero_skip = p.zero_skip ? 1 : 0;
         a.m_total = static_cast<int>(p.batch);
@@ -695,7 +724,7 @@ int run_combine(const CombineProblem& p, hipStream_t st) {
             if (fast) {
                 launch_combine(a, mc, st);
             } else {
-                const int64_t total = static_cast<int64_t>(p.per_group_out ? ng : 1) * mc * p.rows;
+                const int64_t total = static_cast<int64_t>(combine_outputs(a)) * mc * p.rows;
                 const unsigned blocks = static_cast<unsigned>(plm::ceil_div(total, 256));
                 hipLaunchKernelGGL(fp8_combine_scalar_kernel, dim3(blocks), dim3(256), 0, st, a, mc);
             }
@@ -760,21 +789,25 @@ bool moe_dims_bad(int64_t experts, int64_t batch, int64_t inter, int64_t hid, in
 }
 
 // Shared body of the weighted / row-weighted MoE entry points.
+// With out_last, the tables hold one more expert after the `experts` routed
+// ones: it runs in the same two launches and is written, unweighted, to
+// out_last instead of joining the routed sum.
 int weighted_moe(const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp,
                  const uint64_t* dp, const uint64_t* dsp, const float* hidden, const float* route,
                  int64_t route_sg, int64_t route_sm, bool zero_skip, float* out, int64_t experts,
-                 int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
+                 int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc, float* out_last = nullptr) {
     hipStream_t st = plm::current_stream();
-    float* act = static_cast<float*>(plm::workspace(static_cast<size_t>(experts * batch * inter) * sizeof(float)));
+    const int64_t groups = experts + (out_last != nullptr ? 1 : 0);
+    float* act = static_cast<float*>(plm::workspace(static_cast<size_t>(groups * batch * inter) * sizeof(float)));
     if (act == nullptr) return -3;
-    ExpertTables t(gp, gsp, up, usp, dp, dsp, experts);
-    int code = gate_up_phase(t, experts, hidden, act, batch, inter, hid, gsc, st);
+    ExpertTables t(gp, gsp, up, usp, dp, dsp, groups);
+    int code = gate_up_phase(t, groups, hidden, act, batch, inter, hid, gsc, st);
     if (code != 0) return code;
     CombineProblem c;
     std::memset(&c, 0, sizeof(c));
     c.w = t.d.data();
     c.s = t.ds.data();
-    c.ngroups = static_cast<int>(experts);
+    c.ngroups = static_cast<int>(groups);
     c.act = act;
     c.route = route;
     c.route_sg = route_sg;
@@ -782,6 +815,7 @@ int weighted_moe(const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, co
     c.zero_skip = zero_skip;
     c.per_group_out = false;
     c.out = out;
+    c.out_last = out_last;
     c.batch = batch;
     c.rows = hid;
     c.K = inter;
@@ -933,6 +967,21 @@ PLM_EXPORT int fp8_e4m3_block_mlp_many_weighted_f32(const uint64_t* gp, const ui
     if (moe_dims_bad(expert_count, batch, inter, hid, gsc, dsc)) return plm::fail(-2, "bad dimensions");
     return weighted_moe(gp, gsp, up, usp, dp, dsp, hidden, route_weights, 1, 0, false, out, expert_count,
                         batch, inter, hid, gsc, dsc);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_many_weighted_shared_f32(const uint64_t* gp, const uint64_t* gsp,
+                                                           const uint64_t* up, const uint64_t* usp,
+                                                           const uint64_t* dp, const uint64_t* dsp,
+                                                           const float* hidden, const float* route_weights,
+                                                           float* out, float* out_shared, int64_t expert_count,
+                                                           int64_t batch, int64_t inter, int64_t hid, int64_t gsc,
+                                                           int64_t dsc) {
+    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden || !route_weights || !out || !out_shared)
+        return plm::fail(-1, "null pointer");
+    if (moe_dims_bad(expert_count, batch, inter, hid, gsc, dsc)) return plm::fail(-2, "bad dimensions");
+    if (expert_count + 1 > kMaxGroups) return plm::fail(-2, "at most %d routed experts with a shared one", kMaxGroups - 1);
+    return weighted_moe(gp, gsp, up, usp, dp, dsp, hidden, route_weights, 1, 0, false, out, expert_count, batch,
+                        inter, hid, gsc, dsc, out_shared);
 }
 
 PLM_EXPORT int fp8_e4m3_block_mlp_many_weighted_avx512_f32(

@@ -59,6 +59,10 @@ class MoEOutput:
 ExpertWeights = Sequence[torch.Tensor]  # gate, gate_scale_inv, up, up_scale_inv, down, down_scale_inv
 
 
+def _same_shapes(a: ExpertWeights, b: ExpertWeights) -> bool:
+    return all(tuple(ta.shape) == tuple(tb.shape) for ta, tb in zip(a, b))
+
+
 def run_fp8_moe(hidden: torch.Tensor, route_indices: torch.Tensor, route_weights: torch.Tensor,
                 experts: Mapping[int, ExpertWeights], shared: ExpertWeights | None = None, *,
                 dtype: torch.dtype = torch.bfloat16) -> MoEOutput:
@@ -85,6 +89,7 @@ def run_fp8_moe(hidden: torch.Tensor, route_indices: torch.Tensor, route_weights
     out = torch.zeros_like(flat, dtype=dtype)
     items = [experts[e] for e, _r, _t in jobs]
     path = ""
+    shared_out = None
     many_on = not _enabled("PCKETLM_DISABLE_NATIVE_FP8_MLP_MANY")
 
     if jobs and m > 1 and _enabled("PCKETLM_ENABLE_FP8_MOE_PAIR_WEIGHTED_MANY") \
@@ -111,7 +116,11 @@ def run_fp8_moe(hidden: torch.Tensor, route_indices: torch.Tensor, route_weights
         path = "row_weighted"
     elif jobs and m == 1 and many_on and native.native_fp8_mlp_many_weighted_available():
         route = torch.stack([weights[rows[0], tops[0]] for _e, rows, tops in jobs]).to(torch.float32)
-        y = native.fp8_e4m3_block_mlp_many_weighted_f32(items, x, route)
+        if shared is not None and len(items) < 64 and _same_shapes(items[0], shared):
+            # routed and shared experts in the same two launches, same values
+            y, shared_out = native.fp8_e4m3_block_mlp_many_weighted_shared_f32(items, shared, x, route)
+        else:
+            y = native.fp8_e4m3_block_mlp_many_weighted_f32(items, x, route)
         out += y.to(dtype)
         path = "weighted"
     else:
@@ -127,5 +136,7 @@ def run_fp8_moe(hidden: torch.Tensor, route_indices: torch.Tensor, route_weights
             out[rows] += y * route
 
     if shared is not None:
-        out = out + native.fp8_e4m3_block_mlp_f32(*shared, x).to(dtype)
+        if shared_out is None:
+            shared_out = native.fp8_e4m3_block_mlp_f32(*shared, x)
+        out = out + shared_out.to(dtype)
     return MoEOutput(output=out.reshape(hidden.shape).contiguous(), selected_experts=selected, path=path)

@@ -423,6 +423,32 @@ def fp8_e4m3_block_mlp_many_weighted_f32(items, hidden, route_weights) -> torch.
                      "Native FP8 weighted many-MLP", items, hidden, route_weights, per_row=False)
 
 
+def fp8_e4m3_block_mlp_many_weighted_shared_f32(items, shared, hidden, route_weights):
+    """The routed experts (as fp8_e4m3_block_mlp_many_weighted_f32) and the
+    shared expert (as fp8_e4m3_block_mlp_f32) in two launches: the pair of
+    calls of src/pcketlm/core/runtime/fp8_source.py:1643-1646 and 1849-1859.
+    The shared expert has the routed experts' shapes.  Returns (routed,
+    shared_out), both fp32 [M, H] with the separate calls' values."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_FP8_LINEAR", "Native FP8 weighted many-MLP with shared expert")
+    dev = _target_device(hidden, *(items[0] if items else ()))
+    if not items:
+        raise ValueError("items must not be empty")
+    ex = _Experts(list(items) + [shared], hidden, dev)
+    count = ex.count - 1
+    route = _on(route_weights, dev, torch.float32).reshape(-1)
+    if int(route.numel()) != count:
+        raise ValueError("route_weights length must match item count")
+    batch = int(ex.x.shape[0])
+    out = torch.empty((batch, ex.hid), dtype=torch.float32, device=dev)
+    out_shared = torch.empty((batch, ex.hid), dtype=torch.float32, device=dev)
+    with _launch(lib, dev):
+        code = lib.fp8_e4m3_block_mlp_many_weighted_shared_f32(*ex.table_args(), _p(ex.x), _p(route), _p(out),
+                                                               _p(out_shared), count, batch, ex.inter, ex.hid,
+                                                               ex.gsc, ex.dsc)
+    _check("fp8_e4m3_block_mlp_many_weighted_shared_f32", code)
+    return _home(out, hidden), _home(out_shared, hidden)
+
+
 def fp8_e4m3_block_mlp_many_weighted_avx512_f32(items, hidden, route_weights) -> torch.Tensor:
     """src/pcketlm/native/__init__.py:3951-4022 (same device kernel as the scalar name)."""
     return _weighted("fp8_e4m3_block_mlp_many_weighted_avx512_f32", "PCKETLM_DISABLE_NATIVE_FP8_AVX512",

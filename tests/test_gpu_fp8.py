@@ -269,6 +269,36 @@ def test_deepseek_moe_layer_shapes_vs_oracle(nat, oracle_mod):
     assert rel_l2(host(yr), oracle_mod.fp8_mlp_many_row_weighted(items, x, rroute)) < TOL
 
 
+def test_weighted_with_shared_expert_equals_separate_calls(nat, oracle_mod, golden):
+    """Routed + shared experts in two launches give the separate calls'
+    values: the DeepSeek-V3 layer (8 routed + shared, M=1) and the small
+    golden experts at one and two activation rows."""
+    items = []
+    for e in range(9):
+        g, gs = synth_fp8(2048, 7168, 700 + 3 * e)
+        u, us = synth_fp8(2048, 7168, 701 + 3 * e)
+        d, ds = synth_fp8(7168, 2048, 702 + 3 * e)
+        items.append((g, gs, u, us, d, ds))
+    di = cuda_items(items)
+    xh = synth_x(1, 7168, 610)
+    x = dev(xh)
+    route_h = np.random.default_rng(4).uniform(0.05, 0.4, 8).astype(np.float32)
+    route = dev(route_h)
+    y, ys = nat.fp8_e4m3_block_mlp_many_weighted_shared_f32(di[:8], di[8], x, route)
+    assert torch.equal(y, nat.fp8_e4m3_block_mlp_many_weighted_f32(di[:8], x, route))
+    assert torch.equal(ys, nat.fp8_e4m3_block_mlp_f32(*di[8], x))
+    assert rel_l2(host(y), oracle_mod.fp8_mlp_many_weighted(items[:8], xh, route_h)) < TOL
+    assert rel_l2(host(ys), oracle_mod.fp8_mlp(*items[8], xh)) < TOL
+    gd = golden("fp8_gemv")
+    wt = cuda_items(items_from(gd, "wt"))
+    for m in (1, 2):
+        xs = dev(np.repeat(gd["wt_x"], m, axis=0) * np.arange(1, m + 1, dtype=np.float32)[:, None])
+        r = dev(gd["wt_route"][:2])
+        y2, ys2 = nat.fp8_e4m3_block_mlp_many_weighted_shared_f32(wt[:2], wt[2], xs, r)
+        assert torch.equal(y2, nat.fp8_e4m3_block_mlp_many_weighted_f32(wt[:2], xs, r))
+        assert torch.equal(ys2, nat.fp8_e4m3_block_mlp_f32(*wt[2], xs))
+
+
 # --------------------------------------------------------------------------- DeepSeek session
 
 def test_ds_session_combine_kat_and_counters(nat):
