@@ -297,6 +297,23 @@ def test_weighted_with_shared_expert_equals_separate_calls(nat, oracle_mod, gold
         y2, ys2 = nat.fp8_e4m3_block_mlp_many_weighted_shared_f32(wt[:2], wt[2], xs, r)
         assert torch.equal(y2, nat.fp8_e4m3_block_mlp_many_weighted_f32(wt[:2], xs, r))
         assert torch.equal(ys2, nat.fp8_e4m3_block_mlp_f32(*wt[2], xs))
+    # K not a multiple of 16: both phases take the one-thread-per-output kernels
+    odd = []
+    for e in range(4):
+        g, gs = synth_fp8(40, 72, 800 + 3 * e)
+        u, us = synth_fp8(40, 72, 801 + 3 * e)
+        d, ds = synth_fp8(72, 40, 802 + 3 * e)
+        odd.append((g, gs, u, us, d, ds))
+    do = cuda_items(odd)
+    xo_h = synth_x(2, 72, 620)
+    xo = dev(xo_h)
+    ro_h = np.array([0.5, 0.25, 0.125], dtype=np.float32)
+    ro = dev(ro_h)
+    y3, ys3 = nat.fp8_e4m3_block_mlp_many_weighted_shared_f32(do[:3], do[3], xo, ro)
+    assert torch.equal(y3, nat.fp8_e4m3_block_mlp_many_weighted_f32(do[:3], xo, ro))
+    assert torch.equal(ys3, nat.fp8_e4m3_block_mlp_f32(*do[3], xo))
+    assert rel_l2(host(y3), oracle_mod.fp8_mlp_many_weighted(odd[:3], xo_h, ro_h)) < TOL
+    assert rel_l2(host(ys3), oracle_mod.fp8_mlp(*odd[3], xo_h)) < TOL
 
 
 # --------------------------------------------------------------------------- DeepSeek session
