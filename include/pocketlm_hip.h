@@ -185,6 +185,44 @@ int fp8_e4m3_block_mlp_many_pair_weighted_f32(
     int64_t batch, int64_t intermediate_rows, int64_t hidden_cols, int64_t gate_scale_cols,
     int64_t down_scale_cols);
 
+/* bf16-activation twins.  The reference wrappers cast the activations to
+ * fp32 before these calls (native/__init__.py:3451 linear, 3500 dual, 3568
+ * MLP, 3834 row-weighted, 3910 pair-weighted); the twins take bf16
+ * activations [batch, hidden] as they are and widen them on the device.  The
+ * widening is exact, so each twin returns exactly the values of its fp32
+ * entry point for the widened activations; they only read half the
+ * activation bytes, which matters at 2..8 activation rows.  Arguments and
+ * codes are otherwise those of the fp32 entry point. */
+int fp8_e4m3_block_linear_bf16x_f32(const uint8_t* fp8_weight, const float* scale_inv,
+                                    const uint16_t* hidden_bf16, float* out, int64_t batch,
+                                    int64_t out_rows, int64_t in_cols, int64_t scale_cols);
+int fp8_e4m3_block_dual_linear_bf16x_f32(const uint8_t* weight_a, const float* scale_inv_a,
+                                         const uint8_t* weight_b, const float* scale_inv_b,
+                                         const uint16_t* hidden_bf16, float* out_a, float* out_b,
+                                         int64_t batch, int64_t out_rows, int64_t in_cols,
+                                         int64_t scale_cols);
+int fp8_e4m3_block_mlp_bf16x_f32(const uint8_t* gate_weight, const float* gate_scale_inv,
+                                 const uint8_t* up_weight, const float* up_scale_inv,
+                                 const uint8_t* down_weight, const float* down_scale_inv,
+                                 const uint16_t* hidden_bf16, float* out, int64_t batch,
+                                 int64_t intermediate_rows, int64_t hidden_cols,
+                                 int64_t gate_scale_cols, int64_t down_scale_cols);
+int fp8_e4m3_block_mlp_many_row_weighted_bf16x_f32(
+    const uint64_t* gate_weight_ptrs, const uint64_t* gate_scale_ptrs,
+    const uint64_t* up_weight_ptrs, const uint64_t* up_scale_ptrs,
+    const uint64_t* down_weight_ptrs, const uint64_t* down_scale_ptrs, const uint16_t* hidden_bf16,
+    const float* route_weights, float* out, int64_t expert_count, int64_t batch,
+    int64_t intermediate_rows, int64_t hidden_cols, int64_t gate_scale_cols,
+    int64_t down_scale_cols);
+int fp8_e4m3_block_mlp_many_pair_weighted_bf16x_f32(
+    const uint64_t* gate_weight_ptrs, const uint64_t* gate_scale_ptrs,
+    const uint64_t* up_weight_ptrs, const uint64_t* up_scale_ptrs,
+    const uint64_t* down_weight_ptrs, const uint64_t* down_scale_ptrs, const uint16_t* hidden_bf16,
+    const int64_t* pair_item_indices, const int64_t* pair_row_indices,
+    const float* pair_weights, float* out, int64_t expert_count, int64_t pair_count,
+    int64_t batch, int64_t intermediate_rows, int64_t hidden_cols, int64_t gate_scale_cols,
+    int64_t down_scale_cols);
+
 /* --------------------------------------------------------------------- Q4 */
 /* Per-row symmetric Q4 (src/pcketlm/core/model_import/q4_quantize.py:48-71):
  * two's-complement nibbles flat over the whole tensor, element 2i in the low

@@ -40,7 +40,8 @@ constexpr int kMaxM = 8;        // activation rows per launch; larger batches ar
 struct RowsArgs {
     const uint8_t* w[2][kMaxGroups];
     const float* s[2][kMaxGroups];
-    const float* x;       // activations [m_total][x_stride]
+    const float* x;       // activations [m_total][x_stride] (fp32), or
+    const uint16_t* xb;   // the same as bf16 (non-null: read these; bf16 -> fp32 is exact)
     float* out[2];        // outputs, element (g, m, row) at ((g*m_total + m) * out_ld + row)
     int64_t x_stride;
     int64_t out_ld;
@@ -109,7 +110,26 @@ __device__ __forceinline__ void load_x16(const float* p, float* x) {
     }
 }
 
-template <int M, int TR, int NWT, bool SILU>
+// 16 activations of row m at column col, from the fp32 or (XB) the bf16
+// copy; both give the same fp32 values.
+template <bool XB>
+__device__ __forceinline__ void load_row_x16(const RowsArgs& a, int m, int64_t col, float* x) {
+    const int64_t off = static_cast<int64_t>(a.m0 + m) * a.x_stride + col;
+    if constexpr (XB) {
+        const uint4* p = reinterpret_cast<const uint4*>(a.xb + off);
+        const uint4 h0 = p[0], h1 = p[1];
+        const uint32_t h[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            x[2 * j] = __uint_as_float(h[j] << 16);
+            x[2 * j + 1] = __uint_as_float(h[j] & 0xFFFF0000u);
+        }
+    } else {
+        load_x16(a.x + off, x);
+    }
+}
+
+template <int M, int TR, int NWT, bool SILU, bool XB>
 __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
     constexpr int V = NWT * TR * M;
     __shared__ float red[kMaxWaves * V];
@@ -160,7 +180,7 @@ __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
                 // one activation row: decode each weight row right before its
                 // dot, so a larger tile needs no more registers (same arithmetic)
                 float xv[16];
-                load_x16(a.x + static_cast<int64_t>(a.m0) * a.x_stride + col, xv);
+                load_row_x16<XB>(a, 0, col, xv);
 #pragma unroll
                 for (int i = 0; i < NWT; ++i)
 #pragma unroll
@@ -185,7 +205,7 @@ __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
                     float xv[16];
-                    load_x16(a.x + static_cast<int64_t>(a.m0 + m) * a.x_stride + col, xv);
+                    load_row_x16<XB>(a, m, col, xv);
 #pragma unroll
                     for (int i = 0; i < NWT; ++i)
 #pragma unroll
@@ -214,7 +234,7 @@ __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 float xv[16];
-                load_x16(a.x + static_cast<int64_t>(a.m0 + m) * a.x_stride + col, xv);
+                load_row_x16<XB>(a, m, col, xv);
 #pragma unroll
                 for (int i = 0; i < NWT; ++i)
 #pragma unroll
@@ -389,7 +409,11 @@ __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
 // (small test shapes).  One thread per output element; the per-row arithmetic
 // is again independent of the batch size.
 
-__device__ float scalar_row_dot(const uint8_t* w, const float* s, const float* x, int64_t K) {
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
+
+// x is fp32, or bf16 when xb is non-null.
+__device__ float scalar_row_dot(const uint8_t* w, const float* s, const float* x, int64_t K,
+                                const uint16_t* xb = nullptr) {
     float acc = 0.0f;
     for (int64_t c0 = 0; c0 < K; c0 += 128) {
         const int64_t c1 = c0 + 128 < K ? c0 + 128 : K;
@@ -399,7 +423,7 @@ __device__ float scalar_row_dot(const uint8_t* w, const float* s, const float* x
             float v[4];
             plm_decode4_e4m3(byte, v);
             const float wv = (v[0] != v[0]) ? 0.0f : v[0];
-            blk = fmaf(x[c], wv, blk);
+            blk = fmaf(xb != nullptr ? bf16_bits_to_f32(xb[c]) : x[c], wv, blk);
         }
         acc = fmaf(blk, s[c0 >> 7], acc);
     }
@@ -422,8 +446,9 @@ __global__ void fp8_rows_scalar_kernel(const RowsArgs a, int mcount, int ngroups
             v[i] = 0.0f;
             continue;
         }
-        v[i] = scalar_row_dot(W + row * a.K, S + (row >> 7) * a.scale_cols,
-                              a.x + static_cast<int64_t>(a.m0 + m) * a.x_stride, a.K);
+        const int64_t xo = static_cast<int64_t>(a.m0 + m) * a.x_stride;
+        v[i] = scalar_row_dot(W + row * a.K, S + (row >> 7) * a.scale_cols, a.x + xo, a.K,
+                              a.xb != nullptr ? a.xb + xo : nullptr);
     }
     bool live = true;
     for (int i = 0; i < NWT; ++i) live = live && a.w[i][g] != nullptr && a.s[i][g] != nullptr;
@@ -513,8 +538,13 @@ void launch_rows_tr(const RowsArgs& a, int ngroups, hipStream_t st) {
     b.tiles_per_group = static_cast<int>(plm::ceil_div(a.rows, TR));
     const int nw = waves_for(a.nchunks);
     const int64_t grid = static_cast<int64_t>(b.tiles_per_group) * ngroups;
-    hipLaunchKernelGGL((fp8_rows_kernel<M, TR, NWT, SILU>), dim3(static_cast<unsigned>(grid)),
-                       dim3(nw * plm::kWave), 0, st, b);
+    if (a.xb != nullptr) {
+        hipLaunchKernelGGL((fp8_rows_kernel<M, TR, NWT, SILU, true>), dim3(static_cast<unsigned>(grid)),
+                           dim3(nw * plm::kWave), 0, st, b);
+    } else {
+        hipLaunchKernelGGL((fp8_rows_kernel<M, TR, NWT, SILU, false>), dim3(static_cast<unsigned>(grid)),
+                           dim3(nw * plm::kWave), 0, st, b);
+    }
 }
 
 template <int M, int NWT, bool SILU>
@@ -598,6 +628,7 @@ struct RowsProblem {
     bool silu;
     int ngroups;
     const float* x;
+    const uint16_t* xb;   // bf16 activations instead of x (one of the two is set)
     int64_t x_stride;
     float* out[2];
     int64_t out_ld;
@@ -608,7 +639,11 @@ struct RowsProblem {
 };
 
 bool rows_fast_ok(const RowsProblem& p) {
-    if (p.K % 16 != 0 || p.x_stride % 4 != 0 || !plm::aligned16(p.x)) return false;
+    if (p.xb != nullptr) {
+        if (p.K % 16 != 0 || p.x_stride % 8 != 0 || !plm::aligned16(p.xb)) return false;
+    } else if (p.K % 16 != 0 || p.x_stride % 4 != 0 || !plm::aligned16(p.x)) {
+        return false;
+    }
     for (int i = 0; i < p.nwt; ++i)
         for (int g = 0; g < p.ngroups; ++g)
             if (!plm::aligned16(p.w[i][g])) return false;
@@ -627,6 +662,7 @@ int run_rows(const RowsProblem& p, hipStream_t st) {
                 a.s[i][g] = p.s[i][g0 + g];
             }
         a.x = p.x;
+        a.xb = p.xb;
         a.x_stride = p.x_stride;
         // Output offsets of this group batch: element (g, m, row) lives at
         // ((g0 + g) * batch + m) * out_ld + row.
@@ -759,8 +795,15 @@ struct ExpertTables {
     }
 };
 
+// Activations as the caller passed them: fp32, or bf16 (the bf16 twins of
+// the entry points; bf16 -> fp32 is exact, so both give the same results).
+struct Act {
+    const float* f32;
+    const uint16_t* bf16;
+};
+
 // Phase 1 of every SwiGLU path: act[e][m][row] = silu(gate_e . x_m) * (up_e . x_m).
-int gate_up_phase(const ExpertTables& t, int64_t experts, const float* hidden, float* act,
+int gate_up_phase(const ExpertTables& t, int64_t experts, Act hidden, float* act,
                   int64_t batch, int64_t inter, int64_t hid, int64_t gsc, hipStream_t st) {
     RowsProblem p;
     std::memset(&p, 0, sizeof(p));
@@ -771,7 +814,8 @@ int gate_up_phase(const ExpertTables& t, int64_t experts, const float* hidden, f
     p.nwt = 2;
     p.silu = true;
     p.ngroups = static_cast<int>(experts);
-    p.x = hidden;
+    p.x = hidden.f32;
+    p.xb = hidden.bf16;
     p.x_stride = hid;
     p.out[0] = act;
     p.out[1] = nullptr;
@@ -793,7 +837,7 @@ bool moe_dims_bad(int64_t experts, int64_t batch, int64_t inter, int64_t hid, in
 // ones: it runs in the same two launches and is written, unweighted, to
 // out_last instead of joining the routed sum.
 int weighted_moe(const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp,
-                 const uint64_t* dp, const uint64_t* dsp, const float* hidden, const float* route,
+                 const uint64_t* dp, const uint64_t* dsp, Act hidden, const float* route,
                  int64_t route_sg, int64_t route_sm, bool zero_skip, float* out, int64_t experts,
                  int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc, float* out_last = nullptr) {
     hipStream_t st = plm::current_stream();
@@ -823,14 +867,8 @@ int weighted_moe(const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, co
     return run_combine(c, st);
 }
 
-}  // namespace
-
-// ====================================================================== C ABI
-
-PLM_EXPORT int fp8_e4m3_block_linear_f32(const uint8_t* fp8_weight, const float* scale_inv,
-                                         const float* hidden, float* out, int64_t batch,
-                                         int64_t out_rows, int64_t in_cols, int64_t scale_cols) {
-    if (!fp8_weight || !scale_inv || !hidden || !out) return plm::fail(-1, "null pointer");
+int linear_impl(const uint8_t* fp8_weight, const float* scale_inv, Act hidden, float* out, int64_t batch,
+                int64_t out_rows, int64_t in_cols, int64_t scale_cols) {
     if (batch <= 0 || out_rows <= 0 || in_cols <= 0 || scale_cols < plm::ceil_div(in_cols, 128))
         return plm::fail(-2, "bad dimensions");
     const uint8_t* w[1] = {fp8_weight};
@@ -841,7 +879,8 @@ PLM_EXPORT int fp8_e4m3_block_linear_f32(const uint8_t* fp8_weight, const float*
     p.s[0] = s;
     p.nwt = 1;
     p.ngroups = 1;
-    p.x = hidden;
+    p.x = hidden.f32;
+    p.xb = hidden.bf16;
     p.x_stride = in_cols;
     p.out[0] = out;
     p.out_ld = out_rows;
@@ -852,11 +891,9 @@ PLM_EXPORT int fp8_e4m3_block_linear_f32(const uint8_t* fp8_weight, const float*
     return run_rows(p, plm::current_stream());
 }
 
-PLM_EXPORT int fp8_e4m3_block_dual_linear_f32(const uint8_t* wa, const float* sa, const uint8_t* wb,
-                                              const float* sb, const float* hidden, float* out_a,
-                                              float* out_b, int64_t batch, int64_t out_rows,
-                                              int64_t in_cols, int64_t scale_cols) {
-    if (!wa || !sa || !wb || !sb || !hidden || !out_a || !out_b) return plm::fail(-1, "null pointer");
+int dual_linear_impl(const uint8_t* wa, const float* sa, const uint8_t* wb, const float* sb, Act hidden,
+                     float* out_a, float* out_b, int64_t batch, int64_t out_rows, int64_t in_cols,
+                     int64_t scale_cols) {
     if (batch <= 0 || out_rows <= 0 || in_cols <= 0 || scale_cols < plm::ceil_div(in_cols, 128))
         return plm::fail(-2, "bad dimensions");
     const uint8_t* w0[1] = {wa};
@@ -872,7 +909,8 @@ PLM_EXPORT int fp8_e4m3_block_dual_linear_f32(const uint8_t* wa, const float* sa
     p.nwt = 2;
     p.silu = false;
     p.ngroups = 1;
-    p.x = hidden;
+    p.x = hidden.f32;
+    p.xb = hidden.bf16;
     p.x_stride = in_cols;
     p.out[0] = out_a;
     p.out[1] = out_b;
@@ -884,15 +922,10 @@ PLM_EXPORT int fp8_e4m3_block_dual_linear_f32(const uint8_t* wa, const float* sa
     return run_rows(p, plm::current_stream());
 }
 
-PLM_EXPORT int fp8_e4m3_block_mlp_f32(const uint8_t* gate_weight, const float* gate_scale_inv,
-                                      const uint8_t* up_weight, const float* up_scale_inv,
-                                      const uint8_t* down_weight, const float* down_scale_inv,
-                                      const float* hidden, float* out, int64_t batch,
-                                      int64_t intermediate_rows, int64_t hidden_cols,
-                                      int64_t gate_scale_cols, int64_t down_scale_cols) {
-    if (!gate_weight || !gate_scale_inv || !up_weight || !up_scale_inv || !down_weight || !down_scale_inv ||
-        !hidden || !out)
-        return plm::fail(-1, "null pointer");
+int mlp_impl(const uint8_t* gate_weight, const float* gate_scale_inv, const uint8_t* up_weight,
+             const float* up_scale_inv, const uint8_t* down_weight, const float* down_scale_inv, Act hidden,
+             float* out, int64_t batch, int64_t intermediate_rows, int64_t hidden_cols, int64_t gate_scale_cols,
+             int64_t down_scale_cols) {
     if (moe_dims_bad(1, batch, intermediate_rows, hidden_cols, gate_scale_cols, down_scale_cols))
         return plm::fail(-2, "bad dimensions");
     const uint64_t gp = reinterpret_cast<uintptr_t>(gate_weight), gsp = reinterpret_cast<uintptr_t>(gate_scale_inv);
@@ -918,99 +951,10 @@ PLM_EXPORT int fp8_e4m3_block_mlp_f32(const uint8_t* gate_weight, const float* g
     return run_combine(c, st);
 }
 
-PLM_EXPORT int fp8_e4m3_block_mlp_avx512_f32(const uint8_t* gate_weight, const float* gate_scale_inv,
-                                             const uint8_t* up_weight, const float* up_scale_inv,
-                                             const uint8_t* down_weight, const float* down_scale_inv,
-                                             const float* hidden, float* out, int64_t batch,
-                                             int64_t intermediate_rows, int64_t hidden_cols,
-                                             int64_t gate_scale_cols, int64_t down_scale_cols) {
-    return fp8_e4m3_block_mlp_f32(gate_weight, gate_scale_inv, up_weight, up_scale_inv, down_weight,
-                                  down_scale_inv, hidden, out, batch, intermediate_rows, hidden_cols,
-                                  gate_scale_cols, down_scale_cols);
-}
-
-PLM_EXPORT int fp8_e4m3_block_mlp_many_f32(const uint64_t* gp, const uint64_t* gsp, const uint64_t* up,
-                                           const uint64_t* usp, const uint64_t* dp, const uint64_t* dsp,
-                                           const float* hidden, float* out, int64_t expert_count,
-                                           int64_t batch, int64_t inter, int64_t hid, int64_t gsc,
-                                           int64_t dsc) {
-    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden || !out) return plm::fail(-1, "null pointer");
-    if (moe_dims_bad(expert_count, batch, inter, hid, gsc, dsc)) return plm::fail(-2, "bad dimensions");
-    hipStream_t st = plm::current_stream();
-    float* act = static_cast<float*>(plm::workspace(static_cast<size_t>(expert_count * batch * inter) * sizeof(float)));
-    if (act == nullptr) return -3;
-    ExpertTables t(gp, gsp, up, usp, dp, dsp, expert_count);
-    int code = gate_up_phase(t, expert_count, hidden, act, batch, inter, hid, gsc, st);
-    if (code != 0) return code;
-    CombineProblem c;
-    std::memset(&c, 0, sizeof(c));
-    c.w = t.d.data();
-    c.s = t.ds.data();
-    c.ngroups = static_cast<int>(expert_count);
-    c.act = act;
-    c.per_group_out = true;
-    c.out = out;
-    c.batch = batch;
-    c.rows = hid;
-    c.K = inter;
-    c.scale_cols = dsc;
-    return run_combine(c, st);
-}
-
-PLM_EXPORT int fp8_e4m3_block_mlp_many_weighted_f32(const uint64_t* gp, const uint64_t* gsp, const uint64_t* up,
-                                                    const uint64_t* usp, const uint64_t* dp, const uint64_t* dsp,
-                                                    const float* hidden, const float* route_weights, float* out,
-                                                    int64_t expert_count, int64_t batch, int64_t inter,
-                                                    int64_t hid, int64_t gsc, int64_t dsc) {
-    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden || !route_weights || !out)
-        return plm::fail(-1, "null pointer");
-    if (moe_dims_bad(expert_count, batch, inter, hid, gsc, dsc)) return plm::fail(-2, "bad dimensions");
-    return weighted_moe(gp, gsp, up, usp, dp, dsp, hidden, route_weights, 1, 0, false, out, expert_count,
-                        batch, inter, hid, gsc, dsc);
-}
-
-PLM_EXPORT int fp8_e4m3_block_mlp_many_weighted_shared_f32(const uint64_t* gp, const uint64_t* gsp,
-                                                           const uint64_t* up, const uint64_t* usp,
-                                                           const uint64_t* dp, const uint64_t* dsp,
-                                                           const float* hidden, const float* route_weights,
-                                                           float* out, float* out_shared, int64_t expert_count,
-                                                           int64_t batch, int64_t inter, int64_t hid, int64_t gsc,
-                                                           int64_t dsc) {
-    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden || !route_weights || !out || !out_shared)
-        return plm::fail(-1, "null pointer");
-    if (moe_dims_bad(expert_count, batch, inter, hid, gsc, dsc)) return plm::fail(-2, "bad dimensions");
-    if (expert_count + 1 > kMaxGroups) return plm::fail(-2, "at most %d routed experts with a shared one", kMaxGroups - 1);
-    return weighted_moe(gp, gsp, up, usp, dp, dsp, hidden, route_weights, 1, 0, false, out, expert_count, batch,
-                        inter, hid, gsc, dsc, out_shared);
-}
-
-PLM_EXPORT int fp8_e4m3_block_mlp_many_weighted_avx512_f32(
-    const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp, const uint64_t* dp,
-    const uint64_t* dsp, const float* hidden, const float* route_weights, float* out, int64_t expert_count,
-    int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
-    return fp8_e4m3_block_mlp_many_weighted_f32(gp, gsp, up, usp, dp, dsp, hidden, route_weights, out,
-                                                expert_count, batch, inter, hid, gsc, dsc);
-}
-
-PLM_EXPORT int fp8_e4m3_block_mlp_many_row_weighted_f32(
-    const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp, const uint64_t* dp,
-    const uint64_t* dsp, const float* hidden, const float* route_weights, float* out, int64_t expert_count,
-    int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
-    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden || !route_weights || !out)
-        return plm::fail(-1, "null pointer");
-    if (moe_dims_bad(expert_count, batch, inter, hid, gsc, dsc)) return plm::fail(-2, "bad dimensions");
-    return weighted_moe(gp, gsp, up, usp, dp, dsp, hidden, route_weights, batch, 1, true, out, expert_count,
-                        batch, inter, hid, gsc, dsc);
-}
-
-PLM_EXPORT int fp8_e4m3_block_mlp_many_pair_weighted_f32(
-    const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp, const uint64_t* dp,
-    const uint64_t* dsp, const float* hidden, const int64_t* pair_item_indices, const int64_t* pair_row_indices,
-    const float* pair_weights, float* out, int64_t expert_count, int64_t pair_count, int64_t batch, int64_t inter,
-    int64_t hid, int64_t gsc, int64_t dsc) {
-    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden || !pair_item_indices || !pair_row_indices ||
-        !pair_weights || !out)
-        return plm::fail(-1, "null pointer");
+int pair_weighted_impl(const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp,
+                       const uint64_t* dp, const uint64_t* dsp, Act hidden, const int64_t* pair_item_indices,
+                       const int64_t* pair_row_indices, const float* pair_weights, float* out, int64_t expert_count,
+                       int64_t pair_count, int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
     if (pair_count < 0 || moe_dims_bad(expert_count, batch, inter, hid, gsc, dsc))
         return plm::fail(-2, "bad dimensions");
     hipStream_t st = plm::current_stream();
@@ -1059,6 +1003,191 @@ PLM_EXPORT int fp8_e4m3_block_mlp_many_pair_weighted_f32(
     c.K = inter;
     c.scale_cols = dsc;
     return run_combine(c, st);
+}
+
+}  // namespace
+
+// ====================================================================== C ABI
+
+PLM_EXPORT int fp8_e4m3_block_linear_f32(const uint8_t* fp8_weight, const float* scale_inv,
+                                         const float* hidden, float* out, int64_t batch,
+                                         int64_t out_rows, int64_t in_cols, int64_t scale_cols) {
+    if (!fp8_weight || !scale_inv || !hidden || !out) return plm::fail(-1, "null pointer");
+    return linear_impl(fp8_weight, scale_inv, Act{hidden, nullptr}, out, batch, out_rows, in_cols, scale_cols);
+}
+
+PLM_EXPORT int fp8_e4m3_block_linear_bf16x_f32(const uint8_t* fp8_weight, const float* scale_inv,
+                                               const uint16_t* hidden_bf16, float* out, int64_t batch,
+                                               int64_t out_rows, int64_t in_cols, int64_t scale_cols) {
+    if (!fp8_weight || !scale_inv || !hidden_bf16 || !out) return plm::fail(-1, "null pointer");
+    return linear_impl(fp8_weight, scale_inv, Act{nullptr, hidden_bf16}, out, batch, out_rows, in_cols, scale_cols);
+}
+
+PLM_EXPORT int fp8_e4m3_block_dual_linear_f32(const uint8_t* wa, const float* sa, const uint8_t* wb,
+                                              const float* sb, const float* hidden, float* out_a,
+                                              float* out_b, int64_t batch, int64_t out_rows,
+                                              int64_t in_cols, int64_t scale_cols) {
+    if (!wa || !sa || !wb || !sb || !hidden || !out_a || !out_b) return plm::fail(-1, "null pointer");
+    return dual_linear_impl(wa, sa, wb, sb, Act{hidden, nullptr}, out_a, out_b, batch, out_rows, in_cols,
+                            scale_cols);
+}
+
+PLM_EXPORT int fp8_e4m3_block_dual_linear_bf16x_f32(const uint8_t* wa, const float* sa, const uint8_t* wb,
+                                                    const float* sb, const uint16_t* hidden_bf16, float* out_a,
+                                                    float* out_b, int64_t batch, int64_t out_rows,
+                                                    int64_t in_cols, int64_t scale_cols) {
+    if (!wa || !sa || !wb || !sb || !hidden_bf16 || !out_a || !out_b) return plm::fail(-1, "null pointer");
+    return dual_linear_impl(wa, sa, wb, sb, Act{nullptr, hidden_bf16}, out_a, out_b, batch, out_rows, in_cols,
+                            scale_cols);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_f32(const uint8_t* gate_weight, const float* gate_scale_inv,
+                                      const uint8_t* up_weight, const float* up_scale_inv,
+                                      const uint8_t* down_weight, const float* down_scale_inv,
+                                      const float* hidden, float* out, int64_t batch,
+                                      int64_t intermediate_rows, int64_t hidden_cols,
+                                      int64_t gate_scale_cols, int64_t down_scale_cols) {
+    if (!gate_weight || !gate_scale_inv || !up_weight || !up_scale_inv || !down_weight || !down_scale_inv ||
+        !hidden || !out)
+        return plm::fail(-1, "null pointer");
+    return mlp_impl(gate_weight, gate_scale_inv, up_weight, up_scale_inv, down_weight, down_scale_inv,
+                    Act{hidden, nullptr}, out, batch, intermediate_rows, hidden_cols, gate_scale_cols,
+                    down_scale_cols);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_bf16x_f32(const uint8_t* gate_weight, const float* gate_scale_inv,
+                                            const uint8_t* up_weight, const float* up_scale_inv,
+                                            const uint8_t* down_weight, const float* down_scale_inv,
+                                            const uint16_t* hidden_bf16, float* out, int64_t batch,
+                                            int64_t intermediate_rows, int64_t hidden_cols,
+                                            int64_t gate_scale_cols, int64_t down_scale_cols) {
+    if (!gate_weight || !gate_scale_inv || !up_weight || !up_scale_inv || !down_weight || !down_scale_inv ||
+        !hidden_bf16 || !out)
+        return plm::fail(-1, "null pointer");
+    return mlp_impl(gate_weight, gate_scale_inv, up_weight, up_scale_inv, down_weight, down_scale_inv,
+                    Act{nullptr, hidden_bf16}, out, batch, intermediate_rows, hidden_cols, gate_scale_cols,
+                    down_scale_cols);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_avx512_f32(const uint8_t* gate_weight, const float* gate_scale_inv,
+                                             const uint8_t* up_weight, const float* up_scale_inv,
+                                             const uint8_t* down_weight, const float* down_scale_inv,
+                                             const float* hidden, float* out, int64_t batch,
+                                             int64_t intermediate_rows, int64_t hidden_cols,
+                                             int64_t gate_scale_cols, int64_t down_scale_cols) {
+    return fp8_e4m3_block_mlp_f32(gate_weight, gate_scale_inv, up_weight, up_scale_inv, down_weight,
+                                  down_scale_inv, hidden, out, batch, intermediate_rows, hidden_cols,
+                                  gate_scale_cols, down_scale_cols);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_many_f32(const uint64_t* gp, const uint64_t* gsp, const uint64_t* up,
+                                           const uint64_t* usp, const uint64_t* dp, const uint64_t* dsp,
+                                           const float* hidden, float* out, int64_t expert_count,
+                                           int64_t batch, int64_t inter, int64_t hid, int64_t gsc,
+                                           int64_t dsc) {
+    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden || !out) return plm::fail(-1, "null pointer");
+    if (moe_dims_bad(expert_count, batch, inter, hid, gsc, dsc)) return plm::fail(-2, "bad dimensions");
+    hipStream_t st = plm::current_stream();
+    float* act = static_cast<float*>(plm::workspace(static_cast<size_t>(expert_count * batch * inter) * sizeof(float)));
+    if (act == nullptr) return -3;
+    ExpertTables t(gp, gsp, up, usp, dp, dsp, expert_count);
+    int code = gate_up_phase(t, expert_count, Act{hidden, nullptr}, act, batch, inter, hid, gsc, st);
+    if (code != 0) return code;
+    CombineProblem c;
+    std::memset(&c, 0, sizeof(c));
+    c.w = t.d.data();
+    c.s = t.ds.data();
+    c.ngroups = static_cast<int>(expert_count);
+    c.act = act;
+    c.per_group_out = true;
+    c.out = out;
+    c.batch = batch;
+    c.rows = hid;
+    c.K = inter;
+    c.scale_cols = dsc;
+    return run_combine(c, st);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_many_weighted_f32(const uint64_t* gp, const uint64_t* gsp, const uint64_t* up,
+                                                    const uint64_t* usp, const uint64_t* dp, const uint64_t* dsp,
+                                                    const float* hidden, const float* route_weights, float* out,
+                                                    int64_t expert_count, int64_t batch, int64_t inter,
+                                                    int64_t hid, int64_t gsc, int64_t dsc) {
+    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden || !route_weights || !out)
+        return plm::fail(-1, "null pointer");
+    if (moe_dims_bad(expert_count, batch, inter, hid, gsc, dsc)) return plm::fail(-2, "bad dimensions");
+    return weighted_moe(gp, gsp, up, usp, dp, dsp, Act{hidden, nullptr}, route_weights, 1, 0, false, out,
+                        expert_count, batch, inter, hid, gsc, dsc);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_many_weighted_shared_f32(const uint64_t* gp, const uint64_t* gsp,
+                                                           const uint64_t* up, const uint64_t* usp,
+                                                           const uint64_t* dp, const uint64_t* dsp,
+                                                           const float* hidden, const float* route_weights,
+                                                           float* out, float* out_shared, int64_t expert_count,
+                                                           int64_t batch, int64_t inter, int64_t hid, int64_t gsc,
+                                                           int64_t dsc) {
+    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden || !route_weights || !out || !out_shared)
+        return plm::fail(-1, "null pointer");
+    if (moe_dims_bad(expert_count, batch, inter, hid, gsc, dsc)) return plm::fail(-2, "bad dimensions");
+    if (expert_count + 1 > kMaxGroups) return plm::fail(-2, "at most %d routed experts with a shared one", kMaxGroups - 1);
+    return weighted_moe(gp, gsp, up, usp, dp, dsp, Act{hidden, nullptr}, route_weights, 1, 0, false, out,
+                        expert_count, batch, inter, hid, gsc, dsc, out_shared);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_many_weighted_avx512_f32(
+    const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp, const uint64_t* dp,
+    const uint64_t* dsp, const float* hidden, const float* route_weights, float* out, int64_t expert_count,
+    int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
+    return fp8_e4m3_block_mlp_many_weighted_f32(gp, gsp, up, usp, dp, dsp, hidden, route_weights, out,
+                                                expert_count, batch, inter, hid, gsc, dsc);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_many_row_weighted_f32(
+    const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp, const uint64_t* dp,
+    const uint64_t* dsp, const float* hidden, const float* route_weights, float* out, int64_t expert_count,
+    int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
+    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden || !route_weights || !out)
+        return plm::fail(-1, "null pointer");
+    if (moe_dims_bad(expert_count, batch, inter, hid, gsc, dsc)) return plm::fail(-2, "bad dimensions");
+    return weighted_moe(gp, gsp, up, usp, dp, dsp, Act{hidden, nullptr}, route_weights, batch, 1, true, out,
+                        expert_count, batch, inter, hid, gsc, dsc);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_many_row_weighted_bf16x_f32(
+    const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp, const uint64_t* dp,
+    const uint64_t* dsp, const uint16_t* hidden_bf16, const float* route_weights, float* out, int64_t expert_count,
+    int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
+    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden_bf16 || !route_weights || !out)
+        return plm::fail(-1, "null pointer");
+    if (moe_dims_bad(expert_count, batch, inter, hid, gsc, dsc)) return plm::fail(-2, "bad dimensions");
+    return weighted_moe(gp, gsp, up, usp, dp, dsp, Act{nullptr, hidden_bf16}, route_weights, batch, 1, true, out,
+                        expert_count, batch, inter, hid, gsc, dsc);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_many_pair_weighted_f32(
+    const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp, const uint64_t* dp,
+    const uint64_t* dsp, const float* hidden, const int64_t* pair_item_indices, const int64_t* pair_row_indices,
+    const float* pair_weights, float* out, int64_t expert_count, int64_t pair_count, int64_t batch, int64_t inter,
+    int64_t hid, int64_t gsc, int64_t dsc) {
+    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden || !pair_item_indices || !pair_row_indices ||
+        !pair_weights || !out)
+        return plm::fail(-1, "null pointer");
+    return pair_weighted_impl(gp, gsp, up, usp, dp, dsp, Act{hidden, nullptr}, pair_item_indices, pair_row_indices,
+                              pair_weights, out, expert_count, pair_count, batch, inter, hid, gsc, dsc);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_many_pair_weighted_bf16x_f32(
+    const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp, const uint64_t* dp,
+    const uint64_t* dsp, const uint16_t* hidden_bf16, const int64_t* pair_item_indices,
+    const int64_t* pair_row_indices, const float* pair_weights, float* out, int64_t expert_count, int64_t pair_count,
+    int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
+    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden_bf16 || !pair_item_indices || !pair_row_indices ||
+        !pair_weights || !out)
+        return plm::fail(-1, "null pointer");
+    return pair_weighted_impl(gp, gsp, up, usp, dp, dsp, Act{nullptr, hidden_bf16}, pair_item_indices,
+                              pair_row_indices, pair_weights, out, expert_count, pair_count, batch, inter, hid, gsc,
+                              dsc);
 }
 
 // Used by the DeepSeek session entry points (ds_session.hip).

@@ -17,6 +17,10 @@ purpose:
   package: a missing library raises.
 * FP8 weights may be given as ``torch.uint8`` or ``torch.float8_e4m3fn``;
   both are read as raw e4m3 bytes.
+* bf16 activations go to the ``*_bf16x_f32`` twin of an FP8 entry point
+  where one exists, instead of being widened to fp32 first as the reference
+  wrappers do: the twin widens them exactly on the device, so the results
+  are the same, and reads half the activation bytes.
 """
 
 from __future__ import annotations
@@ -236,6 +240,20 @@ def _hidden_f32(hidden: torch.Tensor, dev: torch.device) -> torch.Tensor:
     return _on(hidden, dev).reshape(-1, int(hidden.shape[-1])).to(torch.float32).contiguous()
 
 
+def _hidden_in(hidden: torch.Tensor, dev: torch.device) -> tuple[torch.Tensor, bool]:
+    """Activations for an entry point with a bf16 twin: bf16 ones stay bf16
+    (the twin widens them on the device, exactly, so the results are those of
+    the reference wrapper's cast to fp32), others become fp32."""
+    if hidden.dtype == torch.bfloat16:
+        return _on(hidden, dev).reshape(-1, int(hidden.shape[-1])).contiguous(), True
+    return _hidden_f32(hidden, dev), False
+
+
+def _twin(name: str, bf16: bool) -> str:
+    """The bf16-activation twin of an fp32 entry point name."""
+    return name[:-len("_f32")] + "_bf16x_f32" if bf16 else name
+
+
 def fp8_e4m3_block_linear_f32(fp8_weight: torch.Tensor, scale_inv: torch.Tensor, hidden: torch.Tensor) -> torch.Tensor:
     """src/pcketlm/native/__init__.py:3442-3476 -> fp8_linear.cpp:50-117."""
     lib = _require("PCKETLM_DISABLE_NATIVE_FP8_LINEAR", "Native FP8 linear")
@@ -244,7 +262,7 @@ def fp8_e4m3_block_linear_f32(fp8_weight: torch.Tensor, scale_inv: torch.Tensor,
     if scale_inv.ndim != 2:
         raise ValueError("scale_inv must have shape [scale_rows, scale_cols]")
     dev = _target_device(fp8_weight, scale_inv, hidden)
-    x = _hidden_f32(hidden, dev)
+    x, bf16 = _hidden_in(hidden, dev)
     w = _fp8_bytes(fp8_weight, dev)
     s = _on(scale_inv, dev, torch.float32)
     out_rows, in_cols = int(w.shape[0]), int(w.shape[1])
@@ -254,8 +272,8 @@ def fp8_e4m3_block_linear_f32(fp8_weight: torch.Tensor, scale_inv: torch.Tensor,
         raise ValueError("scale_inv shape does not match FP8 128x128 block layout")
     out = torch.empty((int(x.shape[0]), out_rows), dtype=torch.float32, device=dev)
     with _launch(lib, dev):
-        code = lib.fp8_e4m3_block_linear_f32(_p(w), _p(s), _p(x), _p(out), int(x.shape[0]), out_rows, in_cols,
-                                             (in_cols + 127) // 128)
+        code = getattr(lib, _twin("fp8_e4m3_block_linear_f32", bf16))(_p(w), _p(s), _p(x), _p(out), int(x.shape[0]),
+                                                                    out_rows, in_cols, (in_cols + 127) // 128)
     _check("fp8_e4m3_block_linear_f32", code)
     return _home(out, hidden)
 
@@ -278,7 +296,7 @@ def fp8_e4m3_block_dual_linear_f32(
     sa, sb = _on(scale_inv_a, dev, torch.float32), _on(scale_inv_b, dev, torch.float32)
     if tuple(sa.shape) != tuple(sb.shape):
         raise ValueError("dual FP8 scales must have matching shapes")
-    x = _hidden_f32(hidden, dev)
+    x, bf16 = _hidden_in(hidden, dev)
     out_rows, in_cols = int(wa.shape[0]), int(wa.shape[1])
     if int(x.shape[1]) != in_cols:
         raise ValueError("hidden input size does not match FP8 weight columns")
@@ -287,8 +305,9 @@ def fp8_e4m3_block_dual_linear_f32(
     out_a = torch.empty((int(x.shape[0]), out_rows), dtype=torch.float32, device=dev)
     out_b = torch.empty_like(out_a)
     with _launch(lib, dev):
-        code = lib.fp8_e4m3_block_dual_linear_f32(_p(wa), _p(sa), _p(wb), _p(sb), _p(x), _p(out_a), _p(out_b),
-                                                  int(x.shape[0]), out_rows, in_cols, (in_cols + 127) // 128)
+        code = getattr(lib, _twin("fp8_e4m3_block_dual_linear_f32", bf16))(
+            _p(wa), _p(sa), _p(wb), _p(sb), _p(x), _p(out_a), _p(out_b), int(x.shape[0]), out_rows, in_cols,
+            (in_cols + 127) // 128)
     _check("fp8_e4m3_block_dual_linear_f32", code)
     return _home(out_a, hidden), _home(out_b, hidden)
 
@@ -311,22 +330,23 @@ def _mlp_common(gate_weight, gate_scale_inv, up_weight, up_scale_inv, down_weigh
         raise ValueError("FP8 MLP gate scale shape does not match 128x128 block layout")
     if tuple(ds.shape) != eds:
         raise ValueError("FP8 MLP down scale shape does not match 128x128 block layout")
-    x = _hidden_f32(hidden, dev)
+    x, bf16 = _hidden_in(hidden, dev)
     if int(x.shape[1]) != hid:
         raise ValueError("hidden input size does not match FP8 MLP input size")
-    return g, gs, u, us, d, ds, x, inter, hid, egs[1], eds[1]
+    return g, gs, u, us, d, ds, x, bf16, inter, hid, egs[1], eds[1]
 
 
 def _run_mlp(symbol: str, kill: str, what: str, gate_weight, gate_scale_inv, up_weight, up_scale_inv, down_weight,
              down_scale_inv, hidden) -> torch.Tensor:
     lib = _require(kill, what)
     dev = _target_device(gate_weight, up_weight, down_weight, hidden)
-    g, gs, u, us, d, ds, x, inter, hid, gsc, dsc = _mlp_common(
+    g, gs, u, us, d, ds, x, bf16, inter, hid, gsc, dsc = _mlp_common(
         gate_weight, gate_scale_inv, up_weight, up_scale_inv, down_weight, down_scale_inv, hidden, dev)
     out = torch.empty((int(x.shape[0]), hid), dtype=torch.float32, device=dev)
+    entry = "fp8_e4m3_block_mlp_bf16x_f32" if bf16 else symbol  # one kernel behind both MLP names
     with _launch(lib, dev):
-        code = getattr(lib, symbol)(_p(g), _p(gs), _p(u), _p(us), _p(d), _p(ds), _p(x), _p(out), int(x.shape[0]),
-                                    inter, hid, gsc, dsc)
+        code = getattr(lib, entry)(_p(g), _p(gs), _p(u), _p(us), _p(d), _p(ds), _p(x), _p(out), int(x.shape[0]),
+                                   inter, hid, gsc, dsc)
     _check(symbol, code)
     return _home(out, hidden)
 
@@ -348,7 +368,7 @@ def fp8_e4m3_block_mlp_avx512_f32(gate_weight, gate_scale_inv, up_weight, up_sca
 class _Experts:
     """Validated expert weights on one device plus the six host address tables."""
 
-    def __init__(self, items, hidden, dev: torch.device):
+    def __init__(self, items, hidden, dev: torch.device, bf16_ok: bool = False):
         if not items:
             raise ValueError("items must not be empty")
         first = _fp8_bytes(items[0][0], dev)
@@ -375,7 +395,8 @@ class _Experts:
         self.prepared = prepared
         self.count = len(prepared)
         self.tables = [(ctypes.c_uint64 * self.count)(*[int(p[i].data_ptr()) for p in prepared]) for i in range(6)]
-        self.x = _hidden_f32(hidden, dev)
+        # bf16_ok: the caller has a bf16 twin to send bf16 activations to
+        self.x, self.bf16 = _hidden_in(hidden, dev) if bf16_ok else (_hidden_f32(hidden, dev), False)
         if int(self.x.shape[1]) != self.hid:
             raise ValueError("hidden input size does not match FP8 MLP input size")
 
@@ -399,7 +420,7 @@ def fp8_e4m3_block_mlp_many_f32(items, hidden: torch.Tensor) -> torch.Tensor:
 def _weighted(symbol: str, kill: str, what: str, items, hidden, route_weights, *, per_row: bool) -> torch.Tensor:
     lib = _require(kill, what)
     dev = _target_device(hidden, *(items[0] if items else ()))
-    ex = _Experts(items, hidden, dev)
+    ex = _Experts(items, hidden, dev, bf16_ok=symbol == "fp8_e4m3_block_mlp_many_row_weighted_f32")
     batch = int(ex.x.shape[0])
     if per_row:
         route = _on(route_weights, dev, torch.float32)
@@ -411,8 +432,8 @@ def _weighted(symbol: str, kill: str, what: str, items, hidden, route_weights, *
             raise ValueError("route_weights length must match item count")
     out = torch.empty((batch, ex.hid), dtype=torch.float32, device=dev)
     with _launch(lib, dev):
-        code = getattr(lib, symbol)(*ex.table_args(), _p(ex.x), _p(route), _p(out), ex.count, batch, ex.inter,
-                                    ex.hid, ex.gsc, ex.dsc)
+        code = getattr(lib, _twin(symbol, ex.bf16))(*ex.table_args(), _p(ex.x), _p(route), _p(out), ex.count,
+                                                    batch, ex.inter, ex.hid, ex.gsc, ex.dsc)
     _check(symbol, code)
     return _home(out, hidden)
 
@@ -466,7 +487,7 @@ def fp8_e4m3_block_mlp_many_pair_weighted_f32(items, hidden, pair_item_indices, 
     """src/pcketlm/native/__init__.py:3870-3948 -> fp8_linear.cpp:833-980."""
     lib = _require("PCKETLM_DISABLE_NATIVE_FP8_LINEAR", "Native FP8 pair-weighted many-MLP")
     dev = _target_device(hidden, *(items[0] if items else ()))
-    ex = _Experts(items, hidden, dev)
+    ex = _Experts(items, hidden, dev, bf16_ok=True)
     pi = _on(pair_item_indices, dev, torch.int64).reshape(-1)
     pr = _on(pair_row_indices, dev, torch.int64).reshape(-1)
     pw = _on(pair_weights, dev, torch.float32).reshape(-1)
@@ -475,9 +496,9 @@ def fp8_e4m3_block_mlp_many_pair_weighted_f32(items, hidden, pair_item_indices, 
     batch = int(ex.x.shape[0])
     out = torch.empty((batch, ex.hid), dtype=torch.float32, device=dev)
     with _launch(lib, dev):
-        code = lib.fp8_e4m3_block_mlp_many_pair_weighted_f32(*ex.table_args(), _p(ex.x), _p(pi), _p(pr), _p(pw),
-                                                             _p(out), ex.count, int(pi.numel()), batch, ex.inter,
-                                                             ex.hid, ex.gsc, ex.dsc)
+        code = getattr(lib, _twin("fp8_e4m3_block_mlp_many_pair_weighted_f32", ex.bf16))(
+            *ex.table_args(), _p(ex.x), _p(pi), _p(pr), _p(pw), _p(out), ex.count, int(pi.numel()), batch, ex.inter,
+            ex.hid, ex.gsc, ex.dsc)
     _check("fp8_e4m3_block_mlp_many_pair_weighted_f32", code)
     return _home(out, hidden)
 

@@ -316,6 +316,46 @@ def test_weighted_with_shared_expert_equals_separate_calls(nat, oracle_mod, gold
     assert rel_l2(host(ys3), oracle_mod.fp8_mlp(*odd[3], xo_h)) < TOL
 
 
+def test_bf16_activation_twins_equal_fp32_calls(nat):
+    """bf16 activations go to the *_bf16x_f32 twins, which widen them on the
+    device: every twin returns exactly what its fp32 entry point returns for
+    the widened activations (the reference wrappers' cast), at 1..8 rows,
+    batch rows equal single-row calls, and the odd-K scalar path agrees."""
+    w, s = synth_fp8(1536, 7168, 900)
+    x16 = dev(synth_x(8, 7168, 901)).to(torch.bfloat16)
+    for m in (1, 2, 3, 4, 8):
+        y16 = nat.fp8_e4m3_block_linear_f32(dev(w), dev(s), x16[:m])
+        assert torch.equal(y16, nat.fp8_e4m3_block_linear_f32(dev(w), dev(s), x16[:m].float()))
+    rows = torch.cat([nat.fp8_e4m3_block_linear_f32(dev(w), dev(s), x16[i:i + 1]) for i in range(5)])
+    assert torch.equal(rows, nat.fp8_e4m3_block_linear_f32(dev(w), dev(s), x16[:5]))
+    wb, sb = synth_fp8(1536, 7168, 902)
+    a16, b16 = nat.fp8_e4m3_block_dual_linear_f32(dev(w), dev(s), dev(wb), dev(sb), x16[:4])
+    a32, b32 = nat.fp8_e4m3_block_dual_linear_f32(dev(w), dev(s), dev(wb), dev(sb), x16[:4].float())
+    assert torch.equal(a16, a32) and torch.equal(b16, b32)
+    items = []
+    for e in range(3):
+        g, gs = synth_fp8(256, 7168, 910 + 3 * e)
+        u, us = synth_fp8(256, 7168, 911 + 3 * e)
+        d, ds = synth_fp8(7168, 256, 912 + 3 * e)
+        items.append((g, gs, u, us, d, ds))
+    di = cuda_items(items)
+    assert torch.equal(nat.fp8_e4m3_block_mlp_f32(*di[0], x16[:3]), nat.fp8_e4m3_block_mlp_f32(*di[0], x16[:3].float()))
+    route = dev((np.random.default_rng(5).uniform(0.0, 0.5, (3, 4)) *
+                 (np.random.default_rng(6).uniform(size=(3, 4)) > 0.3)).astype(np.float32))
+    assert torch.equal(nat.fp8_e4m3_block_mlp_many_row_weighted_f32(di, x16[:4], route),
+                       nat.fp8_e4m3_block_mlp_many_row_weighted_f32(di, x16[:4].float(), route))
+    pi = torch.tensor([0, 0, 1, 2, 2], dtype=torch.int64, device="cuda")
+    pr = torch.tensor([0, 3, 1, 0, 2], dtype=torch.int64, device="cuda")
+    pw = torch.tensor([0.25, 0.5, 0.125, 0.75, 0.375], device="cuda")
+    assert torch.equal(nat.fp8_e4m3_block_mlp_many_pair_weighted_f32(di, x16[:4], pi, pr, pw),
+                       nat.fp8_e4m3_block_mlp_many_pair_weighted_f32(di, x16[:4].float(), pi, pr, pw))
+    # K not a multiple of 16: the one-thread-per-output kernel reads bf16 too
+    wo, so = synth_fp8(40, 72, 920)
+    xo = dev(synth_x(3, 72, 921)).to(torch.bfloat16)
+    assert torch.equal(nat.fp8_e4m3_block_linear_f32(dev(wo), dev(so), xo),
+                       nat.fp8_e4m3_block_linear_f32(dev(wo), dev(so), xo.float()))
+
+
 # --------------------------------------------------------------------------- DeepSeek session
 
 def test_ds_session_combine_kat_and_counters(nat):
