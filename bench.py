@@ -557,7 +557,7 @@ def table(args):
         return (g[0], g[1], u[0], u[1], d[0], d[1])
 
     layers = [[expert() for _ in range(9)] for _ in range(3)]  # 3 x 396 MB
-    x = torch.randn((1, 7168), generator=gen, device="cuda").to(torch.bfloat16).float()
+    x = torch.randn((1, 7168), generator=gen, device="cuda").to(torch.bfloat16)  # bf16 hidden state
     logits = torch.randn((1, 256), generator=gen, device="cuda")
     _idx, rw = native.route_deepseek(logits)
     rw = rw.float().reshape(-1).contiguous()
@@ -567,7 +567,7 @@ def table(args):
     # one call per layer: the 8 routed experts (route-weighted sum) and the
     # shared expert (its own output) in one gate/up and one down launch
     moe_tables = [[(ctypes.c_uint64 * 9)(*[t[i].data_ptr() for t in layer]) for i in range(6)] for layer in layers]
-    calls = [lambda t=tables: lib.fp8_e4m3_block_mlp_many_weighted_shared_f32(
+    calls = [lambda t=tables: lib.fp8_e4m3_block_mlp_many_weighted_shared_bf16x_f32(
         *[ctypes.cast(a, ctypes.c_void_p) for a in t], ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(rw.data_ptr()),
         ctypes.c_void_p(y.data_ptr()), ctypes.c_void_p(ys.data_ptr()), 8, 1, 2048, 7168, 56, 16)
         for tables in moe_tables]
@@ -575,7 +575,7 @@ def table(args):
     per_expert = 3 * 2048 * 7168 + 3 * 4 * 16 * 56
     for fn in calls:
         if fn() != 0:
-            raise RuntimeError("fp8_e4m3_block_mlp_many_weighted_shared_f32 failed")
+            raise RuntimeError("fp8_e4m3_block_mlp_many_weighted_shared_bf16x_f32 failed")
     torch.cuda.synchronize()
     launches = [calls[i % len(calls)] for i in range(30)]
     med = timer.run(launches) / len(launches)
@@ -588,7 +588,7 @@ def table(args):
         # the oracle's weighted many-expert MLP plus the shared expert's MLP on one layer
         routed = [tuple(t.cpu().numpy() for t in e) for e in layers[0][:8]]
         shared = tuple(t.cpu().numpy() for t in layers[0][8])
-        hx, hr = x.cpu().numpy(), rw.cpu().numpy()
+        hx, hr = x.float().cpu().numpy(), rw.cpu().numpy()
         t0 = time.perf_counter()
         n = 0
         while True:

@@ -187,7 +187,8 @@ int fp8_e4m3_block_mlp_many_pair_weighted_f32(
 
 /* bf16-activation twins.  The reference wrappers cast the activations to
  * fp32 before these calls (native/__init__.py:3451 linear, 3500 dual, 3568
- * MLP, 3834 row-weighted, 3910 pair-weighted); the twins take bf16
+ * MLP, 3760 weighted, 3834 row-weighted, 3910 pair-weighted; the routed +
+ * shared call has no reference wrapper); the twins take bf16
  * activations [batch, hidden] as they are and widen them on the device.  The
  * widening is exact, so each twin returns exactly the values of its fp32
  * entry point for the widened activations; they only read half the
@@ -207,6 +208,20 @@ int fp8_e4m3_block_mlp_bf16x_f32(const uint8_t* gate_weight, const float* gate_s
                                  const uint16_t* hidden_bf16, float* out, int64_t batch,
                                  int64_t intermediate_rows, int64_t hidden_cols,
                                  int64_t gate_scale_cols, int64_t down_scale_cols);
+int fp8_e4m3_block_mlp_many_weighted_bf16x_f32(
+    const uint64_t* gate_weight_ptrs, const uint64_t* gate_scale_ptrs,
+    const uint64_t* up_weight_ptrs, const uint64_t* up_scale_ptrs,
+    const uint64_t* down_weight_ptrs, const uint64_t* down_scale_ptrs, const uint16_t* hidden_bf16,
+    const float* route_weights, float* out, int64_t expert_count, int64_t batch,
+    int64_t intermediate_rows, int64_t hidden_cols, int64_t gate_scale_cols,
+    int64_t down_scale_cols);
+int fp8_e4m3_block_mlp_many_weighted_shared_bf16x_f32(
+    const uint64_t* gate_weight_ptrs, const uint64_t* gate_scale_ptrs,
+    const uint64_t* up_weight_ptrs, const uint64_t* up_scale_ptrs,
+    const uint64_t* down_weight_ptrs, const uint64_t* down_scale_ptrs, const uint16_t* hidden_bf16,
+    const float* route_weights, float* out, float* out_shared, int64_t expert_count, int64_t batch,
+    int64_t intermediate_rows, int64_t hidden_cols, int64_t gate_scale_cols,
+    int64_t down_scale_cols);
 int fp8_e4m3_block_mlp_many_row_weighted_bf16x_f32(
     const uint64_t* gate_weight_ptrs, const uint64_t* gate_scale_ptrs,
     const uint64_t* up_weight_ptrs, const uint64_t* up_scale_ptrs,

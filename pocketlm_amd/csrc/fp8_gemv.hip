@@ -1135,6 +1135,31 @@ PLM_EXPORT int fp8_e4m3_block_mlp_many_weighted_shared_f32(const uint64_t* gp, c
                         expert_count, batch, inter, hid, gsc, dsc, out_shared);
 }
 
+PLM_EXPORT int fp8_e4m3_block_mlp_many_weighted_bf16x_f32(const uint64_t* gp, const uint64_t* gsp,
+                                                          const uint64_t* up, const uint64_t* usp,
+                                                          const uint64_t* dp, const uint64_t* dsp,
+                                                          const uint16_t* hidden_bf16, const float* route_weights,
+                                                          float* out, int64_t expert_count, int64_t batch,
+                                                          int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
+    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden_bf16 || !route_weights || !out)
+        return plm::fail(-1, "null pointer");
+    if (moe_dims_bad(expert_count, batch, inter, hid, gsc, dsc)) return plm::fail(-2, "bad dimensions");
+    return weighted_moe(gp, gsp, up, usp, dp, dsp, Act{nullptr, hidden_bf16}, route_weights, 1, 0, false, out,
+                        expert_count, batch, inter, hid, gsc, dsc);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_many_weighted_shared_bf16x_f32(
+    const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp, const uint64_t* dp,
+    const uint64_t* dsp, const uint16_t* hidden_bf16, const float* route_weights, float* out, float* out_shared,
+    int64_t expert_count, int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
+    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden_bf16 || !route_weights || !out || !out_shared)
+        return plm::fail(-1, "null pointer");
+    if (moe_dims_bad(expert_count, batch, inter, hid, gsc, dsc)) return plm::fail(-2, "bad dimensions");
+    if (expert_count + 1 > kMaxGroups) return plm::fail(-2, "at most %d routed experts with a shared one", kMaxGroups - 1);
+    return weighted_moe(gp, gsp, up, usp, dp, dsp, Act{nullptr, hidden_bf16}, route_weights, 1, 0, false, out,
+                        expert_count, batch, inter, hid, gsc, dsc, out_shared);
+}
+
 PLM_EXPORT int fp8_e4m3_block_mlp_many_weighted_avx512_f32(
     const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp, const uint64_t* dp,
     const uint64_t* dsp, const float* hidden, const float* route_weights, float* out, int64_t expert_count,

@@ -420,7 +420,8 @@ def fp8_e4m3_block_mlp_many_f32(items, hidden: torch.Tensor) -> torch.Tensor:
 def _weighted(symbol: str, kill: str, what: str, items, hidden, route_weights, *, per_row: bool) -> torch.Tensor:
     lib = _require(kill, what)
     dev = _target_device(hidden, *(items[0] if items else ()))
-    ex = _Experts(items, hidden, dev, bf16_ok=symbol == "fp8_e4m3_block_mlp_many_row_weighted_f32")
+    ex = _Experts(items, hidden, dev, bf16_ok=symbol in ("fp8_e4m3_block_mlp_many_row_weighted_f32",
+                                                         "fp8_e4m3_block_mlp_many_weighted_f32"))
     batch = int(ex.x.shape[0])
     if per_row:
         route = _on(route_weights, dev, torch.float32)
@@ -454,7 +455,7 @@ def fp8_e4m3_block_mlp_many_weighted_shared_f32(items, shared, hidden, route_wei
     dev = _target_device(hidden, *(items[0] if items else ()))
     if not items:
         raise ValueError("items must not be empty")
-    ex = _Experts(list(items) + [shared], hidden, dev)
+    ex = _Experts(list(items) + [shared], hidden, dev, bf16_ok=True)
     count = ex.count - 1
     route = _on(route_weights, dev, torch.float32).reshape(-1)
     if int(route.numel()) != count:
@@ -463,9 +464,9 @@ def fp8_e4m3_block_mlp_many_weighted_shared_f32(items, shared, hidden, route_wei
     out = torch.empty((batch, ex.hid), dtype=torch.float32, device=dev)
     out_shared = torch.empty((batch, ex.hid), dtype=torch.float32, device=dev)
     with _launch(lib, dev):
-        code = lib.fp8_e4m3_block_mlp_many_weighted_shared_f32(*ex.table_args(), _p(ex.x), _p(route), _p(out),
-                                                               _p(out_shared), count, batch, ex.inter, ex.hid,
-                                                               ex.gsc, ex.dsc)
+        code = getattr(lib, _twin("fp8_e4m3_block_mlp_many_weighted_shared_f32", ex.bf16))(
+            *ex.table_args(), _p(ex.x), _p(route), _p(out), _p(out_shared), count, batch, ex.inter, ex.hid, ex.gsc,
+            ex.dsc)
     _check("fp8_e4m3_block_mlp_many_weighted_shared_f32", code)
     return _home(out, hidden), _home(out_shared, hidden)
 

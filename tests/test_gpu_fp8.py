@@ -344,6 +344,12 @@ def test_bf16_activation_twins_equal_fp32_calls(nat):
                  (np.random.default_rng(6).uniform(size=(3, 4)) > 0.3)).astype(np.float32))
     assert torch.equal(nat.fp8_e4m3_block_mlp_many_row_weighted_f32(di, x16[:4], route),
                        nat.fp8_e4m3_block_mlp_many_row_weighted_f32(di, x16[:4].float(), route))
+    rw = dev(np.array([0.5, 0.25], dtype=np.float32))
+    assert torch.equal(nat.fp8_e4m3_block_mlp_many_weighted_f32(di[:2], x16[:1], rw),
+                       nat.fp8_e4m3_block_mlp_many_weighted_f32(di[:2], x16[:1].float(), rw))
+    ya, ysa = nat.fp8_e4m3_block_mlp_many_weighted_shared_f32(di[:2], di[2], x16[:1], rw)
+    yb, ysb = nat.fp8_e4m3_block_mlp_many_weighted_shared_f32(di[:2], di[2], x16[:1].float(), rw)
+    assert torch.equal(ya, yb) and torch.equal(ysa, ysb)
     pi = torch.tensor([0, 0, 1, 2, 2], dtype=torch.int64, device="cuda")
     pr = torch.tensor([0, 3, 1, 0, 2], dtype=torch.int64, device="cuda")
     pw = torch.tensor([0.25, 0.5, 0.125, 0.75, 0.375], device="cuda")
