@@ -47,6 +47,9 @@ def _args(argv=None):
     ap.add_argument("--table-out", default=None, help="also write the table to this file")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample length")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default=None,
+                    help="table: measure only the workloads whose name contains one of these comma-separated "
+                         "strings (for profiling one workload)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="run a few default steps, then a plain 256 MiB device copy, for counter runs "
                          "(rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE); prints nothing else")
@@ -297,8 +300,14 @@ def table(args):
     lib = _lib.load()
     timer = Timer(torch)
     rows_out = []
+    only = [t for t in (args.only or "").split(",") if t]
+
+    def want(*names):
+        return not only or any(t in n for n in names for t in only)
 
     def measure(name, m, make_calls, nbytes, cpu_fn=None, cpu_kind="port"):
+        if not want(name):
+            return
         calls = make_calls()
         for fn in calls[: min(len(calls), 8)]:
             code = fn()
@@ -341,6 +350,8 @@ def table(args):
     for name, rows, cols in (("fp8 linear 2048x7168", 2048, 7168), ("fp8 q_a 1536x7168", 1536, 7168),
                              ("fp8 kv_a 576x7168", 576, 7168), ("fp8 o 7168x16384", 7168, 16384),
                              ("fp8 expert gate/up 2048x7168", 2048, 7168), ("fp8 expert down 7168x2048", 7168, 2048)):
+        if not want(name):
+            continue
         count = max(2, math.ceil(MALL_BYTES / (rows * cols)))
         sets = fp8_sets(rows, cols, count)
         host_w, host_s = sets[0][0].cpu().numpy(), sets[0][1].cpu().numpy()
@@ -365,10 +376,10 @@ def table(args):
         torch.cuda.empty_cache()
 
     # ---- FP8 dequant (config 1 matrix)
-    sets = fp8_sets(2048, 7168, 24)
+    sets = fp8_sets(2048, 7168, 24) if want("fp8 dequant") else []
     out16 = torch.empty((2048, 7168), device="cuda", dtype=torch.float16)
     lib.pocketlm_set_stream(_stream_ptr(torch))
-    hw, hs = sets[0][0].cpu().numpy(), sets[0][1].cpu().numpy()
+    hw, hs = (sets[0][0].cpu().numpy(), sets[0][1].cpu().numpy()) if sets else (None, None)
     measure("fp8 dequant->fp16 2048x7168", 1,
             lambda: [lambda w=w, s=s: lib.fp8_e4m3_dequant_to_fp16(ctypes.c_void_p(w.data_ptr()),
                                                                  ctypes.c_void_p(s.data_ptr()),
@@ -380,7 +391,7 @@ def table(args):
 
     # ---- Q4 (config 2)
     shapes = [(18944, 3584), (18944, 3584), (3584, 18944)]
-    qsets = _q4_sets(torch, formats, shapes, 10)
+    qsets = _q4_sets(torch, formats, shapes, 10 if want("q4") else 1)
     xq = torch.randn((3584,), generator=gen, device="cuda").to(torch.float16)
     xd = torch.randn((18944,), generator=gen, device="cuda").to(torch.float16)
     yq = torch.empty((18944,), device="cuda")
@@ -432,6 +443,8 @@ def table(args):
     # ---- row8 (config 3)
     for name, rows, cols in (("row8 q/o 3584x3584", 3584, 3584), ("row8 k/v 512x3584", 512, 3584),
                              ("row8 gate/up 18944x3584", 18944, 3584), ("row8 down 3584x18944", 3584, 18944)):
+        if not want(name, name.replace("row8", "row8 f32-x")):
+            continue
         count = max(2, math.ceil(MALL_BYTES / (2 * rows * cols)))
         packs = []
         for _ in range(count):
@@ -461,149 +474,157 @@ def table(args):
         del packs
         torch.cuda.empty_cache()
 
-    # ---- row8 dense decode layer (config 3) as the decode calls it: q/k/v in one
-    # launch, o on the fp32 attention output, gate/up in one launch, down on the
-    # fp32 intermediate (Qwen2.5-7B: 466 MB of packed weights per layer)
-    H, I, KV = 3584, 18944, 512
-    shapes = {"q": (H, H), "k": (KV, H), "v": (KV, H), "o": (H, H), "gate": (I, H), "up": (I, H), "down": (H, I)}
+    def dense_layer():
+        # ---- row8 dense decode layer (config 3) as the decode calls it: q/k/v in one
+        # launch, o on the fp32 attention output, gate/up in one launch, down on the
+        # fp32 intermediate (Qwen2.5-7B: 466 MB of packed weights per layer)
+        H, I, KV = 3584, 18944, 512
+        shapes = {"q": (H, H), "k": (KV, H), "v": (KV, H), "o": (H, H), "gate": (I, H), "up": (I, H), "down": (H, I)}
 
-    def packed(rows, cols):
-        w = torch.randn((rows, cols), generator=gen, device="cuda").mul_(0.02).to(torch.float16)
-        p = native.pack_weight_rows8(w)
-        del w
-        return p
+        def packed(rows, cols):
+            w = torch.randn((rows, cols), generator=gen, device="cuda").mul_(0.02).to(torch.float16)
+            p = native.pack_weight_rows8(w)
+            del w
+            return p
 
-    dense = [{k: packed(*v) for k, v in shapes.items()} for _ in range(3)]  # 3 x 466 MB
-    h16 = torch.randn((H,), generator=gen, device="cuda").to(torch.float16)
-    attn = torch.randn((H,), generator=gen, device="cuda")
-    act = torch.randn((I,), generator=gen, device="cuda")
-    outs = {k: torch.empty((v[0],), device="cuda") for k, v in shapes.items()}
-    lib.pocketlm_set_stream(_stream_ptr(torch))
+        dense = [{k: packed(*v) for k, v in shapes.items()} for _ in range(3)]  # 3 x 466 MB
+        h16 = torch.randn((H,), generator=gen, device="cuda").to(torch.float16)
+        attn = torch.randn((H,), generator=gen, device="cuda")
+        act = torch.randn((I,), generator=gen, device="cuda")
+        outs = {k: torch.empty((v[0],), device="cuda") for k, v in shapes.items()}
+        lib.pocketlm_set_stream(_stream_ptr(torch))
 
-    def many(layer, names):
-        pp = (ctypes.c_void_p * len(names))(*[layer[n].data_ptr() for n in names])
-        bp = (ctypes.c_void_p * len(names))()
-        op = (ctypes.c_void_p * len(names))(*[outs[n].data_ptr() for n in names])
-        rr = (ctypes.c_longlong * len(names))(*[shapes[n][0] for n in names])
-        keep = (pp, bp, op, rr)
-        return lambda keep=keep: lib.native_packed_gemv_rows8_many(
-            ctypes.c_void_p(h16.data_ptr()), ctypes.cast(keep[0], ctypes.c_void_p), ctypes.cast(keep[1], ctypes.c_void_p),
-            ctypes.cast(keep[2], ctypes.c_void_p), ctypes.cast(keep[3], ctypes.c_void_p), len(names), H, 0)
+        def many(layer, names):
+            pp = (ctypes.c_void_p * len(names))(*[layer[n].data_ptr() for n in names])
+            bp = (ctypes.c_void_p * len(names))()
+            op = (ctypes.c_void_p * len(names))(*[outs[n].data_ptr() for n in names])
+            rr = (ctypes.c_longlong * len(names))(*[shapes[n][0] for n in names])
+            keep = (pp, bp, op, rr)
+            return lambda keep=keep: lib.native_packed_gemv_rows8_many(
+                ctypes.c_void_p(h16.data_ptr()), ctypes.cast(keep[0], ctypes.c_void_p), ctypes.cast(keep[1], ctypes.c_void_p),
+                ctypes.cast(keep[2], ctypes.c_void_p), ctypes.cast(keep[3], ctypes.c_void_p), len(names), H, 0)
 
-    def f32x(layer, name, x):
-        rows, cols = shapes[name]
-        return lambda: lib.native_packed_gemv_rows8_f32_hidden(ctypes.c_void_p(x.data_ptr()),
-                                                               ctypes.c_void_p(layer[name].data_ptr()),
-                                                               ctypes.c_void_p(outs[name].data_ptr()), rows, cols, 0)
+        def f32x(layer, name, x):
+            rows, cols = shapes[name]
+            return lambda: lib.native_packed_gemv_rows8_f32_hidden(ctypes.c_void_p(x.data_ptr()),
+                                                                   ctypes.c_void_p(layer[name].data_ptr()),
+                                                                   ctypes.c_void_p(outs[name].data_ptr()), rows, cols, 0)
 
-    def wbytes(names):
-        return sum(2 * math.ceil(shapes[n][0] / 8) * 8 * shapes[n][1] + 4 * shapes[n][0] for n in names)
+        def wbytes(names):
+            return sum(2 * math.ceil(shapes[n][0] / 8) * 8 * shapes[n][1] + 4 * shapes[n][0] for n in names)
 
-    host = {k: dense[0][k].cpu().view(torch.int16).numpy().view(np.uint16) for k in shapes}
-    hh16 = h16.cpu().view(torch.int16).numpy().view(np.uint16)
-    hattn, hact = attn.cpu().numpy(), act.cpu().numpy()
+        host = {k: dense[0][k].cpu().view(torch.int16).numpy().view(np.uint16) for k in shapes}
+        hh16 = h16.cpu().view(torch.int16).numpy().view(np.uint16)
+        hattn, hact = attn.cpu().numpy(), act.cpu().numpy()
 
-    def cpu_many(names):
-        return lambda: [oracle.packed_gemv_rows8(hh16, host[n], shapes[n][0], shapes[n][1], 0) for n in names]
+        def cpu_many(names):
+            return lambda: [oracle.packed_gemv_rows8(hh16, host[n], shapes[n][0], shapes[n][1], 0) for n in names]
 
-    measure("row8 q/k/v (one launch)", 1, lambda: [many(l, ["q", "k", "v"]) for l in dense],
-            wbytes(["q", "k", "v"]) + 2 * H, cpu_many(["q", "k", "v"]))
-    measure("row8 gate/up (one launch)", 1, lambda: [many(l, ["gate", "up"]) for l in dense],
-            wbytes(["gate", "up"]) + 2 * H, cpu_many(["gate", "up"]))
+        measure("row8 q/k/v (one launch)", 1, lambda: [many(l, ["q", "k", "v"]) for l in dense],
+                wbytes(["q", "k", "v"]) + 2 * H, cpu_many(["q", "k", "v"]))
+        measure("row8 gate/up (one launch)", 1, lambda: [many(l, ["gate", "up"]) for l in dense],
+                wbytes(["gate", "up"]) + 2 * H, cpu_many(["gate", "up"]))
 
-    def layer_calls():
-        out = []
-        for l in dense:
-            out += [many(l, ["q", "k", "v"]), f32x(l, "o", attn), many(l, ["gate", "up"]), f32x(l, "down", act)]
-        return out
+        def layer_calls():
+            out = []
+            for l in dense:
+                out += [many(l, ["q", "k", "v"]), f32x(l, "o", attn), many(l, ["gate", "up"]), f32x(l, "down", act)]
+            return out
 
-    def cpu_layer():
-        cpu_many(["q", "k", "v"])()
-        oracle.packed_gemv_rows8_f32_hidden(hattn, host["o"], H, H, 0)
-        cpu_many(["gate", "up"])()
-        oracle.packed_gemv_rows8_f32_hidden(hact, host["down"], H, I, 0)
+        def cpu_layer():
+            cpu_many(["q", "k", "v"])()
+            oracle.packed_gemv_rows8_f32_hidden(hattn, host["o"], H, H, 0)
+            cpu_many(["gate", "up"])()
+            oracle.packed_gemv_rows8_f32_hidden(hact, host["down"], H, I, 0)
 
-    layer_bytes = wbytes(list(shapes)) + 2 * H * 2 + 4 * H + 4 * I
-    calls = layer_calls()
-    for fn in calls:
-        fn()
-    torch.cuda.synchronize()
-    launches = [calls[i % len(calls)] for i in range(4 * 30)]
-    med = timer.run(launches) / 30
-    gbs = layer_bytes / (med / 1e3) / 1e9
-    cpu_us = cpu_gbs = None
-    if not args.no_cpu:
-        t0 = time.perf_counter()
-        n = 0
-        while True:
-            cpu_layer()
-            n += 1
-            if time.perf_counter() - t0 > 1.5:
-                break
-        cpu_us = (time.perf_counter() - t0) / n * 1e6
-        cpu_gbs = layer_bytes / (cpu_us / 1e6) / 1e9
-    print(f"{'row8 dense layer (4 launches)':40s} M=1  {1e3 * med:9.2f} us  {gbs:8.1f} GB/s  "
-          f"{100 * gbs / PEAK_HBM_GBS:5.1f}%", flush=True)
-    rows_out.append(("row8 dense layer (4 launches)", 1, 1e3 * med, gbs, 100 * gbs / PEAK_HBM_GBS, cpu_us, cpu_gbs,
-                     "port"))
-    del dense, host
-    torch.cuda.empty_cache()
+        layer_bytes = wbytes(list(shapes)) + 2 * H * 2 + 4 * H + 4 * I
+        calls = layer_calls()
+        for fn in calls:
+            fn()
+        torch.cuda.synchronize()
+        launches = [calls[i % len(calls)] for i in range(4 * 30)]
+        med = timer.run(launches) / 30
+        gbs = layer_bytes / (med / 1e3) / 1e9
+        cpu_us = cpu_gbs = None
+        if not args.no_cpu:
+            t0 = time.perf_counter()
+            n = 0
+            while True:
+                cpu_layer()
+                n += 1
+                if time.perf_counter() - t0 > 1.5:
+                    break
+            cpu_us = (time.perf_counter() - t0) / n * 1e6
+            cpu_gbs = layer_bytes / (cpu_us / 1e6) / 1e9
+        print(f"{'row8 dense layer (4 launches)':40s} M=1  {1e3 * med:9.2f} us  {gbs:8.1f} GB/s  "
+              f"{100 * gbs / PEAK_HBM_GBS:5.1f}%", flush=True)
+        rows_out.append(("row8 dense layer (4 launches)", 1, 1e3 * med, gbs, 100 * gbs / PEAK_HBM_GBS, cpu_us, cpu_gbs,
+                         "port"))
+        del dense, host
+        torch.cuda.empty_cache()
 
-    # ---- DeepSeek-V3 MoE layer decode (config 4): 8 routed (weighted) + shared MLP
-    def expert():
-        g = fp8_sets(2048, 7168, 1)[0]
-        u = fp8_sets(2048, 7168, 1)[0]
-        d = fp8_sets(7168, 2048, 1)[0]
-        return (g[0], g[1], u[0], u[1], d[0], d[1])
+    if want("row8 dense", "row8 q/k/v (one", "row8 gate/up (one"):
+        dense_layer()
 
-    layers = [[expert() for _ in range(9)] for _ in range(3)]  # 3 x 396 MB
-    x = torch.randn((1, 7168), generator=gen, device="cuda").to(torch.bfloat16)  # bf16 hidden state
-    logits = torch.randn((1, 256), generator=gen, device="cuda")
-    _idx, rw = native.route_deepseek(logits)
-    rw = rw.float().reshape(-1).contiguous()
-    y = torch.empty((1, 7168), device="cuda")
-    ys = torch.empty((1, 7168), device="cuda")
-    lib.pocketlm_set_stream(_stream_ptr(torch))
-    # one call per layer: the 8 routed experts (route-weighted sum) and the
-    # shared expert (its own output) in one gate/up and one down launch
-    moe_tables = [[(ctypes.c_uint64 * 9)(*[t[i].data_ptr() for t in layer]) for i in range(6)] for layer in layers]
-    calls = [lambda t=tables: lib.fp8_e4m3_block_mlp_many_weighted_shared_bf16x_f32(
-        *[ctypes.cast(a, ctypes.c_void_p) for a in t], ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(rw.data_ptr()),
-        ctypes.c_void_p(y.data_ptr()), ctypes.c_void_p(ys.data_ptr()), 8, 1, 2048, 7168, 56, 16)
-        for tables in moe_tables]
+    def moe_layer():
+        # ---- DeepSeek-V3 MoE layer decode (config 4): 8 routed (weighted) + shared MLP
+        def expert():
+            g = fp8_sets(2048, 7168, 1)[0]
+            u = fp8_sets(2048, 7168, 1)[0]
+            d = fp8_sets(7168, 2048, 1)[0]
+            return (g[0], g[1], u[0], u[1], d[0], d[1])
 
-    per_expert = 3 * 2048 * 7168 + 3 * 4 * 16 * 56
-    for fn in calls:
-        if fn() != 0:
-            raise RuntimeError("fp8_e4m3_block_mlp_many_weighted_shared_bf16x_f32 failed")
-    torch.cuda.synchronize()
-    launches = [calls[i % len(calls)] for i in range(30)]
-    med = timer.run(launches) / len(launches)
-    nbytes = 9 * per_expert + 2 * 7168 * 4
-    gbs = nbytes / (med / 1e3) / 1e9
-    print(f"{'ds-v3 MoE layer (8 routed + shared, 2 launches)':40s} M=1  {1e3 * med:9.2f} us  {gbs:8.1f} GB/s  "
-          f"{100 * gbs / PEAK_HBM_GBS:5.1f}%", flush=True)
-    cpu_us = cpu_gbs = None
-    if not args.no_cpu:
-        # the oracle's weighted many-expert MLP plus the shared expert's MLP on one layer
-        routed = [tuple(t.cpu().numpy() for t in e) for e in layers[0][:8]]
-        shared = tuple(t.cpu().numpy() for t in layers[0][8])
-        hx, hr = x.float().cpu().numpy(), rw.cpu().numpy()
-        t0 = time.perf_counter()
-        n = 0
-        while True:
-            oracle.fp8_mlp_many_weighted(routed, hx, hr)
-            oracle.fp8_mlp(*shared, hx)
-            n += 1
-            if time.perf_counter() - t0 > 1.5:
-                break
-        cpu_us = (time.perf_counter() - t0) / n * 1e6
-        cpu_gbs = nbytes / (cpu_us / 1e6) / 1e9
-        del routed, shared
-    rows_out.append(("ds-v3 MoE layer (8 routed + shared, 2 launches)", 1, 1e3 * med, gbs, 100 * gbs / PEAK_HBM_GBS,
-                     cpu_us, cpu_gbs, "port"))
-    del layers
-    torch.cuda.empty_cache()
+        layers = [[expert() for _ in range(9)] for _ in range(3)]  # 3 x 396 MB
+        x = torch.randn((1, 7168), generator=gen, device="cuda").to(torch.bfloat16)  # bf16 hidden state
+        logits = torch.randn((1, 256), generator=gen, device="cuda")
+        _idx, rw = native.route_deepseek(logits)
+        rw = rw.float().reshape(-1).contiguous()
+        y = torch.empty((1, 7168), device="cuda")
+        ys = torch.empty((1, 7168), device="cuda")
+        lib.pocketlm_set_stream(_stream_ptr(torch))
+        # one call per layer: the 8 routed experts (route-weighted sum) and the
+        # shared expert (its own output) in one gate/up and one down launch
+        moe_tables = [[(ctypes.c_uint64 * 9)(*[t[i].data_ptr() for t in layer]) for i in range(6)] for layer in layers]
+        calls = [lambda t=tables: lib.fp8_e4m3_block_mlp_many_weighted_shared_bf16x_f32(
+            *[ctypes.cast(a, ctypes.c_void_p) for a in t], ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(rw.data_ptr()),
+            ctypes.c_void_p(y.data_ptr()), ctypes.c_void_p(ys.data_ptr()), 8, 1, 2048, 7168, 56, 16)
+            for tables in moe_tables]
+
+        per_expert = 3 * 2048 * 7168 + 3 * 4 * 16 * 56
+        for fn in calls:
+            if fn() != 0:
+                raise RuntimeError("fp8_e4m3_block_mlp_many_weighted_shared_bf16x_f32 failed")
+        torch.cuda.synchronize()
+        launches = [calls[i % len(calls)] for i in range(30)]
+        med = timer.run(launches) / len(launches)
+        nbytes = 9 * per_expert + 2 * 7168 * 4
+        gbs = nbytes / (med / 1e3) / 1e9
+        print(f"{'ds-v3 MoE layer (8 routed + shared, 2 launches)':40s} M=1  {1e3 * med:9.2f} us  {gbs:8.1f} GB/s  "
+              f"{100 * gbs / PEAK_HBM_GBS:5.1f}%", flush=True)
+        cpu_us = cpu_gbs = None
+        if not args.no_cpu:
+            # the oracle's weighted many-expert MLP plus the shared expert's MLP on one layer
+            routed = [tuple(t.cpu().numpy() for t in e) for e in layers[0][:8]]
+            shared = tuple(t.cpu().numpy() for t in layers[0][8])
+            hx, hr = x.float().cpu().numpy(), rw.cpu().numpy()
+            t0 = time.perf_counter()
+            n = 0
+            while True:
+                oracle.fp8_mlp_many_weighted(routed, hx, hr)
+                oracle.fp8_mlp(*shared, hx)
+                n += 1
+                if time.perf_counter() - t0 > 1.5:
+                    break
+            cpu_us = (time.perf_counter() - t0) / n * 1e6
+            cpu_gbs = nbytes / (cpu_us / 1e6) / 1e9
+            del routed, shared
+        rows_out.append(("ds-v3 MoE layer (8 routed + shared, 2 launches)", 1, 1e3 * med, gbs, 100 * gbs / PEAK_HBM_GBS,
+                         cpu_us, cpu_gbs, "port"))
+        del layers
+        torch.cuda.empty_cache()
+
+    if want("ds-v3 MoE layer"):
+        moe_layer()
 
     lines = [f"CPU: the oracle's restatement (kind \"port\"), {oracle.num_threads()} OpenMP threads, "
              "weights warm in host RAM; about 1.5 s of calls per row.", "",
