@@ -375,6 +375,35 @@ def table(args):
         del sets
         torch.cuda.empty_cache()
 
+    # ---- q_a and kv_a from one hidden state in one launch (configuration 5's
+    # attention input projections)
+    if want("fp8 q_a + kv_a"):
+        count = max(2, math.ceil(MALL_BYTES / ((1536 + 576) * 7168)))
+        qa, kva = fp8_sets(1536, 7168, count), fp8_sets(576, 7168, count)
+        hq = (qa[0][0].cpu().numpy(), qa[0][1].cpu().numpy(), kva[0][0].cpu().numpy(), kva[0][1].cpu().numpy())
+        rows_arr = (ctypes.c_int64 * 2)(1536, 576)
+        for m in (1, 2, 4, 8):
+            x = torch.randn((m, 7168), generator=gen, device="cuda").to(torch.bfloat16)
+            yq, yk = torch.empty((m, 1536), device="cuda"), torch.empty((m, 576), device="cuda")
+            outs_arr = (ctypes.c_uint64 * 2)(yq.data_ptr(), yk.data_ptr())
+            tabs = [((ctypes.c_uint64 * 2)(a[0].data_ptr(), b[0].data_ptr()),
+                     (ctypes.c_uint64 * 2)(a[1].data_ptr(), b[1].data_ptr())) for a, b in zip(qa, kva)]
+            lib.pocketlm_set_stream(_stream_ptr(torch))
+
+            def make(tabs=tabs, x=x, outs_arr=outs_arr, m=m):
+                return [lambda t=t: lib.fp8_e4m3_block_linear_many_bf16x_f32(
+                    ctypes.cast(t[0], ctypes.c_void_p), ctypes.cast(t[1], ctypes.c_void_p), ctypes.c_void_p(x.data_ptr()),
+                    ctypes.cast(outs_arr, ctypes.c_void_p), ctypes.cast(rows_arr, ctypes.c_void_p), 2, m, 7168, 56)
+                    for t in tabs]
+
+            xh = x.float().cpu().numpy()
+            measure("fp8 q_a + kv_a (one launch)", m, make,
+                    fp8_bytes(1536, 7168, m) + fp8_bytes(576, 7168, m) - 2 * m * 7168,
+                    lambda xh=xh: (oracle.fp8_linear(hq[0], hq[1], xh, batch_reuse=True),
+                                   oracle.fp8_linear(hq[2], hq[3], xh, batch_reuse=True)))
+        del qa, kva
+        torch.cuda.empty_cache()
+
     # ---- FP8 dequant (config 1 matrix)
     sets = fp8_sets(2048, 7168, 24) if want("fp8 dequant") else []
     out16 = torch.empty((2048, 7168), device="cuda", dtype=torch.float16)

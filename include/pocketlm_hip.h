@@ -185,6 +185,20 @@ int fp8_e4m3_block_mlp_many_pair_weighted_f32(
     int64_t batch, int64_t intermediate_rows, int64_t hidden_cols, int64_t gate_scale_cols,
     int64_t down_scale_cols);
 
+/* No single reference counterpart: several FP8 linears sharing one hidden
+ * (fp8_linear.cpp:50-117 each), such as the q_a and kv_a projections that
+ * the DeepSeek attention computes from the same hidden state
+ * (fp8_source.py:1943-1945 and 1967-1969), in one launch.  count
+ * (1..8) weights of out_rows[i] x in_cols with their scale grids; output i
+ * is fp32 [batch, out_rows[i]] at out_ptrs[i].  The three address arrays are
+ * host arrays of device addresses, as in the MoE entry points.  Each output
+ * has the values of fp8_e4m3_block_linear_f32 on that weight.  Codes as
+ * fp8_e4m3_block_linear_f32 (-2 also for count outside 1..8). */
+int fp8_e4m3_block_linear_many_f32(const uint64_t* weight_ptrs, const uint64_t* scale_ptrs,
+                                   const float* hidden, const uint64_t* out_ptrs,
+                                   const int64_t* out_rows, int64_t count, int64_t batch,
+                                   int64_t in_cols, int64_t scale_cols);
+
 /* bf16-activation twins.  The reference wrappers cast the activations to
  * fp32 before these calls (native/__init__.py:3451 linear, 3500 dual, 3568
  * MLP, 3760 weighted, 3834 row-weighted, 3910 pair-weighted; the routed +
@@ -197,6 +211,10 @@ int fp8_e4m3_block_mlp_many_pair_weighted_f32(
 int fp8_e4m3_block_linear_bf16x_f32(const uint8_t* fp8_weight, const float* scale_inv,
                                     const uint16_t* hidden_bf16, float* out, int64_t batch,
                                     int64_t out_rows, int64_t in_cols, int64_t scale_cols);
+int fp8_e4m3_block_linear_many_bf16x_f32(const uint64_t* weight_ptrs, const uint64_t* scale_ptrs,
+                                         const uint16_t* hidden_bf16, const uint64_t* out_ptrs,
+                                         const int64_t* out_rows, int64_t count, int64_t batch,
+                                         int64_t in_cols, int64_t scale_cols);
 int fp8_e4m3_block_dual_linear_bf16x_f32(const uint8_t* weight_a, const float* scale_inv_a,
                                          const uint8_t* weight_b, const float* scale_inv_b,
                                          const uint16_t* hidden_bf16, float* out_a, float* out_b,

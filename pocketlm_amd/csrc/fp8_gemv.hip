@@ -36,6 +36,7 @@ namespace {
 constexpr int kMaxGroups = 64;  // experts per launch (pointer tables travel as kernel arguments)
 constexpr int kMaxWaves = 8;
 constexpr int kMaxM = 8;        // activation rows per launch; larger batches are split
+constexpr int kMaxVar = 8;      // matrices of different row counts per many-linear launch
 
 struct RowsArgs {
     const uint8_t* w[2][kMaxGroups];
@@ -52,6 +53,14 @@ struct RowsArgs {
     int nchunks;
     int m_total;
     int m0;
+    // Groups of different row counts (the many-linear entry point, one weight
+    // per group): group g owns tiles [vtile[g], vtile[g+1]) of the grid and
+    // writes its vrows[g] rows to vout[g] as [m_total][vrows[g]].  nvar = 0:
+    // uniform groups as above.
+    int nvar;
+    int vtile[kMaxVar + 1];
+    int64_t vrows[kMaxVar];
+    float* vout[kMaxVar];
 };
 
 struct CombineArgs {
@@ -136,8 +145,18 @@ __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
     const int nw = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63;
-    const int g = blockIdx.x / a.tiles_per_group;
-    const int64_t row0 = static_cast<int64_t>(blockIdx.x - g * a.tiles_per_group) * TR;
+    int g;
+    int64_t row0, rows = a.rows;
+    if (a.nvar > 0) {
+        g = 0;
+        for (int i = 1; i < a.nvar; ++i)
+            if (static_cast<int>(blockIdx.x) >= a.vtile[i]) g = i;
+        row0 = static_cast<int64_t>(blockIdx.x - a.vtile[g]) * TR;
+        rows = a.vrows[g];
+    } else {
+        g = blockIdx.x / a.tiles_per_group;
+        row0 = static_cast<int64_t>(blockIdx.x - g * a.tiles_per_group) * TR;
+    }
 
     const uint8_t* W[NWT];
     const float* S[NWT];
@@ -170,7 +189,7 @@ __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
             for (int i = 0; i < NWT; ++i)
 #pragma unroll
                 for (int r = 0; r < TR; ++r) {
-                    const int64_t rr = row0 + r < a.rows ? row0 + r : a.rows - 1;
+                    const int64_t rr = row0 + r < rows ? row0 + r : rows - 1;
                     q[i][r] = *reinterpret_cast<const uint4*>(W[i] + rr * a.K + col);
                 }
             float sc[NWT];
@@ -265,7 +284,7 @@ __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
         const int r = t / M;
         const int m = t - r * M;
         const int64_t row = row0 + r;
-        if (row >= a.rows) continue;
+        if (row >= rows) continue;
         float v[NWT];
 #pragma unroll
         for (int i = 0; i < NWT; ++i) {
@@ -277,6 +296,10 @@ __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
         if constexpr (SILU) {
             a.out[0][o] = plm_silu_mul(v[0], v[1]);
         } else {
+            if (a.nvar > 0) {
+                a.vout[g][static_cast<int64_t>(a.m0 + m) * rows + row] = v[0];
+                continue;
+            }
 #pragma unroll
             for (int i = 0; i < NWT; ++i) a.out[i][o] = v[i];
         }
@@ -537,7 +560,13 @@ void launch_rows_tr(const RowsArgs& a, int ngroups, hipStream_t st) {
     RowsArgs b = a;
     b.tiles_per_group = static_cast<int>(plm::ceil_div(a.rows, TR));
     const int nw = waves_for(a.nchunks);
-    const int64_t grid = static_cast<int64_t>(b.tiles_per_group) * ngroups;
+    int64_t grid = static_cast<int64_t>(b.tiles_per_group) * ngroups;
+    if (a.nvar > 0) {
+        b.vtile[0] = 0;
+        for (int i = 0; i < a.nvar; ++i)
+            b.vtile[i + 1] = b.vtile[i] + static_cast<int>(plm::ceil_div(a.vrows[i], TR));
+        grid = b.vtile[a.nvar];
+    }
     if (a.xb != nullptr) {
         hipLaunchKernelGGL((fp8_rows_kernel<M, TR, NWT, SILU, true>), dim3(static_cast<unsigned>(grid)),
                            dim3(nw * plm::kWave), 0, st, b);
@@ -552,7 +581,12 @@ void launch_rows_m(const RowsArgs& a, int ngroups, hipStream_t st) {
     // (at three or more activation rows the wide tile's re-decoding and
     // registers cost more than the activation reads it saves)
     if constexpr (NWT == 1 && M <= 2) {
-        if (wide_tile_fits(a.rows, ngroups, waves_for(a.nchunks))) {
+        int64_t all_rows = a.rows;
+        if (a.nvar > 0) {
+            all_rows = 0;
+            for (int i = 0; i < a.nvar; ++i) all_rows += a.vrows[i];
+        }
+        if (wide_tile_fits(all_rows, a.nvar > 0 ? 1 : ngroups, waves_for(a.nchunks))) {
             launch_rows_tr<M, 8, 1, SILU>(a, ngroups, st);
             return;
         }
@@ -636,6 +670,9 @@ struct RowsProblem {
     int64_t rows;
     int64_t K;
     int64_t scale_cols;
+    int nvar;             // > 0: ngroups single weights of vrows[g] rows each, written to vout[g]
+    int64_t vrows[kMaxVar];
+    float* vout[kMaxVar];
 };
 
 bool rows_fast_ok(const RowsProblem& p) {
@@ -652,6 +689,8 @@ bool rows_fast_ok(const RowsProblem& p) {
 
 int run_rows(const RowsProblem& p, hipStream_t st) {
     const bool fast = rows_fast_ok(p);
+    if (p.nvar > 0 && (!fast || p.nwt != 1 || p.ngroups != p.nvar || p.nvar > kMaxVar))
+        return plm::fail(-2, "variable-row groups need the vector path and one weight per group");
     for (int g0 = 0; g0 < p.ngroups; g0 += kMaxGroups) {
         const int ng = std::min(kMaxGroups, p.ngroups - g0);
         RowsArgs a;
@@ -675,6 +714,11 @@ int run_rows(const RowsProblem& p, hipStream_t st) {
         a.scale_cols = p.scale_cols;
         a.nchunks = static_cast<int>(plm::ceil_div(p.K, plm::kChunkBytes));
         a.m_total = static_cast<int>(p.batch);
+        a.nvar = p.nvar;
+        for (int i = 0; i < p.nvar; ++i) {
+            a.vrows[i] = p.vrows[i];
+            a.vout[i] = p.vout[i];
+        }
         for (int64_t m0 = 0; m0 < p.batch; m0 += kMaxM) {
             const int mc = static_cast<int>(std::min<int64_t>(kMaxM, p.batch - m0));
             a.m0 = static_cast<int>(m0);
@@ -1005,6 +1049,47 @@ int pair_weighted_impl(const uint64_t* gp, const uint64_t* gsp, const uint64_t* 
     return run_combine(c, st);
 }
 
+// Several weights of different row counts sharing the activations, in one
+// launch when the vector path applies (else one call per weight; the per-row
+// arithmetic is the same either way).
+int linear_many_impl(const uint64_t* weight_ptrs, const uint64_t* scale_ptrs, Act hidden, const uint64_t* out_ptrs,
+                     const int64_t* out_rows, int64_t count, int64_t batch, int64_t in_cols, int64_t scale_cols) {
+    if (count <= 0 || count > kMaxVar) return plm::fail(-2, "1..%d weights per call", kMaxVar);
+    if (batch <= 0 || in_cols <= 0 || scale_cols < plm::ceil_div(in_cols, 128)) return plm::fail(-2, "bad dimensions");
+    const uint8_t* w[kMaxVar];
+    const float* s[kMaxVar];
+    RowsProblem p;
+    std::memset(&p, 0, sizeof(p));
+    int64_t max_rows = 0;
+    for (int64_t i = 0; i < count; ++i) {
+        w[i] = reinterpret_cast<const uint8_t*>(static_cast<uintptr_t>(weight_ptrs[i]));
+        s[i] = reinterpret_cast<const float*>(static_cast<uintptr_t>(scale_ptrs[i]));
+        p.vout[i] = reinterpret_cast<float*>(static_cast<uintptr_t>(out_ptrs[i]));
+        p.vrows[i] = out_rows[i];
+        if (!w[i] || !s[i] || !p.vout[i]) return plm::fail(-1, "null pointer");
+        if (out_rows[i] <= 0) return plm::fail(-2, "bad dimensions");
+        max_rows = std::max(max_rows, out_rows[i]);
+    }
+    p.w[0] = w;
+    p.s[0] = s;
+    p.nwt = 1;
+    p.ngroups = static_cast<int>(count);
+    p.nvar = static_cast<int>(count);
+    p.x = hidden.f32;
+    p.xb = hidden.bf16;
+    p.x_stride = in_cols;
+    p.batch = batch;
+    p.rows = max_rows;
+    p.K = in_cols;
+    p.scale_cols = scale_cols;
+    if (rows_fast_ok(p)) return run_rows(p, plm::current_stream());
+    for (int64_t i = 0; i < count; ++i) {
+        const int code = linear_impl(w[i], s[i], hidden, p.vout[i], batch, out_rows[i], in_cols, scale_cols);
+        if (code != 0) return code;
+    }
+    return 0;
+}
+
 }  // namespace
 
 // ====================================================================== C ABI
@@ -1021,6 +1106,23 @@ PLM_EXPORT int fp8_e4m3_block_linear_bf16x_f32(const uint8_t* fp8_weight, const 
                                                int64_t out_rows, int64_t in_cols, int64_t scale_cols) {
     if (!fp8_weight || !scale_inv || !hidden_bf16 || !out) return plm::fail(-1, "null pointer");
     return linear_impl(fp8_weight, scale_inv, Act{nullptr, hidden_bf16}, out, batch, out_rows, in_cols, scale_cols);
+}
+
+PLM_EXPORT int fp8_e4m3_block_linear_many_f32(const uint64_t* weight_ptrs, const uint64_t* scale_ptrs,
+                                              const float* hidden, const uint64_t* out_ptrs, const int64_t* out_rows,
+                                              int64_t count, int64_t batch, int64_t in_cols, int64_t scale_cols) {
+    if (!weight_ptrs || !scale_ptrs || !hidden || !out_ptrs || !out_rows) return plm::fail(-1, "null pointer");
+    return linear_many_impl(weight_ptrs, scale_ptrs, Act{hidden, nullptr}, out_ptrs, out_rows, count, batch, in_cols,
+                            scale_cols);
+}
+
+PLM_EXPORT int fp8_e4m3_block_linear_many_bf16x_f32(const uint64_t* weight_ptrs, const uint64_t* scale_ptrs,
+                                                    const uint16_t* hidden_bf16, const uint64_t* out_ptrs,
+                                                    const int64_t* out_rows, int64_t count, int64_t batch,
+                                                    int64_t in_cols, int64_t scale_cols) {
+    if (!weight_ptrs || !scale_ptrs || !hidden_bf16 || !out_ptrs || !out_rows) return plm::fail(-1, "null pointer");
+    return linear_many_impl(weight_ptrs, scale_ptrs, Act{nullptr, hidden_bf16}, out_ptrs, out_rows, count, batch,
+                            in_cols, scale_cols);
 }
 
 PLM_EXPORT int fp8_e4m3_block_dual_linear_f32(const uint8_t* wa, const float* sa, const uint8_t* wb,

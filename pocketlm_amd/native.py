@@ -278,6 +278,44 @@ def fp8_e4m3_block_linear_f32(fp8_weight: torch.Tensor, scale_inv: torch.Tensor,
     return _home(out, hidden)
 
 
+def fp8_e4m3_block_linear_many_f32(weights, hidden: torch.Tensor) -> list[torch.Tensor]:
+    """Several fp8_e4m3_block_linear_f32 calls on one hidden (for example
+    the q_a and kv_a projections, src/pcketlm/core/runtime/fp8_source.py:
+    1943-1945 and 1967-1969) in one launch.  weights: (fp8_weight,
+    scale_inv) pairs with the same in_cols.  Returns one fp32 [M, rows_i]
+    output per weight, with the single calls' values."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_FP8_LINEAR", "Native FP8 linear")
+    if not 1 <= len(weights) <= 8:
+        raise ValueError("1 to 8 weights per call")
+    dev = _target_device(hidden, *[w for w, _s in weights])
+    x, bf16 = _hidden_in(hidden, dev)
+    in_cols = int(x.shape[1])
+    ws, ss = [], []
+    for fp8_weight, scale_inv in weights:
+        if fp8_weight.ndim != 2:
+            raise ValueError("fp8_weight must have shape [out_rows, in_cols]")
+        w, sc = _fp8_bytes(fp8_weight, dev), _on(scale_inv, dev, torch.float32)
+        if int(w.shape[1]) != in_cols:
+            raise ValueError("hidden input size does not match FP8 weight columns")
+        if tuple(sc.shape) != ((int(w.shape[0]) + 127) // 128, (in_cols + 127) // 128):
+            raise ValueError("scale_inv shape does not match FP8 128x128 block layout")
+        ws.append(w)
+        ss.append(sc)
+    batch = int(x.shape[0])
+    outs = [torch.empty((batch, int(w.shape[0])), dtype=torch.float32, device=dev) for w in ws]
+    n = len(ws)
+    wp = (ctypes.c_uint64 * n)(*[int(w.data_ptr()) for w in ws])
+    sp = (ctypes.c_uint64 * n)(*[int(t.data_ptr()) for t in ss])
+    op = (ctypes.c_uint64 * n)(*[int(o.data_ptr()) for o in outs])
+    rp = (ctypes.c_int64 * n)(*[int(w.shape[0]) for w in ws])
+    with _launch(lib, dev):
+        code = getattr(lib, _twin("fp8_e4m3_block_linear_many_f32", bf16))(
+            ctypes.cast(wp, ctypes.c_void_p), ctypes.cast(sp, ctypes.c_void_p), _p(x), ctypes.cast(op, ctypes.c_void_p),
+            ctypes.cast(rp, ctypes.c_void_p), n, batch, in_cols, (in_cols + 127) // 128)
+    _check("fp8_e4m3_block_linear_many_f32", code)
+    return [_home(o, hidden) for o in outs]
+
+
 def fp8_e4m3_block_dual_linear_f32(
     fp8_weight_a: torch.Tensor,
     scale_inv_a: torch.Tensor,

@@ -362,6 +362,27 @@ def test_bf16_activation_twins_equal_fp32_calls(nat):
                        nat.fp8_e4m3_block_linear_f32(dev(wo), dev(so), xo.float()))
 
 
+def test_linear_many_equals_single_linears(nat):
+    """q_a and kv_a (and a third, odd-sized weight) from one hidden in one
+    launch: every output equals its single linear call, fp32 and bf16
+    activations, 1..8 and 11 rows; an odd K falls back to single calls."""
+    mats = [synth_fp8(1536, 7168, 930), synth_fp8(576, 7168, 931), synth_fp8(200, 7168, 932)]
+    dm = [(dev(w), dev(s)) for w, s in mats]
+    x32 = dev(synth_x(11, 7168, 933))
+    for m in (1, 2, 3, 8, 11):
+        for xx in (x32[:m], x32[:m].to(torch.bfloat16)):
+            outs = nat.fp8_e4m3_block_linear_many_f32(dm, xx)
+            for (w, s), y in zip(dm, outs):
+                assert torch.equal(y, nat.fp8_e4m3_block_linear_f32(w, s, xx)), m
+    odd = [synth_fp8(40, 72, 934), synth_fp8(24, 72, 935)]
+    do = [(dev(w), dev(s)) for w, s in odd]
+    xo = dev(synth_x(2, 72, 936))
+    for (w, s), y in zip(do, nat.fp8_e4m3_block_linear_many_f32(do, xo)):
+        assert torch.equal(y, nat.fp8_e4m3_block_linear_f32(w, s, xo))
+    with pytest.raises(ValueError, match="1 to 8 weights"):
+        nat.fp8_e4m3_block_linear_many_f32(dm * 3, x32[:1])
+
+
 # --------------------------------------------------------------------------- DeepSeek session
 
 def test_ds_session_combine_kat_and_counters(nat):
