@@ -21,10 +21,15 @@
 //     a 16-byte partial comes out NaN re-decodes that span with NaN -> 0.
 //
 // fp8_rows_kernel  : rows of one or more experts sharing the activations
-//                    (linear, dual, gate/up phase with the SiLU epilogue).
+//                    (linear, dual, gate/up phase with the SiLU epilogue, and
+//                    several weights of different row counts in one grid);
+//                    the activations are fp32, or bf16 widened in the kernel
+//                    (the *_bf16x_f32 entry points; widening is exact).
 // fp8_combine_kernel: rows whose K range is the concatenation of several
 //                    experts' down matrices, each with its own activations
-//                    and route weight (down phase + routed combine).
+//                    and route weight (down phase + routed combine); a last
+//                    group can be split off into its own output (the shared
+//                    expert beside the routed sum).
 #include <algorithm>
 #include <cstring>
 #include <vector>
