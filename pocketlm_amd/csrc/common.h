@@ -38,6 +38,12 @@ int check_launch(const char* where);
 // stream; growing waits for the stream before releasing the old block.
 // Returns nullptr on allocation failure (after recording the error).
 void* workspace(size_t bytes);
+// Device words private to the kernels of one (device, stream), zero when
+// first handed out and kept until the process ends (nothing else writes
+// them), for records that must survive other calls' use of the workspace.
+// Returns nullptr on allocation failure.
+constexpr int kStreamWords = 64;
+unsigned* stream_words();
 
 // Number of compute units of the current device (cached).
 int cu_count();

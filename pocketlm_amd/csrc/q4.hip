@@ -236,11 +236,11 @@ __device__ __forceinline__ plm_half8 q4_mfma_c8_inplace() {
 // plane 0 is hi = fp16(v') and plane 1 is lo = fp16((v' - hi) * 2^11), so
 // hi + lo * 2^-11 carries 22 significant bits (the split follows the /16, so
 // no bits are lost to it).  A value that fp16 cannot hold (|v| >= 65504, inf,
-// NaN) records the call's sequence number in a word of the stream's
-// workspace, and that call's down phase reads the fp32 activations instead.
-// Calls on one stream are ordered, and each stream has its own workspace, so
-// concurrent calls cannot overwrite each other's record; a stale word can
-// only equal a later call's number by chance, which selects the exact path.
+// NaN) records the call's sequence number in a word private to the stream
+// (zero at first), and that call's down phase reads the fp32 activations
+// instead.  Calls on one stream are ordered, and each stream has its own
+// word, so concurrent calls cannot overwrite each other's record; the word
+// only ever holds an earlier call's number, which selects nothing.
 __device__ __forceinline__ void q4_store_planes(uint4* base, int64_t k, float v, unsigned seq, unsigned* record) {
     if (!(fabsf(v) < 65504.0f)) atomicExch(record, seq);
     const int64_t s = k >> 9;
@@ -753,12 +753,14 @@ PLM_EXPORT int q4_moe_selected_forward_u16(const uint16_t* hidden, const uint8_t
     // vector, after it in the workspace).
     const bool planes = fast1 && fast2;
     const int64_t planes_stride = stride / 4;  // uint4 per expert
-    // workspace: [256-byte header holding the overflow record][fp32 act][planes]
-    char* ws = static_cast<char*>(
-        plm::workspace(256 + static_cast<size_t>(S * stride) * sizeof(float) * (planes ? 2 : 1)));
+    // The overflow record lives in the stream's private words (zero until a
+    // call records into it, written by nothing else); the workspace, which
+    // other entry points on the stream reuse, holds [fp32 act][planes].
+    unsigned* overflow = plm::stream_words();
+    if (overflow == nullptr) return 2;
+    char* ws = static_cast<char*>(plm::workspace(static_cast<size_t>(S * stride) * sizeof(float) * (planes ? 2 : 1)));
     if (ws == nullptr) return 2;
-    unsigned* overflow = reinterpret_cast<unsigned*>(ws);
-    float* act = reinterpret_cast<float*>(ws + 256);
+    float* act = reinterpret_cast<float*>(ws);
     uint4* bplanes = planes ? reinterpret_cast<uint4*>(act + S * stride) : nullptr;
     static std::atomic<unsigned> call_seq{0};
     unsigned seq = ++call_seq;

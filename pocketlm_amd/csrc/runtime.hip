@@ -23,6 +23,7 @@ struct Arena {
 
 std::mutex g_arena_mu;
 std::map<std::pair<int, hipStream_t>, Arena> g_arenas;
+std::map<std::pair<int, hipStream_t>, unsigned*> g_words;
 
 }  // namespace
 
@@ -84,6 +85,29 @@ void* workspace(size_t bytes) {
     }
     a.size = rounded;
     return a.ptr;
+}
+
+unsigned* stream_words() {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) {
+        hip_fail(err, "hipGetDevice");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_arena_mu);
+    unsigned*& w = g_words[{dev, t_stream}];
+    if (w == nullptr) {
+        void* p = nullptr;
+        err = hipMalloc(&p, kStreamWords * sizeof(unsigned));
+        if (err == hipSuccess) err = hipMemsetAsync(p, 0, kStreamWords * sizeof(unsigned), t_stream);
+        if (err != hipSuccess) {
+            if (p != nullptr) hipFree(p);
+            hip_fail(err, "stream words");
+            return nullptr;
+        }
+        w = static_cast<unsigned*>(p);
+    }
+    return w;
 }
 
 int cu_count() {
