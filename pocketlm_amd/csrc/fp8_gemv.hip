@@ -560,6 +560,18 @@ bool wide_tile_fits(int64_t rows, int64_t groups, int nw) {
     return plm::ceil_div(rows, 8) * groups * nw >= kTileWaves;
 }
 
+// With one weight, halving the tile to 2 rows pays when 4-row tiles would
+// leave CUs idle (fewer tiles than CUs) or load them unevenly (the busiest
+// CU's share of ceil(tiles / CUs) is above the mean by more than it would be
+// with twice the tiles): 1536 rows give 384 tiles of 4, 1.5 per CU, against
+// 768 of 2, 3 per CU.  Where both divide evenly (2048, 3072 rows) the
+// 4-row tile reads the activations half as often and stays.
+bool narrow_tile_balances(int64_t tiles4) {
+    const int64_t cus = plm::cu_count();
+    const int64_t tiles2 = 2 * tiles4;
+    return tiles4 < cus || plm::ceil_div(tiles2, cus) * tiles4 < plm::ceil_div(tiles4, cus) * tiles2;
+}
+
 template <int M, int TR, int NWT, bool SILU>
 void launch_rows_tr(const RowsArgs& a, int ngroups, hipStream_t st) {
     RowsArgs b = a;
@@ -583,16 +595,27 @@ void launch_rows_tr(const RowsArgs& a, int ngroups, hipStream_t st) {
 
 template <int M, int NWT, bool SILU>
 void launch_rows_m(const RowsArgs& a, int ngroups, hipStream_t st) {
-    // (at three or more activation rows the wide tile's re-decoding and
-    // registers cost more than the activation reads it saves)
-    if constexpr (NWT == 1 && M <= 2) {
+    if constexpr (NWT == 1) {
         int64_t all_rows = a.rows;
+        int64_t tiles4 = plm::ceil_div(a.rows, 4) * ngroups;
         if (a.nvar > 0) {
             all_rows = 0;
-            for (int i = 0; i < a.nvar; ++i) all_rows += a.vrows[i];
+            tiles4 = 0;
+            for (int i = 0; i < a.nvar; ++i) {
+                all_rows += a.vrows[i];
+                tiles4 += plm::ceil_div(a.vrows[i], 4);
+            }
         }
-        if (wide_tile_fits(all_rows, a.nvar > 0 ? 1 : ngroups, waves_for(a.nchunks))) {
-            launch_rows_tr<M, 8, 1, SILU>(a, ngroups, st);
+        // (at three or more activation rows the wide tile's re-decoding and
+        // registers cost more than the activation reads it saves)
+        if constexpr (M <= 2) {
+            if (wide_tile_fits(all_rows, a.nvar > 0 ? 1 : ngroups, waves_for(a.nchunks))) {
+                launch_rows_tr<M, 8, 1, SILU>(a, ngroups, st);
+                return;
+            }
+        }
+        if (narrow_tile_balances(tiles4)) {
+            launch_rows_tr<M, 2, 1, SILU>(a, ngroups, st);
             return;
         }
     }
