@@ -630,6 +630,36 @@ def table(args):
         gbs = nbytes / (med / 1e3) / 1e9
         print(f"{'ds-v3 MoE layer (8 routed + shared, 2 launches)':40s} M=1  {1e3 * med:9.2f} us  {gbs:8.1f} GB/s  "
               f"{100 * gbs / PEAK_HBM_GBS:5.1f}%", flush=True)
+        # the same layers with the experts chosen on the device: a table of all
+        # 256 expert slots per layer (the router's 8 filled), the router's
+        # device outputs, a plan launch, the two MoE launches and the bf16 tail
+        idx_dev = _idx.reshape(1, -1).contiguous()
+        dev_tables = []
+        for layer in layers:
+            addr = torch.zeros((6, 256), dtype=torch.int64)
+            for j, e in enumerate(idx_dev[0].tolist()):
+                for r in range(6):
+                    addr[r, e] = layer[j][r].data_ptr()
+            dev_tables.append((addr.cuda(), (ctypes.c_uint64 * 6)(*[t.data_ptr() for t in layer[8]])))
+        ybf = torch.empty((1, 7168), dtype=torch.bfloat16, device="cuda")
+        rejected = torch.zeros((1,), dtype=torch.int32, device="cuda")
+        dev_calls = [lambda t=t: lib.fp8_e4m3_block_moe_device_routed_bf16x_f32(
+            ctypes.c_void_p(t[0].data_ptr()), 256, ctypes.c_void_p(idx_dev.data_ptr()), ctypes.c_void_p(rw.data_ptr()),
+            8, ctypes.cast(t[1], ctypes.c_void_p), ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr()),
+            ctypes.c_void_p(ys.data_ptr()), ctypes.c_void_p(ybf.data_ptr()), ctypes.c_void_p(rejected.data_ptr()),
+            1, 2048, 7168, 56, 16) for t in dev_tables]
+        for fn in dev_calls:
+            if fn() != 0:
+                raise RuntimeError("fp8_e4m3_block_moe_device_routed_bf16x_f32 failed")
+        torch.cuda.synchronize()
+        if int(rejected.item()) != 0:
+            raise RuntimeError("the device plan left out router indices")
+        dev_launches = [dev_calls[i % len(dev_calls)] for i in range(30)]
+        dev_med = timer.run(dev_launches) / len(dev_launches)
+        dev_gbs = nbytes / (dev_med / 1e3) / 1e9
+        dev_name = "ds-v3 MoE layer, device-routed (2 launches, bf16 output)"
+        print(f"{dev_name:40s} M=1  {1e3 * dev_med:9.2f} us  {dev_gbs:8.1f} GB/s  {100 * dev_gbs / PEAK_HBM_GBS:5.1f}%",
+              flush=True)
         cpu_us = cpu_gbs = None
         if not args.no_cpu:
             # the oracle's weighted many-expert MLP plus the shared expert's MLP on one layer
@@ -649,7 +679,8 @@ def table(args):
             del routed, shared
         rows_out.append(("ds-v3 MoE layer (8 routed + shared, 2 launches)", 1, 1e3 * med, gbs, 100 * gbs / PEAK_HBM_GBS,
                          cpu_us, cpu_gbs, "port"))
-        del layers
+        rows_out.append((dev_name, 1, 1e3 * dev_med, dev_gbs, 100 * dev_gbs / PEAK_HBM_GBS, cpu_us, cpu_gbs, "port"))
+        del layers, dev_tables
         torch.cuda.empty_cache()
 
     if want("ds-v3 MoE layer"):

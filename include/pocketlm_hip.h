@@ -382,6 +382,49 @@ int ds_route_topk_f32(const float* logits, const float* bias, int64_t batch, int
                       int64_t top_k, int64_t n_groups, int64_t topk_groups, int scoring,
                       float route_scale, int64_t* out_indices, float* out_weights);
 
+/* New export: run_fp8_moe (src/pcketlm/core/runtime/fp8_source.py:1569-1884)
+ * with the experts chosen on the device.  The reference reads the router's
+ * indices on the host (sorted unique experts, 1600) before it calls the
+ * weighted (M == 1, fp8_linear.cpp:475-589) or row-weighted (M > 1,
+ * 591-831) kernel, adds the shared expert's MLP (1849-1859) and sums in
+ * bf16 (1762, 1861-1862).  Here the router's outputs stay in HBM:
+ *   expert_table   device uint64 [6][num_experts]: gate, gate scale_inv, up,
+ *                  up scale_inv, down, down scale_inv addresses of every
+ *                  expert (0 = absent: contributes nothing when chosen);
+ *   route_indices  device int64 [batch][top_k], route_weights device fp32
+ *                  [batch][top_k] (ds_route_topk_f32's outputs);
+ *   shared_ptrs    host uint64 [6] of the shared expert, or NULL;
+ *   out            device fp32 [batch][hidden_dim], the route-weighted sum
+ *                  over the distinct chosen experts in ascending order;
+ *   out_shared     device fp32 [batch][hidden_dim] (required with a shared
+ *                  expert);
+ *   out_bf16       device bf16 [batch][hidden_dim] = bf16(bf16(out) +
+ *                  bf16(out_shared)), NaN as 0x7FC0, or NULL;
+ *   rejected       device int32, or NULL: receives the number of choices
+ *                  outside [0, num_experts) (left out) plus those of an
+ *                  expert whose weight addresses are not 16-byte aligned
+ *                  (scales: 4), which contributes nothing.
+ * Same values as the host-routed calls given the same experts.  Three
+ * launches' worth of work in two: the gate/up launch finds each expert
+ * among the choices, the down launch computes the shared expert and the
+ * bf16 tail beside the routed sum.  batch 1..8, batch * top_k <= 64,
+ * hidden_dim and intermediate_rows multiples of 16, hidden 16-byte
+ * aligned.  Codes -1 null, -2 bad dims, -3 workspace. */
+int fp8_e4m3_block_moe_device_routed_f32(const uint64_t* expert_table, int64_t num_experts,
+                                         const int64_t* route_indices, const float* route_weights,
+                                         int64_t top_k, const uint64_t* shared_ptrs, const float* hidden,
+                                         float* out, float* out_shared, uint16_t* out_bf16, int* rejected,
+                                         int64_t batch, int64_t intermediate_rows, int64_t hidden_dim,
+                                         int64_t gate_scale_cols, int64_t down_scale_cols);
+/* The same with bf16 activations (the decode path's), widened exactly. */
+int fp8_e4m3_block_moe_device_routed_bf16x_f32(const uint64_t* expert_table, int64_t num_experts,
+                                               const int64_t* route_indices, const float* route_weights,
+                                               int64_t top_k, const uint64_t* shared_ptrs,
+                                               const uint16_t* hidden_bf16, float* out, float* out_shared,
+                                               uint16_t* out_bf16, int* rejected, int64_t batch,
+                                               int64_t intermediate_rows, int64_t hidden_dim,
+                                               int64_t gate_scale_cols, int64_t down_scale_cols);
+
 #ifdef __cplusplus
 }
 #endif

@@ -55,6 +55,8 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "fp8_e4m3_block_mlp_bf16x_f32": (_i32, [_vp] * 8 + [_i64] * 5),
     "fp8_e4m3_block_mlp_many_weighted_bf16x_f32": (_i32, [_vp] * 9 + [_i64] * 6),
     "fp8_e4m3_block_mlp_many_weighted_shared_bf16x_f32": (_i32, [_vp] * 10 + [_i64] * 6),
+    "fp8_e4m3_block_moe_device_routed_f32": (_i32, [_vp, _i64, _vp, _vp, _i64] + [_vp] * 6 + [_i64] * 5),
+    "fp8_e4m3_block_moe_device_routed_bf16x_f32": (_i32, [_vp, _i64, _vp, _vp, _i64] + [_vp] * 6 + [_i64] * 5),
     "fp8_e4m3_block_mlp_many_row_weighted_bf16x_f32": (_i32, [_vp] * 9 + [_i64] * 6),
     "fp8_e4m3_block_mlp_many_pair_weighted_bf16x_f32": (_i32, [_vp] * 11 + [_i64] * 7),
     "fp8_e4m3_block_mlp_many_weighted_avx512_f32": (_i32, [_vp] * 9 + [_i64] * 6),

@@ -31,6 +31,8 @@
 //                    group can be split off into its own output (the shared
 //                    expert beside the routed sum).
 #include <algorithm>
+#include <cstddef>
+#include <cstdint>
 #include <cstring>
 #include <vector>
 
@@ -42,6 +44,18 @@ constexpr int kMaxGroups = 64;  // experts per launch (pointer tables travel as 
 constexpr int kMaxWaves = 8;
 constexpr int kMaxM = 8;        // activation rows per launch; larger batches are split
 constexpr int kMaxVar = 8;      // matrices of different row counts per many-linear launch
+
+// Experts chosen on the device (the device-routed MoE).  moe_plan_kernel
+// writes, for the sorted distinct experts of the router's [batch][top_k]
+// indices, their six addresses (gate w/s, up w/s, down w/s; one row of tab
+// per role) and the dense route matrix [group][batch].
+constexpr int kPlanRoles = 6;
+struct MoePlan {
+    uint64_t tab[kPlanRoles][kMaxGroups];
+    float route[kMaxGroups * kMaxM];
+    int count;     // distinct accepted experts
+    int pad[63];
+};
 
 struct RowsArgs {
     const uint8_t* w[2][kMaxGroups];
@@ -66,6 +80,12 @@ struct RowsArgs {
     int vtile[kMaxVar + 1];
     int64_t vrows[kMaxVar];
     float* vout[kMaxVar];
+    // Device-chosen groups (the gate/up phase of the device-routed MoE):
+    // group g < ndev takes its addresses from plan (tab rows 0-3), and only
+    // the first plan->count of them run; group g >= ndev uses argument slot
+    // g - ndev.  ndev = 0: all groups from the arguments.
+    const MoePlan* plan;
+    int ndev;
 };
 
 struct CombineArgs {
@@ -91,6 +111,10 @@ struct CombineArgs {
     int zero_skip;        // skip (g, m) whose route is exactly 0
     int m_total;
     int m0;
+    const MoePlan* plan;  // as in RowsArgs (tab rows 4-5 for the down matrices)
+    int ndev;
+    int fused;            // split_last computed inside the routed tiles (fp8_combine_kernel FUSED)
+    uint16_t* out_bf16;   // fused only: bf16(bf16(out) + bf16(out_last)), or null
 };
 
 __device__ __forceinline__ float dot16(const float* w, const float* x) {
@@ -126,6 +150,81 @@ __device__ __forceinline__ void load_x16(const float* p, float* x) {
 
 // 16 activations of row m at column col, from the fp32 or (XB) the bf16
 // copy; both give the same fp32 values.
+// One wave (the whole workgroup) writes the plan of the router's
+// n = batch * top_k choices (n <= 64) as run_fp8_moe builds it on the host
+// (fp8_source.py:1600, 1653-1716): the distinct in-range experts in
+// ascending order, their addresses from the device table [6][num_experts],
+// and the route matrix [group][batch] (a row's weight for the expert, 0 when
+// the row did not choose it; a repeated index within a row keeps its first
+// weight).  An index outside [0, num_experts) is left out; an expert whose
+// weight addresses are not 16-byte aligned (scales: 4) keeps its group but
+// gets null addresses, so it contributes nothing.  Both are counted in
+// *rejected.
+static_assert(kMaxGroups == 64, "moe_plan_kernel maps one lane to each group");
+__global__ __launch_bounds__(64) void moe_plan_kernel(const uint64_t* __restrict__ table, int64_t num_experts,
+                                                      const int64_t* __restrict__ idx,
+                                                      const float* __restrict__ wts, int batch, int top_k,
+                                                      MoePlan* __restrict__ plan, int* __restrict__ rejected) {
+    __shared__ int64_t key[64];
+    __shared__ float kw[64];
+    __shared__ int first[64];
+    __shared__ int64_t sel[kMaxGroups];
+    const int lane = threadIdx.x;
+    const int n = batch * top_k;
+    // every load is issued before the first use: two memory round trips
+    int64_t e = lane < n ? idx[lane] : -1;
+    const float wj = lane < n ? wts[lane] : 0.0f;
+    const bool in_range = e >= 0 && e < num_experts;
+    uint64_t addr[kPlanRoles];
+#pragma unroll
+    for (int r = 0; r < kPlanRoles; ++r) addr[r] = in_range ? table[r * num_experts + e] : 0;
+    bool aligned = true;
+#pragma unroll
+    for (int r = 0; r < kPlanRoles; ++r) aligned = aligned && (addr[r] & ((r & 1) ? 3u : 15u)) == 0;
+    const bool bad = lane < n && !(in_range && aligned);
+    if (!in_range) e = -1;
+    key[lane] = e;
+    kw[lane] = wj;
+    __syncthreads();
+    int f = e >= 0;
+    for (int i = 0; i < lane; ++i) f = f && key[i] != e;
+    first[lane] = f;
+    __syncthreads();
+    int count = 0;
+    int rank = 0;
+    for (int i = 0; i < n; ++i) {
+        const int fi = first[i];
+        count += fi;
+        rank += fi && key[i] < e;
+    }
+    if (f) {
+        sel[rank] = e;
+#pragma unroll
+        for (int r = 0; r < kPlanRoles; ++r) plan->tab[r][rank] = aligned ? addr[r] : 0;
+    }
+    if (lane >= count) {
+#pragma unroll
+        for (int r = 0; r < kPlanRoles; ++r) plan->tab[r][lane] = 0;
+    }
+    __syncthreads();
+    for (int t = lane; t < kMaxGroups * batch; t += 64) {
+        const int g = t / batch;
+        const int m = t - g * batch;
+        float w = 0.0f;
+        if (g < count) {
+            const int64_t want = sel[g];
+            for (int kk = top_k - 1; kk >= 0; --kk)  // the first of repeated choices wins
+                if (key[m * top_k + kk] == want) w = kw[m * top_k + kk];
+        }
+        plan->route[t] = w;
+    }
+    const unsigned long long badmask = __ballot(bad);
+    if (lane == 0) {
+        plan->count = count;
+        if (rejected != nullptr) *rejected = __popcll(badmask);
+    }
+}
+
 template <bool XB>
 __device__ __forceinline__ void load_row_x16(const RowsArgs& a, int m, int64_t col, float* x) {
     const int64_t off = static_cast<int64_t>(a.m0 + m) * a.x_stride + col;
@@ -165,13 +264,29 @@ __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
 
     const uint8_t* W[NWT];
     const float* S[NWT];
+    int ga = g;  // argument slot
+    if constexpr (NWT == 2 && SILU) {
+        // (device-chosen groups exist only for the gate/up phase of the MoE)
+        if (g < a.ndev) {
+            if (g >= a.plan->count) return;  // the router chose fewer experts (uniform: before any barrier)
+#pragma unroll
+            for (int i = 0; i < NWT; ++i) {
+                W[i] = reinterpret_cast<const uint8_t*>(a.plan->tab[2 * i][g]);
+                S[i] = reinterpret_cast<const float*>(a.plan->tab[2 * i + 1][g]);
+            }
+        }
+        ga = g - a.ndev;
+    }
+    if (ga >= 0) {
+#pragma unroll
+        for (int i = 0; i < NWT; ++i) {
+            W[i] = a.w[i][ga];
+            S[i] = a.s[i][ga];
+        }
+    }
     bool live = true;
 #pragma unroll
-    for (int i = 0; i < NWT; ++i) {
-        W[i] = a.w[i][g];
-        S[i] = a.s[i][g];
-        live = live && W[i] != nullptr && S[i] != nullptr;
-    }
+    for (int i = 0; i < NWT; ++i) live = live && W[i] != nullptr && S[i] != nullptr;
 
     float acc[NWT][TR][M];
 #pragma unroll
@@ -311,10 +426,106 @@ __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
     }
 }
 
+// bf16 bits of v rounded to nearest even (finite and infinite v).
+__device__ __forceinline__ uint32_t bf16_rne_bits(float v) {
+    const uint32_t b = __float_as_uint(v);
+    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float bf16_value(float v) { return v != v ? v : __uint_as_float(bf16_rne_bits(v) << 16); }
+
+// The reference's bf16 tail of the MoE (fp8_source.py:1597, 1762, 1861-1862),
+// done by torch on the host there: a bf16 tensor of zeros, plus
+// routed.to(bf16), plus shared.to(bf16).  Each bf16 add is an fp32 add
+// rounded to nearest even, and a NaN sum comes out as 0x7FC0.
+__device__ __forceinline__ uint16_t moe_bf16_tail(float routed, float shared, bool has_shared) {
+    float v = 0.0f + bf16_value(routed);  // exact; -0 becomes +0 as in zeros + x
+    if (has_shared) v = v + bf16_value(shared);
+    return static_cast<uint16_t>(v != v ? 0x7FC0u : bf16_rne_bits(v));
+}
+
+// One (group g, chunk cc) item of the down phase for a tile of TR rows:
+// acc[r][m] += route(g, m) * scale * (D_g[row0 + r, chunk] . act_g,m[chunk]).
 template <int M, int TR>
+__device__ __forceinline__ void combine_chunk(const CombineArgs& a, int g, int cc, bool weighted, int64_t row0,
+                                              int lane, float (&acc)[TR][M]) {
+    const int64_t col = static_cast<int64_t>(cc) * plm::kChunkBytes + lane * 16;
+    const uint8_t* W;
+    const float* S;
+    if (g < a.ndev) {
+        W = reinterpret_cast<const uint8_t*>(a.plan->tab[4][g]);
+        S = reinterpret_cast<const float*>(a.plan->tab[5][g]);
+    } else {
+        W = a.w[g - a.ndev];
+        S = a.s[g - a.ndev];
+    }
+    if (W == nullptr || S == nullptr) return;
+    float rw[M];
+    bool any = false;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        rw[m] = a.route && weighted ? a.route[static_cast<int64_t>(a.g_base + g) * a.route_sg +
+                                              static_cast<int64_t>(a.m0 + m) * a.route_sm]
+                                    : 1.0f;
+        any = any || !(a.zero_skip && rw[m] == 0.0f);
+    }
+    if (!any || col >= a.K) return;
+    uint4 q[TR];
+#pragma unroll
+    for (int r = 0; r < TR; ++r) {
+        const int64_t rr = row0 + r < a.rows ? row0 + r : a.rows - 1;
+        q[r] = *reinterpret_cast<const uint4*>(W + rr * a.K + col);
+    }
+    const float sc = S[(row0 >> 7) * a.scale_cols + (col >> 7)];
+    if constexpr (M == 1) {
+        // one activation row: decode each weight row right before its dot,
+        // so a larger tile needs no more registers (same arithmetic)
+        if (a.zero_skip && rw[0] == 0.0f) return;
+        float xv[16];
+        load_x16(a.act + (static_cast<int64_t>(a.g_base + g) * a.m_total + a.m0) * a.K + col, xv);
+#pragma unroll
+        for (int r = 0; r < TR; ++r) {
+            float w16[16];
+            decode16(q[r], w16);
+            float p = dot16(w16, xv);
+            if (p != p) {
+                zero_nans16(w16);
+                p = dot16(w16, xv);
+            }
+            acc[r][0] = fmaf(p * sc, rw[0], acc[r][0]);
+        }
+        return;
+    }
+    float wv[TR][16];
+#pragma unroll
+    for (int r = 0; r < TR; ++r) decode16(q[r], wv[r]);
+    bool fixed = false;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        if (a.zero_skip && rw[m] == 0.0f) continue;
+        float xv[16];
+        load_x16(a.act + (static_cast<int64_t>(a.g_base + g) * a.m_total + a.m0 + m) * a.K + col, xv);
+#pragma unroll
+        for (int r = 0; r < TR; ++r) {
+            float p = dot16(wv[r], xv);
+            if (!fixed && p != p) {
+                zero_nans16(wv[r]);
+                p = dot16(wv[r], xv);
+            }
+            acc[r][m] = fmaf(p * sc, rw[m], acc[r][m]);
+        }
+        fixed = true;
+    }
+}
+
+// FUSED (the device-routed MoE): one workgroup computes both the routed sum
+// and the split-off last group (the shared expert) of its rows, each with
+// the item-to-wave assignment of the split tiles, and also writes the bf16
+// tail of the two when out_bf16 is set.
+template <int M, int TR, bool FUSED>
 __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
     constexpr int V = TR * M;
-    __shared__ float red[kMaxWaves * V];
+    __shared__ float red[(FUSED ? 2 : 1) * kMaxWaves * V];
     const int nw = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63;
@@ -328,7 +539,7 @@ __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
         tile -= g_lo * a.tiles_per_group;
     } else if (a.split_last) {
         g_hi = a.ngroups - 1;
-        if (tile >= a.tiles_per_group) {
+        if (!FUSED && tile >= a.tiles_per_group) {
             tile -= a.tiles_per_group;
             g_lo = g_hi;
             g_hi = a.ngroups;
@@ -336,6 +547,10 @@ __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
         }
     }
     const int64_t row0 = static_cast<int64_t>(tile) * TR;
+    // Device-chosen groups past the router's count are left out.  The items
+    // before them keep their wave assignment (item c goes to wave c % nw), so
+    // the sums are those of a call given just the chosen groups.
+    if (a.ndev > 0 && !last) g_hi = min(g_hi, a.plan->count);
 
     float acc[TR][M];
 #pragma unroll
@@ -346,69 +561,8 @@ __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
     const int nchunks = (g_hi - g_lo) * a.cps;
     for (int c = wave; c < nchunks; c += nw) {
         const int gi = c / a.cps;
-        const int g = g_lo + gi;
-        const int64_t col = static_cast<int64_t>(c - gi * a.cps) * plm::kChunkBytes + lane * 16;
-        const uint8_t* W = a.w[g];
-        const float* S = a.s[g];
-        if (W == nullptr || S == nullptr) continue;
-        float rw[M];
-        bool any = false;
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            rw[m] = a.route && !last ? a.route[static_cast<int64_t>(a.g_base + g) * a.route_sg +
-                                               static_cast<int64_t>(a.m0 + m) * a.route_sm]
-                                     : 1.0f;
-            any = any || !(a.zero_skip && rw[m] == 0.0f);
-        }
-        if (!any || col >= a.K) continue;
-        uint4 q[TR];
-#pragma unroll
-        for (int r = 0; r < TR; ++r) {
-            const int64_t rr = row0 + r < a.rows ? row0 + r : a.rows - 1;
-            q[r] = *reinterpret_cast<const uint4*>(W + rr * a.K + col);
-        }
-        const float sc = S[(row0 >> 7) * a.scale_cols + (col >> 7)];
-        if constexpr (M == 1) {
-            // one activation row: decode each weight row right before its dot,
-            // so a larger tile needs no more registers (same arithmetic)
-            if (a.zero_skip && rw[0] == 0.0f) continue;
-            float xv[16];
-            load_x16(a.act + (static_cast<int64_t>(a.g_base + g) * a.m_total + a.m0) * a.K + col, xv);
-#pragma unroll
-            for (int r = 0; r < TR; ++r) {
-                float w16[16];
-                decode16(q[r], w16);
-                float p = dot16(w16, xv);
-                if (p != p) {
-                    zero_nans16(w16);
-                    p = dot16(w16, xv);
-                }
-                acc[r][0] = fmaf(p * sc, rw[0], acc[r][0]);
-            }
-            continue;
-        }
-        float wv[TR][16];
-#pragma unroll
-        for (int r = 0; r < TR; ++r) decode16(q[r], wv[r]);
-        bool fixed = false;
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            if (a.zero_skip && rw[m] == 0.0f) continue;
-            float xv[16];
-            load_x16(a.act + (static_cast<int64_t>(a.g_base + g) * a.m_total + a.m0 + m) * a.K + col, xv);
-#pragma unroll
-            for (int r = 0; r < TR; ++r) {
-                float p = dot16(wv[r], xv);
-                if (!fixed && p != p) {
-                    zero_nans16(wv[r]);
-                    p = dot16(wv[r], xv);
-                }
-                acc[r][m] = fmaf(p * sc, rw[m], acc[r][m]);
-            }
-            fixed = true;
-        }
+        combine_chunk<M, TR>(a, g_lo + gi, c - gi * a.cps, !last, row0, lane, acc);
     }
-
 #pragma unroll
     for (int r = 0; r < TR; ++r)
 #pragma unroll
@@ -416,6 +570,24 @@ __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
             const float t = plm_wave_sum(acc[r][m]);
             if (lane == kSumLane) red[wave * V + r * M + m] = t;
         }
+    if constexpr (FUSED) {
+        // the split-off group in the same registers (its items on the waves
+        // a tile of its own would give them)
+        if (a.split_last) {
+#pragma unroll
+            for (int r = 0; r < TR; ++r)
+#pragma unroll
+                for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
+            for (int c = wave; c < a.cps; c += nw) combine_chunk<M, TR>(a, a.ngroups - 1, c, false, row0, lane, acc);
+#pragma unroll
+            for (int r = 0; r < TR; ++r)
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const float t = plm_wave_sum(acc[r][m]);
+                    if (lane == kSumLane) red[(kMaxWaves + wave) * V + r * M + m] = t;
+                }
+        }
+    }
     __syncthreads();
 
     for (int t = threadIdx.x; t < V; t += blockDim.x) {
@@ -426,9 +598,19 @@ __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
         float v = 0.0f;
         for (int w = 0; w < nw; ++w) v += red[w * V + t];
         int64_t o = static_cast<int64_t>(a.m0 + m) * a.rows + row;
-        if (a.per_group_out) o += static_cast<int64_t>(a.g_base + g_lo) * a.m_total * a.rows;
-        float* dst = last ? a.out_last : a.out;
-        dst[o] = a.accumulate ? dst[o] + v : v;
+        if constexpr (FUSED) {
+            float v2 = 0.0f;
+            if (a.split_last) {
+                for (int w = 0; w < nw; ++w) v2 += red[(kMaxWaves + w) * V + t];
+                a.out_last[o] = v2;
+            }
+            a.out[o] = v;
+            if (a.out_bf16 != nullptr) a.out_bf16[o] = moe_bf16_tail(v, v2, a.split_last != 0);
+        } else {
+            if (a.per_group_out) o += static_cast<int64_t>(a.g_base + g_lo) * a.m_total * a.rows;
+            float* dst = last ? a.out_last : a.out;
+            dst[o] = a.accumulate ? dst[o] + v : v;
+        }
     }
 }
 
@@ -531,6 +713,7 @@ __global__ void scatter_pairs_kernel(const int64_t* items, const int64_t* rows, 
     if (blockIdx.x != 0 || threadIdx.x != 0) return;
     for (int64_t p = 0; p < pairs; ++p) route[items[p] * batch + rows[p]] += w[p];
 }
+
 
 // ------------------------------------------------------------------ dispatch
 
@@ -644,7 +827,7 @@ int combine_segments(const CombineArgs& a) {
 }
 
 int combine_outputs(const CombineArgs& a) {
-    return a.per_group_out ? a.ngroups : (a.split_last ? 2 : 1);
+    return a.per_group_out ? a.ngroups : (a.split_last && !a.fused ? 2 : 1);
 }
 
 template <int M, int TR>
@@ -654,13 +837,20 @@ void launch_combine_tr(const CombineArgs& a, hipStream_t st) {
     b.tiles_per_group = tiles;
     const int nw = waves_for(combine_segments(a) * a.cps);
     const int64_t grid = static_cast<int64_t>(tiles) * combine_outputs(a);
-    hipLaunchKernelGGL((fp8_combine_kernel<M, TR>), dim3(static_cast<unsigned>(grid)),
-                       dim3(nw * plm::kWave), 0, st, b);
+    if (a.fused) {
+        hipLaunchKernelGGL((fp8_combine_kernel<M, TR, true>), dim3(static_cast<unsigned>(grid)),
+                           dim3(nw * plm::kWave), 0, st, b);
+    } else {
+        hipLaunchKernelGGL((fp8_combine_kernel<M, TR, false>), dim3(static_cast<unsigned>(grid)),
+                           dim3(nw * plm::kWave), 0, st, b);
+    }
 }
 
 template <int M>
 void launch_combine_m(const CombineArgs& a, hipStream_t st) {
     if constexpr (M == 1) {
+        // (fused tiles also carry the split-off group: 4-row tiles keep the
+        // grid at several workgroups per CU)
         if (wide_tile_fits(a.rows, combine_outputs(a), waves_for(combine_segments(a) * a.cps))) {
             launch_combine_tr<1, 8>(a, st);
             return;
@@ -1077,6 +1267,95 @@ int pair_weighted_impl(const uint64_t* gp, const uint64_t* gsp, const uint64_t* 
     return run_combine(c, st);
 }
 
+// The MoE with the experts chosen on the device: the router's indices and
+// weights stay in HBM.  A one-wave kernel writes the plan (the chosen
+// experts' addresses out of a device table of all experts, and the route
+// matrix) that the gate/up and down launches read.  Same values as the host-routed calls given the same experts
+// in ascending order (the weighted call at batch 1, the row-weighted one
+// above it; with a shared expert, its merged form), the shared expert and
+// the bf16 tail computed by the down launch's workgroups.
+int device_routed_impl(const uint64_t* table, int64_t num_experts, const int64_t* idx, const float* wts,
+                       int64_t top_k, const uint64_t* shared, Act hidden, float* out, float* out_shared,
+                       uint16_t* out_bf16, int* rejected, int64_t batch, int64_t inter, int64_t hid, int64_t gsc,
+                       int64_t dsc) {
+    if (num_experts <= 0 || num_experts > INT32_MAX || top_k <= 0 || batch <= 0 || batch > kMaxM ||
+        batch * top_k > kMaxGroups)
+        return plm::fail(-2, "bad dimensions (batch 1..%d, batch * top_k <= %d)", kMaxM, kMaxGroups);
+    if (moe_dims_bad(1, batch, inter, hid, gsc, dsc)) return plm::fail(-2, "bad dimensions");
+    const void* x = hidden.f32 != nullptr ? static_cast<const void*>(hidden.f32) : static_cast<const void*>(hidden.bf16);
+    if (hid % 16 != 0 || inter % 16 != 0 || !plm::aligned16(x))
+        return plm::fail(-2, "device routing needs sizes that are multiples of 16 and 16-byte aligned activations");
+    if (shared != nullptr) {
+        for (int r = 0; r < kPlanRoles; ++r)
+            if (shared[r] == 0) return plm::fail(-1, "null pointer");
+        if ((shared[0] | shared[2] | shared[4]) & 15u) return plm::fail(-2, "shared expert weights must be 16-byte aligned");
+    }
+    hipStream_t st = plm::current_stream();
+    const int ndev = static_cast<int>(batch * top_k);
+    const int groups = ndev + (shared != nullptr ? 1 : 0);
+    const size_t act_bytes =
+        static_cast<size_t>(plm::ceil_div(static_cast<int64_t>(groups) * batch * inter * 4, 256) * 256);
+    char* ws = static_cast<char*>(plm::workspace(act_bytes + sizeof(MoePlan)));
+    if (ws == nullptr) return -3;
+    float* act = reinterpret_cast<float*>(ws);
+    MoePlan* plan = reinterpret_cast<MoePlan*>(ws + act_bytes);
+    hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(64), 0, st, table, num_experts, idx, wts,
+                       static_cast<int>(batch), static_cast<int>(top_k), plan, rejected);
+    int code = plm::check_launch("moe plan kernel");
+    if (code != 0) return code;
+
+    RowsArgs a;
+    std::memset(&a, 0, sizeof(a));
+    if (shared != nullptr) {
+        a.w[0][0] = reinterpret_cast<const uint8_t*>(static_cast<uintptr_t>(shared[0]));
+        a.s[0][0] = reinterpret_cast<const float*>(static_cast<uintptr_t>(shared[1]));
+        a.w[1][0] = reinterpret_cast<const uint8_t*>(static_cast<uintptr_t>(shared[2]));
+        a.s[1][0] = reinterpret_cast<const float*>(static_cast<uintptr_t>(shared[3]));
+    }
+    a.x = hidden.f32;
+    a.xb = hidden.bf16;
+    a.x_stride = hid;
+    a.out[0] = act;
+    a.out_ld = inter;
+    a.rows = inter;
+    a.K = hid;
+    a.scale_cols = gsc;
+    a.nchunks = static_cast<int>(plm::ceil_div(hid, plm::kChunkBytes));
+    a.m_total = static_cast<int>(batch);
+    a.plan = plan;
+    a.ndev = ndev;
+    launch_rows<2, true>(a, static_cast<int>(batch), groups, st);
+    code = plm::check_launch("fp8 rows kernel");
+    if (code != 0) return code;
+
+    CombineArgs c;
+    std::memset(&c, 0, sizeof(c));
+    if (shared != nullptr) {
+        c.w[0] = reinterpret_cast<const uint8_t*>(static_cast<uintptr_t>(shared[4]));
+        c.s[0] = reinterpret_cast<const float*>(static_cast<uintptr_t>(shared[5]));
+    }
+    c.act = act;
+    c.route = reinterpret_cast<const float*>(reinterpret_cast<const char*>(plan) + offsetof(MoePlan, route));
+    c.route_sg = batch;
+    c.route_sm = 1;
+    c.zero_skip = batch > 1 ? 1 : 0;
+    c.out = out;
+    c.split_last = shared != nullptr ? 1 : 0;
+    c.out_last = shared != nullptr ? out_shared : nullptr;
+    c.rows = hid;
+    c.K = inter;
+    c.scale_cols = dsc;
+    c.ngroups = groups;
+    c.cps = static_cast<int>(plm::ceil_div(inter, plm::kChunkBytes));
+    c.m_total = static_cast<int>(batch);
+    c.plan = plan;
+    c.ndev = ndev;
+    c.fused = 1;
+    c.out_bf16 = out_bf16;
+    launch_combine(c, static_cast<int>(batch), st);
+    return plm::check_launch("fp8 combine kernel");
+}
+
 // Several weights of different row counts sharing the activations, in one
 // launch when the vector path applies (else one call per weight; the per-row
 // arithmetic is the same either way).
@@ -1342,6 +1621,31 @@ PLM_EXPORT int fp8_e4m3_block_mlp_many_pair_weighted_bf16x_f32(
         return plm::fail(-1, "null pointer");
     return pair_weighted_impl(gp, gsp, up, usp, dp, dsp, Act{nullptr, hidden_bf16}, pair_item_indices,
                               pair_row_indices, pair_weights, out, expert_count, pair_count, batch, inter, hid, gsc,
+                              dsc);
+}
+
+PLM_EXPORT int fp8_e4m3_block_moe_device_routed_f32(const uint64_t* expert_table, int64_t num_experts,
+                                                    const int64_t* route_indices, const float* route_weights,
+                                                    int64_t top_k, const uint64_t* shared_ptrs, const float* hidden,
+                                                    float* out, float* out_shared, uint16_t* out_bf16,
+                                                    int* rejected, int64_t batch, int64_t inter, int64_t hid,
+                                                    int64_t gsc, int64_t dsc) {
+    if (!expert_table || !route_indices || !route_weights || !hidden || !out || (shared_ptrs && !out_shared))
+        return plm::fail(-1, "null pointer");
+    return device_routed_impl(expert_table, num_experts, route_indices, route_weights, top_k, shared_ptrs,
+                              Act{hidden, nullptr}, out, out_shared, out_bf16, rejected, batch, inter, hid, gsc, dsc);
+}
+
+PLM_EXPORT int fp8_e4m3_block_moe_device_routed_bf16x_f32(const uint64_t* expert_table, int64_t num_experts,
+                                                          const int64_t* route_indices, const float* route_weights,
+                                                          int64_t top_k, const uint64_t* shared_ptrs,
+                                                          const uint16_t* hidden_bf16, float* out, float* out_shared,
+                                                          uint16_t* out_bf16, int* rejected, int64_t batch,
+                                                          int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
+    if (!expert_table || !route_indices || !route_weights || !hidden_bf16 || !out || (shared_ptrs && !out_shared))
+        return plm::fail(-1, "null pointer");
+    return device_routed_impl(expert_table, num_experts, route_indices, route_weights, top_k, shared_ptrs,
+                              Act{nullptr, hidden_bf16}, out, out_shared, out_bf16, rejected, batch, inter, hid, gsc,
                               dsc);
 }
 

@@ -19,6 +19,12 @@ same environment flags and the same bf16 accumulation:
 The shared expert's MLP is added last (1838-1862); every add into the output
 is a bf16 add.  Expert selection (sorted unique ids of the router's
 indices) needs the indices on the host, as in the reference.
+
+run_fp8_moe_device keeps the router's outputs on the device instead: the
+experts are chosen by a plan kernel from a device table of every expert
+(native.FP8ExpertTable), and the bf16 tail is done by the library, so the
+layer issues no host read-back.  Its values are those of the weighted path
+at M == 1 and of the row-weighted path at M > 1.
 """
 
 from __future__ import annotations
@@ -31,7 +37,7 @@ import torch
 
 from . import native
 
-__all__ = ["MoEOutput", "run_fp8_moe"]
+__all__ = ["MoEOutput", "run_fp8_moe", "run_fp8_moe_device"]
 
 
 def _enabled(name: str) -> bool:
@@ -140,3 +146,25 @@ def run_fp8_moe(hidden: torch.Tensor, route_indices: torch.Tensor, route_weights
             shared_out = native.fp8_e4m3_block_mlp_f32(*shared, x)
         out = out + shared_out.to(dtype)
     return MoEOutput(output=out.reshape(hidden.shape).contiguous(), selected_experts=selected, path=path)
+
+
+def run_fp8_moe_device(hidden: torch.Tensor, route_indices: torch.Tensor, route_weights: torch.Tensor,
+                       table: "native.FP8ExpertTable", shared: ExpertWeights | None = None, *,
+                       dtype: torch.dtype = torch.bfloat16) -> MoEOutput:
+    """run_fp8_moe with the experts chosen on the device (no host read-back
+    of the router's indices; at most 8 rows and 64 choices per call).
+
+    table holds every routed expert of the layer; route_indices / route_weights
+    are the router's [M, k] device tensors (route_deepseek).  selected_experts
+    is left empty: reading it would need the host round trip this path avoids.
+    """
+    flat = hidden.reshape(-1, hidden.shape[-1])
+    res = native.fp8_e4m3_block_moe_device_routed_f32(table, flat.to(dtype), route_indices, route_weights, shared,
+                                                      bf16_output=dtype == torch.bfloat16)
+    if res.output is not None:
+        out = res.output
+    else:
+        out = torch.zeros_like(flat, dtype=dtype) + res.routed.to(dtype)
+        if res.shared is not None:
+            out = out + res.shared.to(dtype)
+    return MoEOutput(output=out.reshape(hidden.shape).contiguous(), selected_experts=[], path="device_routed")

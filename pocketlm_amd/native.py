@@ -29,6 +29,7 @@ import ctypes
 import os
 from collections import OrderedDict
 from contextlib import contextmanager
+from dataclasses import dataclass
 
 import torch
 
@@ -406,7 +407,7 @@ def fp8_e4m3_block_mlp_avx512_f32(gate_weight, gate_scale_inv, up_weight, up_sca
 class _Experts:
     """Validated expert weights on one device plus the six host address tables."""
 
-    def __init__(self, items, hidden, dev: torch.device, bf16_ok: bool = False):
+    def __init__(self, items, hidden, dev: torch.device, bf16_ok: bool = False, check_hidden: bool = True):
         if not items:
             raise ValueError("items must not be empty")
         first = _fp8_bytes(items[0][0], dev)
@@ -433,6 +434,8 @@ class _Experts:
         self.prepared = prepared
         self.count = len(prepared)
         self.tables = [(ctypes.c_uint64 * self.count)(*[int(p[i].data_ptr()) for p in prepared]) for i in range(6)]
+        if not check_hidden:  # weights only (the device expert table)
+            return
         # bf16_ok: the caller has a bf16 twin to send bf16 activations to
         self.x, self.bf16 = _hidden_in(hidden, dev) if bf16_ok else (_hidden_f32(hidden, dev), False)
         if int(self.x.shape[1]) != self.hid:
@@ -507,6 +510,99 @@ def fp8_e4m3_block_mlp_many_weighted_shared_f32(items, shared, hidden, route_wei
             ex.dsc)
     _check("fp8_e4m3_block_mlp_many_weighted_shared_f32", code)
     return _home(out, hidden), _home(out_shared, hidden)
+
+
+class FP8ExpertTable:
+    """Every routed expert of one MoE layer resident on one device, and the
+    device table [6, num_experts] int64 of their addresses (rows: gate, gate
+    scale_inv, up, up scale_inv, down, down scale_inv) that the device-routed
+    MoE reads.  ``experts`` maps an expert id to its six tensors (or is a
+    sequence indexed by id); ids without weights get null addresses and
+    contribute nothing when the router picks them.  The table keeps the
+    tensors alive."""
+
+    def __init__(self, experts, num_experts: int, device: torch.device | str | None = None):
+        num_experts = int(num_experts)
+        if num_experts <= 0:
+            raise ValueError("num_experts must be positive")
+        items = experts.items() if hasattr(experts, "items") else enumerate(experts)
+        chosen = {int(k): v for k, v in items if v is not None}
+        if not chosen:
+            raise ValueError("experts must not be empty")
+        if any(k < 0 or k >= num_experts for k in chosen):
+            raise ValueError("expert ids must lie in [0, num_experts)")
+        dev = torch.device(device) if device is not None else _target_device(*next(iter(chosen.values())))
+        if dev.type != "cuda":
+            raise ValueError("the expert table lives on a HIP device")
+        ids = sorted(chosen)
+        ex = _Experts([chosen[k] for k in ids], torch.zeros((1, 1)), dev, check_hidden=False)
+        addr = torch.zeros((6, num_experts), dtype=torch.int64)
+        for col, prepared in zip(ids, ex.prepared):
+            for role in range(6):
+                addr[role, col] = int(prepared[role].data_ptr())
+        self.device = dev
+        self.num_experts = num_experts
+        self.inter, self.hid, self.gsc, self.dsc = ex.inter, ex.hid, ex.gsc, ex.dsc
+        self.table = addr.to(dev)
+        self._keep = ex.prepared
+
+
+@dataclass
+class DeviceRoutedMoE:
+    """Outputs of fp8_e4m3_block_moe_device_routed_f32, all on the device:
+    routed (fp32 [M, H], the route-weighted sum), shared (fp32 [M, H] or
+    None), output (bf16 [M, H]: routed and shared rounded and added as the
+    reference does in bf16, or None) and rejected (int32 [1]: router choices
+    out of range, which are left out, plus those of an expert with misaligned
+    weights, which contributes nothing)."""
+
+    routed: torch.Tensor
+    shared: torch.Tensor | None
+    output: torch.Tensor | None
+    rejected: torch.Tensor
+
+
+def fp8_e4m3_block_moe_device_routed_f32(table: FP8ExpertTable, hidden: torch.Tensor, route_indices: torch.Tensor,
+                                         route_weights: torch.Tensor, shared=None, *,
+                                         bf16_output: bool = True) -> DeviceRoutedMoE:
+    """The routed MoE with the experts chosen on the device: the router's
+    indices [M, k] and weights [M, k] stay in HBM, and no host read-back sits
+    between the router and the experts (run_fp8_moe,
+    src/pcketlm/core/runtime/fp8_source.py:1600-1862, reads the indices on
+    the host).  Same values as the host-routed calls given the chosen
+    experts in ascending order: the weighted kernel at M == 1, the
+    row-weighted one above (fp8_linear.cpp:475-589, 591-831), and the
+    shared expert as fp8_e4m3_block_mlp_f32.  M <= 8 and M * k <= 64."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_FP8_LINEAR", "Native FP8 device-routed MoE")
+    dev = table.device
+    x, bf16 = _hidden_in(hidden, dev)
+    if int(x.shape[1]) != table.hid:
+        raise ValueError("hidden input size does not match FP8 MLP input size")
+    batch = int(x.shape[0])
+    idx = _on(route_indices, dev, torch.int64).reshape(batch, -1)
+    w = _on(route_weights, dev, torch.float32).reshape(batch, -1)
+    if tuple(w.shape) != tuple(idx.shape):
+        raise ValueError("route_weights must have the shape of route_indices")
+    top_k = int(idx.shape[1])
+    shared_arr = None
+    keep = []
+    if shared is not None:
+        sh = _Experts([shared], torch.zeros((1, 1)), dev, check_hidden=False)
+        if (sh.inter, sh.hid) != (table.inter, table.hid):
+            raise ValueError("the shared expert must have the routed experts' shapes")
+        keep.append(sh)
+        shared_arr = (ctypes.c_uint64 * 6)(*[int(t.data_ptr()) for t in sh.prepared[0]])
+    out = torch.empty((batch, table.hid), dtype=torch.float32, device=dev)
+    out_shared = torch.empty_like(out) if shared is not None else None
+    out_bf16 = torch.empty((batch, table.hid), dtype=torch.bfloat16, device=dev) if bf16_output else None
+    rejected = torch.zeros((1,), dtype=torch.int32, device=dev)
+    with _launch(lib, dev):
+        code = getattr(lib, _twin("fp8_e4m3_block_moe_device_routed_f32", bf16))(
+            _p(table.table), table.num_experts, _p(idx), _p(w), top_k,
+            None if shared_arr is None else ctypes.cast(shared_arr, ctypes.c_void_p), _p(x), _p(out),
+            _p(out_shared), _p(out_bf16), _p(rejected), batch, table.inter, table.hid, table.gsc, table.dsc)
+    _check("fp8_e4m3_block_moe_device_routed_f32", code)
+    return DeviceRoutedMoE(out, out_shared, out_bf16, rejected)
 
 
 def fp8_e4m3_block_mlp_many_weighted_avx512_f32(items, hidden, route_weights) -> torch.Tensor:

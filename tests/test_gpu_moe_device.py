@@ -1,0 +1,176 @@
+"""The device-routed MoE (fp8_e4m3_block_moe_device_routed_f32 and its bf16
+twin): the router's device outputs choose the experts out of a device table.
+
+Checked against the host-routed calls given the same experts in ascending
+order (run_fp8_moe's selection, src/pcketlm/core/runtime/fp8_source.py:1600):
+the weighted kernel at M = 1, the row-weighted one above, the shared expert's
+MLP, bit for bit; the bf16 tail against torch's bf16 adds on the CPU
+(fp8_source.py:1762, 1861-1862); left-out indices counted.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def nat():
+    from pocketlm_amd import native
+
+    assert native.native_fp8_linear_available(), "libpocketlm_hip.so must load on the GPU box"
+    return native
+
+
+def _fp8(rows, cols, seed):
+    g = torch.Generator().manual_seed(seed)
+    w = (torch.randn((rows, cols), generator=g) * 0.02).to(torch.float8_e4m3fn).view(torch.uint8)
+    s = torch.rand(((rows + 127) // 128, (cols + 127) // 128), generator=g) * 9e-3 + 1e-3
+    return w.cuda(), s.cuda()
+
+
+def _expert(inter, hid, seed):
+    g, gs = _fp8(inter, hid, seed)
+    u, us = _fp8(inter, hid, seed + 1)
+    d, ds = _fp8(hid, inter, seed + 2)
+    return (g, gs, u, us, d, ds)
+
+
+def _x(m, hid, seed, dtype):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn((m, hid), generator=g).to(torch.bfloat16).to(dtype).cuda()
+
+
+def _host_routed(nat, experts, idx, w, x, shared):
+    """The host-routed calls on the valid chosen experts in ascending order;
+    a row that names an expert twice keeps its first weight."""
+    m, k = idx.shape
+    sel = sorted({int(e) for e in idx.reshape(-1) if int(e) in experts})
+    route = np.zeros((len(sel), m), dtype=np.float32)
+    for r in range(m):
+        seen = set()
+        for j in range(k):
+            e = int(idx[r, j])
+            if e in experts and e not in seen:
+                route[sel.index(e), r] = w[r, j]
+                seen.add(e)
+    items = [experts[e] for e in sel]
+    ys = None
+    if m == 1:
+        rt = torch.from_numpy(route[:, 0].copy()).cuda()
+        if shared is not None:
+            y, ys = nat.fp8_e4m3_block_mlp_many_weighted_shared_f32(items, shared, x, rt)
+        else:
+            y = nat.fp8_e4m3_block_mlp_many_weighted_f32(items, x, rt)
+    else:
+        y = nat.fp8_e4m3_block_mlp_many_row_weighted_f32(items, x, torch.from_numpy(route).cuda())
+        if shared is not None:
+            ys = nat.fp8_e4m3_block_mlp_f32(*shared, x)
+    return y, ys
+
+
+def _bf16_tail(y, ys):
+    """torch's bf16 adds of the reference, on the CPU: zeros + routed, + shared."""
+    out = torch.zeros(y.shape, dtype=torch.bfloat16) + y.cpu().to(torch.bfloat16)
+    if ys is not None:
+        out = out + ys.cpu().to(torch.bfloat16)
+    return out
+
+
+def _check(nat, table, experts, idx, w, x, shared, rejected=0):
+    res = nat.fp8_e4m3_block_moe_device_routed_f32(table, x, torch.from_numpy(idx).cuda(),
+                                                   torch.from_numpy(w).cuda(), shared)
+    y, ys = _host_routed(nat, experts, idx, w, x, shared)
+    torch.cuda.synchronize()
+    assert torch.equal(res.routed, y)
+    if shared is not None:
+        assert torch.equal(res.shared, ys)
+    else:
+        assert res.shared is None
+    assert torch.equal(res.output.cpu().view(torch.int16), _bf16_tail(y, ys).view(torch.int16))
+    assert int(res.rejected.item()) == rejected
+
+
+def _route(rng, m, k, num_experts):
+    idx = np.stack([rng.choice(num_experts, k, replace=False) for _ in range(m)]).astype(np.int64)
+    w = torch.from_numpy(rng.uniform(0.05, 0.5, (m, k)).astype(np.float32)).to(torch.bfloat16).float().numpy()
+    return idx, w
+
+
+def test_device_routed_deepseek_shapes_equal_host_routed(nat):
+    """DeepSeek-V3 experts (gate/up 2048x7168, down 7168x2048): one token
+    with top-8 of 12 resident experts plus the shared expert, and four tokens
+    whose choices overlap."""
+    experts = {e: _expert(2048, 7168, 900 + 3 * e) for e in range(12)}
+    shared = _expert(2048, 7168, 990)
+    table = nat.FP8ExpertTable(experts, 12)
+    rng = np.random.default_rng(21)
+    for m in (1, 4):
+        idx, w = _route(rng, m, 8, 12)
+        x = _x(m, 7168, 30 + m, torch.bfloat16)
+        _check(nat, table, experts, idx, w, x, shared)
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 8])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_device_routed_small_shapes_equal_host_routed(nat, m, dtype):
+    hid, inter, n = 512, 256, 32
+    experts = {e: _expert(inter, hid, 100 + 3 * e) for e in range(n)}
+    shared = _expert(inter, hid, 99)
+    table = nat.FP8ExpertTable(experts, n)
+    rng = np.random.default_rng(m)
+    idx, w = _route(rng, m, 4, n)
+    x = _x(m, hid, 40 + m, dtype)
+    _check(nat, table, experts, idx, w, x, shared)
+    _check(nat, table, experts, idx, w, x, None)
+
+
+def test_device_routed_leaves_out_bad_indices(nat):
+    """Indices outside [0, E) are left out and counted; an expert with a
+    misaligned weight contributes nothing and is counted; a row naming an
+    expert twice keeps its first weight; an id without weights contributes
+    nothing."""
+    hid, inter, n = 512, 256, 16
+    experts = {e: _expert(inter, hid, 300 + 3 * e) for e in range(n) if e != 9}
+    raw = torch.empty(inter * hid + 16, dtype=torch.uint8, device="cuda")
+    raw[1:1 + inter * hid].copy_(experts[5][0].reshape(-1))
+    odd = list(experts[5])
+    odd[0] = raw[1:1 + inter * hid].view(inter, hid)  # 1 byte past a 16-byte boundary
+    with_odd = dict(experts)
+    with_odd[5] = tuple(odd)
+    table = nat.FP8ExpertTable(with_odd, n)
+    idx = np.array([[3, -1, 7, 3], [16, 5, 2, 11], [9, 0, 7, 200]], dtype=np.int64)
+    w = np.array([[0.5, 0.25, 0.125, 0.375], [0.25, 0.5, 0.125, 0.0625], [0.5, 0.25, 0.3125, 0.125]],
+                 dtype=np.float32)
+    x = _x(3, hid, 50, torch.bfloat16)
+    valid = {e: t for e, t in experts.items() if e != 5}
+    # ids 9 (no weights) and 5 (misaligned): the host-routed reference
+    # leaves them out, the device plan keeps them as empty groups, which
+    # shifts the wave split of the later experts, so compare within rounding
+    res = nat.fp8_e4m3_block_moe_device_routed_f32(table, x, torch.from_numpy(idx).cuda(),
+                                                   torch.from_numpy(w).cuda(), None)
+    y, _ys = _host_routed(nat, valid, idx, w, x, None)
+    torch.cuda.synchronize()
+    assert int(res.rejected.item()) == 4  # -1, 16, 200 and the misaligned expert 5
+    err = (res.routed - y).norm() / y.norm()
+    assert float(err) < 1e-6
+    # without them the plan is the host selection exactly
+    idx2 = np.where(idx == 9, 1, np.where(idx == 5, 4, idx))
+    _check(nat, table, valid, idx2, w, x, None, rejected=3)
+
+
+def test_device_routed_argument_errors(nat):
+    hid, inter = 512, 256
+    experts = {0: _expert(inter, hid, 1), 1: _expert(inter, hid, 4)}
+    table = nat.FP8ExpertTable(experts, 2)
+    x = _x(9, hid, 2, torch.bfloat16)
+    idx = torch.zeros((9, 1), dtype=torch.int64, device="cuda")
+    with pytest.raises(RuntimeError, match="code -2"):
+        nat.fp8_e4m3_block_moe_device_routed_f32(table, x, idx, torch.ones((9, 1), device="cuda"))
+    with pytest.raises(ValueError):
+        nat.fp8_e4m3_block_moe_device_routed_f32(table, x[:, :256], idx, torch.ones((9, 1), device="cuda"))
+    with pytest.raises(ValueError):
+        nat.FP8ExpertTable(experts, 1)

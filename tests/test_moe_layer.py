@@ -97,3 +97,31 @@ def test_device_moe_layer_vs_oracle(oracle_mod, monkeypatch, m, env):
     diff = np.abs(got - want)
     assert (diff <= np.abs(want) * 2 ** -7 + 1e-7).all()
     assert (diff == 0).mean() > 0.97
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [1, 3])
+def test_device_routed_layer_equals_host_routed_layer(oracle_mod, monkeypatch, m):
+    """run_fp8_moe_device (experts chosen on the device, bf16 tail in the
+    library) gives run_fp8_moe's bf16 output bit for bit: the weighted path
+    at M = 1, the row-weighted path at M = 3; and the oracle's layer within
+    one bf16 step."""
+    from pocketlm_amd import moe, native
+
+    monkeypatch.setenv("PCKETLM_ENABLE_FP8_MOE_ROW_WEIGHTED_MANY", "1")
+    experts, shared, x, idx, w = _layer(31 + m, m, oracle_mod)
+    dev_experts = {e: tuple(torch.from_numpy(t).cuda() for t in ex) for e, ex in experts.items()}
+    dev_shared = tuple(torch.from_numpy(t).cuda() for t in shared)
+    table = native.FP8ExpertTable(dev_experts, E)
+    xd = torch.from_numpy(x).cuda().to(torch.bfloat16)
+    idx_d = torch.from_numpy(idx).cuda()
+    w_d = torch.from_numpy(w).cuda().to(torch.bfloat16)
+    got = moe.run_fp8_moe_device(xd, idx_d, w_d, table, dev_shared)
+    ref = moe.run_fp8_moe(xd, idx_d, w_d, dev_experts, dev_shared)
+    torch.cuda.synchronize()
+    assert got.path == "device_routed" and ref.path == ("weighted" if m == 1 else "row_weighted")
+    assert got.output.dtype == torch.bfloat16 and tuple(got.output.shape) == (m, H)
+    assert torch.equal(got.output.view(torch.int16), ref.output.view(torch.int16))
+    want, _sel, _path = oracle_mod.run_fp8_moe(x, idx, w, experts, shared, mode="auto" if m == 1 else "row")
+    diff = np.abs(got.output.float().cpu().numpy() - want)
+    assert (diff <= np.abs(want) * 2 ** -7 + 1e-7).all()
