@@ -686,6 +686,10 @@ def table(args):
     if want("ds-v3 MoE layer"):
         moe_layer()
 
+    transfers = []
+    if want("fp8 pack -> HBM"):
+        transfers.append(pack_transfer(torch))
+
     lines = [f"CPU: the oracle's restatement (kind \"port\"), {oracle.num_threads()} OpenMP threads, "
              "weights warm in host RAM; about 1.5 s of calls per row.", "",
              "| workload | M | GPU µs (mean) | GPU GB/s | % of 8 TB/s | CPU µs | CPU GB/s | CPU kind |",
@@ -693,10 +697,76 @@ def table(args):
     for name, m, us, gbs, pct, cus, cgbs, kind in rows_out:
         lines.append(f"| {name} | {m} | {us:.2f} | {gbs:.0f} | {pct:.1f} | "
                      + (f"{cus:.0f} | {cgbs:.2f} | {kind} |" if cus else "— | — | — |"))
+    if transfers:
+        lines += ["", "Weight files to HBM (file in the page cache, median of 5 loads; PCIe 5.0 x16 = 64 GB/s "
+                  "per direction):", "",
+                  "| transfer | MB | ms | GB/s | % of 64 GB/s | mmap + torch .to(device) ms | its GB/s |",
+                  "|---|---|---|---|---|---|---|"]
+        for name, nbytes, ms, base_ms in transfers:
+            lines.append(f"| {name} | {nbytes / 1e6:.1f} | {ms:.1f} | {nbytes / ms / 1e6:.1f} | "
+                         f"{100 * nbytes / ms / 1e6 / 64:.1f} | {base_ms:.1f} | {nbytes / base_ms / 1e6:.1f} |")
     text = "\n".join(lines)
     print(text)
     if args.table_out:
         Path(args.table_out).write_text(text + "\n")
+
+
+def pack_transfer(torch):
+    """One DeepSeek-V3 layer's 8 routed experts (352.5 MB) written as an FP8
+    pack and loaded into HBM by layer and expert id through the native
+    staging pipeline, against the host path of the reference's reader (mmap
+    views, torch.frombuffer, .to(device) per tensor)."""
+    import shutil
+    import tempfile
+
+    from pocketlm_amd import packs
+
+    gen = torch.Generator().manual_seed(7)
+    tensors = {}
+    for e in range(8):
+        for proj, shape in (("gate_proj", (2048, 7168)), ("up_proj", (2048, 7168)), ("down_proj", (7168, 2048))):
+            name = f"model.layers.5.mlp.experts.{e}.{proj}.weight"
+            tensors[name] = torch.randint(0, 255, shape, dtype=torch.uint8, generator=gen)
+            tensors[name + "_scale_inv"] = torch.rand(((shape[0] + 127) // 128, (shape[1] + 127) // 128), generator=gen)
+    nbytes = sum(t.numel() * t.element_size() for t in tensors.values())
+    root = Path(tempfile.mkdtemp(prefix="pack_bench_"))
+    try:
+        packs.write_fp8_pack(tensors, root / "model" / "artifacts" / "fp8_pack", pack_bytes=1 << 30)
+        del tensors
+        reader = packs.FP8PackReader(root / "model")
+        ids = list(range(8))
+        names = [n for n in reader.tensors]
+
+        def native_load():
+            return reader.load_layer_experts(5, ids)
+
+        def torch_load():
+            out = {}
+            for n in names:
+                view = reader.get_tensor_bytes(n)
+                out[n] = torch.frombuffer(view, dtype=torch.uint8).to("cuda")
+                del view
+            return out
+
+        times = {}
+        for label, fn in (("native", native_load), ("torch", torch_load)):
+            fn()
+            torch.cuda.synchronize()
+            runs = []
+            for _ in range(5):
+                t0 = time.perf_counter()
+                res = fn()
+                torch.cuda.synchronize()
+                runs.append((time.perf_counter() - t0) * 1e3)
+                del res
+            times[label] = sorted(runs)[2]
+        reader.close()
+    finally:
+        shutil.rmtree(root, ignore_errors=True)
+    name = "fp8 pack -> HBM, 8 DS-V3 experts"
+    print(f"{name:40s} {nbytes / 1e6:.1f} MB  {times['native']:.1f} ms  {nbytes / times['native'] / 1e6:.1f} GB/s  "
+          f"(mmap + torch .to(device): {times['torch']:.1f} ms)", flush=True)
+    return name, nbytes, times["native"], times["torch"]
 
 
 def pmc_probe(args):

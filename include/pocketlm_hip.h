@@ -382,6 +382,45 @@ int ds_route_topk_f32(const float* logits, const float* bias, int64_t batch, int
                       int64_t top_k, int64_t n_groups, int64_t topk_groups, int scoring,
                       float route_scale, int64_t* out_indices, float* out_weights);
 
+/* ---------------------------------------------------------------- weight files to HBM */
+
+/* New export: byte ranges of a file copied into device memory (current
+ * device), for the reference's on-disk artifacts that it reads into host
+ * memory (FP8 pack spans, src/pcketlm/core/runtime/fp8_pack.py:54-241; row8
+ * artifacts, src/pcketlm/native/row8_artifact_cache.cpp:20-147; Q4
+ * safetensors shards, src/pcketlm/core/model_import/q4_quantize.py:92-168).
+ * Span i is file bytes [file_offsets[i], file_offsets[i] + byte_lengths[i])
+ * to device address device_dsts[i].  Reader threads fill pinned staging
+ * buffers and overlap their reads with the copies; the copies start after
+ * the work queued on the library's stream, and the call returns when the
+ * bytes are in device memory.  Codes -1 null, -2 a span outside the file,
+ * -5 open/read failure, -(1000 + hipError_t). */
+int pocketlm_file_spans_to_device(const char* path, const uint64_t* file_offsets, const uint64_t* byte_lengths,
+                                  const uint64_t* device_dsts, int64_t count);
+
+/* row8_artifact_cache.cpp:20-43: nbytes at offset of a row8 artifact file
+ * (nbytes even and non-zero) loaded into a device buffer the handle owns;
+ * NULL on failure.  Here the bytes land in device memory. */
+void* row8_artifact_load_tensor(const char* path, uint64_t offset, uint64_t nbytes);
+/* row8_artifact_cache.cpp:45-48: frees the handle and its device buffer. */
+void row8_artifact_free_tensor(void* handle);
+/* row8_artifact_cache.cpp:50-56: the handle's data, a device pointer here
+ * (every tensor pointer of this library is one), ready for
+ * native_packed_gemv_rows8. */
+const uint16_t* row8_artifact_tensor_data(void* handle);
+/* row8_artifact_cache.cpp:58-64. */
+uint64_t row8_artifact_tensor_nbytes(void* handle);
+/* row8_artifact_cache.cpp:66-102: a read-only mapping of the whole file
+ * (host memory), NULL on failure. */
+void* row8_artifact_map_file(const char* path);
+/* row8_artifact_cache.cpp:104-120. */
+void row8_artifact_unmap_file(void* handle);
+/* row8_artifact_cache.cpp:122-138: host pointer to [offset, offset + nbytes)
+ * of the mapping, NULL for an odd or out-of-range request. */
+const uint16_t* row8_artifact_mapped_data(void* handle, uint64_t offset, uint64_t nbytes);
+/* row8_artifact_cache.cpp:140-147. */
+uint64_t row8_artifact_mapped_nbytes(void* handle);
+
 /* New export: run_fp8_moe (src/pcketlm/core/runtime/fp8_source.py:1569-1884)
  * with the experts chosen on the device.  The reference reads the router's
  * indices on the host (sorted unique experts, 1600) before it calls the

@@ -30,6 +30,7 @@ import os
 from collections import OrderedDict
 from contextlib import contextmanager
 from dataclasses import dataclass
+from pathlib import Path
 
 import torch
 
@@ -1096,3 +1097,122 @@ def route_deepseek(logits: torch.Tensor, *, top_k: int = 8, n_groups: int = 8, t
                                      0 if scoring_func == "sigmoid" else 1, float(route_scale), _p(idx), _p(w))
     _check("ds_route_topk_f32", code)
     return _home(idx, logits), _home(w.to(torch.bfloat16), logits)
+
+
+# --------------------------------------------------------------------------- weight files to HBM
+
+def native_row8_artifact_available() -> bool:
+    return _available("PCKETLM_DISABLE_NATIVE_ROW8_ARTIFACT")
+
+
+def file_spans_to_device(path: str | Path, spans) -> None:
+    """Copy file byte ranges straight into device tensors: spans is a list of
+    (file_offset, tensor) pairs, each tensor a contiguous device tensor that
+    receives tensor.nbytes bytes from file_offset.  Returns when the bytes
+    are in device memory (pocketlm_file_spans_to_device)."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_FILE_IO", "Native file transfer")
+    spans = [(int(off), t) for off, t in spans if int(t.numel()) > 0]
+    if not spans:
+        return
+    dev = spans[0][1].device
+    for _off, t in spans:
+        if t.device != dev or t.device.type != "cuda" or not t.is_contiguous():
+            raise ValueError("span destinations must be contiguous tensors on one HIP device")
+    n = len(spans)
+    offs = (ctypes.c_uint64 * n)(*[off for off, _t in spans])
+    lens = (ctypes.c_uint64 * n)(*[t.numel() * t.element_size() for _off, t in spans])
+    dsts = (ctypes.c_uint64 * n)(*[t.data_ptr() for _off, t in spans])
+    with _launch(lib, dev):
+        code = lib.pocketlm_file_spans_to_device(str(path).encode("utf-8"), ctypes.cast(offs, ctypes.c_void_p),
+                                                 ctypes.cast(lens, ctypes.c_void_p), ctypes.cast(dsts, ctypes.c_void_p),
+                                                 n)
+    _check("pocketlm_file_spans_to_device", code)
+
+
+class NativeRow8Tensor:
+    """src/pcketlm/native/__init__.py:2017-2049: nbytes at offset of a row8
+    artifact file, loaded by the library.  ptr is a device pointer here."""
+
+    def __init__(self, path: str | Path, offset: int, nbytes: int):
+        lib = _require("PCKETLM_DISABLE_NATIVE_ROW8_ARTIFACT", "Native row8 artifact cache")
+        with _launch(lib, torch.device("cuda", torch.cuda.current_device())):
+            handle = lib.row8_artifact_load_tensor(str(Path(path)).encode("utf-8"), ctypes.c_ulonglong(int(offset)),
+                                                   ctypes.c_ulonglong(int(nbytes)))
+        if not handle:
+            raise OSError(f"row8_artifact_load_tensor failed for {path}")
+        self._lib = lib
+        self._handle = ctypes.c_void_p(handle)
+        self.nbytes = int(lib.row8_artifact_tensor_nbytes(self._handle))
+        ptr = lib.row8_artifact_tensor_data(self._handle)
+        if not ptr or self.nbytes != int(nbytes):
+            self.close()
+            raise OSError(f"row8_artifact_tensor_data failed for {path}")
+        self.ptr = int(ptr)
+        self.path = str(path)
+        self.offset = int(offset)
+
+    def close(self) -> None:
+        if getattr(self, "_handle", None):
+            self._lib.row8_artifact_free_tensor(self._handle)
+            self._handle = None
+            self.ptr = 0
+
+    def __del__(self):  # pragma: no cover - GC safety net
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def load_native_row8_tensor(path: str | Path, offset: int, nbytes: int) -> NativeRow8Tensor:
+    return NativeRow8Tensor(path, offset, nbytes)
+
+
+class NativeRow8MappedFile:
+    """src/pcketlm/native/__init__.py:2056-2090: a read-only host mapping
+    (host memory: needs the library but no device)."""
+
+    def __init__(self, path: str | Path):
+        if _flag("PCKETLM_DISABLE_NATIVE_ROW8_ARTIFACT"):
+            raise RuntimeError("Native row8 artifact cache is unavailable: disabled")
+        try:
+            lib = _lib.load()
+        except OSError as exc:
+            raise RuntimeError(f"Native row8 artifact cache is unavailable: {exc}") from exc
+        handle = lib.row8_artifact_map_file(str(Path(path)).encode("utf-8"))
+        if not handle:
+            raise OSError(f"row8_artifact_map_file failed for {path}")
+        self._lib = lib
+        self._handle = ctypes.c_void_p(handle)
+        self.nbytes = int(lib.row8_artifact_mapped_nbytes(self._handle))
+        self.path = str(path)
+
+    def data_ptr(self, offset: int, nbytes: int) -> int:
+        ptr = self._lib.row8_artifact_mapped_data(self._handle, ctypes.c_ulonglong(int(offset)),
+                                                  ctypes.c_ulonglong(int(nbytes)))
+        if not ptr:
+            raise ValueError("row8 mapped tensor range is invalid")
+        return int(ptr)
+
+    def close(self) -> None:
+        if getattr(self, "_handle", None):
+            self._lib.row8_artifact_unmap_file(self._handle)
+            self._handle = None
+
+    def __del__(self):  # pragma: no cover - GC safety net
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class NativeRow8MappedTensor:
+    def __init__(self, mapped_file: NativeRow8MappedFile, offset: int, nbytes: int):
+        self._mapped_file = mapped_file
+        self.offset = int(offset)
+        self.nbytes = int(nbytes)
+        self.ptr = mapped_file.data_ptr(offset, nbytes)
+
+
+def map_native_row8_file(path: str | Path) -> NativeRow8MappedFile:
+    return NativeRow8MappedFile(path)
