@@ -128,6 +128,23 @@ def test_device_routed_small_shapes_equal_host_routed(nat, m, dtype):
     _check(nat, table, experts, idx, w, x, None)
 
 
+def test_device_routed_at_the_group_limit(nat):
+    """Eight rows of top-8 over 64 experts: 64 routed groups, the plan's
+    limit, plus the shared expert as a 65th group of both launches; a row
+    of all-duplicate choices keeps its first weight."""
+    hid, inter, n = 512, 256, 64
+    experts = {e: _expert(inter, hid, 500 + 3 * e) for e in range(n)}
+    shared = _expert(inter, hid, 497)
+    table = nat.FP8ExpertTable(experts, n)
+    idx = np.arange(64, dtype=np.int64).reshape(8, 8)[:, ::-1].copy()  # every expert once, rows descending
+    w = torch.from_numpy(np.random.default_rng(9).uniform(0.05, 0.5, (8, 8)).astype(np.float32)).to(
+        torch.bfloat16).float().numpy()
+    x = _x(8, hid, 60, torch.bfloat16)
+    _check(nat, table, experts, idx, w, x, shared)
+    idx[3] = 17  # one row names expert 17 eight times
+    _check(nat, table, experts, idx, w, x, shared)
+
+
 def test_device_routed_leaves_out_bad_indices(nat):
     """Indices outside [0, E) are left out and counted; an expert with a
     misaligned weight contributes nothing and is counted; a row naming an
