@@ -680,8 +680,86 @@ def table(args):
         rows_out.append(("ds-v3 MoE layer (8 routed + shared, 2 launches)", 1, 1e3 * med, gbs, 100 * gbs / PEAK_HBM_GBS,
                          cpu_us, cpu_gbs, "port"))
         rows_out.append((dev_name, 1, 1e3 * dev_med, dev_gbs, 100 * dev_gbs / PEAK_HBM_GBS, cpu_us, cpu_gbs, "port"))
+        for name, us in decode_steps(layers, dev_tables, logits, x):
+            gbs_s = nbytes / (us / 1e6) / 1e9
+            rows_out.append((name, 1, us, gbs_s, 100 * gbs_s / PEAK_HBM_GBS, None, None, "port"))
         del layers, dev_tables
         torch.cuda.empty_cache()
+
+    def decode_steps(layers, dev_tables, logits, x):
+        """Whole decode steps, router included, by wall clock over 30 steps:
+        the reference's order (route, read the indices on the host, launch the
+        chosen experts), the device-routed step, and that step replayed as one
+        HIP graph."""
+        k = 8
+        route_w = torch.empty((1, k), device="cuda")
+        yb = torch.empty((1, 7168), dtype=torch.bfloat16, device="cuda")
+        y2 = torch.empty((1, 7168), device="cuda")
+        ys2 = torch.empty((1, 7168), device="cuda")
+        rej = torch.zeros((1,), dtype=torch.int32, device="cuda")
+        idx0, _w0 = native.route_deepseek(logits)
+        slot = {e: j for j, e in enumerate(idx0[0].tolist())}  # expert id -> the layer's j-th expert
+
+        def host_step(i):
+            idx, w = native.route_deepseek(logits)
+            chosen = sorted(idx[0].tolist())  # the host read-back
+            order = [slot[e] for e in chosen]
+            layer = layers[i % len(layers)]
+            tabs = [(ctypes.c_uint64 * 9)(*([layer[j][r].data_ptr() for j in order] + [layer[8][r].data_ptr()]))
+                    for r in range(6)]
+            pos = {e: j for j, e in enumerate(idx[0].tolist())}
+            route_w.copy_(w[0, [pos[e] for e in chosen]].float().reshape(1, k))
+            lib.pocketlm_set_stream(_stream_ptr(torch))
+            rc = lib.fp8_e4m3_block_mlp_many_weighted_shared_bf16x_f32(
+                *[ctypes.cast(t, ctypes.c_void_p) for t in tabs], ctypes.c_void_p(x.data_ptr()),
+                ctypes.c_void_p(route_w.data_ptr()), ctypes.c_void_p(y2.data_ptr()), ctypes.c_void_p(ys2.data_ptr()),
+                k, 1, 2048, 7168, 56, 16)
+            if rc != 0:
+                raise RuntimeError("host-routed step failed")
+            torch.add(y2.to(torch.bfloat16), ys2.to(torch.bfloat16), out=yb)
+
+        def dev_step(i):
+            idx, w = native.route_deepseek(logits)
+            t = dev_tables[i % len(dev_tables)]
+            lib.pocketlm_set_stream(_stream_ptr(torch))
+            rc = lib.fp8_e4m3_block_moe_device_routed_bf16x_f32(
+                ctypes.c_void_p(t[0].data_ptr()), 256, ctypes.c_void_p(idx.data_ptr()),
+                ctypes.c_void_p(w.float().data_ptr()), k, ctypes.cast(t[1], ctypes.c_void_p),
+                ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y2.data_ptr()), ctypes.c_void_p(ys2.data_ptr()),
+                ctypes.c_void_p(yb.data_ptr()), ctypes.c_void_p(rej.data_ptr()), 1, 2048, 7168, 56, 16)
+            if rc != 0:
+                raise RuntimeError("device-routed step failed")
+
+        def wall(fn, n=30):
+            for i in range(3):
+                fn(i)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for i in range(n):
+                fn(i)
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) / n * 1e6
+
+        out = [("ds-v3 router + MoE step, host read-back (reference order)", wall(host_step)),
+               ("ds-v3 router + MoE step, device-routed", wall(dev_step))]
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        graphs = []
+        with torch.cuda.stream(side):
+            for i in range(len(dev_tables)):
+                dev_step(i)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        for i in range(len(dev_tables)):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                dev_step(i)
+            graphs.append(g)
+        out.append(("ds-v3 router + MoE step, device-routed, one HIP graph", wall(lambda i: graphs[i % len(graphs)].replay())))
+        lib.pocketlm_set_stream(_stream_ptr(torch))
+        for name, us in out:
+            print(f"{name:40s} M=1  {us:9.2f} us (wall clock per step)", flush=True)
+        return out
 
     if want("ds-v3 MoE layer"):
         moe_layer()

@@ -136,14 +136,20 @@ __global__ __launch_bounds__(256) void ds_route_kernel(const float* __restrict__
         __syncthreads();
     }
     for (int64_t e = threadIdx.x; e < experts; e += blockDim.x) choice[e] = bias ? score[e] + bias[e] : score[e];
+    __shared__ float gscore[64];
+    __shared__ int keep[64];
+    __shared__ uint32_t taken[128];  // one bit per expert (at most 4096)
+    __shared__ int red_first[4], red_e[4];
+    __shared__ float red_v[4];
+    for (int t = threadIdx.x; t < 128; t += blockDim.x) taken[t] = 0u;
     __syncthreads();
-    if (threadIdx.x != 0) return;
     const float ninf = -__builtin_inff();
     if (n_groups > 1) {
+        // group scores, one thread per group: max, or the sum of the two
+        // largest when a bias is present (the same scan as a sort's top 2)
         const int64_t gsz = experts / n_groups;
-        float gscore[64];
-        bool keep[64];
-        for (int64_t g = 0; g < n_groups; ++g) {
+        if (threadIdx.x < n_groups) {
+            const int64_t g = threadIdx.x;
             float b1 = ninf, b2 = ninf;
             for (int64_t j = 0; j < gsz; ++j) {
                 const float v = choice[g * gsz + j];
@@ -155,35 +161,83 @@ __global__ __launch_bounds__(256) void ds_route_kernel(const float* __restrict__
                 }
             }
             gscore[g] = bias ? b1 + b2 : b1;
-            keep[g] = false;
+            keep[g] = 0;
         }
-        int64_t kg = topk_groups < 1 ? 1 : (topk_groups > n_groups ? n_groups : topk_groups);
-        for (int64_t i = 0; i < kg; ++i) {
-            int64_t best = -1;
-            for (int64_t g = 0; g < n_groups; ++g)
-                if (!keep[g] && (best < 0 || gscore[g] > gscore[best])) best = g;
-            keep[best] = true;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const int64_t kg = topk_groups < 1 ? 1 : (topk_groups > n_groups ? n_groups : topk_groups);
+            for (int64_t i = 0; i < kg; ++i) {
+                int64_t best = -1;
+                for (int64_t g = 0; g < n_groups; ++g)
+                    if (!keep[g] && (best < 0 || gscore[g] > gscore[best])) best = g;
+                keep[best] = 1;
+            }
         }
-        for (int64_t g = 0; g < n_groups; ++g)
-            if (!keep[g])
-                for (int64_t j = 0; j < gsz; ++j) choice[g * gsz + j] = ninf;
+        __syncthreads();
+        for (int64_t e = threadIdx.x; e < experts; e += blockDim.x)
+            if (!keep[e / gsz]) choice[e] = ninf;
+        __syncthreads();
     }
+    // Top-k as k rounds of a block-wide arg max over the experts not taken.
+    // A scan in expert order keeps the first of equal values and never moves
+    // off a NaN it starts from, nor onto one: so a round picks the first free
+    // expert when its choice is NaN, else the largest non-NaN choice, the
+    // lowest id among equals.
     const int64_t k = top_k < 1 ? 1 : (top_k > experts ? experts : top_k);
     int64_t* idx = out_idx + static_cast<int64_t>(blockIdx.x) * top_k;
     float* w = out_w + static_cast<int64_t>(blockIdx.x) * top_k;
-    float sum = 0.0f;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    float sum = 0.0f;  // thread 0
     for (int64_t i = 0; i < k; ++i) {
-        int64_t best = -1;
-        for (int64_t e = 0; e < experts; ++e) {
-            bool taken = false;
-            for (int64_t j = 0; j < i; ++j) taken = taken || idx[j] == e;
-            if (taken) continue;
-            if (best < 0 || choice[e] > choice[best]) best = e;
+        int first = 0x7FFFFFFF;
+        int be = -1;
+        float bv = ninf;
+        for (int64_t e = threadIdx.x; e < experts; e += blockDim.x) {
+            if ((taken[e >> 5] >> (e & 31)) & 1u) continue;
+            if (first == 0x7FFFFFFF) first = static_cast<int>(e);
+            const float v = choice[e];
+            if (v == v && (be < 0 || v > bv)) {
+                bv = v;
+                be = static_cast<int>(e);
+            }
         }
-        idx[i] = best;
-        w[i] = score[best];
-        sum += score[best];
+        for (int off = 32; off > 0; off >>= 1) {
+            const int of = __shfl_xor(first, off);
+            const float ov = __shfl_xor(bv, off);
+            const int oe = __shfl_xor(be, off);
+            first = of < first ? of : first;
+            if (oe >= 0 && (be < 0 || ov > bv || (ov == bv && oe < be))) {
+                bv = ov;
+                be = oe;
+            }
+        }
+        if (lane == 0) {
+            red_first[wave] = first;
+            red_e[wave] = be;
+            red_v[wave] = bv;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int t = 1; t < static_cast<int>(blockDim.x >> 6); ++t) {
+                first = red_first[t] < first ? red_first[t] : first;
+                const int oe = red_e[t];
+                const float ov = red_v[t];
+                if (oe >= 0 && (be < 0 || ov > bv || (ov == bv && oe < be))) {
+                    bv = ov;
+                    be = oe;
+                }
+            }
+            const float cf = choice[first];
+            const int pick = (cf != cf || be < 0) ? first : be;
+            idx[i] = pick;
+            w[i] = score[pick];
+            sum += score[pick];
+            taken[pick >> 5] |= 1u << (pick & 31);
+        }
+        __syncthreads();
     }
+    if (threadIdx.x != 0) return;
     const float denom = sum > 1e-12f ? sum : 1e-12f;
     for (int64_t i = 0; i < k; ++i) {
         const float v = scoring == 0 ? w[i] / denom : w[i];

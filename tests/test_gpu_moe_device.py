@@ -191,3 +191,45 @@ def test_device_routed_argument_errors(nat):
         nat.fp8_e4m3_block_moe_device_routed_f32(table, x[:, :256], idx, torch.ones((9, 1), device="cuda"))
     with pytest.raises(ValueError):
         nat.FP8ExpertTable(experts, 1)
+
+
+def test_router_and_device_routed_moe_replay_in_a_hip_graph(nat):
+    """The DeepSeek router and the device-routed MoE hold no host read-back,
+    so the whole step captures into one HIP graph.  Each replay, with new
+    router logits and hidden state copied into the captured inputs and eager
+    work in between, equals the eager step."""
+    hid, inter, n = 512, 256, 32
+    experts = {e: _expert(inter, hid, 700 + 3 * e) for e in range(n)}
+    shared = _expert(inter, hid, 697)
+    table = nat.FP8ExpertTable(experts, n)
+    gen = torch.Generator(device="cuda").manual_seed(13)
+    logits = torch.randn((2, n), device="cuda", generator=gen)
+    x = torch.randn((2, hid), device="cuda", generator=gen).to(torch.bfloat16)
+
+    def step(lg, hx):
+        idx, w = nat.route_deepseek(lg, top_k=4, n_groups=8, topk_groups=4)
+        return nat.fp8_e4m3_block_moe_device_routed_f32(table, hx, idx, w, shared)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):  # the library's workspace for this stream exists before the capture
+            step(logits, x)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        captured = step(logits, x)
+    busy = torch.randn((256, 256), device="cuda")
+    for trial in range(4):
+        logits.copy_(torch.randn((2, n), device="cuda", generator=gen))
+        x.copy_(torch.randn((2, hid), device="cuda", generator=gen).to(torch.bfloat16))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = step(logits, x)
+        busy = busy @ busy.T / 256.0  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(captured.routed, eager.routed), trial
+        assert torch.equal(captured.shared, eager.shared), trial
+        assert torch.equal(captured.output.view(torch.int16), eager.output.view(torch.int16)), trial
+        assert int(captured.rejected.item()) == 0

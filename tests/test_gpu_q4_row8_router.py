@@ -263,3 +263,66 @@ def test_deepseek_route_kat_and_random(nat, golden, oracle_mod):
         oi, ow = oracle_mod.deepseek_route(logits, bias=b)
         assert host(idx).tolist() == oi.tolist()
         assert np.allclose(host(w.float()), ow, rtol=8e-3)
+
+
+def _route_in_order(logits, top_k, n_groups, topk_groups, bias, scale):
+    """The routing as one in-order scan per step (strict > keeps the first
+    of equal values; a NaN is kept only when it is where a scan starts)."""
+    out_i, out_w = [], []
+    for lg in logits.astype(np.float32):
+        with np.errstate(all="ignore"):
+            score = (np.float32(1) / (np.float32(1) + np.exp(-lg))).astype(np.float32)
+        choice = (score + bias).astype(np.float32) if bias is not None else score.copy()
+        e_n = len(choice)
+        if n_groups > 1:
+            gsz = e_n // n_groups
+            gs = []
+            for g in range(n_groups):
+                b1 = b2 = np.float32(-np.inf)
+                for v in choice[g * gsz:(g + 1) * gsz]:
+                    if v > b1:
+                        b1, b2 = v, b1
+                    elif v > b2:
+                        b2 = v
+                gs.append(np.float32(b1 + b2) if bias is not None else b1)
+            keep = set()
+            for _ in range(max(1, min(topk_groups, n_groups))):
+                best = -1
+                for g in range(n_groups):
+                    if g not in keep and (best < 0 or gs[g] > gs[best]):
+                        best = g
+                keep.add(best)
+            for g in range(n_groups):
+                if g not in keep:
+                    choice[g * gsz:(g + 1) * gsz] = -np.inf
+        taken, sel = set(), []
+        for _ in range(top_k):
+            best = -1
+            for e in range(e_n):
+                if e not in taken and (best < 0 or choice[e] > choice[best]):
+                    best = e
+            taken.add(best)
+            sel.append(best)
+        out_i.append(sel)
+    return np.array(out_i, dtype=np.int64)
+
+
+def test_deepseek_route_ties_nans_and_masked_experts(nat):
+    """The block-wide arg max of the router picks what the in-order scan
+    picks: exact ties (lowest id), NaN logits, and more choices than the
+    kept groups hold (the rest from the masked -inf experts, lowest ids)."""
+    rng = np.random.default_rng(5)
+    tied = rng.choice(np.array([-1.0, 0.0, 0.5, 1.0], dtype=np.float32), size=(6, 256))
+    nans = rng.standard_normal((4, 256)).astype(np.float32)
+    nans[0, 0] = np.nan          # the first expert: a scan starts on it
+    nans[1, [3, 77, 200]] = np.nan
+    nans[2, :] = np.nan
+    nans[3, 5:40] = np.nan
+    bias = (rng.choice(np.array([0.0, 0.25], dtype=np.float32), size=256))
+    for logits in (tied, nans):
+        for b in (None, bias):
+            for top_k, groups, kept in ((8, 8, 4), (40, 8, 1), (8, 1, 1), (16, 4, 2)):
+                idx, _w = nat.route_deepseek(dev(logits), top_k=top_k, n_groups=groups, topk_groups=kept,
+                                             bias=None if b is None else dev(b))
+                want = _route_in_order(logits, top_k, groups, kept, b, 2.5)
+                assert host(idx).tolist() == want.tolist(), (top_k, groups, kept, b is None)
