@@ -114,9 +114,9 @@ __global__ __launch_bounds__(256) void ds_route_kernel(const float* __restrict__
                                                        int64_t experts, int64_t top_k, int64_t n_groups,
                                                        int64_t topk_groups, int scoring, float route_scale,
                                                        int64_t* __restrict__ out_idx, float* __restrict__ out_w) {
-    extern __shared__ float sh[];
-    float* score = sh;              // [experts]
-    float* choice = sh + experts;   // [experts]
+    extern __shared__ float4 sh4[];  // 16-byte aligned: choice is read four values at a time
+    float* score = reinterpret_cast<float*>(sh4);  // [experts]
+    float* choice = score + experts;                // [experts]
     const float* lrow = logits + static_cast<int64_t>(blockIdx.x) * experts;
     if (scoring == 1) {
         // softmax in fp32
@@ -164,8 +164,19 @@ __global__ __launch_bounds__(256) void ds_route_kernel(const float* __restrict__
             keep[g] = 0;
         }
         __syncthreads();
-        if (threadIdx.x == 0) {
-            const int64_t kg = topk_groups < 1 ? 1 : (topk_groups > n_groups ? n_groups : topk_groups);
+        const int64_t kg = topk_groups < 1 ? 1 : (topk_groups > n_groups ? n_groups : topk_groups);
+        bool gnan = false;
+        for (int64_t g = 0; g < n_groups; ++g) gnan = gnan || gscore[g] != gscore[g];
+        if (!gnan) {
+            // without NaNs the rounds keep the groups of rank < kg (a larger
+            // score, or an equal one with a lower index, ranks first)
+            if (threadIdx.x < n_groups) {
+                const int64_t g = threadIdx.x;
+                int64_t r = 0;
+                for (int64_t h = 0; h < n_groups; ++h) r += gscore[h] > gscore[g] || (gscore[h] == gscore[g] && h < g);
+                keep[g] = r < kg;
+            }
+        } else if (threadIdx.x == 0) {
             for (int64_t i = 0; i < kg; ++i) {
                 int64_t best = -1;
                 for (int64_t g = 0; g < n_groups; ++g)
@@ -189,7 +200,57 @@ __global__ __launch_bounds__(256) void ds_route_kernel(const float* __restrict__
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     float sum = 0.0f;  // thread 0
-    for (int64_t i = 0; i < k; ++i) {
+    __shared__ int any_nan;
+    __shared__ float pick_w[1024];  // the ranked picks' scores (at most 1024 experts there)
+    __shared__ float pick_denom;
+    if (threadIdx.x == 0) any_nan = 0;
+    __syncthreads();
+    for (int64_t e = threadIdx.x; e < experts; e += blockDim.x)
+        if (choice[e] != choice[e]) any_nan = 1;
+    __syncthreads();
+    const bool ranked = !any_nan && experts <= 1024;
+    if (ranked) {
+        // Without NaNs the rounds pick the experts in the order of their rank
+        // (how many experts beat them: a larger choice, or an equal one with
+        // a lower id), so one pass finds all k.
+        const int n = static_cast<int>(experts);
+        for (int e = threadIdx.x; e < n; e += blockDim.x) {
+            const float c = choice[e];
+            int r = 0;
+            int j = 0;
+            if ((n & 3) == 0) {  // choice is then 16-byte aligned
+                const float4* c4 = reinterpret_cast<const float4*>(choice);
+#pragma unroll 4
+                for (; j < n; j += 4) {
+                    const float4 q = c4[j >> 2];
+                    r += (q.x > c) || (q.x == c && j < e);
+                    r += (q.y > c) || (q.y == c && j + 1 < e);
+                    r += (q.z > c) || (q.z == c && j + 2 < e);
+                    r += (q.w > c) || (q.w == c && j + 3 < e);
+                }
+            }
+            for (; j < n; ++j) {
+                const float cj = choice[j];
+                r += (cj > c) || (cj == c && j < e);
+            }
+            if (r < k) {
+                idx[r] = e;
+                pick_w[r] = score[e];
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int64_t i = 0; i < k; ++i) sum += pick_w[i];  // in pick order, as the rounds add
+            pick_denom = sum > 1e-12f ? sum : 1e-12f;
+        }
+        __syncthreads();
+        for (int64_t i = threadIdx.x; i < k; i += blockDim.x) {
+            const float v = scoring == 0 ? pick_w[i] / pick_denom : pick_w[i];
+            w[i] = bf16_round(v * route_scale);
+        }
+        return;
+    }
+    for (int64_t i = 0; i < (ranked ? 0 : k); ++i) {
         int first = 0x7FFFFFFF;
         int be = -1;
         float bv = ninf;
