@@ -719,12 +719,12 @@ def table(args):
             torch.add(y2.to(torch.bfloat16), ys2.to(torch.bfloat16), out=yb)
 
         def dev_step(i):
-            idx, w = native.route_deepseek(logits)
+            idx, w = native.route_deepseek(logits, weights_dtype=torch.float32)
             t = dev_tables[i % len(dev_tables)]
             lib.pocketlm_set_stream(_stream_ptr(torch))
             rc = lib.fp8_e4m3_block_moe_device_routed_bf16x_f32(
                 ctypes.c_void_p(t[0].data_ptr()), 256, ctypes.c_void_p(idx.data_ptr()),
-                ctypes.c_void_p(w.float().data_ptr()), k, ctypes.cast(t[1], ctypes.c_void_p),
+                ctypes.c_void_p(w.data_ptr()), k, ctypes.cast(t[1], ctypes.c_void_p),
                 ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y2.data_ptr()), ctypes.c_void_p(ys2.data_ptr()),
                 ctypes.c_void_p(yb.data_ptr()), ctypes.c_void_p(rej.data_ptr()), 1, 2048, 7168, 56, 16)
             if rc != 0:

@@ -155,7 +155,8 @@ def run_fp8_moe_device(hidden: torch.Tensor, route_indices: torch.Tensor, route_
     of the router's indices; at most 8 rows and 64 choices per call).
 
     table holds every routed expert of the layer; route_indices / route_weights
-    are the router's [M, k] device tensors (route_deepseek).  selected_experts
+    are the router's [M, k] device tensors (route_deepseek; its
+    weights_dtype=torch.float32 form skips two conversions).  selected_experts
     is left empty: reading it would need the host round trip this path avoids.
     """
     flat = hidden.reshape(-1, hidden.shape[-1])

@@ -1075,12 +1075,18 @@ def ds_router_topk(hidden: torch.Tensor, router_weights: torch.Tensor, *, k: int
 
 def route_deepseek(logits: torch.Tensor, *, top_k: int = 8, n_groups: int = 8, topk_groups: int = 4,
                    scoring_func: str = "sigmoid", route_scale: float = 2.5,
-                   bias: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+                   bias: torch.Tensor | None = None,
+                   weights_dtype: torch.dtype = torch.bfloat16) -> tuple[torch.Tensor, torch.Tensor]:
     """DeepSeek-V3 routing (src/pcketlm/core/runtime/fp8_source.py:1527-1547 with
     _mask_deepseek_route_groups 5125-5140) from router logits [M, E].
 
-    Returns (indices int64 [M, top_k], weights bfloat16 [M, top_k]).
+    Returns (indices int64 [M, top_k], weights [M, top_k]): bfloat16 as the
+    reference returns them, or with weights_dtype=torch.float32 the same
+    values as fp32 (what the MoE entry points take, without a conversion
+    launch either way).
     """
+    if weights_dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("weights_dtype must be torch.bfloat16 or torch.float32")
     lib = _require("PCKETLM_DISABLE_NATIVE_DS_ROUTER", "Native DeepSeek router")
     if scoring_func not in ("sigmoid", "softmax"):
         raise ValueError("scoring_func must be 'sigmoid' or 'softmax'")
@@ -1096,7 +1102,7 @@ def route_deepseek(logits: torch.Tensor, *, top_k: int = 8, n_groups: int = 8, t
         code = lib.ds_route_topk_f32(_p(lg), _p(b), m, e, k, int(n_groups), int(topk_groups),
                                      0 if scoring_func == "sigmoid" else 1, float(route_scale), _p(idx), _p(w))
     _check("ds_route_topk_f32", code)
-    return _home(idx, logits), _home(w.to(torch.bfloat16), logits)
+    return _home(idx, logits), _home(w if weights_dtype == torch.float32 else w.to(torch.bfloat16), logits)
 
 
 # --------------------------------------------------------------------------- weight files to HBM

@@ -207,7 +207,7 @@ def test_router_and_device_routed_moe_replay_in_a_hip_graph(nat):
     x = torch.randn((2, hid), device="cuda", generator=gen).to(torch.bfloat16)
 
     def step(lg, hx):
-        idx, w = nat.route_deepseek(lg, top_k=4, n_groups=8, topk_groups=4)
+        idx, w = nat.route_deepseek(lg, top_k=4, n_groups=8, topk_groups=4, weights_dtype=torch.float32)
         return nat.fp8_e4m3_block_moe_device_routed_f32(table, hx, idx, w, shared)
 
     side = torch.cuda.Stream()
@@ -220,6 +220,9 @@ def test_router_and_device_routed_moe_replay_in_a_hip_graph(nat):
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=side):
         captured = step(logits, x)
+    idx_b, w_b = nat.route_deepseek(logits, top_k=4, n_groups=8, topk_groups=4)
+    idx_f, w_f = nat.route_deepseek(logits, top_k=4, n_groups=8, topk_groups=4, weights_dtype=torch.float32)
+    assert torch.equal(idx_b, idx_f) and w_b.dtype == torch.bfloat16 and torch.equal(w_b.float(), w_f)
     busy = torch.randn((256, 256), device="cuda")
     for trial in range(4):
         logits.copy_(torch.randn((2, n), device="cuda", generator=gen))
