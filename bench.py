@@ -764,6 +764,24 @@ def table(args):
     if want("ds-v3 MoE layer"):
         moe_layer()
 
+    def lm_head(vocab, hid, label):
+        # vocabulary x hidden bf16 weight (over 1 GB: no copy rotation needed), top 50
+        w = (torch.randn((vocab, hid), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+        h = torch.randn((hid,), generator=gen, device="cuda").to(torch.bfloat16)
+        ids = torch.empty((50,), dtype=torch.int64, device="cuda")
+        lg = torch.empty((50,), device="cuda")
+        lib.pocketlm_set_stream(_stream_ptr(torch))
+        call = lambda: lib.native_lm_head_topk_u16(ctypes.c_void_p(h.data_ptr()), ctypes.c_void_p(w.data_ptr()),
+                                                   ctypes.c_void_p(ids.data_ptr()), ctypes.c_void_p(lg.data_ptr()),
+                                                   vocab, hid, 50, 1, 0)
+        measure(f"lm_head top-50 {label} {vocab}x{hid} (bf16)", 1, lambda: [call], vocab * hid * 2 + hid * 2 + 50 * 12)
+        del w
+
+    if want("lm_head"):
+        lm_head(152064, 3584, "Qwen2.5-7B")
+        lm_head(129280, 7168, "DeepSeek-V3")
+        torch.cuda.empty_cache()
+
     transfers = []
     if want("fp8 pack -> HBM"):
         transfers.append(pack_transfer(torch))

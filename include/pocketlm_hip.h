@@ -382,6 +382,20 @@ int ds_route_topk_f32(const float* logits, const float* bias, int64_t batch, int
                       int64_t top_k, int64_t n_groups, int64_t topk_groups, int scoring,
                       float route_scale, int64_t* out_indices, float* out_weights);
 
+/* ------------------------------------------------------------------ lm_head */
+
+/* fp16_matmul.cpp:155-204 (native_lm_head_topk_u16): the logits of hidden
+ * (u16 [hidden_size], fp16 dtype_code 0 / bf16 1) against every row of weight
+ * (u16 [rows][hidden_size], same type), fp32 accumulation, and the top_k
+ * (row + token_offset, logit) pairs, written in descending order to
+ * out_ids int64 [top_k] / out_logits fp32 [top_k] (all device).  Ties go to
+ * the lower row; NaN logits rank as -inf; with fewer rows than top_k the
+ * remaining slots are -1 / -inf.  top_k <= 64 and ceil(rows / 4096) * top_k
+ * <= 4096 (vocabularies up to 262144 rows at top_k 16).  Codes 1 null,
+ * 2 bad dims, -3 workspace. */
+int native_lm_head_topk_u16(const uint16_t* hidden, const uint16_t* weight, int64_t* out_ids, float* out_logits,
+                            int64_t rows, int64_t hidden_size, int64_t top_k, int dtype_code, int64_t token_offset);
+
 /* ---------------------------------------------------------------- weight files to HBM */
 
 /* New export: byte ranges of a file copied into device memory (current

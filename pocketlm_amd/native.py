@@ -1105,6 +1105,39 @@ def route_deepseek(logits: torch.Tensor, *, top_k: int = 8, n_groups: int = 8, t
     return _home(idx, logits), _home(w if weights_dtype == torch.float32 else w.to(torch.bfloat16), logits)
 
 
+# --------------------------------------------------------------------------- lm_head
+
+def native_lm_head_topk_available() -> bool:
+    return _available("PCKETLM_DISABLE_NATIVE_MATMUL")
+
+
+def lm_head_topk_u16(hidden: torch.Tensor, weight: torch.Tensor, *, top_k: int,
+                     token_offset: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
+    """src/pcketlm/native/__init__.py:2283-2323 -> fp16_matmul.cpp:155-204:
+    the top_k logits of weight [rows, hidden] @ hidden and their token ids
+    (row + token_offset), sorted by logit, descending."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_MATMUL", "Native lm_head top-k")
+    if hidden.dtype != weight.dtype:
+        raise TypeError("lm_head_topk_u16 requires hidden and weight to share dtype")
+    if hidden.dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError("lm_head_topk_u16 requires torch.float16 or torch.bfloat16 tensors")
+    dev = _target_device(weight, hidden)
+    w = _on(weight, dev)
+    if w.ndim != 2:
+        raise ValueError("weight must have shape [rows, hidden_size]")
+    rows, hidden_size = int(w.shape[0]), int(w.shape[1])
+    h = _on(hidden, dev).reshape(-1).contiguous()
+    if int(h.numel()) != hidden_size:
+        raise ValueError("hidden size does not match lm_head weight")
+    ids = torch.empty((int(top_k),), dtype=torch.int64, device=dev)
+    logits = torch.empty((int(top_k),), dtype=torch.float32, device=dev)
+    with _launch(lib, dev):
+        code = lib.native_lm_head_topk_u16(_p(h), _p(w), _p(ids), _p(logits), rows, hidden_size, int(top_k),
+                                           1 if hidden.dtype == torch.bfloat16 else 0, int(token_offset))
+    _check("native_lm_head_topk_u16", code)
+    return _home(logits, hidden), _home(ids, hidden)
+
+
 # --------------------------------------------------------------------------- weight files to HBM
 
 def native_row8_artifact_available() -> bool:
