@@ -782,6 +782,47 @@ def table(args):
         lm_head(129280, 7168, "DeepSeek-V3")
         torch.cuda.empty_cache()
 
+    def dense_layer(ctx_len):
+        # One Qwen2.5-7B decoder layer decode (fp16, row8-packed weights
+        # N(0, 0.02), q/k/v biases) over a ctx_len-row KV cache; the new row
+        # is rolled back after each call so every call sees ctx_len + 1 rows.
+        # Two copies of the weights alternate so that the 466 MB do not stay
+        # in the last-level cache.
+        H, I, nh, nkv = 3584, 18944, 28, 4
+        kvw = H // nh * nkv
+        shapes = [(H, H), (kvw, H), (kvw, H), (H, H), (I, H), (I, H), (H, I)]
+        sets = []
+        for _ in range(2):
+            sets.append([native.pack_weight_rows8((torch.randn(s, generator=gen, device="cuda") * 0.02).half())
+                         for s in shapes])
+        torch.cuda.empty_cache()
+        norms = [(torch.rand(H, generator=gen, device="cuda") + 0.5).half() for _ in range(2)]
+        biases = [(torch.randn(n, generator=gen, device="cuda") * 0.1).half() for n in (H, kvw, kvw)]
+        hid = torch.randn(H, generator=gen, device="cuda").half()
+        out = torch.empty(H, dtype=torch.float16, device="cuda")
+        sess = lib.kv_prefill_init_typed(1, ctx_len + 8, kvw, 0)
+        kv = torch.randn((2, ctx_len, kvw), generator=gen, device="cuda").half()
+        lib.pocketlm_set_stream(_stream_ptr(torch))
+        assert lib.kv_append_committed(sess, 0, kv[0].data_ptr(), kv[1].data_ptr(), ctx_len) == 0
+        p = lambda t: t.data_ptr()  # noqa: E731
+
+        def call_for(ws):
+            args = [sess, 0, p(hid), p(norms[0]), p(norms[1]), *[p(w) for w in ws], *[p(b) for b in biases], None,
+                    None, p(out), H, I, nh, nkv, 1e-6, 1e6]
+            return lambda: lib.kv_dense_layer_decode_u16_ext_packed_rows8(*args) or lib.kv_rollback(sess)
+
+        nbytes = sum(a * b for a, b in shapes) * 2 + 2 * (ctx_len + 1) * kvw * 2 + 8 * H * 2
+        measure(f"dense decode layer Qwen2.5-7B, {ctx_len}-row KV cache (fp16 row8)", 1,
+                lambda: [call_for(ws) for ws in sets], nbytes)
+        torch.cuda.synchronize()
+        lib.kv_free(sess)
+        del sets
+        torch.cuda.empty_cache()
+
+    if want("dense decode layer"):
+        dense_layer(1024)
+        dense_layer(8192)
+
     transfers = []
     if want("fp8 pack -> HBM"):
         transfers.append(pack_transfer(torch))

@@ -478,6 +478,59 @@ int fp8_e4m3_block_moe_device_routed_bf16x_f32(const uint64_t* expert_table, int
                                                int64_t intermediate_rows, int64_t hidden_dim,
                                                int64_t gate_scale_cols, int64_t down_scale_cols);
 
+/* ---------------------------------------------------------------------------
+ * KV session and dense decoder layer decode (src/pcketlm/native/
+ * fp16_kv_cache.cpp).  The cache lives in device memory on the device that
+ * is current at init: [layer][K|V][max_seq_len][kv_width] fp16 (dtype_code 0)
+ * or bf16 (1), committed rows followed by tentative rows.  Lengths are kept
+ * on the host, so commit and rollback move no data.  Row pointers given to
+ * append/copy may be device or host memory; copies run on the library's
+ * stream (pocketlm_set_stream).  Same return codes as the reference. */
+
+/* fp16_kv_cache.cpp:594-611.  NULL on bad arguments or allocation failure. */
+void* kv_prefill_init_typed(int64_t layer_count, int64_t max_seq_len, int64_t kv_width, int dtype_code);
+/* fp16_kv_cache.cpp:613-619 (fp16). */
+void* kv_prefill_init(int64_t layer_count, int64_t max_seq_len, int64_t kv_width);
+/* fp16_kv_cache.cpp:621-624.  Waits for the device before freeing the cache. */
+void kv_free(void* handle);
+/* fp16_kv_cache.cpp:661-669: count rows of kv_width values after the
+ * committed rows (tentative rows move back).  1 bad args, 2 full. */
+int kv_append_committed(void* handle, int64_t layer, const uint16_t* k_new, const uint16_t* v_new, int64_t count);
+/* fp16_kv_cache.cpp:671-679: count rows after the tentative rows. */
+int kv_append_tentative(void* handle, int64_t layer, const uint16_t* k_new, const uint16_t* v_new, int64_t count);
+/* fp16_kv_cache.cpp:681-715: the first min(count, tentative) tentative rows
+ * of every layer become committed. */
+int kv_commit(void* handle, int64_t count);
+/* fp16_kv_cache.cpp:717-728: drop every layer's tentative rows. */
+int kv_rollback(void* handle);
+/* fp16_kv_cache.cpp:730-744.  -1 for a bad layer. */
+int64_t kv_committed_length(void* handle, int64_t layer);
+int64_t kv_tentative_length(void* handle, int64_t layer);
+/* fp16_kv_cache.cpp:746-778: committed (+ tentative) rows into k_out/v_out.
+ * 1 bad args, 2 more rows than max_count. */
+int kv_copy_layer(void* handle, int64_t layer, uint16_t* k_out, uint16_t* v_out, int64_t max_count,
+                  int include_tentative);
+/* fp16_kv_cache.cpp:1533-1589 (with 1398-1531 and the attention decode
+ * 920-1060): one decode step of a dense decoder layer with row8-packed
+ * weights (native_pack_u16_rows8).  Input RMSNorm, q/k/v (+ biases), optional
+ * per-head q/k RMSNorm, RoPE at position committed + tentative, the new k/v
+ * appended as a tentative row, attention over every row of the layer, o
+ * projection, residual, post RMSNorm, SiLU MLP, residual -> out (hidden_size
+ * values of the session's type).  head_dim = hidden_size / num_heads.  All
+ * pointers are device pointers; packed weights 16-byte aligned; biases and
+ * q/k norm weights may be NULL.  Codes: 1 null, 2 bad sizes, 100 + the
+ * attention decode's (1 layer, 2 heads, 3 divisibility, 4 kv_width, 5 cache
+ * full), and 106 for more than 16 query heads per kv head or head_dim > 256
+ * (limits of this build's attention kernel). */
+int kv_dense_layer_decode_u16_ext_packed_rows8(
+    void* handle, int64_t layer, const uint16_t* hidden, const uint16_t* input_norm_weight,
+    const uint16_t* post_norm_weight, const uint16_t* q_weight_packed, const uint16_t* k_weight_packed,
+    const uint16_t* v_weight_packed, const uint16_t* o_weight_packed, const uint16_t* gate_weight_packed,
+    const uint16_t* up_weight_packed, const uint16_t* down_weight_packed, const uint16_t* q_bias,
+    const uint16_t* k_bias, const uint16_t* v_bias, const uint16_t* q_norm_weight, const uint16_t* k_norm_weight,
+    uint16_t* out, int64_t hidden_size, int64_t intermediate_size, int64_t num_heads, int64_t num_kv_heads,
+    float rms_eps, float rope_theta);
+
 #ifdef __cplusplus
 }
 #endif

@@ -65,6 +65,17 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "row8_artifact_unmap_file": (None, [_vp]),
     "row8_artifact_mapped_data": (_vp, [_vp, ctypes.c_ulonglong, ctypes.c_ulonglong]),
     "row8_artifact_mapped_nbytes": (ctypes.c_ulonglong, [_vp]),
+    "kv_prefill_init_typed": (_vp, [_i64, _i64, _i64, _i32]),
+    "kv_prefill_init": (_vp, [_i64, _i64, _i64]),
+    "kv_free": (None, [_vp]),
+    "kv_append_committed": (_i32, [_vp, _i64, _vp, _vp, _i64]),
+    "kv_append_tentative": (_i32, [_vp, _i64, _vp, _vp, _i64]),
+    "kv_commit": (_i32, [_vp, _i64]),
+    "kv_rollback": (_i32, [_vp]),
+    "kv_committed_length": (_i64, [_vp, _i64]),
+    "kv_tentative_length": (_i64, [_vp, _i64]),
+    "kv_copy_layer": (_i32, [_vp, _i64, _vp, _vp, _i64, _i32]),
+    "kv_dense_layer_decode_u16_ext_packed_rows8": (_i32, [_vp, _i64] + [_vp] * 16 + [_i64] * 4 + [_f32, _f32]),
     "fp8_e4m3_block_moe_device_routed_f32": (_i32, [_vp, _i64, _vp, _vp, _i64] + [_vp] * 6 + [_i64] * 5),
     "fp8_e4m3_block_moe_device_routed_bf16x_f32": (_i32, [_vp, _i64, _vp, _vp, _i64] + [_vp] * 6 + [_i64] * 5),
     "fp8_e4m3_block_mlp_many_row_weighted_bf16x_f32": (_i32, [_vp] * 9 + [_i64] * 6),

@@ -10,13 +10,14 @@
 #include <algorithm>
 #include <cstring>
 
-#include "common.h"
+#include "row8.h"
 
 namespace {
 
 constexpr int kMaxWaves = 8;
 constexpr int kUnroll = 8;       // chunks whose loads are issued together
-constexpr int kMaxMats = 8;      // matrices per fused launch
+constexpr int kMaxMats = plm::kRow8MaxMats;  // matrices per fused launch
+using plm::Row8Mat;
 
 __device__ __forceinline__ float u16_to_f32(uint32_t v, int bf16) {
     if (bf16) return __uint_as_float(v << 16);
@@ -36,14 +37,6 @@ __device__ __forceinline__ void decode8(const uint4& q, int bf16, float* w) {
         }
     }
 }
-
-struct Row8Mat {
-    const uint16_t* packed;
-    const uint16_t* bias;  // may be null
-    float* out;
-    int64_t rows;
-    int64_t first_tile;    // prefix sum of tiles (blocks) over the matrices
-};
 
 struct Row8Args {
     Row8Mat mat[kMaxMats];
@@ -180,6 +173,11 @@ int run_row8(const uint16_t* hidden, const float* hidden_f32, const Row8Mat* mat
 }
 
 }  // namespace
+
+int plm::row8_gemv(const uint16_t* hidden, const float* hidden_f32, const Row8Mat* mats, int n, int64_t K,
+                   int dtype_code, hipStream_t st) {
+    return run_row8(hidden, hidden_f32, mats, n, K, dtype_code, st);
+}
 
 PLM_EXPORT int native_pack_u16_rows8(const uint16_t* weight, uint16_t* packed, int64_t rows, int64_t cols) {
     if (!weight || !packed) return plm::fail(1, "null pointer");

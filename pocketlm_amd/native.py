@@ -1255,3 +1255,164 @@ class NativeRow8MappedTensor:
 
 def map_native_row8_file(path: str | Path) -> NativeRow8MappedFile:
     return NativeRow8MappedFile(path)
+
+
+# --------------------------------------------------------------------------- KV session, dense layer decode
+
+def native_fp16_kv_available() -> bool:
+    """src/pcketlm/native/__init__.py native_fp16_kv_available, kill switch
+    PCKETLM_DISABLE_NATIVE_KV."""
+    if _flag("PCKETLM_DISABLE_NATIVE_KV"):
+        return False
+    try:
+        _lib.load()
+    except OSError:
+        return False
+    return torch.cuda.is_available()
+
+
+class NativeKvSession:
+    """src/pcketlm/native/__init__.py:2796-3260 over a device-resident cache
+    (fp16_kv_cache.cpp's session, kv_cache.hip here).  Rows and results are
+    device tensors on the session's device; host tensors passed in are moved
+    there.  Lengths are host-side, so commit/rollback never touch the GPU."""
+
+    def __init__(self, layer_count: int, max_seq_len: int, kv_width: int, dtype: torch.dtype = torch.float16,
+                 device: torch.device | str | None = None):
+        lib = _require("PCKETLM_DISABLE_NATIVE_KV", "Native fp16 KV cache")
+        dtype_code = _u16_storage_dtype_code(dtype)
+        self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        with torch.cuda.device(self.device):
+            handle = lib.kv_prefill_init_typed(int(layer_count), int(max_seq_len), int(kv_width), dtype_code)
+        if not handle:
+            detail = _lib.last_error()
+            raise RuntimeError("kv_prefill_init failed" + (f" ({detail})" if detail else ""))
+        self._lib = lib
+        self._handle = ctypes.c_void_p(handle)
+        self.layer_count = int(layer_count)
+        self.max_seq_len = int(max_seq_len)
+        self.kv_width = int(kv_width)
+        self.dtype = dtype
+
+    @property
+    def handle(self) -> int:
+        if not self._handle:
+            raise RuntimeError("NativeKvSession is closed")
+        return int(self._handle.value)
+
+    def close(self) -> None:
+        if getattr(self, "_handle", None):
+            self._lib.kv_free(self._handle)
+            self._handle = None
+
+    def __del__(self):  # pragma: no cover - GC safety net
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _append(self, fn_name: str, layer: int, k_new: torch.Tensor, v_new: torch.Tensor, count: int) -> None:
+        if k_new.dtype != self.dtype or v_new.dtype != self.dtype:
+            raise TypeError(f"KV cache append requires {self.dtype} tensors")
+        k = _on(k_new, self.device).reshape(-1)
+        v = _on(v_new, self.device).reshape(-1)
+        expected = int(count) * self.kv_width
+        if k.numel() != expected or v.numel() != expected:
+            raise ValueError("KV tensor size does not match count * kv_width")
+        with _launch(self._lib, self.device):
+            code = getattr(self._lib, fn_name)(self._handle, int(layer), _p(k), _p(v), int(count))
+        _check(fn_name, code)
+
+    def append_committed(self, layer: int, k_new: torch.Tensor, v_new: torch.Tensor, count: int) -> None:
+        self._append("kv_append_committed", layer, k_new, v_new, count)
+
+    def append_tentative(self, layer: int, k_new: torch.Tensor, v_new: torch.Tensor, count: int) -> None:
+        self._append("kv_append_tentative", layer, k_new, v_new, count)
+
+    def commit(self, count: int) -> None:
+        _check("kv_commit", self._lib.kv_commit(self._handle, int(count)))
+
+    def rollback(self) -> None:
+        _check("kv_rollback", self._lib.kv_rollback(self._handle))
+
+    def committed_length(self, layer: int) -> int:
+        return int(self._lib.kv_committed_length(self._handle, int(layer)))
+
+    def tentative_length(self, layer: int) -> int:
+        return int(self._lib.kv_tentative_length(self._handle, int(layer)))
+
+    def copy_layer(self, layer: int, *, include_tentative: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+        count = self.committed_length(layer) + (self.tentative_length(layer) if include_tentative else 0)
+        k_out = torch.empty((count, self.kv_width), dtype=self.dtype, device=self.device)
+        v_out = torch.empty((count, self.kv_width), dtype=self.dtype, device=self.device)
+        with _launch(self._lib, self.device):
+            code = self._lib.kv_copy_layer(self._handle, int(layer), _p(k_out), _p(v_out), count,
+                                           1 if include_tentative else 0)
+        _check("kv_copy_layer", code)
+        return k_out, v_out
+
+    def dense_layer_decode_packed_rows8(self, layer: int, hidden: torch.Tensor, input_norm_weight: torch.Tensor,
+                                        post_norm_weight: torch.Tensor, q_weight_packed: torch.Tensor,
+                                        k_weight_packed: torch.Tensor, v_weight_packed: torch.Tensor,
+                                        o_weight_packed: torch.Tensor, gate_weight_packed: torch.Tensor,
+                                        up_weight_packed: torch.Tensor, down_weight_packed: torch.Tensor, *,
+                                        hidden_size: int, intermediate_size: int, num_heads: int, num_kv_heads: int,
+                                        head_dim: int | None = None, rms_eps: float, rope_theta: float,
+                                        q_bias: torch.Tensor | None = None, k_bias: torch.Tensor | None = None,
+                                        v_bias: torch.Tensor | None = None,
+                                        q_norm_weight: torch.Tensor | None = None,
+                                        k_norm_weight: torch.Tensor | None = None) -> torch.Tensor:
+        """src/pcketlm/native/__init__.py:3041-3120 ->
+        kv_dense_layer_decode_u16_ext_packed_rows8 (fp16_kv_cache.cpp:1533).
+        The new k/v row is appended as a tentative row of `layer`."""
+        raw = [hidden, input_norm_weight, post_norm_weight]
+        if any(t.dtype != self.dtype for t in raw):
+            raise TypeError(f"dense_layer_decode_packed_rows8 requires {self.dtype} raw tensors")
+        packed = [q_weight_packed, k_weight_packed, v_weight_packed, o_weight_packed, gate_weight_packed,
+                  up_weight_packed, down_weight_packed]
+        if any(t.dtype != torch.uint16 for t in packed):
+            raise TypeError("packed dense layer weights must be torch.uint16")
+        if head_dim is not None and int(head_dim) * int(num_heads) != int(hidden_size):
+            raise ValueError("head_dim must equal hidden_size // num_heads for this entry point")
+        dev = self.device
+        raw_d = [_on(t, dev).reshape(-1) for t in raw]
+        if raw_d[0].numel() != int(hidden_size):
+            raise ValueError("hidden length does not match hidden_size")
+        H, inter, kvw = int(hidden_size), int(intermediate_size), self.kv_width
+        if int(num_heads) <= 0 or H % int(num_heads) != 0:
+            raise ValueError("hidden_size must be a multiple of num_heads")
+        hd = H // int(num_heads)
+        if any(t.numel() != H for t in raw_d):
+            raise ValueError("hidden and norm weights must hold hidden_size values")
+        packed_d = [_on(t, dev) for t in packed]
+        blocks = lambda rows: (rows + 7) // 8 * 8  # noqa: E731
+        want = [blocks(H) * H, blocks(kvw) * H, blocks(kvw) * H, blocks(H) * H, blocks(inter) * H,
+                blocks(inter) * H, blocks(H) * inter]
+        if [t.numel() for t in packed_d] != want:
+            raise ValueError("packed weight sizes do not match the layer shape")
+        opt = [None if t is None else _on(t, dev).reshape(-1)
+               for t in (q_bias, k_bias, v_bias, q_norm_weight, k_norm_weight)]
+        for t, n in zip(opt, (H, kvw, kvw, hd, hd)):
+            if t is not None and (t.numel() != n or t.dtype != self.dtype):
+                raise ValueError(f"biases and q/k norm weights must be {self.dtype} of the layer's sizes")
+        out = torch.empty((int(hidden_size),), dtype=self.dtype, device=dev)
+        with _launch(self._lib, dev):
+            code = self._lib.kv_dense_layer_decode_u16_ext_packed_rows8(
+                self._handle, int(layer), *[_p(t) for t in raw_d], *[_p(t) for t in packed_d],
+                *[_p(t) for t in opt], _p(out), int(hidden_size), int(intermediate_size), int(num_heads),
+                int(num_kv_heads), float(rms_eps), float(rope_theta))
+        _check("kv_dense_layer_decode_u16_ext_packed_rows8", code)
+        return out
+
+    def dense_layer_prefill_packed_rows8(self, layer: int, hidden: torch.Tensor, *weights: torch.Tensor,
+                                         **kwargs) -> torch.Tensor:
+        """kv_dense_layer_prefill_u16_ext's loop (fp16_kv_cache.cpp:1591-1673)
+        over the packed decode: each row is decoded, then committed."""
+        rows = hidden.reshape(-1, int(kwargs["hidden_size"]))
+        if self.committed_length(layer) + self.tentative_length(layer) + rows.shape[0] > self.max_seq_len:
+            raise RuntimeError("kv_dense_layer_prefill failed with code 4 (cache full)")
+        outs = []
+        for row in rows:
+            outs.append(self.dense_layer_decode_packed_rows8(layer, row, *weights, **kwargs))
+            self.commit(1)
+        return torch.stack(outs)
