@@ -38,6 +38,9 @@ constexpr int kMaxGroup = 16;     // query heads per kv head
 constexpr int kMaxHeadDim = 256;
 constexpr int kDimsPerLane = kMaxHeadDim / plm::kWave;
 constexpr int kMaxSplitLen = 256; // tokens per attention workgroup
+constexpr int kTokUnroll = 4;      // tokens whose loads a wave issues together
+constexpr int kMergeThreads = 256;
+constexpr int kMaxSplits = 4096;   // splits per head the merge stages in LDS
 
 __device__ __forceinline__ float rd16(uint16_t v, bool bf16) {
     if (bf16) return __uint_as_float(static_cast<uint32_t>(v) << 16);
@@ -176,22 +179,41 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(
         q_s[i] = q_rot[static_cast<int64_t>(kvh) * group * hd + i];
     __syncthreads();
 
-    for (int i = wave; i < n; i += kAttnWaves) {
-        const uint16_t* kr = k_cache + (t0 + i) * kv_width + static_cast<int64_t>(kvh) * hd;
-        float acc[kMaxGroup];
+    // Scores: a wave loads the rows of kTokUnroll tokens before using any.
+    for (int i0 = wave; i0 < n; i0 += kAttnWaves * kTokUnroll) {
+        float kv[kTokUnroll][kDimsPerLane];
 #pragma unroll
-        for (int h = 0; h < kMaxGroup; ++h) acc[h] = 0.0f;
-        for (int d = lane; d < hd; d += 64) {
-            const float kv = rd16(kr[d], BF16);
+        for (int u = 0; u < kTokUnroll; ++u) {
+            const int i = min(i0 + u * kAttnWaves, n - 1);
+            const uint16_t* kr = k_cache + (t0 + i) * kv_width + static_cast<int64_t>(kvh) * hd;
 #pragma unroll
-            for (int h = 0; h < kMaxGroup; ++h)
-                if (h < group) acc[h] = fmaf(q_s[h * hd + d], kv, acc[h]);
+            for (int j = 0; j < kDimsPerLane; ++j) {
+                const int d = lane + 64 * j;
+                kv[u][j] = d < hd ? rd16(kr[d], BF16) : 0.0f;
+            }
         }
 #pragma unroll
-        for (int h = 0; h < kMaxGroup; ++h) {
-            if (h < group) {
-                const float s = plm_wave_sum(acc[h]);
-                if (lane == kSumLane) p_s[h * L + i] = s * scale;
+        for (int u = 0; u < kTokUnroll; ++u) {
+            const int i = i0 + u * kAttnWaves;
+            if (i >= n) break;
+            float acc[kMaxGroup];
+#pragma unroll
+            for (int h = 0; h < kMaxGroup; ++h) acc[h] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kDimsPerLane; ++j) {
+                const int d = lane + 64 * j;
+                if (d < hd) {
+#pragma unroll
+                    for (int h = 0; h < kMaxGroup; ++h)
+                        if (h < group) acc[h] = fmaf(q_s[h * hd + d], kv[u][j], acc[h]);
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < kMaxGroup; ++h) {
+                if (h < group) {
+                    const float sum = plm_wave_sum(acc[h]);
+                    if (lane == kSumLane) p_s[h * L + i] = sum * scale;
+                }
             }
         }
     }
@@ -221,16 +243,29 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(
     for (int h = 0; h < kMaxGroup; ++h)
 #pragma unroll
         for (int j = 0; j < kDimsPerLane; ++j) acc[h][j] = 0.0f;
-    for (int i = wave; i < n; i += kAttnWaves) {
-        const uint16_t* vr = v_cache + (t0 + i) * kv_width + static_cast<int64_t>(kvh) * hd;
+    for (int i0 = wave; i0 < n; i0 += kAttnWaves * kTokUnroll) {
+        float vv[kTokUnroll][kDimsPerLane];
 #pragma unroll
-        for (int j = 0; j < kDimsPerLane; ++j) {
-            const int d = lane + 64 * j;
-            if (d < hd) {
-                const float vv = rd16(vr[d], BF16);
+        for (int u = 0; u < kTokUnroll; ++u) {
+            const int i = min(i0 + u * kAttnWaves, n - 1);
+            const uint16_t* vr = v_cache + (t0 + i) * kv_width + static_cast<int64_t>(kvh) * hd;
 #pragma unroll
-                for (int h = 0; h < kMaxGroup; ++h)
-                    if (h < group) acc[h][j] = fmaf(p_s[h * L + i], vv, acc[h][j]);
+            for (int j = 0; j < kDimsPerLane; ++j) {
+                const int d = lane + 64 * j;
+                vv[u][j] = d < hd ? rd16(vr[d], BF16) : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kTokUnroll; ++u) {
+            const int i = i0 + u * kAttnWaves;
+            if (i >= n) break;
+#pragma unroll
+            for (int j = 0; j < kDimsPerLane; ++j) {
+                if (lane + 64 * j < hd) {
+#pragma unroll
+                    for (int h = 0; h < kMaxGroup; ++h)
+                        if (h < group) acc[h][j] = fmaf(p_s[h * L + i], vv[u][j], acc[h][j]);
+                }
             }
         }
     }
@@ -253,23 +288,58 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(
 }
 
 // context[h][d] = sum_s exp(m_s - M) acc_s[d] / sum_s exp(m_s - M) l_s.
-__global__ __launch_bounds__(kMaxHeadDim) void attention_merge_kernel(const float* __restrict__ part,
-                                                                      const float* __restrict__ ml,
-                                                                      float* __restrict__ context, int hd, int group,
-                                                                      int nsplit) {
+// One workgroup per query head: the split factors exp(m_s - M) go to LDS,
+// then thread (c, d) sums splits c, c + C, ... of dimension d with several
+// loads in flight, and the C partial sums are added in LDS.
+__global__ __launch_bounds__(kMergeThreads) void attention_merge_kernel(const float* __restrict__ part,
+                                                                       const float* __restrict__ ml,
+                                                                       float* __restrict__ context, int hd, int group,
+                                                                       int nsplit) {
+    __shared__ float f_s[kMaxSplits];
+    __shared__ float red[kMergeThreads / 64];
+    __shared__ float sums[kMergeThreads];
     const int head = blockIdx.x;
     const int kvh = head / group, hl = head - kvh * group;
-    const int d = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t base = static_cast<int64_t>(kvh) * nsplit * group + hl;  // slot of split s: base + s * group
     float m = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) m = fmaxf(m, ml[((static_cast<int64_t>(kvh) * nsplit + s) * group + hl) * 2]);
-    float den = 0.0f, num = 0.0f;
-    for (int s = 0; s < nsplit; ++s) {
-        const int64_t slot = (static_cast<int64_t>(kvh) * nsplit + s) * group + hl;
+    for (int sp = tid; sp < nsplit; sp += kMergeThreads) m = fmaxf(m, ml[(base + static_cast<int64_t>(sp) * group) * 2]);
+    m = wave_max_all(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float den = 0.0f;
+    for (int sp = tid; sp < nsplit; sp += kMergeThreads) {
+        const int64_t slot = base + static_cast<int64_t>(sp) * group;
         const float f = expf(ml[slot * 2] - m);
+        f_s[sp] = f;
         den += f * ml[slot * 2 + 1];
-        if (d < hd) num += f * part[slot * hd + d];
     }
-    if (d < hd) context[static_cast<int64_t>(head) * hd + d] = num / den;
+    den = block_sum(den, red);  // its barriers also publish f_s
+    const int C = kMergeThreads / hd;  // split lanes per dimension (hd <= kMergeThreads)
+    const int c = tid / hd, d = tid - c * hd;
+    float num = 0.0f;
+    if (c < C) {
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        int sp = c;
+        for (; sp + 3 * C < nsplit; sp += 4 * C) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t slot = base + static_cast<int64_t>(sp + u * C) * group;
+                acc[u] = fmaf(f_s[sp + u * C], part[slot * hd + d], acc[u]);
+            }
+        }
+        for (; sp < nsplit; sp += C) acc[0] = fmaf(f_s[sp], part[(base + static_cast<int64_t>(sp) * group) * hd + d], acc[0]);
+        num = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    }
+    sums[tid] = num;
+    __syncthreads();
+    if (tid < hd) {
+        float t = 0.0f;
+        for (int k = 0; k < C; ++k) t += sums[k * hd + tid];
+        context[static_cast<int64_t>(head) * hd + tid] = t / den;
+    }
 }
 
 // attention_out = storage(proj); resid = hidden + attention_out (fp32);
@@ -393,9 +463,10 @@ struct DenseArgs {
     float eps, theta;
 };
 
-// Attention split length: about two workgroups per CU over (kv head, split).
+// Attention split length: about eight workgroups per CU over (kv head, split),
+// at least 16 tokens each, at most kMaxSplitLen.
 int split_len_for(int64_t T, int64_t nkv) {
-    const int64_t target = std::max<int64_t>(1, 2 * plm::cu_count() / std::max<int64_t>(1, nkv));
+    const int64_t target = std::max<int64_t>(1, 8 * plm::cu_count() / std::max<int64_t>(1, nkv));
     int64_t L = (T + target - 1) / target;
     L = ((L + 15) / 16) * 16;
     return static_cast<int>(std::min<int64_t>(std::max<int64_t>(L, 16), kMaxSplitLen));
@@ -423,7 +494,7 @@ int dense_decode(KvSession* s, int64_t layer, const DenseArgs& a) {
     const int64_t H = a.hidden_size, I = a.inter, T = pos + 1;
     const int L = split_len_for(T, a.nkv);
     const int64_t nsplit = (T + L - 1) / L;
-    if (nsplit > 65535) return plm::fail(106, "context too long for one attention launch");
+    if (nsplit > kMaxSplits) return plm::fail(106, "context too long for one attention launch");
     // workspace: xn u16[H] | q f32[H] | k, v f32[kvw] | q_rot f32[H] | part | ml | ctx f32[H] | proj f32[H]
     //            | resid f32[H] | post u16[H] | gate, up, act f32[I] | mlp f32[H]
     size_t off[16];
@@ -479,8 +550,8 @@ int dense_decode(KvSession* s, int64_t layer, const DenseArgs& a) {
                        dim3(kAttnThreads), lds, stream, q_rot, s->k_rows(layer), s->v_rows(layer), kvw,
                        static_cast<int>(hd), static_cast<int>(group), T, L, scale, part, ml);
     if ((code = plm::check_launch("attention split")) != 0) return code;
-    hipLaunchKernelGGL(attention_merge_kernel, dim3(static_cast<unsigned>(a.nh)),
-                       dim3(static_cast<unsigned>(((hd + 63) / 64) * 64)), 0, stream, part, ml, ctx,
+    hipLaunchKernelGGL(attention_merge_kernel, dim3(static_cast<unsigned>(a.nh)), dim3(kMergeThreads), 0, stream,
+                       part, ml, ctx,
                        static_cast<int>(hd), static_cast<int>(group), static_cast<int>(nsplit));
     if ((code = plm::check_launch("attention merge")) != 0) return code;
     plm::Row8Mat o = {a.o_w, nullptr, proj, H, 0};
