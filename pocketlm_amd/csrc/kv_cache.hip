@@ -10,17 +10,16 @@
 // the host) and attention reads one contiguous run of rows.
 //
 // One decode step is a sequence of launches on the caller's stream:
-//   rms_norm_kernel        input RMSNorm, rounded to the storage type
-//   row8 GEMV              q, k, v (+ biases) in one launch
+//   row8 GEMV              input RMSNorm (rounded to the storage type), then
+//                          q, k, v (+ biases), in one launch
 //   qk_rope_append_kernel  per-head q/k RMSNorm, RoPE, k/v rounded into the cache
 //   attention_split_kernel flash-decode partials over (kv head, token split)
 //   attention_merge_kernel partials -> context (fp32)
 //   row8 GEMV              o projection from the fp32 context
 //   post_attention_kernel  residual add, post RMSNorm
 //   row8 GEMV              gate and up in one launch
-//   silu_mul_kernel        silu(gate) * up
-//   row8 GEMV              down projection from the fp32 activation
-//   residual_out_kernel    residual + mlp, rounded to the storage type
+//   row8 GEMV              down projection of silu(gate) * up, plus the
+//                          residual, rounded to the storage type
 // The weights dominate the bytes (466 MB for a Qwen2.5-7B layer); everything
 // else reads or writes a few hundred KB.
 #include <algorithm>
@@ -36,7 +35,6 @@ constexpr int kAttnThreads = 256;
 constexpr int kAttnWaves = kAttnThreads / plm::kWave;
 constexpr int kMaxGroup = 16;     // query heads per kv head
 constexpr int kMaxHeadDim = 256;
-constexpr int kDimsPerLane = kMaxHeadDim / plm::kWave;
 constexpr int kMaxSplitLen = 256; // tokens per attention workgroup
 constexpr int kTokUnroll = 4;      // tokens whose loads a wave issues together
 constexpr int kMergeThreads = 256;
@@ -80,23 +78,6 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     for (int w = 0; w < nw; ++w) t += red[w];
     __syncthreads();
     return t;
-}
-
-// out = storage(x * (1 / sqrt(mean(x^2) + eps)) * w)   (rms_norm_one, 541-559)
-template <bool BF16>
-__global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const uint16_t* __restrict__ x,
-                                                                 const uint16_t* __restrict__ w,
-                                                                 uint16_t* __restrict__ out, int n, float eps) {
-#pragma clang fp contract(off)
-    __shared__ float red[kNormThreads / 64];
-    float s = 0.0f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = rd16(x[i], BF16);
-        s += v * v;
-    }
-    const float ms = block_sum(s, red) / static_cast<float>(n);
-    const float scale = 1.0f / sqrtf(ms + eps);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = wr16(rd16(x[i], BF16) * scale * rd16(w[i], BF16), BF16);
 }
 
 // Per-head q/k RMSNorm (rms_norm_heads_inplace, 561-584), RoPE at `pos`
@@ -162,7 +143,10 @@ __global__ __launch_bounds__(64) void qk_rope_append_kernel(const float* __restr
 // of kv head kvh for its `group` query heads: scores q.k * scale into LDS,
 // per-head max m and sum l of exp(score - m), and acc = sum exp(score - m) v.
 // Waves take tokens, lanes take head dimensions.
-template <bool BF16>
+// G bounds the query heads per kv head (group <= G), DPL the head dimensions
+// per lane (hd <= 64 * DPL): the unrolled body stays small enough for the
+// instruction cache.
+template <bool BF16, int G, int DPL>
 __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(
     const float* __restrict__ q_rot, const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ v_cache,
     int64_t kv_width, int hd, int group, int64_t T, int L, float scale, float* __restrict__ part,
@@ -181,13 +165,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(
 
     // Scores: a wave loads the rows of kTokUnroll tokens before using any.
     for (int i0 = wave; i0 < n; i0 += kAttnWaves * kTokUnroll) {
-        float kv[kTokUnroll][kDimsPerLane];
+        float kv[kTokUnroll][DPL];
 #pragma unroll
         for (int u = 0; u < kTokUnroll; ++u) {
             const int i = min(i0 + u * kAttnWaves, n - 1);
             const uint16_t* kr = k_cache + (t0 + i) * kv_width + static_cast<int64_t>(kvh) * hd;
 #pragma unroll
-            for (int j = 0; j < kDimsPerLane; ++j) {
+            for (int j = 0; j < DPL; ++j) {
                 const int d = lane + 64 * j;
                 kv[u][j] = d < hd ? rd16(kr[d], BF16) : 0.0f;
             }
@@ -196,20 +180,20 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(
         for (int u = 0; u < kTokUnroll; ++u) {
             const int i = i0 + u * kAttnWaves;
             if (i >= n) break;
-            float acc[kMaxGroup];
+            float acc[G];
 #pragma unroll
-            for (int h = 0; h < kMaxGroup; ++h) acc[h] = 0.0f;
+            for (int h = 0; h < G; ++h) acc[h] = 0.0f;
 #pragma unroll
-            for (int j = 0; j < kDimsPerLane; ++j) {
+            for (int j = 0; j < DPL; ++j) {
                 const int d = lane + 64 * j;
                 if (d < hd) {
 #pragma unroll
-                    for (int h = 0; h < kMaxGroup; ++h)
+                    for (int h = 0; h < G; ++h)
                         if (h < group) acc[h] = fmaf(q_s[h * hd + d], kv[u][j], acc[h]);
                 }
             }
 #pragma unroll
-            for (int h = 0; h < kMaxGroup; ++h) {
+            for (int h = 0; h < G; ++h) {
                 if (h < group) {
                     const float sum = plm_wave_sum(acc[h]);
                     if (lane == kSumLane) p_s[h * L + i] = sum * scale;
@@ -238,19 +222,19 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(
     }
     __syncthreads();
 
-    float acc[kMaxGroup][kDimsPerLane];
+    float acc[G][DPL];
 #pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h)
+    for (int h = 0; h < G; ++h)
 #pragma unroll
-        for (int j = 0; j < kDimsPerLane; ++j) acc[h][j] = 0.0f;
+        for (int j = 0; j < DPL; ++j) acc[h][j] = 0.0f;
     for (int i0 = wave; i0 < n; i0 += kAttnWaves * kTokUnroll) {
-        float vv[kTokUnroll][kDimsPerLane];
+        float vv[kTokUnroll][DPL];
 #pragma unroll
         for (int u = 0; u < kTokUnroll; ++u) {
             const int i = min(i0 + u * kAttnWaves, n - 1);
             const uint16_t* vr = v_cache + (t0 + i) * kv_width + static_cast<int64_t>(kvh) * hd;
 #pragma unroll
-            for (int j = 0; j < kDimsPerLane; ++j) {
+            for (int j = 0; j < DPL; ++j) {
                 const int d = lane + 64 * j;
                 vv[u][j] = d < hd ? rd16(vr[d], BF16) : 0.0f;
             }
@@ -260,10 +244,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(
             const int i = i0 + u * kAttnWaves;
             if (i >= n) break;
 #pragma unroll
-            for (int j = 0; j < kDimsPerLane; ++j) {
+            for (int j = 0; j < DPL; ++j) {
                 if (lane + 64 * j < hd) {
 #pragma unroll
-                    for (int h = 0; h < kMaxGroup; ++h)
+                    for (int h = 0; h < G; ++h)
                         if (h < group) acc[h][j] = fmaf(p_s[h * L + i], vv[u][j], acc[h][j]);
                 }
             }
@@ -273,9 +257,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(
     for (int w = 0; w < kAttnWaves; ++w) {
         if (wave == w) {
 #pragma unroll
-            for (int h = 0; h < kMaxGroup; ++h) {
+            for (int h = 0; h < G; ++h) {
 #pragma unroll
-                for (int j = 0; j < kDimsPerLane; ++j) {
+                for (int j = 0; j < DPL; ++j) {
                     const int d = lane + 64 * j;
                     if (h < group && d < hd) q_s[h * hd + d] = (w == 0 ? 0.0f : q_s[h * hd + d]) + acc[h][j];
                 }
@@ -285,6 +269,39 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(
     }
     float* dst = part + (static_cast<int64_t>(kvh) * nsplit + sp) * group * hd;
     for (int i = threadIdx.x; i < group * hd; i += kAttnThreads) dst[i] = q_s[i];
+}
+
+template <bool BF16, int G>
+void launch_split_g(int dpl, dim3 grid, size_t lds, hipStream_t st, const float* q_rot, const uint16_t* kc,
+                    const uint16_t* vc, int64_t kvw, int hd, int group, int64_t T, int L, float scale, float* part,
+                    float* ml) {
+    if (dpl <= 1) {
+        hipLaunchKernelGGL((attention_split_kernel<BF16, G, 1>), grid, dim3(kAttnThreads), lds, st, q_rot, kc, vc, kvw,
+                           hd, group, T, L, scale, part, ml);
+    } else if (dpl == 2) {
+        hipLaunchKernelGGL((attention_split_kernel<BF16, G, 2>), grid, dim3(kAttnThreads), lds, st, q_rot, kc, vc, kvw,
+                           hd, group, T, L, scale, part, ml);
+    } else {
+        hipLaunchKernelGGL((attention_split_kernel<BF16, G, 4>), grid, dim3(kAttnThreads), lds, st, q_rot, kc, vc, kvw,
+                           hd, group, T, L, scale, part, ml);
+    }
+}
+
+template <bool BF16>
+void launch_split(dim3 grid, size_t lds, hipStream_t st, const float* q_rot, const uint16_t* kc, const uint16_t* vc,
+                  int64_t kvw, int hd, int group, int64_t T, int L, float scale, float* part, float* ml) {
+    const int dpl = (hd + 63) / 64;
+    if (group <= 1) {
+        launch_split_g<BF16, 1>(dpl, grid, lds, st, q_rot, kc, vc, kvw, hd, group, T, L, scale, part, ml);
+    } else if (group <= 2) {
+        launch_split_g<BF16, 2>(dpl, grid, lds, st, q_rot, kc, vc, kvw, hd, group, T, L, scale, part, ml);
+    } else if (group <= 4) {
+        launch_split_g<BF16, 4>(dpl, grid, lds, st, q_rot, kc, vc, kvw, hd, group, T, L, scale, part, ml);
+    } else if (group <= 8) {
+        launch_split_g<BF16, 8>(dpl, grid, lds, st, q_rot, kc, vc, kvw, hd, group, T, L, scale, part, ml);
+    } else {
+        launch_split_g<BF16, kMaxGroup>(dpl, grid, lds, st, q_rot, kc, vc, kvw, hd, group, T, L, scale, part, ml);
+    }
 }
 
 // context[h][d] = sum_s exp(m_s - M) acc_s[d] / sum_s exp(m_s - M) l_s.
@@ -363,25 +380,6 @@ __global__ __launch_bounds__(kNormThreads) void post_attention_kernel(const uint
     const float scale = 1.0f / sqrtf(ms + eps);
     for (int i = threadIdx.x; i < n; i += blockDim.x)
         post[i] = wr16(rd16(wr16(resid[i], BF16), BF16) * scale * rd16(w[i], BF16), BF16);
-}
-
-// act = gate / (1 + exp(-gate)) * up   (1509-1513)
-__global__ void silu_mul_kernel(const float* __restrict__ gate, const float* __restrict__ up, float* __restrict__ act,
-                                int64_t n) {
-#pragma clang fp contract(off)
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i < n) {
-        const float g = gate[i];
-        act[i] = (g / (1.0f + expf(-g))) * up[i];
-    }
-}
-
-// out = storage(resid + mlp)   (1527-1529)
-template <bool BF16>
-__global__ void residual_out_kernel(const float* __restrict__ resid, const float* __restrict__ mlp,
-                                    uint16_t* __restrict__ out, int64_t n) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i < n) out[i] = wr16(resid[i] + mlp[i], BF16);
 }
 
 struct LayerLengths {
@@ -495,16 +493,15 @@ int dense_decode(KvSession* s, int64_t layer, const DenseArgs& a) {
     const int L = split_len_for(T, a.nkv);
     const int64_t nsplit = (T + L - 1) / L;
     if (nsplit > kMaxSplits) return plm::fail(106, "context too long for one attention launch");
-    // workspace: xn u16[H] | q f32[H] | k, v f32[kvw] | q_rot f32[H] | part | ml | ctx f32[H] | proj f32[H]
-    //            | resid f32[H] | post u16[H] | gate, up, act f32[I] | mlp f32[H]
-    size_t off[16];
-    size_t sz[] = {static_cast<size_t>(H) * 2, static_cast<size_t>(H) * 4, static_cast<size_t>(kvw) * 4,
-                   static_cast<size_t>(kvw) * 4, static_cast<size_t>(H) * 4,
-                   static_cast<size_t>(a.nh * nsplit * hd) * 4, static_cast<size_t>(a.nh * nsplit) * 8,
-                   static_cast<size_t>(H) * 4, static_cast<size_t>(H) * 4, static_cast<size_t>(H) * 4,
-                   static_cast<size_t>(H) * 2, static_cast<size_t>(I) * 4, static_cast<size_t>(I) * 4,
-                   static_cast<size_t>(I) * 4, static_cast<size_t>(H) * 4};
-    const int nbuf = static_cast<int>(sizeof(sz) / sizeof(sz[0]));
+    // workspace: q f32[H] | k, v f32[kvw] | q_rot f32[H] | part | ml | ctx f32[H] | proj f32[H] | resid f32[H]
+    //            | post u16[H] | gate, up f32[I]
+    const size_t sz[] = {static_cast<size_t>(H) * 4, static_cast<size_t>(kvw) * 4, static_cast<size_t>(kvw) * 4,
+                         static_cast<size_t>(H) * 4, static_cast<size_t>(a.nh * nsplit * hd) * 4,
+                         static_cast<size_t>(a.nh * nsplit) * 8, static_cast<size_t>(H) * 4,
+                         static_cast<size_t>(H) * 4, static_cast<size_t>(H) * 4, static_cast<size_t>(H) * 2,
+                         static_cast<size_t>(I) * 4, static_cast<size_t>(I) * 4};
+    constexpr int nbuf = static_cast<int>(sizeof(sz) / sizeof(sz[0]));
+    size_t off[nbuf];
     size_t total = 0;
     for (int i = 0; i < nbuf; ++i) {
         off[i] = total;
@@ -512,30 +509,28 @@ int dense_decode(KvSession* s, int64_t layer, const DenseArgs& a) {
     }
     char* ws = static_cast<char*>(plm::workspace(total));
     if (ws == nullptr) return plm::fail(108, "workspace");
-    uint16_t* xn = reinterpret_cast<uint16_t*>(ws + off[0]);
-    float* q = reinterpret_cast<float*>(ws + off[1]);
-    float* k = reinterpret_cast<float*>(ws + off[2]);
-    float* v = reinterpret_cast<float*>(ws + off[3]);
-    float* q_rot = reinterpret_cast<float*>(ws + off[4]);
-    float* part = reinterpret_cast<float*>(ws + off[5]);
-    float* ml = reinterpret_cast<float*>(ws + off[6]);
-    float* ctx = reinterpret_cast<float*>(ws + off[7]);
-    float* proj = reinterpret_cast<float*>(ws + off[8]);
-    float* resid = reinterpret_cast<float*>(ws + off[9]);
-    uint16_t* post = reinterpret_cast<uint16_t*>(ws + off[10]);
-    float* gate = reinterpret_cast<float*>(ws + off[11]);
-    float* up = reinterpret_cast<float*>(ws + off[12]);
-    float* act = reinterpret_cast<float*>(ws + off[13]);
-    float* mlp = reinterpret_cast<float*>(ws + off[14]);
+    float* q = reinterpret_cast<float*>(ws + off[0]);
+    float* k = reinterpret_cast<float*>(ws + off[1]);
+    float* v = reinterpret_cast<float*>(ws + off[2]);
+    float* q_rot = reinterpret_cast<float*>(ws + off[3]);
+    float* part = reinterpret_cast<float*>(ws + off[4]);
+    float* ml = reinterpret_cast<float*>(ws + off[5]);
+    float* ctx = reinterpret_cast<float*>(ws + off[6]);
+    float* proj = reinterpret_cast<float*>(ws + off[7]);
+    float* resid = reinterpret_cast<float*>(ws + off[8]);
+    uint16_t* post = reinterpret_cast<uint16_t*>(ws + off[9]);
+    float* gate = reinterpret_cast<float*>(ws + off[10]);
+    float* up = reinterpret_cast<float*>(ws + off[11]);
     const hipStream_t stream = plm::current_stream();
     const int dc = BF16 ? 1 : 0;
     int code = 0;
 
-    hipLaunchKernelGGL((rms_norm_kernel<BF16>), dim3(1), dim3(kNormThreads), 0, stream, a.hidden, a.input_norm, xn,
-                       static_cast<int>(H), a.eps);
-    if ((code = plm::check_launch("input rms norm")) != 0) return code;
-    plm::Row8Mat qkv[3] = {{a.q_w, a.q_bias, q, H, 0}, {a.k_w, a.k_bias, k, kvw, 0}, {a.v_w, a.v_bias, v, kvw, 0}};
-    if ((code = plm::row8_gemv(xn, nullptr, qkv, 3, H, dc, stream)) != 0) return code;
+    plm::Row8X x_in;  // the input RMSNorm is the q/k/v launch's prologue
+    x_in.u16 = a.hidden;
+    x_in.norm_w = a.input_norm;
+    x_in.eps = a.eps;
+    plm::Row8Mat qkv[3] = {{a.q_w, a.q_bias, q, H}, {a.k_w, a.k_bias, k, kvw}, {a.v_w, a.v_bias, v, kvw}};
+    if ((code = plm::row8_gemv_x(x_in, qkv, 3, H, dc, stream)) != 0) return code;
     uint16_t* k_row = s->k_rows(layer) + pos * kvw;
     uint16_t* v_row = s->v_rows(layer) + pos * kvw;
     hipLaunchKernelGGL((qk_rope_append_kernel<BF16>), dim3(static_cast<unsigned>(a.nh + a.nkv)), dim3(64), 0, stream,
@@ -546,29 +541,26 @@ int dense_decode(KvSession* s, int64_t layer, const DenseArgs& a) {
 
     const size_t lds = static_cast<size_t>(group) * (hd + L) * sizeof(float);
     const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
-    hipLaunchKernelGGL((attention_split_kernel<BF16>), dim3(static_cast<unsigned>(a.nkv), static_cast<unsigned>(nsplit)),
-                       dim3(kAttnThreads), lds, stream, q_rot, s->k_rows(layer), s->v_rows(layer), kvw,
-                       static_cast<int>(hd), static_cast<int>(group), T, L, scale, part, ml);
+    launch_split<BF16>(dim3(static_cast<unsigned>(a.nkv), static_cast<unsigned>(nsplit)), lds, stream, q_rot,
+                       s->k_rows(layer), s->v_rows(layer), kvw, static_cast<int>(hd), static_cast<int>(group), T, L,
+                       scale, part, ml);
     if ((code = plm::check_launch("attention split")) != 0) return code;
     hipLaunchKernelGGL(attention_merge_kernel, dim3(static_cast<unsigned>(a.nh)), dim3(kMergeThreads), 0, stream,
                        part, ml, ctx,
                        static_cast<int>(hd), static_cast<int>(group), static_cast<int>(nsplit));
     if ((code = plm::check_launch("attention merge")) != 0) return code;
-    plm::Row8Mat o = {a.o_w, nullptr, proj, H, 0};
+    plm::Row8Mat o = {a.o_w, nullptr, proj, H};
     if ((code = plm::row8_gemv(nullptr, ctx, &o, 1, H, dc, stream)) != 0) return code;
     hipLaunchKernelGGL((post_attention_kernel<BF16>), dim3(1), dim3(kNormThreads), 0, stream, a.hidden, proj,
                        a.post_norm, resid, post, static_cast<int>(H), a.eps);
     if ((code = plm::check_launch("post attention norm")) != 0) return code;
-    plm::Row8Mat gu[2] = {{a.gate_w, nullptr, gate, I, 0}, {a.up_w, nullptr, up, I, 0}};
+    plm::Row8Mat gu[2] = {{a.gate_w, nullptr, gate, I}, {a.up_w, nullptr, up, I}};
     if ((code = plm::row8_gemv(post, nullptr, gu, 2, H, dc, stream)) != 0) return code;
-    hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>(plm::ceil_div(I, 256))), dim3(256), 0, stream,
-                       gate, up, act, I);
-    if ((code = plm::check_launch("silu")) != 0) return code;
-    plm::Row8Mat down = {a.down_w, nullptr, mlp, H, 0};
-    if ((code = plm::row8_gemv(nullptr, act, &down, 1, I, dc, stream)) != 0) return code;
-    hipLaunchKernelGGL((residual_out_kernel<BF16>), dim3(static_cast<unsigned>(plm::ceil_div(H, 256))), dim3(256), 0,
-                       stream, resid, mlp, a.out, H);
-    return plm::check_launch("residual out");
+    plm::Row8X x_act;  // SiLU(gate) * up is read by the down launch, which adds the residual
+    x_act.f32 = gate;
+    x_act.f32_b = up;
+    plm::Row8Mat down = {a.down_w, nullptr, nullptr, H, 0, resid, a.out};
+    return plm::row8_gemv_x(x_act, &down, 1, I, dc, stream);
 }
 
 }  // namespace

@@ -38,10 +38,25 @@ __device__ __forceinline__ void decode8(const uint4& q, int bf16, float* w) {
     }
 }
 
+// Activation source of a launch (template parameter XM).
+enum XMode { kXU16 = 0, kXF32 = 1, kXSilu = 2, kXNorm = 3 };
+
+// fp32 -> fp16 (round to nearest even) / bf16 (add 0x7FFF + lsb, truncate).
+__device__ __forceinline__ uint16_t f32_to_u16(float v, bool bf16) {
+    if (bf16) {
+        const uint32_t bits = __float_as_uint(v);
+        return static_cast<uint16_t>((bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16);
+    }
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+}
+
 struct Row8Args {
     Row8Mat mat[kMaxMats];
     const uint16_t* hidden;      // fp16 / bf16 activations (same type as the weights), or
     const float* hidden_f32;     // fp32 activations
+    const float* hidden_b;       // kXSilu: the up values
+    const uint16_t* norm_w;      // kXNorm: the norm weight
+    float eps;
     int64_t K;
     int nmats;
     int nchunks;           // ceil(K / 64)
@@ -49,8 +64,9 @@ struct Row8Args {
 };
 
 // One workgroup = one 8-row block of one matrix; its waves split the columns.
-template <bool BF16, bool XF32>
+template <bool BF16, int XM>
 __global__ __launch_bounds__(512) void row8_gemv_kernel(const Row8Args a) {
+#pragma clang fp contract(off)
     __shared__ float red[kMaxWaves * 8];
     const int nw = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -62,6 +78,22 @@ __global__ __launch_bounds__(512) void row8_gemv_kernel(const Row8Args a) {
     const Row8Mat m = a.mat[mi];
     const int64_t blk = blockIdx.x - m.first_tile;
     const uint16_t* base = m.packed + blk * a.K * 8;
+
+    float scale = 1.0f;
+    if (XM == kXNorm) {  // every workgroup reduces the (small) hidden vector itself
+        float ss = 0.0f;
+        for (int64_t i = threadIdx.x; i < a.K; i += blockDim.x) {
+            const float v = u16_to_f32(a.hidden[i], BF16);
+            ss += v * v;
+        }
+        const float t = plm_wave_sum(ss);
+        if (lane == kSumLane) red[wave] = t;
+        __syncthreads();
+        ss = 0.0f;
+        for (int w = 0; w < nw; ++w) ss += red[w];
+        scale = 1.0f / sqrtf(ss / static_cast<float>(a.K) + a.eps);
+        __syncthreads();
+    }
 
     float acc[8];
 #pragma unroll
@@ -78,7 +110,18 @@ __global__ __launch_bounds__(512) void row8_gemv_kernel(const Row8Args a) {
             const bool ok = c0 + u * nw < a.nchunks && col < a.K;
             const int64_t cc = ok ? col : a.K - 1;
             q[u] = *reinterpret_cast<const uint4*>(base + cc * 8);
-            const float xh = XF32 ? a.hidden_f32[cc] : u16_to_f32(a.hidden[cc], BF16);
+            float xh;
+            if (XM == kXU16) {
+                xh = u16_to_f32(a.hidden[cc], BF16);
+            } else if (XM == kXF32) {
+                xh = a.hidden_f32[cc];
+            } else if (XM == kXSilu) {
+                const float g = a.hidden_f32[cc];
+                xh = (g / (1.0f + expf(-g))) * a.hidden_b[cc];
+            } else {
+                const float n = u16_to_f32(a.hidden[cc], BF16) * scale * u16_to_f32(a.norm_w[cc], BF16);
+                xh = u16_to_f32(f32_to_u16(n, BF16), BF16);
+            }
             xv[u] = ok ? xh : 0.0f;
         }
 #pragma unroll
@@ -102,7 +145,11 @@ __global__ __launch_bounds__(512) void row8_gemv_kernel(const Row8Args a) {
             float v = 0.0f;
             for (int w = 0; w < nw; ++w) v += red[w * 8 + l];
             if (m.bias) v += u16_to_f32(m.bias[row], BF16);
-            m.out[row] = v;
+            if (m.out16) {
+                m.out16[row] = f32_to_u16(m.resid[row] + v, BF16);
+            } else {
+                m.out[row] = v;
+            }
         }
     }
 }
@@ -134,8 +181,7 @@ __global__ void pack_rows8_kernel(const uint16_t* __restrict__ w, uint16_t* __re
     }
 }
 
-int run_row8(const uint16_t* hidden, const float* hidden_f32, const Row8Mat* mats, int n, int64_t K, int dtype_code,
-             hipStream_t st) {
+int run_row8(const plm::Row8X& x, const Row8Mat* mats, int n, int64_t K, int dtype_code, hipStream_t st) {
     Row8Args a;
     std::memset(&a, 0, sizeof(a));
     int64_t tiles = 0;
@@ -149,8 +195,11 @@ int run_row8(const uint16_t* hidden, const float* hidden_f32, const Row8Mat* mat
         ++used;
     }
     if (used == 0) return 0;  // nothing to write
-    a.hidden = hidden;
-    a.hidden_f32 = hidden_f32;
+    a.hidden = x.u16;
+    a.hidden_f32 = x.f32;
+    a.hidden_b = x.f32_b;
+    a.norm_w = x.norm_w;
+    a.eps = x.eps;
     a.K = K;
     a.nmats = used;
     a.nchunks = static_cast<int>(plm::ceil_div(K, 64));
@@ -158,16 +207,18 @@ int run_row8(const uint16_t* hidden, const float* hidden_f32, const Row8Mat* mat
     const int nw = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(a.nchunks, kMaxWaves)));
     if (tiles > 0x7FFFFFFF) return plm::fail(2, "too many row blocks");
     const dim3 grid(static_cast<unsigned>(tiles)), block(nw * plm::kWave);
-    if (hidden_f32 != nullptr) {
-        if (dtype_code == 1) {
-            hipLaunchKernelGGL((row8_gemv_kernel<true, true>), grid, block, 0, st, a);
-        } else {
-            hipLaunchKernelGGL((row8_gemv_kernel<false, true>), grid, block, 0, st, a);
-        }
-    } else if (dtype_code == 1) {
-        hipLaunchKernelGGL((row8_gemv_kernel<true, false>), grid, block, 0, st, a);
+    const int xm = x.f32 != nullptr ? (x.f32_b != nullptr ? kXSilu : kXF32) : (x.norm_w != nullptr ? kXNorm : kXU16);
+    auto launch = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, st, a); };
+    if (dtype_code == 1) {
+        if (xm == kXU16) launch(row8_gemv_kernel<true, kXU16>);
+        else if (xm == kXF32) launch(row8_gemv_kernel<true, kXF32>);
+        else if (xm == kXSilu) launch(row8_gemv_kernel<true, kXSilu>);
+        else launch(row8_gemv_kernel<true, kXNorm>);
     } else {
-        hipLaunchKernelGGL((row8_gemv_kernel<false, false>), grid, block, 0, st, a);
+        if (xm == kXU16) launch(row8_gemv_kernel<false, kXU16>);
+        else if (xm == kXF32) launch(row8_gemv_kernel<false, kXF32>);
+        else if (xm == kXSilu) launch(row8_gemv_kernel<false, kXSilu>);
+        else launch(row8_gemv_kernel<false, kXNorm>);
     }
     return plm::check_launch("row8 gemv kernel");
 }
@@ -176,7 +227,14 @@ int run_row8(const uint16_t* hidden, const float* hidden_f32, const Row8Mat* mat
 
 int plm::row8_gemv(const uint16_t* hidden, const float* hidden_f32, const Row8Mat* mats, int n, int64_t K,
                    int dtype_code, hipStream_t st) {
-    return run_row8(hidden, hidden_f32, mats, n, K, dtype_code, st);
+    plm::Row8X x;
+    x.u16 = hidden_f32 == nullptr ? hidden : nullptr;
+    x.f32 = hidden_f32;
+    return run_row8(x, mats, n, K, dtype_code, st);
+}
+
+int plm::row8_gemv_x(const Row8X& x, const Row8Mat* mats, int n, int64_t K, int dtype_code, hipStream_t st) {
+    return run_row8(x, mats, n, K, dtype_code, st);
 }
 
 PLM_EXPORT int native_pack_u16_rows8(const uint16_t* weight, uint16_t* packed, int64_t rows, int64_t cols) {
@@ -199,7 +257,7 @@ PLM_EXPORT int native_packed_gemv_rows8(const uint16_t* hidden, const uint16_t* 
     m.out = out;
     m.rows = rows;
     m.first_tile = 0;
-    return run_row8(hidden, nullptr, &m, 1, cols, dtype_code, plm::current_stream());
+    return plm::row8_gemv(hidden, nullptr, &m, 1, cols, dtype_code, plm::current_stream());
 }
 
 PLM_EXPORT int native_packed_gemv_rows8_many(const uint16_t* hidden, const uint16_t* const* packed_ptrs,
@@ -217,7 +275,7 @@ PLM_EXPORT int native_packed_gemv_rows8_many(const uint16_t* hidden, const uint1
         mats[i].rows = rows[i];
         mats[i].first_tile = 0;
     }
-    return run_row8(hidden, nullptr, mats, static_cast<int>(count), cols, dtype_code, plm::current_stream());
+    return plm::row8_gemv(hidden, nullptr, mats, static_cast<int>(count), cols, dtype_code, plm::current_stream());
 }
 
 PLM_EXPORT int native_packed_gemv_rows8_f32_hidden(const float* hidden, const uint16_t* packed, float* out, int64_t rows,
@@ -230,5 +288,5 @@ PLM_EXPORT int native_packed_gemv_rows8_f32_hidden(const float* hidden, const ui
     m.out = out;
     m.rows = rows;
     m.first_tile = 0;
-    return run_row8(nullptr, hidden, &m, 1, cols, dtype_code, plm::current_stream());
+    return plm::row8_gemv(nullptr, hidden, &m, 1, cols, dtype_code, plm::current_stream());
 }
