@@ -37,7 +37,7 @@ constexpr int kMaxGroup = 16;     // query heads per kv head
 constexpr int kMaxHeadDim = 256;
 constexpr int kMaxSplitLen = 256; // tokens per attention workgroup
 constexpr int kTokUnroll = 4;      // tokens whose loads a wave issues together
-constexpr int kMergeThreads = 256;
+constexpr int kMergeThreads = 1024;
 constexpr int kMaxSplits = 4096;   // splits per head the merge stages in LDS
 
 __device__ __forceinline__ float rd16(uint16_t v, bool bf16) {
@@ -163,17 +163,22 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(
         q_s[i] = q_rot[static_cast<int64_t>(kvh) * group * hd + i];
     __syncthreads();
 
-    // Scores: a wave loads the rows of kTokUnroll tokens before using any.
+    // Scores: a wave loads the rows of kTokUnroll tokens before using any;
+    // the V rows of its first tokens are loaded at the same time (vpre) so
+    // that the value pass does not start with a full memory latency.
+    float vpre[kTokUnroll][DPL];
     for (int i0 = wave; i0 < n; i0 += kAttnWaves * kTokUnroll) {
         float kv[kTokUnroll][DPL];
 #pragma unroll
         for (int u = 0; u < kTokUnroll; ++u) {
             const int i = min(i0 + u * kAttnWaves, n - 1);
             const uint16_t* kr = k_cache + (t0 + i) * kv_width + static_cast<int64_t>(kvh) * hd;
+            const uint16_t* vr = v_cache + (t0 + i) * kv_width + static_cast<int64_t>(kvh) * hd;
 #pragma unroll
             for (int j = 0; j < DPL; ++j) {
                 const int d = lane + 64 * j;
                 kv[u][j] = d < hd ? rd16(kr[d], BF16) : 0.0f;
+                if (i0 == wave) vpre[u][j] = d < hd ? rd16(vr[d], BF16) : 0.0f;
             }
         }
 #pragma unroll
@@ -236,7 +241,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(
 #pragma unroll
             for (int j = 0; j < DPL; ++j) {
                 const int d = lane + 64 * j;
-                vv[u][j] = d < hd ? rd16(vr[d], BF16) : 0.0f;
+                vv[u][j] = i0 == wave ? vpre[u][j] : (d < hd ? rd16(vr[d], BF16) : 0.0f);
             }
         }
 #pragma unroll
@@ -324,7 +329,8 @@ __global__ __launch_bounds__(kMergeThreads) void attention_merge_kernel(const fl
     m = wave_max_all(m);
     if (lane == 0) red[wave] = m;
     __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    m = red[0];
+    for (int w = 1; w < kMergeThreads / 64; ++w) m = fmaxf(m, red[w]);
     __syncthreads();
     float den = 0.0f;
     for (int sp = tid; sp < nsplit; sp += kMergeThreads) {
