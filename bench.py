@@ -4,22 +4,37 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W]      # one JSON line
     python bench.py --table [--table-out FILE]               # every workload
 
-Default workload (one JSON line): Q4 dequant+GEMV over one Qwen2.5-7B MLP,
-i.e. the gate and up matrices [18944, 3584] and the down matrix
-[3584, 18944], per-row symmetric Q4 from N(0, 0.02) weights, times one fp16
-activation row ~N(0, 1) (M = 1).  One step = one call of the reference's Q4
-MLP entry point q4_moe_selected_forward_u16 (one selected expert, route
-weight 1.0): a fused gate/up + SiLU launch and a down launch.  Weight copies are rotated over more than 1 GB so
-that the 256 MB Infinity Cache cannot serve them; inputs are resident in HBM
-before the timed region starts.
+Default line: one decode token through a DeepSeek-V3 MoE layer (hidden 7168,
+256 routed experts + 1 shared expert, moe_inter 2048, SwiGLU; every expert's
+gate/up [2048, 7168] and down [7168, 2048] FP8 e4m3 from N(0, 0.02) with
+fp32 128x128-block scale_inv ~U(1e-3, 1e-2)).  All 257 experts (11.3 GB) are
+resident in HBM, so the 256 MB Infinity Cache cannot serve the chosen ones.
+One step = one token (M = 1, a bf16 hidden state ~N(0, 1)) as the device
+path runs it:
+
+  1. ds_route_topk_f32 on fresh router logits ~N(0, 1): sigmoid scores,
+     8 groups of which the best 4 are kept (group score = max: no
+     correction bias), top 8, normalised, x2.5;
+  2. fp8_e4m3_block_moe_device_routed_bf16x_f32: the plan of the chosen
+     experts, gate/up + SiLU for the 8 chosen experts and the shared expert
+     in one launch, down + route-weighted sum + the shared expert + the bf16
+     output in another.
+
+The roofline is taken over the MoE layer's own launches (plan, gate/up,
+down): the same steps with the router's outputs computed beforehand, timed
+in a separate region.  The line also carries "m8": the speculative / MTP
+verifier batch, M = 8 bf16 activation rows, on the 7168 x 16384 output
+projection (each weight byte read once per batch), and "verifier": every
+DeepSeek-V3 projection shape of that batch at M = 1 and M = 8.
 
 Timing: the stream is held by a short sleep kernel while the timed launches
 are queued; one HIP event pair on the launch stream brackets all of them, and
-the GPU runs them back to back.  ms/step and the average launch duration come
-from that pair.
+the GPU runs them back to back.
 
-The ``cpu_baseline`` leg runs the CPU oracle's restatement of the same
-entry point (OpenMP, all host threads) on a bounded sample of the workload.
+cpu_baseline: the reference's own fp8_linear.cpp, compiled from its source
+into oracle/_ref (fp8_e4m3_block_mlp_many_weighted_f32 for the 8 routed
+experts + fp8_e4m3_block_mlp_f32 for the shared expert, as run_fp8_moe calls
+them at M = 1), on the host's cores and on one thread, on a bounded sample.
 """
 
 from __future__ import annotations
@@ -29,6 +44,7 @@ import ctypes
 import json
 import math
 import os
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -36,6 +52,10 @@ from pathlib import Path
 REPO = Path(__file__).resolve().parent
 PEAK_HBM_GBS = 8000.0
 MALL_BYTES = 1 << 30  # rotate at least this many distinct weight bytes
+
+# DeepSeek-V3 MoE layer
+HID, INTER, N_ROUTED, TOP_K = 7168, 2048, 256, 8
+N_GROUPS, TOPK_GROUPS, ROUTE_SCALE = 8, 4, 2.5
 
 
 def _args(argv=None):
@@ -45,7 +65,7 @@ def _args(argv=None):
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--table", action="store_true", help="measure every workload, print a markdown table")
     ap.add_argument("--table-out", default=None, help="also write the table to this file")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample length")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length (all threads)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None,
                     help="table: measure only the workloads whose name contains one of these comma-separated "
@@ -79,10 +99,12 @@ class Timer:
         ms = max(a.elapsed_time(b), 1e-3)
         return 2_000_000 / ms
 
-    def run(self, launches, hold_ms: float = 30.0) -> float:
+    def run(self, launches, hold_ms: float | None = None) -> float:
         """launches: zero-arg callables, each enqueuing kernels on the current
         stream.  Returns the total GPU time of all of them in ms."""
         torch = self.torch
+        if hold_ms is None:
+            hold_ms = max(30.0, 0.1 * len(launches))
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         torch.cuda._sleep(int(self.cycles_per_ms * hold_ms))
@@ -98,7 +120,427 @@ def _stream_ptr(torch):
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
-# --------------------------------------------------------------------------- workloads
+def _vp(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+# --------------------------------------------------------------------------- byte counts
+
+def fp8_bytes(rows, cols, m):
+    """FP8 GEMV: weights, fp32 scale grid, bf16 activations, fp32 outputs."""
+    return rows * cols + 4 * math.ceil(rows / 128) * math.ceil(cols / 128) + 2 * m * cols + 4 * m * rows
+
+
+def expert_bytes(hidden=HID, inter=INTER):
+    """One SwiGLU expert at rest: gate, up [inter, hidden] and down
+    [hidden, inter] e4m3 bytes and their fp32 scale grids."""
+    grid_gu = math.ceil(inter / 128) * math.ceil(hidden / 128)
+    grid_d = math.ceil(hidden / 128) * math.ceil(inter / 128)
+    return 3 * inter * hidden + 4 * (2 * grid_gu + grid_d)
+
+
+def moe_layer_bytes(m=1):
+    """One MoE layer step: the 8 chosen + the shared expert at rest, the
+    bf16 hidden rows in, the fp32 layer output rows out."""
+    return (TOP_K + 1) * expert_bytes() + 2 * m * HID + 4 * m * HID
+
+
+def moe_step_bytes(m=1):
+    """... plus the router logits read by the routing launch."""
+    return moe_layer_bytes(m) + 4 * m * N_ROUTED
+
+
+# --------------------------------------------------------------------------- DeepSeek-V3 MoE layer
+
+class MoEPool:
+    """The 256 routed experts and the shared expert of one DeepSeek-V3 MoE
+    layer in HBM, the device table of the routed experts' addresses
+    ([6][256] int64: gate w/s, up w/s, down w/s) and the shared expert's."""
+
+    def __init__(self, torch, seed=20261201):
+        self.torch = torch
+        gen = torch.Generator(device="cuda").manual_seed(seed)
+        self.experts = []
+        for _ in range(N_ROUTED + 1):
+            t = []
+            for rows, cols in ((INTER, HID), (INTER, HID), (HID, INTER)):
+                w = torch.randn((rows, cols), generator=gen, device="cuda").mul_(0.02)
+                t.append(w.to(torch.float8_e4m3fn).view(torch.uint8))
+                del w
+                t.append(torch.rand((math.ceil(rows / 128), math.ceil(cols / 128)), generator=gen,
+                                    device="cuda").mul_(9e-3).add_(1e-3))
+            self.experts.append(t)
+        addr = torch.tensor([[self.experts[e][r].data_ptr() for e in range(N_ROUTED)] for r in range(6)],
+                            dtype=torch.int64)
+        self.table = addr.cuda()
+        self.shared = (ctypes.c_uint64 * 6)(*[t.data_ptr() for t in self.experts[N_ROUTED]])
+        torch.cuda.synchronize()
+
+    def nbytes(self):
+        return sum(t.numel() * t.element_size() for e in self.experts for t in e)
+
+
+class MoEStep:
+    """One decode token through the layer, as the device path runs it."""
+
+    def __init__(self, torch, lib, pool, nsteps, seed=7):
+        self.torch, self.lib, self.pool = torch, lib, pool
+        gen = torch.Generator(device="cuda").manual_seed(seed)
+        self.nsteps = nsteps
+        self.logits = torch.randn((nsteps, N_ROUTED), generator=gen, device="cuda")
+        self.x = torch.randn((nsteps, HID), generator=gen, device="cuda").to(torch.bfloat16)
+        self.idx = torch.empty((nsteps, TOP_K), dtype=torch.int64, device="cuda")
+        self.w = torch.empty((nsteps, TOP_K), dtype=torch.float32, device="cuda")
+        self.y = torch.empty((1, HID), device="cuda")
+        self.ys = torch.empty((1, HID), device="cuda")
+        self.ybf = torch.empty((1, HID), dtype=torch.bfloat16, device="cuda")
+        self.rejected = torch.zeros((1,), dtype=torch.int32, device="cuda")
+        self.row_bytes = {"logits": 4 * N_ROUTED, "x": 2 * HID, "idx": 8 * TOP_K, "w": 4 * TOP_K}
+
+    def _at(self, t, i, name):
+        return ctypes.c_void_p(t.data_ptr() + i * self.row_bytes[name])
+
+    def route(self, i):
+        code = self.lib.ds_route_topk_f32(self._at(self.logits, i, "logits"), None, 1, N_ROUTED, TOP_K, N_GROUPS,
+                                          TOPK_GROUPS, 0, ROUTE_SCALE, self._at(self.idx, i, "idx"),
+                                          self._at(self.w, i, "w"))
+        if code != 0:
+            raise RuntimeError(f"ds_route_topk_f32 failed with code {code}")
+
+    def moe(self, i):
+        code = self.lib.fp8_e4m3_block_moe_device_routed_bf16x_f32(
+            _vp(self.pool.table), N_ROUTED, self._at(self.idx, i, "idx"), self._at(self.w, i, "w"), TOP_K,
+            ctypes.cast(self.pool.shared, ctypes.c_void_p), self._at(self.x, i, "x"), _vp(self.y), _vp(self.ys),
+            _vp(self.ybf), _vp(self.rejected), 1, INTER, HID, math.ceil(HID / 128), math.ceil(INTER / 128))
+        if code != 0:
+            raise RuntimeError(f"fp8_e4m3_block_moe_device_routed_bf16x_f32 failed with code {code}")
+
+    def step(self, i):
+        self.route(i)
+        self.moe(i)
+
+
+def bench_moe_layer(torch, lib, timer, steps, warmup):
+    pool = MoEPool(torch)
+    total = warmup + steps
+    st = MoEStep(torch, lib, pool, total)
+    lib.pocketlm_set_stream(_stream_ptr(torch))
+    for i in range(warmup):
+        st.step(i)
+    torch.cuda.synchronize()
+    if int(st.rejected.item()) != 0:
+        raise RuntimeError("the device plan left out router indices")
+    # the headline: K steps, router included
+    ms_steps = timer.run([lambda i=i: st.step(warmup + i) for i in range(steps)])
+    # the roofline region: the MoE layer's own launches on the same K tokens,
+    # the router's outputs (already written by the timed steps) read as they are
+    ms_moe = timer.run([lambda i=i: st.moe(warmup + i) for i in range(steps)])
+    chosen = st.idx[warmup:].cpu()
+    distinct = len(set(chosen.reshape(-1).tolist()))
+    return {"pool": pool, "step": st, "ms_per_step": ms_steps / steps, "ms_per_moe": ms_moe / steps,
+            "distinct_experts": distinct}
+
+
+# --------------------------------------------------------------------------- verifier batch (FP8 projections)
+
+VERIFIER_SHAPES = (("q_a", 1536, 7168), ("kv_a", 576, 7168), ("o", 7168, 16384),
+                   ("expert gate/up", 2048, 7168), ("expert down", 7168, 2048))
+
+
+def bench_verifier(torch, lib, timer, pool, ms=(1, 8), reps=200):
+    """Each DeepSeek-V3 projection of the verifier batch at M rows of bf16
+    activations, through fp8_e4m3_block_linear_bf16x_f32.  The expert shapes
+    rotate over the pool's 256 experts; q_a and kv_a over the first rows of
+    the pool's gate matrices (row-major, so a prefix of rows is a weight of
+    its own); o over 9 copies of its own (1.06 GB)."""
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    o_sets = []
+    for _ in range(max(2, math.ceil(MALL_BYTES / (7168 * 16384)))):
+        w = torch.randn((7168, 16384), generator=gen, device="cuda").mul_(0.02).to(torch.float8_e4m3fn)
+        s = torch.rand((56, 128), generator=gen, device="cuda").mul_(9e-3).add_(1e-3)
+        o_sets.append((w.view(torch.uint8), s))
+    ex = pool.experts[:N_ROUTED]
+    sources = {
+        "q_a": [(e[0], e[1]) for e in ex],
+        "kv_a": [(e[0], e[1]) for e in ex],
+        "o": o_sets,
+        "expert gate/up": [(e[0], e[1]) for e in ex],
+        "expert down": [(e[4], e[5]) for e in ex],
+    }
+    out = []
+    lib.pocketlm_set_stream(_stream_ptr(torch))
+    for name, rows, cols in VERIFIER_SHAPES:
+        sets = sources[name]
+        for m in ms:
+            x = torch.randn((m, cols), generator=gen, device="cuda").to(torch.bfloat16)
+            y = torch.empty((m, rows), device="cuda")
+            sc = math.ceil(cols / 128)
+
+            def call(w, s, x=x, y=y, m=m, rows=rows, cols=cols, sc=sc):
+                code = lib.fp8_e4m3_block_linear_bf16x_f32(_vp(w), _vp(s), _vp(x), _vp(y), m, rows, cols, sc)
+                if code != 0:
+                    raise RuntimeError(f"fp8_e4m3_block_linear_bf16x_f32 failed with code {code}")
+
+            for w, s in sets[:4]:
+                call(w, s)
+            torch.cuda.synchronize()
+            n = reps
+            ms_total = timer.run([lambda j=j: call(*sets[j % len(sets)]) for j in range(n)])
+            us = 1e3 * ms_total / n
+            nbytes = fp8_bytes(rows, cols, m)
+            gbs = nbytes / us / 1e3
+            out.append({"shape": f"{name} {rows}x{cols}", "m": m, "us": round(us, 3), "bytes": nbytes,
+                        "gb_s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)})
+    del o_sets
+    torch.cuda.empty_cache()
+    return out
+
+
+# --------------------------------------------------------------------------- CPU baseline
+
+def _host_info():
+    info = {"nproc": os.cpu_count()}
+    try:
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in txt.splitlines():
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "Model name":
+                info["model"] = v
+            elif k == "Socket(s)":
+                info["sockets"] = int(v) if v.isdigit() else v
+            elif k == "CPU(s)":
+                info["cpus"] = int(v) if v.isdigit() else v
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        info["affinity"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        pass
+    return info
+
+
+def _ref_lib():
+    """The reference's fp8_linear.cpp built from its source (oracle/_ref), or None."""
+    path = REPO / "oracle" / "_ref" / "libref_fp8_linear.so"
+    if not path.exists():
+        return None
+    lib = ctypes.CDLL(str(path))
+    vp, i64 = ctypes.c_void_p, ctypes.c_longlong
+    lib.fp8_e4m3_block_mlp_many_weighted_f32.argtypes = [vp] * 9 + [i64] * 6
+    lib.fp8_e4m3_block_mlp_f32.argtypes = [vp] * 8 + [i64] * 5
+    lib.fp8_e4m3_block_linear_f32.argtypes = [vp] * 4 + [i64] * 4
+    for f in (lib.fp8_e4m3_block_mlp_many_weighted_f32, lib.fp8_e4m3_block_mlp_f32, lib.fp8_e4m3_block_linear_f32):
+        f.restype = ctypes.c_int
+    return lib
+
+
+def _omp():
+    """The OpenMP runtime the reference build links (to set its thread count)."""
+    gomp = ctypes.CDLL("libgomp.so.1")
+    gomp.omp_set_num_threads.argtypes = [ctypes.c_int]
+    gomp.omp_get_max_threads.restype = ctypes.c_int
+    return gomp
+
+
+def _timed_calls(fn, seconds, min_calls=2):
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and n >= min_calls:
+            return n, el
+
+
+def cpu_moe_baseline(torch, r, seconds):
+    """The reference's CPU MoE layer (8 routed, route-weighted + shared) on
+    the experts step 0 chose, weights warm in host RAM, all threads and one."""
+    import numpy as np
+
+    st, pool = r["step"], r["pool"]
+    warm = 0
+    idx = st.idx[warm].cpu().tolist()
+    wts = st.w[warm].cpu().tolist()
+    order = sorted(range(TOP_K), key=lambda j: idx[j])  # run_fp8_moe's sorted distinct experts
+    routed = [[t.cpu().numpy() for t in pool.experts[idx[j]]] for j in order]
+    shared = [t.cpu().numpy() for t in pool.experts[N_ROUTED]]
+    route = np.array([wts[j] for j in order], dtype=np.float32)
+    hidden = st.x[warm:warm + 1].float().cpu().numpy()
+    out = np.empty((1, HID), dtype=np.float32)
+    out_s = np.empty((1, HID), dtype=np.float32)
+    ref = _ref_lib()
+    kind = "reference"
+    if ref is not None:
+        tabs = [np.array([e[k].ctypes.data for e in routed], dtype=np.uint64) for k in range(6)]
+
+        def layer():
+            c1 = ref.fp8_e4m3_block_mlp_many_weighted_f32(*[t.ctypes.data for t in tabs], hidden.ctypes.data,
+                                                          route.ctypes.data, out.ctypes.data, TOP_K, 1, INTER,
+                                                          HID, 56, 16)
+            c2 = ref.fp8_e4m3_block_mlp_f32(*[t.ctypes.data for t in shared], hidden.ctypes.data, out_s.ctypes.data,
+                                            1, INTER, HID, 56, 16)
+            if c1 != 0 or c2 != 0:
+                raise RuntimeError(f"reference MoE returned {c1}, {c2}")
+    else:
+        import oracle
+
+        kind = "port"
+
+        def layer():
+            oracle.fp8_mlp_many_weighted([tuple(e) for e in routed], hidden, route)
+            oracle.fp8_mlp(*shared, hidden)
+
+    omp = _omp()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or omp.omp_get_max_threads()
+    omp.omp_set_num_threads(threads)
+    n_all, el_all = _timed_calls(layer, seconds)
+    omp.omp_set_num_threads(1)
+    n_one, el_one = _timed_calls(layer, seconds / 2)
+    omp.omp_set_num_threads(threads)
+    nbytes = moe_layer_bytes(1)
+    us_all, us_one = el_all / n_all * 1e6, el_one / n_one * 1e6
+    return {
+        "value": round(nbytes / us_all / 1e3, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": kind,
+        "us_per_step": round(us_all, 1),
+        "sample": (f"{n_all} calls of the reference's fp8_e4m3_block_mlp_many_weighted_f32 (8 routed experts) + "
+                   f"fp8_e4m3_block_mlp_f32 (shared expert), fp8_linear.cpp built from source with g++ -O2 "
+                   f"-fopenmp, on the experts of the first timed token, {el_all:.1f} s on {threads} OpenMP "
+                   f"threads, weights warm in host RAM" if kind == "reference" else
+                   f"{n_all} calls of the oracle's restatement, {el_all:.1f} s on {threads} threads"),
+        "single_thread": {"value": round(nbytes / us_one / 1e3, 3), "unit": "GB/s", "us_per_step": round(us_one, 1),
+                          "calls": n_one},
+        "host": _host_info(),
+    }
+
+
+def cpu_verifier_baseline(seconds_each=2.0):
+    """The reference's fp8_e4m3_block_linear_f32 on the 7168 x 16384 output
+    projection at M = 8, in both of its modes: the default (each activation
+    row re-reads the weight, fp8_linear.cpp:96-116) and batch reuse (one
+    pass over the weight for the whole batch, fp8_linear.cpp:68-94,
+    PCKETLM_ENABLE_NATIVE_FP8_BATCH_REUSE=1)."""
+    import numpy as np
+
+    ref = _ref_lib()
+    if ref is None:
+        return None
+    rng = np.random.default_rng(5)
+    w = rng.integers(0, 0x7E, size=(7168, 16384), dtype=np.uint8)  # finite e4m3 bytes
+    s = rng.uniform(1e-3, 1e-2, size=(56, 128)).astype(np.float32)
+    x = rng.standard_normal((8, 16384)).astype(np.float32)
+    y = np.empty((8, 7168), dtype=np.float32)
+    res = {}
+    old = os.environ.get("PCKETLM_ENABLE_NATIVE_FP8_BATCH_REUSE")
+    try:
+        for mode, flag in (("default (W re-read per row)", None), ("batch reuse (W read once)", "1")):
+            if flag is None:
+                os.environ.pop("PCKETLM_ENABLE_NATIVE_FP8_BATCH_REUSE", None)
+            else:
+                os.environ["PCKETLM_ENABLE_NATIVE_FP8_BATCH_REUSE"] = flag
+            n, el = _timed_calls(lambda: ref.fp8_e4m3_block_linear_f32(w.ctypes.data, s.ctypes.data, x.ctypes.data,
+                                                                        y.ctypes.data, 8, 7168, 16384, 128),
+                                 seconds_each)
+            us = el / n * 1e6
+            res[mode] = {"us": round(us, 1), "gb_s": round(fp8_bytes(7168, 16384, 8) / us / 1e3, 3), "calls": n}
+    finally:
+        if old is None:
+            os.environ.pop("PCKETLM_ENABLE_NATIVE_FP8_BATCH_REUSE", None)
+        else:
+            os.environ["PCKETLM_ENABLE_NATIVE_FP8_BATCH_REUSE"] = old
+    return res
+
+
+def _traffic(workload):
+    """HBM bytes per step from the committed counter runs (FETCH_SIZE and
+    WRITE_SIZE scaled by a plain copy's reading; profiles/traffic.json), or
+    None when they are absent."""
+    f = REPO / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        entry = json.loads(f.read_text()).get(workload) or {}
+        return entry.get("bytes_per_step")
+    except (OSError, ValueError, AttributeError):
+        return None
+
+
+def main_line(args):
+    import torch
+
+    from pocketlm_amd import _lib
+
+    torch.cuda.set_device(0)
+    lib = _lib.load()
+    if lib.pocketlm_device_available() != 1:
+        raise RuntimeError("libpocketlm_hip.so reports no gfx950 device")
+    timer = Timer(torch)
+    r = bench_moe_layer(torch, lib, timer, args.steps, args.warmup)
+    ms = r["ms_per_step"]
+    value = moe_step_bytes(1) / (ms / 1e3) / 1e9
+    moe_ms = r["ms_per_moe"]
+    achieved = moe_layer_bytes(1) / (moe_ms / 1e3) / 1e9
+    roof = {
+        "bound": "hbm",
+        "kernel": "the MoE layer's launches of fp8_e4m3_block_moe_device_routed_bf16x_f32: moe_plan_kernel, "
+                  "fp8_rows_kernel (gate/up + SiLU, 8 chosen + shared expert), fp8_combine_kernel (down, "
+                  "route-weighted sum, shared expert, bf16 output)",
+        "achieved": round(achieved, 2),
+        "peak": PEAK_HBM_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / PEAK_HBM_GBS, 4),
+        "traffic": _traffic("moe_layer"),
+        "traffic_unit": "HBM bytes per MoE layer call (all its launches)",
+        "us_per_launch_group": round(1e3 * moe_ms, 3),
+        "bytes_per_launch_group": moe_layer_bytes(1),
+    }
+    ver = bench_verifier(torch, lib, timer, r["pool"])
+    o8 = next(v for v in ver if v["shape"].startswith("o ") and v["m"] == 8)
+    m8 = {"workload": "speculative / MTP verifier batch: FP8 output projection 7168x16384, M=8 bf16 rows, "
+                      "fp8_e4m3_block_linear_bf16x_f32 (each weight byte read once per batch)",
+          "us": o8["us"], "value": o8["gb_s"], "unit": "GB/s", "frac": o8["frac"], "bytes": o8["bytes"]}
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_moe_baseline(torch, r, args.cpu_seconds)
+        cv = cpu_verifier_baseline()
+        if cv is not None:
+            m8["cpu_reference"] = {"kind": "reference", "threads": cpu["cores"], **{k: v for k, v in cv.items()}}
+    line = {
+        "metric": "dequant-GEMV µs & achieved HBM GB/s (% of peak) at M=1 and M=8",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_step": round(1e3 * ms, 3),
+        "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8 e4m3 weights x bf16 activations, fp32 accumulate",
+        "data": "synthetic (e4m3 weights from N(0,0.02), scale_inv ~U(1e-3,1e-2), router logits and hidden ~N(0,1))",
+        "config": {
+            "workload": "DeepSeek-V3 MoE layer decode, M=1: hidden 7168, 256 routed + 1 shared expert resident "
+                        "(11.3 GB), moe_inter 2048, sigmoid routing (8 groups keep 4, top 8, x2.5) on fresh logits "
+                        "per token, SwiGLU, bf16 output; step = ds_route_topk_f32 + "
+                        "fp8_e4m3_block_moe_device_routed_bf16x_f32",
+            "bytes_per_step": moe_step_bytes(1),
+            "distinct_experts_in_timed_steps": r["distinct_experts"],
+        },
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "m8": m8,
+        "verifier": ver,
+    }
+    print(json.dumps(line), flush=True)
+
+
+# --------------------------------------------------------------------------- Q4 workloads (table)
 
 def _q4_sets(torch, fmt, shapes, nsets, seed=20261201):
     """nsets copies of Q4 matrices of the given [rows, cols] shapes (device)."""
@@ -119,10 +561,6 @@ def _q4_sets(torch, fmt, shapes, nsets, seed=20261201):
 def q4_bytes(rows, cols):
     # packed weights + fp16 scales + fp16 x + fp32 y
     return rows * cols // 2 + 2 * rows + 2 * cols + 4 * rows
-
-
-def fp8_bytes(rows, cols, m):
-    return rows * cols + 4 * math.ceil(rows / 128) * math.ceil(cols / 128) + 2 * m * cols + 4 * m * rows
 
 
 def mlp_bytes(hidden, inter):
@@ -180,112 +618,6 @@ def bench_q4_mlp(torch, lib, fmt, steps, warmup, timer, hidden=3584, inter=18944
         "hidden": hidden,
         "inter": inter,
     }
-
-
-def cpu_q4_baseline(torch, sample, seconds):
-    import numpy as np
-
-    import oracle
-
-    def u16(t):
-        return t.cpu().view(torch.int16).numpy().view(np.uint16)
-
-    mats = sample["host_set"]
-    expert = []
-    for p, s, _r, _c in mats:
-        expert += [p.cpu().numpy(), u16(s)]
-    x16 = u16(sample["x"])
-    hidden, inter = sample["hidden"], sample["inter"]
-    route = np.ones(1, np.float32)
-    steps = 0
-    t0 = time.perf_counter()
-    while True:
-        oracle.q4_moe_selected(x16, [tuple(expert)], route, hidden, inter)
-        steps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    gbs = sample["step_bytes"] * steps / el / 1e9
-    return {
-        "value": round(gbs, 3),
-        "unit": "GB/s",
-        "cores": oracle.num_threads(),
-        "kind": "port",
-        "sample": f"{steps} calls of the oracle's restatement of q4_moe_selected_forward_u16 (Qwen2.5-7B MLP, "
-                  f"one expert, M=1) on one weight copy, {el:.1f} s, {el / steps * 1e6:.0f} us/call, "
-                  f"weights warm in host RAM",
-    }
-
-
-def _traffic(workload):
-    """HBM bytes per step from the committed counter runs (FETCH_SIZE and
-    WRITE_SIZE scaled by a plain copy's reading; profiles/traffic.json), or
-    None when they are absent."""
-    f = REPO / "profiles" / "traffic.json"
-    if not f.exists():
-        return None
-    try:
-        entry = json.loads(f.read_text()).get(workload) or {}
-        return entry.get("bytes_per_step")
-    except (OSError, ValueError, AttributeError):
-        return None
-
-
-def main_line(args):
-    import torch
-
-    from pocketlm_amd import _lib, formats
-
-    torch.cuda.set_device(0)
-    lib = _lib.load()
-    if lib.pocketlm_device_available() != 1:
-        raise RuntimeError("libpocketlm_hip.so reports no gfx950 device")
-    timer = Timer(torch)
-    r = bench_q4_mlp(torch, lib, formats, args.steps, args.warmup, timer)
-    ms = r["ms_per_step"]
-    value = r["step_bytes"] / (ms / 1e3) / 1e9
-    # The step is two launches of the Q4 row-dot kernels (gate/up + SiLU,
-    # then down); the roofline is taken over both, from the same events.
-    roof = {
-        "bound": "hbm",
-        "kernel": "q4_rows_kernel (gate/up + SiLU) + q4_down_kernel (down + combine), one MLP call",
-        "achieved": round(value, 2),
-        "peak": PEAK_HBM_GBS,
-        "unit": "GB/s",
-        "frac": round(value / PEAK_HBM_GBS, 4),
-        "traffic": _traffic("q4_mlp"),
-        "traffic_unit": "bytes per step (both launches)",
-        "launches_per_step": 2,
-        "bytes_per_step": r["step_bytes"],
-    }
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_q4_baseline(torch, r, args.cpu_seconds)
-    line = {
-        "metric": "dequant-GEMV µs & achieved HBM GB/s (% of peak) at M=1 and M=8",
-        "value": round(value, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
-        "us_per_step": round(1e3 * ms, 3),
-        "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "q4 weights, fp16 x, fp32 accumulate",
-        "data": "synthetic (N(0,0.02) weights quantized with the reference Q4 scheme, x ~ N(0,1) fp16)",
-        "config": {
-            "workload": "Q4 dequant+GEMV, Qwen2.5-7B MLP: gate/up [18944,3584] + down [3584,18944], M=1, "
-                        "through q4_moe_selected_forward_u16 (one expert, route 1.0)",
-            "bytes_per_step": r["step_bytes"],
-            "weight_copies_rotated": r["nsets"],
-        },
-        "roofline": roof,
-        "cpu_baseline": cpu,
-    }
-    print(json.dumps(line), flush=True)
 
 
 # --------------------------------------------------------------------------- table mode
@@ -907,24 +1239,25 @@ def pack_transfer(torch):
 
 
 def pmc_probe(args):
-    """Counter calibration workload: 5 default steps, then 3 copies of a
-    256 MiB fp32 buffer (256 MiB read + 256 MiB written per copy).  The
-    copy's FETCH_SIZE / WRITE_SIZE readings give the factor that turns the
-    counters into bytes."""
+    """Counter calibration workload: 10 default steps (router + MoE layer),
+    then 3 copies of a 256 MiB fp32 buffer (256 MiB read + 256 MiB written
+    per copy).  The copy's FETCH_SIZE / WRITE_SIZE readings give the factor
+    that turns the counters into bytes."""
     import torch
 
-    from pocketlm_amd import _lib, formats
+    from pocketlm_amd import _lib
 
     torch.cuda.set_device(0)
     lib = _lib.load()
     timer = Timer(torch)
-    bench_q4_mlp(torch, lib, formats, 5, 2, timer)
+    bench_moe_layer(torch, lib, timer, 10, 2)
+    torch.cuda.synchronize()
     src = torch.ones(64 << 20, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print("pmc probe done: 7 MLP calls, 3 copies of 268435456 bytes", flush=True)
+    print("pmc probe done: 12 + 10 + 10 MoE layer steps, 3 copies of 268435456 bytes", flush=True)
 
 
 def main(argv=None):

@@ -364,6 +364,38 @@ int ds_moe_layer_forward_fp8_f32(void* handle, const uint64_t* gate_weight_ptrs,
                                  int64_t gate_scale_cols, int64_t down_scale_cols,
                                  float* hidden_out);
 
+/* Callback bridges of the session (ds_forward.cpp:369-512), with the
+ * reference's callback types (ds_forward.cpp:20-43).  Each calls its
+ * callback once, checks the element count it reports (code 20 when it
+ * differs), copies that many fp32 values from the callback's buffer (host
+ * or device memory) to the output (host or device memory) on the calling
+ * thread's stream and waits for the copy, since the callback's buffer is
+ * only guaranteed for the duration of the call.  Codes 1 null handle /
+ * pointer / callback, 2 bad dims (bad layer index for the attention
+ * bridge), 10+k when the callback returns k or a null buffer, 20 count
+ * mismatch, -(1000+err) copy failure.  Counters as in the reference:
+ * callback_invocations += 1 per callback; on success monolithic_calls += 1
+ * and attention_invocations += 1 (attention), layers_executed += num_layers
+ * (decode), num_layers * n_tokens (prefill), num_layers * k (verify). */
+typedef int (*pocketlm_ds_attention_callback)(int64_t layer_idx, const float* hidden_in, int64_t batch,
+                                              int64_t hidden_dim, const float** out, int64_t* out_count);
+typedef int (*pocketlm_ds_decode_callback)(int64_t input_token_id, const float** out, int64_t* out_count);
+typedef int (*pocketlm_ds_prefill_callback)(const int64_t* input_token_ids, int64_t n_tokens, const float** out,
+                                            int64_t* out_count);
+typedef int (*pocketlm_ds_verify_callback)(const int64_t* candidate_token_ids, int64_t k, const float** out,
+                                           int64_t* out_count);
+int ds_attention_layer_forward_f32(void* handle, int64_t layer_idx, const float* hidden_in, int64_t batch,
+                                   int64_t hidden_dim, pocketlm_ds_attention_callback attention_callback,
+                                   float* hidden_out);
+int ds_forward_decode_f32(void* handle, int64_t input_token_id, pocketlm_ds_decode_callback decode_callback,
+                          float* output_logits, int64_t vocab_size);
+int ds_forward_prefill_f32(void* handle, const int64_t* input_token_ids, int64_t n_tokens,
+                           pocketlm_ds_prefill_callback prefill_callback, float* output_final_logits,
+                           int64_t vocab_size);
+int ds_forward_verify_f32(void* handle, const int64_t* candidate_token_ids, int64_t k,
+                          pocketlm_ds_verify_callback verify_callback, float* output_logits_per_position,
+                          int64_t vocab_size);
+
 /* ds_forward.cpp:879-955: softmax top-k router over u16 (fp16/bf16) hidden
  * [hidden_dim] and router weights [num_experts, hidden_dim] (device);
  * output_expert_ids int64 [k] and output_weights fp32 [k] (device).
@@ -530,6 +562,44 @@ int kv_dense_layer_decode_u16_ext_packed_rows8(
     const uint16_t* k_bias, const uint16_t* v_bias, const uint16_t* q_norm_weight, const uint16_t* k_norm_weight,
     uint16_t* out, int64_t hidden_size, int64_t intermediate_size, int64_t num_heads, int64_t num_kv_heads,
     float rms_eps, float rope_theta);
+
+/* The entry points over row-major (unpacked) weights that the reference's
+ * KV loader binds unconditionally (native/__init__.py:2615-2745):
+ * kv_attention_decode_fp16 (fp16_kv_cache.cpp:780-918),
+ * kv_attention_decode_u16_ext (920-1060), kv_dense_layer_decode_fp16
+ * (1206-1260) and kv_dense_layer_decode_u16_ext (1398-1531).  Same
+ * arguments.  They are not implemented by this library: after the
+ * reference's argument checks (code 1 for a bad handle, layer or null
+ * pointer, 2 for non-positive sizes) they return 90, with the reason in
+ * pocketlm_last_error().  A caller packs each weight once with
+ * native_pack_u16_rows8 and calls kv_dense_layer_decode_u16_ext_packed_rows8,
+ * which runs the same layer. */
+int kv_attention_decode_fp16(void* handle, int64_t layer, const uint16_t* hidden, const uint16_t* q_weight,
+                             const uint16_t* k_weight, const uint16_t* v_weight, const uint16_t* o_weight,
+                             uint16_t* out, int64_t hidden_size, int64_t num_attention_heads,
+                             int64_t num_key_value_heads, float rope_theta);
+int kv_attention_decode_u16_ext(void* handle, int64_t layer, const uint16_t* hidden, const uint16_t* q_weight,
+                                const uint16_t* k_weight, const uint16_t* v_weight, const uint16_t* o_weight,
+                                const uint16_t* q_bias, const uint16_t* k_bias, const uint16_t* v_bias,
+                                const uint16_t* q_norm_weight, const uint16_t* k_norm_weight, uint16_t* out,
+                                int64_t hidden_size, int64_t num_attention_heads, int64_t num_key_value_heads,
+                                float rope_theta, float rms_eps);
+int kv_dense_layer_decode_fp16(void* handle, int64_t layer, const uint16_t* hidden,
+                               const uint16_t* input_norm_weight, const uint16_t* post_norm_weight,
+                               const uint16_t* q_weight, const uint16_t* k_weight, const uint16_t* v_weight,
+                               const uint16_t* o_weight, const uint16_t* gate_weight, const uint16_t* up_weight,
+                               const uint16_t* down_weight, uint16_t* out, int64_t hidden_size,
+                               int64_t intermediate_size, int64_t num_heads, int64_t num_kv_heads, float rms_eps,
+                               float rope_theta);
+int kv_dense_layer_decode_u16_ext(void* handle, int64_t layer, const uint16_t* hidden,
+                                  const uint16_t* input_norm_weight, const uint16_t* post_norm_weight,
+                                  const uint16_t* q_weight, const uint16_t* k_weight, const uint16_t* v_weight,
+                                  const uint16_t* o_weight, const uint16_t* gate_weight, const uint16_t* up_weight,
+                                  const uint16_t* down_weight, const uint16_t* q_bias, const uint16_t* k_bias,
+                                  const uint16_t* v_bias, const uint16_t* q_norm_weight,
+                                  const uint16_t* k_norm_weight, uint16_t* out, int64_t hidden_size,
+                                  int64_t intermediate_size, int64_t num_heads, int64_t num_kv_heads, float rms_eps,
+                                  float rope_theta);
 
 #ifdef __cplusplus
 }

@@ -29,6 +29,16 @@ DS_TENSOR_CALLBACK = ctypes.CFUNCTYPE(
     ctypes.POINTER(ctypes.c_longlong),
 )
 
+DS_ATTENTION_CALLBACK = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_longlong, ctypes.c_void_p, ctypes.c_longlong,
+                                         ctypes.c_longlong, ctypes.POINTER(ctypes.c_void_p),
+                                         ctypes.POINTER(ctypes.c_longlong))
+DS_DECODE_CALLBACK = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_longlong, ctypes.POINTER(ctypes.c_void_p),
+                                      ctypes.POINTER(ctypes.c_longlong))
+DS_PREFILL_CALLBACK = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_longlong,
+                                       ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_longlong))
+DS_VERIFY_CALLBACK = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_longlong,
+                                      ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_longlong))
+
 # name: (restype, argtypes)
 _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pocketlm_set_stream": (_i32, [_vp]),
@@ -107,6 +117,14 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ds_moe_layer_forward_fp8_f32": (_i32, [_vp] * 9 + [_i64] * 6 + [_vp]),
     "ds_router_topk_u16": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp]),
     "ds_route_topk_f32": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _f32, _vp, _vp]),
+    "ds_attention_layer_forward_f32": (_i32, [_vp, _i64, _vp, _i64, _i64, DS_ATTENTION_CALLBACK, _vp]),
+    "ds_forward_decode_f32": (_i32, [_vp, _i64, DS_DECODE_CALLBACK, _vp, _i64]),
+    "ds_forward_prefill_f32": (_i32, [_vp, _vp, _i64, DS_PREFILL_CALLBACK, _vp, _i64]),
+    "ds_forward_verify_f32": (_i32, [_vp, _vp, _i64, DS_VERIFY_CALLBACK, _vp, _i64]),
+    "kv_attention_decode_fp16": (_i32, [_vp, _i64] + [_vp] * 6 + [_i64] * 3 + [_f32]),
+    "kv_attention_decode_u16_ext": (_i32, [_vp, _i64] + [_vp] * 11 + [_i64] * 3 + [_f32, _f32]),
+    "kv_dense_layer_decode_fp16": (_i32, [_vp, _i64] + [_vp] * 11 + [_i64] * 4 + [_f32, _f32]),
+    "kv_dense_layer_decode_u16_ext": (_i32, [_vp, _i64] + [_vp] * 16 + [_i64] * 4 + [_f32, _f32]),
 }
 
 _LIB: ctypes.CDLL | None = None

@@ -407,6 +407,101 @@ PLM_EXPORT int ds_moe_layer_forward_fp8_f32(void* handle, const uint64_t* gp, co
     return 0;
 }
 
+namespace {
+
+// The callback owns its buffer only for the duration of the call, so the
+// copy is waited for before returning (the reference copies with memcpy).
+int copy_callback_out(float* dst, const float* src, int64_t count) {
+    const hipStream_t st = plm::current_stream();
+    hipError_t err = hipMemcpyAsync(dst, src, static_cast<size_t>(count) * sizeof(float), hipMemcpyDefault, st);
+    if (err == hipSuccess) err = hipStreamSynchronize(st);
+    return err == hipSuccess ? 0 : plm::hip_fail(err, "callback output copy");
+}
+
+}  // namespace
+
+PLM_EXPORT int ds_attention_layer_forward_f32(void* handle, int64_t layer_idx, const float* hidden_in, int64_t batch,
+                                              int64_t hidden_dim, pocketlm_ds_attention_callback attention_callback,
+                                              float* hidden_out) {
+    plm::clear_error();
+    Session* s = static_cast<Session*>(handle);
+    if (s == nullptr || hidden_in == nullptr || attention_callback == nullptr || hidden_out == nullptr) return 1;
+    if (layer_idx < 0 || layer_idx >= s->num_layers || batch <= 0 || hidden_dim <= 0) return 2;
+    const float* cb_out = nullptr;
+    int64_t cb_count = 0;
+    const int code = attention_callback(layer_idx, hidden_in, batch, hidden_dim, &cb_out, &cb_count);
+    s->callback_invocations += 1;
+    if (code != 0 || cb_out == nullptr) return 10 + code;
+    if (cb_count != batch * hidden_dim) return 20;
+    const int c = copy_callback_out(hidden_out, cb_out, cb_count);
+    if (c != 0) return c;
+    s->monolithic_calls += 1;
+    s->attention_invocations += 1;
+    return 0;
+}
+
+PLM_EXPORT int ds_forward_decode_f32(void* handle, int64_t input_token_id, pocketlm_ds_decode_callback decode_callback,
+                                     float* output_logits, int64_t vocab_size) {
+    plm::clear_error();
+    Session* s = static_cast<Session*>(handle);
+    if (s == nullptr || decode_callback == nullptr || output_logits == nullptr) return 1;
+    if (vocab_size <= 0) return 2;
+    const float* cb_out = nullptr;
+    int64_t cb_count = 0;
+    const int code = decode_callback(input_token_id, &cb_out, &cb_count);
+    s->callback_invocations += 1;
+    if (code != 0 || cb_out == nullptr) return 10 + code;
+    if (cb_count != vocab_size) return 20;
+    const int c = copy_callback_out(output_logits, cb_out, cb_count);
+    if (c != 0) return c;
+    s->monolithic_calls += 1;
+    s->layers_executed += s->num_layers;
+    return 0;
+}
+
+PLM_EXPORT int ds_forward_prefill_f32(void* handle, const int64_t* input_token_ids, int64_t n_tokens,
+                                      pocketlm_ds_prefill_callback prefill_callback, float* output_final_logits,
+                                      int64_t vocab_size) {
+    plm::clear_error();
+    Session* s = static_cast<Session*>(handle);
+    if (s == nullptr || input_token_ids == nullptr || prefill_callback == nullptr || output_final_logits == nullptr)
+        return 1;
+    if (n_tokens <= 0 || vocab_size <= 0) return 2;
+    const float* cb_out = nullptr;
+    int64_t cb_count = 0;
+    const int code = prefill_callback(input_token_ids, n_tokens, &cb_out, &cb_count);
+    s->callback_invocations += 1;
+    if (code != 0 || cb_out == nullptr) return 10 + code;
+    if (cb_count != vocab_size) return 20;
+    const int c = copy_callback_out(output_final_logits, cb_out, cb_count);
+    if (c != 0) return c;
+    s->monolithic_calls += 1;
+    s->layers_executed += s->num_layers * n_tokens;
+    return 0;
+}
+
+PLM_EXPORT int ds_forward_verify_f32(void* handle, const int64_t* candidate_token_ids, int64_t k,
+                                     pocketlm_ds_verify_callback verify_callback, float* output_logits_per_position,
+                                     int64_t vocab_size) {
+    plm::clear_error();
+    Session* s = static_cast<Session*>(handle);
+    if (s == nullptr || candidate_token_ids == nullptr || verify_callback == nullptr ||
+        output_logits_per_position == nullptr)
+        return 1;
+    if (k <= 0 || vocab_size <= 0) return 2;
+    const float* cb_out = nullptr;
+    int64_t cb_count = 0;
+    const int code = verify_callback(candidate_token_ids, k, &cb_out, &cb_count);
+    s->callback_invocations += 1;
+    if (code != 0 || cb_out == nullptr) return 10 + code;
+    if (cb_count != k * vocab_size) return 20;
+    const int c = copy_callback_out(output_logits_per_position, cb_out, cb_count);
+    if (c != 0) return c;
+    s->monolithic_calls += 1;
+    s->layers_executed += s->num_layers * k;
+    return 0;
+}
+
 PLM_EXPORT int ds_router_topk_u16(const uint16_t* hidden_u16, const uint16_t* router_weights_u16, int64_t hidden_dim,
                                   int64_t num_experts, int64_t k, int64_t dtype_code, int64_t* output_expert_ids,
                                   float* output_weights) {

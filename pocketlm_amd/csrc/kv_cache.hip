@@ -666,6 +666,81 @@ PLM_EXPORT int kv_copy_layer(void* handle, int64_t layer, uint16_t* k_out, uint1
     return code;
 }
 
+namespace {
+
+// The row-major (unpacked) entry points: the reference's argument checks,
+// then "not implemented" (code 90).
+int rowmajor_unsupported(const char* name) {
+    return plm::fail(90, "%s: row-major weights are not supported by this library; pack each weight once with "
+                         "native_pack_u16_rows8 and call kv_dense_layer_decode_u16_ext_packed_rows8", name);
+}
+
+}  // namespace
+
+PLM_EXPORT int kv_attention_decode_fp16(void* handle, int64_t layer, const uint16_t* hidden, const uint16_t* q_weight,
+                                        const uint16_t* k_weight, const uint16_t* v_weight, const uint16_t* o_weight,
+                                        uint16_t* out, int64_t hidden_size, int64_t num_attention_heads,
+                                        int64_t num_key_value_heads, float rope_theta) {
+    (void)rope_theta;
+    plm::clear_error();
+    if (!valid_layer(static_cast<KvSession*>(handle), layer) || !hidden || !q_weight || !k_weight || !v_weight ||
+        !o_weight || !out)
+        return 1;
+    if (hidden_size <= 0 || num_attention_heads <= 0 || num_key_value_heads <= 0) return 2;
+    return rowmajor_unsupported("kv_attention_decode_fp16");
+}
+
+PLM_EXPORT int kv_attention_decode_u16_ext(void* handle, int64_t layer, const uint16_t* hidden,
+                                           const uint16_t* q_weight, const uint16_t* k_weight,
+                                           const uint16_t* v_weight, const uint16_t* o_weight, const uint16_t* q_bias,
+                                           const uint16_t* k_bias, const uint16_t* v_bias,
+                                           const uint16_t* q_norm_weight, const uint16_t* k_norm_weight,
+                                           uint16_t* out, int64_t hidden_size, int64_t num_attention_heads,
+                                           int64_t num_key_value_heads, float rope_theta, float rms_eps) {
+    (void)q_bias, (void)k_bias, (void)v_bias, (void)q_norm_weight, (void)k_norm_weight, (void)rope_theta,
+        (void)rms_eps;
+    plm::clear_error();
+    if (!valid_layer(static_cast<KvSession*>(handle), layer) || !hidden || !q_weight || !k_weight || !v_weight ||
+        !o_weight || !out)
+        return 1;
+    if (hidden_size <= 0 || num_attention_heads <= 0 || num_key_value_heads <= 0) return 2;
+    return rowmajor_unsupported("kv_attention_decode_u16_ext");
+}
+
+PLM_EXPORT int kv_dense_layer_decode_fp16(void* handle, int64_t layer, const uint16_t* hidden,
+                                          const uint16_t* input_norm_weight, const uint16_t* post_norm_weight,
+                                          const uint16_t* q_weight, const uint16_t* k_weight,
+                                          const uint16_t* v_weight, const uint16_t* o_weight,
+                                          const uint16_t* gate_weight, const uint16_t* up_weight,
+                                          const uint16_t* down_weight, uint16_t* out, int64_t hidden_size,
+                                          int64_t intermediate_size, int64_t num_heads, int64_t num_kv_heads,
+                                          float rms_eps, float rope_theta) {
+    (void)layer, (void)num_heads, (void)num_kv_heads, (void)rms_eps, (void)rope_theta;
+    plm::clear_error();
+    if (handle == nullptr || !hidden || !input_norm_weight || !post_norm_weight || !q_weight || !k_weight ||
+        !v_weight || !o_weight || !gate_weight || !up_weight || !down_weight || !out)
+        return 1;
+    if (hidden_size <= 0 || intermediate_size <= 0) return 2;
+    return rowmajor_unsupported("kv_dense_layer_decode_fp16");
+}
+
+PLM_EXPORT int kv_dense_layer_decode_u16_ext(
+    void* handle, int64_t layer, const uint16_t* hidden, const uint16_t* input_norm_weight,
+    const uint16_t* post_norm_weight, const uint16_t* q_weight, const uint16_t* k_weight, const uint16_t* v_weight,
+    const uint16_t* o_weight, const uint16_t* gate_weight, const uint16_t* up_weight, const uint16_t* down_weight,
+    const uint16_t* q_bias, const uint16_t* k_bias, const uint16_t* v_bias, const uint16_t* q_norm_weight,
+    const uint16_t* k_norm_weight, uint16_t* out, int64_t hidden_size, int64_t intermediate_size, int64_t num_heads,
+    int64_t num_kv_heads, float rms_eps, float rope_theta) {
+    (void)layer, (void)q_bias, (void)k_bias, (void)v_bias, (void)q_norm_weight, (void)k_norm_weight, (void)num_heads,
+        (void)num_kv_heads, (void)rms_eps, (void)rope_theta;
+    plm::clear_error();
+    if (handle == nullptr || !hidden || !input_norm_weight || !post_norm_weight || !q_weight || !k_weight ||
+        !v_weight || !o_weight || !gate_weight || !up_weight || !down_weight || !out)
+        return 1;
+    if (hidden_size <= 0 || intermediate_size <= 0) return 2;
+    return rowmajor_unsupported("kv_dense_layer_decode_u16_ext");
+}
+
 PLM_EXPORT int kv_dense_layer_decode_u16_ext_packed_rows8(
     void* handle, int64_t layer, const uint16_t* hidden, const uint16_t* input_norm_weight,
     const uint16_t* post_norm_weight, const uint16_t* q_weight_packed, const uint16_t* k_weight_packed,
