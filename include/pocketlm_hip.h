@@ -509,6 +509,25 @@ int fp8_e4m3_block_moe_device_routed_bf16x_f32(const uint64_t* expert_table, int
                                                uint16_t* out_bf16, int* rejected, int64_t batch,
                                                int64_t intermediate_rows, int64_t hidden_dim,
                                                int64_t gate_scale_cols, int64_t down_scale_cols);
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): fp8_e4m3_block_moe_device_routed_bf16x_f32 with its
+ * scratch (the fp32 activations [groups][batch][intermediate_rows], 256-byte
+ * aligned, then the expert plan) in a fixed 8 MiB device array of the
+ * library instead of its workspace.  It calls no hipMalloc or hipFree: the
+ * array's address is looked up once per device, on the first call made with
+ * that device current.  Same arguments, results and codes, plus -2 when a
+ * call needs more than the 8 MiB (groups = batch * top_k + 1 with a shared
+ * expert: batch 8, top_k 8 and intermediate_rows 2048 need 4.3 MB).  Every
+ * call on a device shares its array, so calls that overlap on one device
+ * (two streams, or two threads) race; nothing in it needs to start at zero. */
+int fp8_e4m3_block_moe_device_routed_bf16x_f32_noalloc(const uint64_t* expert_table, int64_t num_experts,
+                                                       const int64_t* route_indices, const float* route_weights,
+                                                       int64_t top_k, const uint64_t* shared_ptrs,
+                                                       const uint16_t* hidden_bf16, float* out, float* out_shared,
+                                                       uint16_t* out_bf16, int* rejected, int64_t batch,
+                                                       int64_t intermediate_rows, int64_t hidden_dim,
+                                                       int64_t gate_scale_cols, int64_t down_scale_cols);
 
 /* ---------------------------------------------------------------------------
  * KV session and dense decoder layer decode (src/pcketlm/native/

@@ -34,6 +34,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "common.h"
@@ -1274,10 +1275,12 @@ int pair_weighted_impl(const uint64_t* gp, const uint64_t* gsp, const uint64_t* 
 // in ascending order (the weighted call at batch 1, the row-weighted one
 // above it; with a shared expert, its merged form), the shared expert and
 // the bf16 tail computed by the down launch's workgroups.
+// fixed: a block the caller provides (fixed_bytes long) instead of the
+// library's workspace, for the entry point that allocates nothing.
 int device_routed_impl(const uint64_t* table, int64_t num_experts, const int64_t* idx, const float* wts,
                        int64_t top_k, const uint64_t* shared, Act hidden, float* out, float* out_shared,
                        uint16_t* out_bf16, int* rejected, int64_t batch, int64_t inter, int64_t hid, int64_t gsc,
-                       int64_t dsc) {
+                       int64_t dsc, char* fixed = nullptr, size_t fixed_bytes = 0) {
     if (num_experts <= 0 || num_experts > INT32_MAX || top_k <= 0 || batch <= 0 || batch > kMaxM ||
         batch * top_k > kMaxGroups)
         return plm::fail(-2, "bad dimensions (batch 1..%d, batch * top_k <= %d)", kMaxM, kMaxGroups);
@@ -1295,8 +1298,16 @@ int device_routed_impl(const uint64_t* table, int64_t num_experts, const int64_t
     const int groups = ndev + (shared != nullptr ? 1 : 0);
     const size_t act_bytes =
         static_cast<size_t>(plm::ceil_div(static_cast<int64_t>(groups) * batch * inter * 4, 256) * 256);
-    char* ws = static_cast<char*>(plm::workspace(act_bytes + sizeof(MoePlan)));
-    if (ws == nullptr) return -3;
+    char* ws;
+    if (fixed != nullptr) {
+        if (act_bytes + sizeof(MoePlan) > fixed_bytes)
+            return plm::fail(-2, "the call needs %zu bytes of scratch, more than the %zu this entry point holds",
+                             act_bytes + sizeof(MoePlan), fixed_bytes);
+        ws = fixed;
+    } else {
+        ws = static_cast<char*>(plm::workspace(act_bytes + sizeof(MoePlan)));
+        if (ws == nullptr) return -3;
+    }
     float* act = reinterpret_cast<float*>(ws);
     MoePlan* plan = reinterpret_cast<MoePlan*>(ws + act_bytes);
     hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(64), 0, st, table, num_experts, idx, wts,
@@ -1394,6 +1405,41 @@ int linear_many_impl(const uint64_t* weight_ptrs, const uint64_t* scale_ptrs, Ac
         const int code = linear_impl(w[i], s[i], hidden, p.vout[i], batch, out_rows[i], in_cols, scale_cols);
         if (code != 0) return code;
     }
+    return 0;
+}
+
+}  // namespace
+
+// ------------------------------------------------------- allocation-free entry point
+// fp8_e4m3_block_moe_device_routed_bf16x_f32_noalloc keeps its scratch (the
+// activations and the plan) in this array instead of the library's
+// workspace, so it never allocates.  Each device holds its own copy for the
+// life of the process; every call on a device shares it.
+constexpr size_t kNoAllocScratchBytes = static_cast<size_t>(8) << 20;  // 8 MiB
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+char* g_scratch_dev[kMaxDevices] = {};  // the array's device address, per device
+
+// The array's address on the current device, looked up the first time a
+// device calls (with that device current) and kept.  In host code the
+// array's name is not a device address: only this pointer is passed on.
+int scratch_address(char** out) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return plm::hip_fail(err, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return plm::fail(-2, "device %d beyond the %d this library tracks", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_dev[dev] == nullptr) {
+        void* p = nullptr;
+        err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess) return plm::hip_fail(err, "hipGetSymbolAddress(scratch)");
+        g_scratch_dev[dev] = static_cast<char*>(p);
+    }
+    *out = g_scratch_dev[dev];
     return 0;
 }
 
@@ -1647,6 +1693,20 @@ PLM_EXPORT int fp8_e4m3_block_moe_device_routed_bf16x_f32(const uint64_t* expert
     return device_routed_impl(expert_table, num_experts, route_indices, route_weights, top_k, shared_ptrs,
                               Act{nullptr, hidden_bf16}, out, out_shared, out_bf16, rejected, batch, inter, hid, gsc,
                               dsc);
+}
+
+PLM_EXPORT int fp8_e4m3_block_moe_device_routed_bf16x_f32_noalloc(
+    const uint64_t* expert_table, int64_t num_experts, const int64_t* route_indices, const float* route_weights,
+    int64_t top_k, const uint64_t* shared_ptrs, const uint16_t* hidden_bf16, float* out, float* out_shared,
+    uint16_t* out_bf16, int* rejected, int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
+    if (!expert_table || !route_indices || !route_weights || !hidden_bf16 || !out || (shared_ptrs && !out_shared))
+        return plm::fail(-1, "null pointer");
+    char* buf = nullptr;
+    const int code = scratch_address(&buf);
+    if (code != 0) return code;
+    return device_routed_impl(expert_table, num_experts, route_indices, route_weights, top_k, shared_ptrs,
+                              Act{nullptr, hidden_bf16}, out, out_shared, out_bf16, rejected, batch, inter, hid, gsc,
+                              dsc, buf, kNoAllocScratchBytes);
 }
 
 // Used by the DeepSeek session entry points (ds_session.hip).
