@@ -12,17 +12,19 @@ resident in HBM, so the 256 MB Infinity Cache cannot serve the chosen ones.
 One step = one token (M = 1, a bf16 hidden state ~N(0, 1)) as the device
 path runs it:
 
-  1. ds_route_topk_f32 on fresh router logits ~N(0, 1): sigmoid scores,
-     8 groups of which the best 4 are kept (group score = max: no
-     correction bias), top 8, normalised, x2.5;
-  2. fp8_e4m3_block_moe_device_routed_bf16x_f32: the plan of the chosen
-     experts, gate/up + SiLU for the 8 chosen experts and the shared expert
-     in one launch, down + route-weighted sum + the shared expert + the bf16
-     output in another.
+fp8_e4m3_block_moe_from_logits_bf16x_f32 on fresh router logits ~N(0, 1),
+three launches:
+
+  1. routing (sigmoid scores, 8 groups of which the best 4 are kept, group
+     score = max: no correction bias, top 8, normalised, x2.5; the choices
+     of ds_route_topk_f32) and the plan of the chosen experts;
+  2. gate/up + SiLU for the 8 chosen experts and the shared expert;
+  3. down + route-weighted sum + the shared expert + the bf16 output.
 
 The roofline is taken over the MoE layer's own launches (plan, gate/up,
-down): the same steps with the router's outputs computed beforehand, timed
-in a separate region.  The line also carries "m8": the speculative / MTP
+down): fp8_e4m3_block_moe_device_routed_bf16x_f32 on the router outputs the
+timed steps wrote, timed in a separate region.  The same steps as two calls
+(ds_route_topk_f32, then the device-routed MoE) are timed too.  The line also carries "m8": the speculative / MTP
 verifier batch, M = 8 bf16 activation rows, on the 7168 x 16384 output
 projection (each weight byte read once per batch), and "verifier": every
 DeepSeek-V3 projection shape of that batch at M = 1 and M = 8.
@@ -215,7 +217,19 @@ class MoEStep:
         if code != 0:
             raise RuntimeError(f"fp8_e4m3_block_moe_device_routed_bf16x_f32 failed with code {code}")
 
+    def fused(self, i):
+        code = self.lib.fp8_e4m3_block_moe_from_logits_bf16x_f32(
+            self._at(self.logits, i, "logits"), None, N_GROUPS, TOPK_GROUPS, 0, ROUTE_SCALE, _vp(self.pool.table),
+            N_ROUTED, TOP_K, ctypes.cast(self.pool.shared, ctypes.c_void_p), self._at(self.x, i, "x"), _vp(self.y),
+            _vp(self.ys), _vp(self.ybf), self._at(self.idx, i, "idx"), self._at(self.w, i, "w"), _vp(self.rejected),
+            1, INTER, HID, math.ceil(HID / 128), math.ceil(INTER / 128))
+        if code != 0:
+            raise RuntimeError(f"fp8_e4m3_block_moe_from_logits_bf16x_f32 failed with code {code}")
+
     def step(self, i):
+        self.fused(i)
+
+    def two_calls(self, i):
         self.route(i)
         self.moe(i)
 
@@ -237,8 +251,10 @@ def bench_moe_layer(torch, lib, timer, steps, warmup):
     ms_moe = timer.run([lambda i=i: st.moe(warmup + i) for i in range(steps)])
     chosen = st.idx[warmup:].cpu()
     distinct = len(set(chosen.reshape(-1).tolist()))
+    # the same steps as two calls: the router, then the device-routed MoE
+    ms_two = timer.run([lambda i=i: st.two_calls(warmup + i) for i in range(steps)])
     return {"pool": pool, "step": st, "ms_per_step": ms_steps / steps, "ms_per_moe": ms_moe / steps,
-            "distinct_experts": distinct}
+            "ms_per_two_calls": ms_two / steps, "distinct_experts": distinct}
 
 
 # --------------------------------------------------------------------------- verifier batch (FP8 projections)
@@ -518,6 +534,7 @@ def main_line(args):
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
         "us_per_step": round(1e3 * ms, 3),
+        "us_per_step_router_then_moe": round(1e3 * r["ms_per_two_calls"], 3),
         "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
         "higher_is_better": True,
         "scaling": "weak",
@@ -527,8 +544,8 @@ def main_line(args):
         "config": {
             "workload": "DeepSeek-V3 MoE layer decode, M=1: hidden 7168, 256 routed + 1 shared expert resident "
                         "(11.3 GB), moe_inter 2048, sigmoid routing (8 groups keep 4, top 8, x2.5) on fresh logits "
-                        "per token, SwiGLU, bf16 output; step = ds_route_topk_f32 + "
-                        "fp8_e4m3_block_moe_device_routed_bf16x_f32",
+                        "per token, SwiGLU, bf16 output; step = fp8_e4m3_block_moe_from_logits_bf16x_f32 "
+                        "(route + plan, gate/up, down)",
             "bytes_per_step": moe_step_bytes(1),
             "distinct_experts_in_timed_steps": r["distinct_experts"],
         },
@@ -1239,7 +1256,8 @@ def pack_transfer(torch):
 
 
 def pmc_probe(args):
-    """Counter calibration workload: 10 default steps (router + MoE layer),
+    """Counter calibration workload: bench_moe_layer with 2 warm-up and 10
+    timed steps (12 fused steps, 10 MoE-only calls, 10 router + MoE pairs),
     then 3 copies of a 256 MiB fp32 buffer (256 MiB read + 256 MiB written
     per copy).  The copy's FETCH_SIZE / WRITE_SIZE readings give the factor
     that turns the counters into bytes."""
@@ -1257,7 +1275,7 @@ def pmc_probe(args):
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print("pmc probe done: 12 + 10 + 10 MoE layer steps, 3 copies of 268435456 bytes", flush=True)
+    print("pmc probe done: 12 fused steps, 10 + 10 MoE layer calls, 3 copies of 268435456 bytes", flush=True)
 
 
 def main(argv=None):

@@ -509,6 +509,26 @@ int fp8_e4m3_block_moe_device_routed_bf16x_f32(const uint64_t* expert_table, int
                                                uint16_t* out_bf16, int* rejected, int64_t batch,
                                                int64_t intermediate_rows, int64_t hidden_dim,
                                                int64_t gate_scale_cols, int64_t down_scale_cols);
+/* New export: one DeepSeek-V3 MoE layer from the router's logits, the work
+ * of run_fp8_router followed by run_fp8_moe (src/pcketlm/core/runtime/
+ * fp8_source.py:1500-1566, 1569-1884) with no host round trip: the routing
+ * of ds_route_topk_f32 (logits fp32 [batch, num_experts], bias or NULL,
+ * n_groups / topk_groups / scoring / route_scale as there) and the plan of
+ * fp8_e4m3_block_moe_device_routed_bf16x_f32 run as one launch, then the
+ * same gate/up and down launches.  out_indices int64 [batch, top_k] and
+ * out_weights fp32 [batch, top_k] receive the router's choices and weights
+ * (both NULL to skip).  Results equal ds_route_topk_f32 followed by
+ * fp8_e4m3_block_moe_device_routed_bf16x_f32, bit for bit.  Codes -1 null,
+ * -2 bad dims (as both), -3 workspace. */
+int fp8_e4m3_block_moe_from_logits_bf16x_f32(const float* router_logits, const float* router_bias, int64_t n_groups,
+                                             int64_t topk_groups, int scoring, float route_scale,
+                                             const uint64_t* expert_table, int64_t num_experts, int64_t top_k,
+                                             const uint64_t* shared_ptrs, const uint16_t* hidden_bf16, float* out,
+                                             float* out_shared, uint16_t* out_bf16, int64_t* out_indices,
+                                             float* out_weights, int* rejected, int64_t batch,
+                                             int64_t intermediate_rows, int64_t hidden_dim, int64_t gate_scale_cols,
+                                             int64_t down_scale_cols);
+
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): fp8_e4m3_block_moe_device_routed_bf16x_f32 with its

@@ -88,6 +88,8 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "kv_dense_layer_decode_u16_ext_packed_rows8": (_i32, [_vp, _i64] + [_vp] * 16 + [_i64] * 4 + [_f32, _f32]),
     "fp8_e4m3_block_moe_device_routed_f32": (_i32, [_vp, _i64, _vp, _vp, _i64] + [_vp] * 6 + [_i64] * 5),
     "fp8_e4m3_block_moe_device_routed_bf16x_f32": (_i32, [_vp, _i64, _vp, _vp, _i64] + [_vp] * 6 + [_i64] * 5),
+    "fp8_e4m3_block_moe_from_logits_bf16x_f32": (_i32, [_vp, _vp, _i64, _i64, _i32, _f32, _vp, _i64, _i64] + [_vp] * 8
+                                                 + [_i64] * 5),
     "fp8_e4m3_block_moe_device_routed_bf16x_f32_noalloc": (_i32, [_vp, _i64, _vp, _vp, _i64] + [_vp] * 6 + [_i64] * 5),
     "fp8_e4m3_block_mlp_many_row_weighted_bf16x_f32": (_i32, [_vp] * 9 + [_i64] * 6),
     "fp8_e4m3_block_mlp_many_pair_weighted_bf16x_f32": (_i32, [_vp] * 11 + [_i64] * 7),

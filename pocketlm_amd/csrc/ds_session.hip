@@ -8,6 +8,7 @@
 #include <vector>
 
 #include "common.h"
+#include "route.h"
 
 int plm_weighted_moe_fp8(const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp,
                          const uint64_t* dp, const uint64_t* dsp, const float* hidden, const float* route,
@@ -100,210 +101,19 @@ __global__ __launch_bounds__(256) void softmax_router_kernel(const uint16_t* __r
     *status = 0;
 }
 
-__device__ __forceinline__ float bf16_round(float v) {
-    // float -> bfloat16 as torch computes it here: round to nearest even,
-    // every NaN -> 0xFFFF.
-    const uint32_t b = __float_as_uint(v);
-    if ((b & 0x7FFFFFFFu) > 0x7F800000u) return __uint_as_float(0xFFFF0000u);
-    return __uint_as_float(((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16) << 16);
-}
-
-// DeepSeek-V3 routing of one token row per workgroup.  Ties between exactly
-// equal scores select the lower expert / group index.
-__global__ __launch_bounds__(256) void ds_route_kernel(const float* __restrict__ logits, const float* __restrict__ bias,
-                                                       int64_t experts, int64_t top_k, int64_t n_groups,
-                                                       int64_t topk_groups, int scoring, float route_scale,
-                                                       int64_t* __restrict__ out_idx, float* __restrict__ out_w) {
-    extern __shared__ float4 sh4[];  // 16-byte aligned: choice is read four values at a time
-    float* score = reinterpret_cast<float*>(sh4);  // [experts]
-    float* choice = score + experts;                // [experts]
-    const float* lrow = logits + static_cast<int64_t>(blockIdx.x) * experts;
-    if (scoring == 1) {
-        // softmax in fp32
-        if (threadIdx.x == 0) {
-            float mx = lrow[0];
-            for (int64_t e = 1; e < experts; ++e) mx = lrow[e] > mx ? lrow[e] : mx;
-            float den = 0.0f;
-            for (int64_t e = 0; e < experts; ++e) {
-                score[e] = expf(lrow[e] - mx);
-                den += score[e];
-            }
-            for (int64_t e = 0; e < experts; ++e) score[e] = score[e] / den;
-        }
-        __syncthreads();
-    } else {
-        for (int64_t e = threadIdx.x; e < experts; e += blockDim.x) score[e] = 1.0f / (1.0f + expf(-lrow[e]));
-        __syncthreads();
-    }
-    for (int64_t e = threadIdx.x; e < experts; e += blockDim.x) choice[e] = bias ? score[e] + bias[e] : score[e];
-    __shared__ float gscore[64];
-    __shared__ int keep[64];
-    __shared__ uint32_t taken[128];  // one bit per expert (at most 4096)
-    __shared__ int red_first[4], red_e[4];
-    __shared__ float red_v[4];
-    for (int t = threadIdx.x; t < 128; t += blockDim.x) taken[t] = 0u;
-    __syncthreads();
-    const float ninf = -__builtin_inff();
-    if (n_groups > 1) {
-        // group scores, one thread per group: max, or the sum of the two
-        // largest when a bias is present (the same scan as a sort's top 2)
-        const int64_t gsz = experts / n_groups;
-        if (threadIdx.x < n_groups) {
-            const int64_t g = threadIdx.x;
-            float b1 = ninf, b2 = ninf;
-            for (int64_t j = 0; j < gsz; ++j) {
-                const float v = choice[g * gsz + j];
-                if (v > b1) {
-                    b2 = b1;
-                    b1 = v;
-                } else if (v > b2) {
-                    b2 = v;
-                }
-            }
-            gscore[g] = bias ? b1 + b2 : b1;
-            keep[g] = 0;
-        }
-        __syncthreads();
-        const int64_t kg = topk_groups < 1 ? 1 : (topk_groups > n_groups ? n_groups : topk_groups);
-        bool gnan = false;
-        for (int64_t g = 0; g < n_groups; ++g) gnan = gnan || gscore[g] != gscore[g];
-        if (!gnan) {
-            // without NaNs the rounds keep the groups of rank < kg (a larger
-            // score, or an equal one with a lower index, ranks first)
-            if (threadIdx.x < n_groups) {
-                const int64_t g = threadIdx.x;
-                int64_t r = 0;
-                for (int64_t h = 0; h < n_groups; ++h) r += gscore[h] > gscore[g] || (gscore[h] == gscore[g] && h < g);
-                keep[g] = r < kg;
-            }
-        } else if (threadIdx.x == 0) {
-            for (int64_t i = 0; i < kg; ++i) {
-                int64_t best = -1;
-                for (int64_t g = 0; g < n_groups; ++g)
-                    if (!keep[g] && (best < 0 || gscore[g] > gscore[best])) best = g;
-                keep[best] = 1;
-            }
-        }
-        __syncthreads();
-        for (int64_t e = threadIdx.x; e < experts; e += blockDim.x)
-            if (!keep[e / gsz]) choice[e] = ninf;
-        __syncthreads();
-    }
-    // Top-k as k rounds of a block-wide arg max over the experts not taken.
-    // A scan in expert order keeps the first of equal values and never moves
-    // off a NaN it starts from, nor onto one: so a round picks the first free
-    // expert when its choice is NaN, else the largest non-NaN choice, the
-    // lowest id among equals.
-    const int64_t k = top_k < 1 ? 1 : (top_k > experts ? experts : top_k);
-    int64_t* idx = out_idx + static_cast<int64_t>(blockIdx.x) * top_k;
-    float* w = out_w + static_cast<int64_t>(blockIdx.x) * top_k;
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    float sum = 0.0f;  // thread 0
-    __shared__ int any_nan;
-    __shared__ float pick_w[1024];  // the ranked picks' scores (at most 1024 experts there)
-    __shared__ float pick_denom;
-    if (threadIdx.x == 0) any_nan = 0;
-    __syncthreads();
-    for (int64_t e = threadIdx.x; e < experts; e += blockDim.x)
-        if (choice[e] != choice[e]) any_nan = 1;
-    __syncthreads();
-    const bool ranked = !any_nan && experts <= 1024;
-    if (ranked) {
-        // Without NaNs the rounds pick the experts in the order of their rank
-        // (how many experts beat them: a larger choice, or an equal one with
-        // a lower id), so one pass finds all k.
-        const int n = static_cast<int>(experts);
-        for (int e = threadIdx.x; e < n; e += blockDim.x) {
-            const float c = choice[e];
-            int r = 0;
-            int j = 0;
-            if ((n & 3) == 0) {  // choice is then 16-byte aligned
-                const float4* c4 = reinterpret_cast<const float4*>(choice);
-#pragma unroll 4
-                for (; j < n; j += 4) {
-                    const float4 q = c4[j >> 2];
-                    r += (q.x > c) || (q.x == c && j < e);
-                    r += (q.y > c) || (q.y == c && j + 1 < e);
-                    r += (q.z > c) || (q.z == c && j + 2 < e);
-                    r += (q.w > c) || (q.w == c && j + 3 < e);
-                }
-            }
-            for (; j < n; ++j) {
-                const float cj = choice[j];
-                r += (cj > c) || (cj == c && j < e);
-            }
-            if (r < k) {
-                idx[r] = e;
-                pick_w[r] = score[e];
-            }
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            for (int64_t i = 0; i < k; ++i) sum += pick_w[i];  // in pick order, as the rounds add
-            pick_denom = sum > 1e-12f ? sum : 1e-12f;
-        }
-        __syncthreads();
-        for (int64_t i = threadIdx.x; i < k; i += blockDim.x) {
-            const float v = scoring == 0 ? pick_w[i] / pick_denom : pick_w[i];
-            w[i] = bf16_round(v * route_scale);
-        }
-        return;
-    }
-    for (int64_t i = 0; i < (ranked ? 0 : k); ++i) {
-        int first = 0x7FFFFFFF;
-        int be = -1;
-        float bv = ninf;
-        for (int64_t e = threadIdx.x; e < experts; e += blockDim.x) {
-            if ((taken[e >> 5] >> (e & 31)) & 1u) continue;
-            if (first == 0x7FFFFFFF) first = static_cast<int>(e);
-            const float v = choice[e];
-            if (v == v && (be < 0 || v > bv)) {
-                bv = v;
-                be = static_cast<int>(e);
-            }
-        }
-        for (int off = 32; off > 0; off >>= 1) {
-            const int of = __shfl_xor(first, off);
-            const float ov = __shfl_xor(bv, off);
-            const int oe = __shfl_xor(be, off);
-            first = of < first ? of : first;
-            if (oe >= 0 && (be < 0 || ov > bv || (ov == bv && oe < be))) {
-                bv = ov;
-                be = oe;
-            }
-        }
-        if (lane == 0) {
-            red_first[wave] = first;
-            red_e[wave] = be;
-            red_v[wave] = bv;
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            for (int t = 1; t < static_cast<int>(blockDim.x >> 6); ++t) {
-                first = red_first[t] < first ? red_first[t] : first;
-                const int oe = red_e[t];
-                const float ov = red_v[t];
-                if (oe >= 0 && (be < 0 || ov > bv || (ov == bv && oe < be))) {
-                    bv = ov;
-                    be = oe;
-                }
-            }
-            const float cf = choice[first];
-            const int pick = (cf != cf || be < 0) ? first : be;
-            idx[i] = pick;
-            w[i] = score[pick];
-            sum += score[pick];
-            taken[pick >> 5] |= 1u << (pick & 31);
-        }
-        __syncthreads();
-    }
-    if (threadIdx.x != 0) return;
-    const float denom = sum > 1e-12f ? sum : 1e-12f;
-    for (int64_t i = 0; i < k; ++i) {
-        const float v = scoring == 0 ? w[i] / denom : w[i];
-        w[i] = bf16_round(v * route_scale);
-    }
+// DeepSeek-V3 routing, one token row per one-wave workgroup (route.h).
+template <int J>
+__global__ __launch_bounds__(64) void ds_route_kernel(const float* __restrict__ logits, const float* __restrict__ bias,
+                                                      int experts, int top_k, int n_groups, int topk_groups,
+                                                      int scoring, float route_scale, int64_t* __restrict__ out_idx,
+                                                      float* __restrict__ out_w) {
+    extern __shared__ float4 sh4[];  // 16-byte aligned
+    float* choice = reinterpret_cast<float*>(sh4);  // [experts]
+    float* score = choice + ((experts + 3) & ~3);   // [experts]
+    __shared__ RouteWave rw;
+    const int64_t row = blockIdx.x;
+    plm_route_wave<J>(logits + row * experts, bias, experts, top_k, n_groups, topk_groups, scoring, route_scale, score,
+                      choice, rw, out_idx + row * top_k, out_w + row * top_k);
 }
 
 }  // namespace
@@ -530,9 +340,11 @@ PLM_EXPORT int ds_route_topk_f32(const float* logits, const float* bias, int64_t
     if (batch <= 0 || num_experts <= 0 || top_k <= 0 || top_k > num_experts || n_groups <= 0 || n_groups > 64 ||
         num_experts % n_groups != 0 || num_experts > 4096 || (scoring != 0 && scoring != 1))
         return plm::fail(2, "bad dimensions");
-    const size_t shmem = static_cast<size_t>(2 * num_experts) * sizeof(float);
-    hipLaunchKernelGGL(ds_route_kernel, dim3(static_cast<unsigned>(batch)), dim3(256), shmem, plm::current_stream(),
-                       logits, bias, num_experts, top_k, n_groups, topk_groups, scoring, route_scale, out_indices,
-                       out_weights);
+    const size_t shmem = static_cast<size_t>(2 * ((num_experts + 3) & ~int64_t(3))) * sizeof(float);
+    const int j = plm_route_j(static_cast<int>(num_experts));
+    auto kern = j == 4 ? ds_route_kernel<4> : (j == 16 ? ds_route_kernel<16> : ds_route_kernel<64>);
+    hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(batch)), dim3(64), shmem, plm::current_stream(), logits, bias,
+                       static_cast<int>(num_experts), static_cast<int>(top_k), static_cast<int>(n_groups),
+                       static_cast<int>(topk_groups), scoring, route_scale, out_indices, out_weights);
     return plm::check_launch("ds route kernel");
 }

@@ -38,6 +38,7 @@
 #include <vector>
 
 #include "common.h"
+#include "route.h"
 
 namespace {
 
@@ -149,8 +150,87 @@ __device__ __forceinline__ void load_x16(const float* p, float* x) {
     }
 }
 
-// 16 activations of row m at column col, from the fp32 or (XB) the bf16
-// copy; both give the same fp32 values.
+static_assert(kMaxGroups == 64, "the plan maps one lane of the first wave to each group");
+struct PlanShared {
+    int64_t key[64];
+    float kw[64];
+    int first[64];
+    int64_t sel[kMaxGroups];
+};
+
+// Run by a whole workgroup (every thread calls it: it synchronises the
+// workgroup); the first wave does the work.
+__device__ void plan_from_choices(const uint64_t* __restrict__ table, int64_t num_experts, const int64_t* idx,
+                                  const float* wts, int batch, int top_k, MoePlan* __restrict__ plan,
+                                  int* __restrict__ rejected, PlanShared& ps) {
+    const int lane = threadIdx.x;
+    const bool w0 = lane < 64;
+    const int n = batch * top_k;
+    int64_t e = -1;
+    uint64_t addr[kPlanRoles] = {0, 0, 0, 0, 0, 0};
+    bool aligned = true, bad = false;
+    if (w0) {
+        // every load is issued before the first use: two memory round trips
+        e = lane < n ? idx[lane] : -1;
+        const float wj = lane < n ? wts[lane] : 0.0f;
+        const bool in_range = e >= 0 && e < num_experts;
+#pragma unroll
+        for (int r = 0; r < kPlanRoles; ++r) addr[r] = in_range ? table[r * num_experts + e] : 0;
+#pragma unroll
+        for (int r = 0; r < kPlanRoles; ++r) aligned = aligned && (addr[r] & ((r & 1) ? 3u : 15u)) == 0;
+        bad = lane < n && !(in_range && aligned);
+        if (!in_range) e = -1;
+        ps.key[lane] = e;
+        ps.kw[lane] = wj;
+    }
+    __syncthreads();
+    int f = 0;
+    if (w0) {
+        f = e >= 0;
+        if (f)
+            for (int i = 0; i < lane; ++i) f = f && ps.key[i] != e;
+        ps.first[lane] = f;
+    }
+    __syncthreads();
+    int count = 0;
+    if (w0) {
+        int rank = 0;
+        for (int i = 0; i < n; ++i) {
+            const int fi = ps.first[i];
+            count += fi;
+            rank += fi && ps.key[i] < e;
+        }
+        if (f) {
+            ps.sel[rank] = e;
+#pragma unroll
+            for (int r = 0; r < kPlanRoles; ++r) plan->tab[r][rank] = aligned ? addr[r] : 0;
+        }
+        if (lane >= count) {
+#pragma unroll
+            for (int r = 0; r < kPlanRoles; ++r) plan->tab[r][lane] = 0;
+        }
+    }
+    __syncthreads();
+    if (w0) {
+        for (int t = lane; t < kMaxGroups * batch; t += 64) {
+            const int g = t / batch;
+            const int m = t - g * batch;
+            float w = 0.0f;
+            if (g < count) {
+                const int64_t want = ps.sel[g];
+                for (int kk = top_k - 1; kk >= 0; --kk)  // the first of repeated choices wins
+                    if (ps.key[m * top_k + kk] == want) w = ps.kw[m * top_k + kk];
+            }
+            plan->route[t] = w;
+        }
+        const unsigned long long badmask = __ballot(bad);
+        if (lane == 0) {
+            plan->count = count;
+            if (rejected != nullptr) *rejected = __popcll(badmask);
+        }
+    }
+}
+
 // One wave (the whole workgroup) writes the plan of the router's
 // n = batch * top_k choices (n <= 64) as run_fp8_moe builds it on the host
 // (fp8_source.py:1600, 1653-1716): the distinct in-range experts in
@@ -161,71 +241,132 @@ __device__ __forceinline__ void load_x16(const float* p, float* x) {
 // weight addresses are not 16-byte aligned (scales: 4) keeps its group but
 // gets null addresses, so it contributes nothing.  Both are counted in
 // *rejected.
-static_assert(kMaxGroups == 64, "moe_plan_kernel maps one lane to each group");
 __global__ __launch_bounds__(64) void moe_plan_kernel(const uint64_t* __restrict__ table, int64_t num_experts,
                                                       const int64_t* __restrict__ idx,
                                                       const float* __restrict__ wts, int batch, int top_k,
                                                       MoePlan* __restrict__ plan, int* __restrict__ rejected) {
-    __shared__ int64_t key[64];
-    __shared__ float kw[64];
-    __shared__ int first[64];
-    __shared__ int64_t sel[kMaxGroups];
-    const int lane = threadIdx.x;
-    const int n = batch * top_k;
-    // every load is issued before the first use: two memory round trips
-    int64_t e = lane < n ? idx[lane] : -1;
-    const float wj = lane < n ? wts[lane] : 0.0f;
-    const bool in_range = e >= 0 && e < num_experts;
-    uint64_t addr[kPlanRoles];
+    __shared__ PlanShared ps;
+    plan_from_choices(table, num_experts, idx, wts, batch, top_k, plan, rejected, ps);
+}
+
+// The router and the plan in one launch: DeepSeek-V3 routing of every row's
+// logits (route.h, the same choices and weights as ds_route_topk_f32), one
+// wave per row, then the plan of those choices.  The choices and weights
+// are also written to idx_out / w_out when those are not null.
+//
+// Up to 256 experts (4 per lane) the plan is built from registers: wave 0
+// loads its lanes' rows of the expert table while the logits load, and the
+// routing waves leave in LDS which of each lane's experts every row picked
+// and with what weight.  The experts picked by any row, in ascending order,
+// are then numbered by a prefix count over the lanes (the lanes hold
+// ascending experts).  Wider tables go through plan_from_choices.
+template <int J>
+__global__ __launch_bounds__(512) void moe_route_plan_kernel(const float* __restrict__ logits,
+                                                            const float* __restrict__ bias, int experts, int batch,
+                                                            int top_k, int n_groups, int topk_groups, int scoring,
+                                                            float route_scale, const uint64_t* __restrict__ table,
+                                                            int64_t* idx_out, float* w_out,
+                                                            MoePlan* __restrict__ plan, int* __restrict__ rejected) {
+    extern __shared__ float4 sh4[];
+    const int waves = static_cast<int>(blockDim.x >> 6);
+    const int wave = static_cast<int>(threadIdx.x >> 6);
+    const int lane = static_cast<int>(threadIdx.x & 63);
+    const int e4 = (experts + 3) & ~3;
+    float* route_lds = reinterpret_cast<float*>(sh4);  // [waves][2][e4]
+    float* choice = route_lds + 2 * e4 * wave;
+    float* score = choice + e4;
+    __shared__ RouteWave rw[8];
+    if constexpr (J == 4) {
+        float* wdense = route_lds + 2 * e4 * waves;  // [batch][e4]: each row's weights, 0 where not picked
+        __shared__ uint64_t picked[kMaxM][64];       // [row][lane]: bits of the lane's picked experts
+        uint64_t tab[kPlanRoles][4];
+        if (wave == 0) {
 #pragma unroll
-    for (int r = 0; r < kPlanRoles; ++r) addr[r] = in_range ? table[r * num_experts + e] : 0;
-    bool aligned = true;
+            for (int r = 0; r < kPlanRoles; ++r)
 #pragma unroll
-    for (int r = 0; r < kPlanRoles; ++r) aligned = aligned && (addr[r] & ((r & 1) ? 3u : 15u)) == 0;
-    const bool bad = lane < n && !(in_range && aligned);
-    if (!in_range) e = -1;
-    key[lane] = e;
-    kw[lane] = wj;
-    __syncthreads();
-    int f = e >= 0;
-    for (int i = 0; i < lane; ++i) f = f && key[i] != e;
-    first[lane] = f;
-    __syncthreads();
-    int count = 0;
-    int rank = 0;
-    for (int i = 0; i < n; ++i) {
-        const int fi = first[i];
-        count += fi;
-        rank += fi && key[i] < e;
-    }
-    if (f) {
-        sel[rank] = e;
-#pragma unroll
-        for (int r = 0; r < kPlanRoles; ++r) plan->tab[r][rank] = aligned ? addr[r] : 0;
-    }
-    if (lane >= count) {
-#pragma unroll
-        for (int r = 0; r < kPlanRoles; ++r) plan->tab[r][lane] = 0;
-    }
-    __syncthreads();
-    for (int t = lane; t < kMaxGroups * batch; t += 64) {
-        const int g = t / batch;
-        const int m = t - g * batch;
-        float w = 0.0f;
-        if (g < count) {
-            const int64_t want = sel[g];
-            for (int kk = top_k - 1; kk >= 0; --kk)  // the first of repeated choices wins
-                if (key[m * top_k + kk] == want) w = kw[m * top_k + kk];
+                for (int j = 0; j < 4; ++j) {
+                    const int e = 4 * lane + j;
+                    tab[r][j] = e < experts ? table[static_cast<int64_t>(r) * experts + e] : 0;
+                }
         }
-        plan->route[t] = w;
-    }
-    const unsigned long long badmask = __ballot(bad);
-    if (lane == 0) {
-        plan->count = count;
-        if (rejected != nullptr) *rejected = __popcll(badmask);
+        for (int m = wave; m < batch; m += waves)
+            plm_route_wave<4>(logits + static_cast<int64_t>(m) * experts, bias, experts, top_k, n_groups, topk_groups,
+                              scoring, route_scale, score, choice, rw[wave],
+                              idx_out != nullptr ? idx_out + static_cast<int64_t>(m) * top_k : nullptr,
+                              idx_out != nullptr ? w_out + static_cast<int64_t>(m) * top_k : nullptr, picked[m],
+                              wdense + m * e4);
+        __syncthreads();
+        if (wave != 0) return;
+        // every row's picks and weights of this lane's experts, read at once
+        uint64_t pm[kMaxM];
+        float4 wv[kMaxM];
+        const bool owns = 4 * lane < experts;
+#pragma unroll
+        for (int m = 0; m < kMaxM; ++m) {
+            pm[m] = m < batch ? picked[m][lane] : 0;
+            wv[m] = m < batch && owns ? *reinterpret_cast<const float4*>(wdense + m * e4 + 4 * lane)
+                                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        uint64_t u = 0;
+#pragma unroll
+        for (int m = 0; m < kMaxM; ++m) u |= pm[m];
+        const uint64_t below = (1ull << lane) - 1;
+        int rank = 0, count = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint64_t b = __ballot((u >> j) & 1ull);
+            rank += __popcll(b & below);
+            count += __popcll(b);
+        }
+        int bad = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (!((u >> j) & 1ull)) continue;
+            bool aligned = true;
+#pragma unroll
+            for (int r = 0; r < kPlanRoles; ++r) aligned = aligned && (tab[r][j] & ((r & 1) ? 3u : 15u)) == 0;
+#pragma unroll
+            for (int r = 0; r < kPlanRoles; ++r) plan->tab[r][rank] = aligned ? tab[r][j] : 0;
+#pragma unroll
+            for (int m = 0; m < kMaxM; ++m) {
+                if (m >= batch) break;
+                plan->route[rank * batch + m] = reinterpret_cast<const float*>(&wv[m])[j];
+                if (!aligned) bad += static_cast<int>((pm[m] >> j) & 1ull);
+            }
+            ++rank;
+        }
+        if (lane >= count) {
+#pragma unroll
+            for (int r = 0; r < kPlanRoles; ++r) plan->tab[r][lane] = 0;
+            for (int m = 0; m < batch; ++m) plan->route[lane * batch + m] = 0.0f;
+        }
+        int total_bad = 0;  // bad <= 4 * kMaxM
+#pragma unroll
+        for (int bit = 0; bit < 6; ++bit) total_bad += __popcll(__ballot((bad >> bit) & 1)) << bit;
+        if (lane == 0) {
+            plan->count = count;
+            if (rejected != nullptr) *rejected = total_bad;
+        }
+    } else {
+        __shared__ PlanShared ps;
+        __shared__ int64_t kidx[kMaxGroups];
+        __shared__ float kwt[kMaxGroups];
+        for (int m = wave; m < batch; m += waves)
+            plm_route_wave<J>(logits + static_cast<int64_t>(m) * experts, bias, experts, top_k, n_groups, topk_groups,
+                              scoring, route_scale, score, choice, rw[wave], kidx + m * top_k, kwt + m * top_k);
+        __syncthreads();
+        const int n = batch * top_k;
+        if (idx_out != nullptr)
+            for (int t = threadIdx.x; t < n; t += blockDim.x) {
+                idx_out[t] = kidx[t];
+                w_out[t] = kwt[t];
+            }
+        plan_from_choices(table, experts, kidx, kwt, batch, top_k, plan, rejected, ps);
     }
 }
 
+// 16 activations of row m at column col, from the fp32 or (XB) the bf16
+// copy; both give the same fp32 values.
 template <bool XB>
 __device__ __forceinline__ void load_row_x16(const RowsArgs& a, int m, int64_t col, float* x) {
     const int64_t off = static_cast<int64_t>(a.m0 + m) * a.x_stride + col;
@@ -1277,10 +1418,23 @@ int pair_weighted_impl(const uint64_t* gp, const uint64_t* gsp, const uint64_t* 
 // the bf16 tail computed by the down launch's workgroups.
 // fixed: a block the caller provides (fixed_bytes long) instead of the
 // library's workspace, for the entry point that allocates nothing.
+// Routing done in the same launch as the plan: the router's logits and
+// settings (ds_route_topk_f32's arguments).  idx / wts then receive the
+// choices and weights (when not null) instead of providing them.
+struct RouteFromLogits {
+    const float* logits;
+    const float* bias;
+    int n_groups;
+    int topk_groups;
+    int scoring;
+    float route_scale;
+};
+
 int device_routed_impl(const uint64_t* table, int64_t num_experts, const int64_t* idx, const float* wts,
                        int64_t top_k, const uint64_t* shared, Act hidden, float* out, float* out_shared,
                        uint16_t* out_bf16, int* rejected, int64_t batch, int64_t inter, int64_t hid, int64_t gsc,
-                       int64_t dsc, char* fixed = nullptr, size_t fixed_bytes = 0) {
+                       int64_t dsc, char* fixed = nullptr, size_t fixed_bytes = 0,
+                       const RouteFromLogits* route = nullptr) {
     if (num_experts <= 0 || num_experts > INT32_MAX || top_k <= 0 || batch <= 0 || batch > kMaxM ||
         batch * top_k > kMaxGroups)
         return plm::fail(-2, "bad dimensions (batch 1..%d, batch * top_k <= %d)", kMaxM, kMaxGroups);
@@ -1310,8 +1464,23 @@ int device_routed_impl(const uint64_t* table, int64_t num_experts, const int64_t
     }
     float* act = reinterpret_cast<float*>(ws);
     MoePlan* plan = reinterpret_cast<MoePlan*>(ws + act_bytes);
-    hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(64), 0, st, table, num_experts, idx, wts,
-                       static_cast<int>(batch), static_cast<int>(top_k), plan, rejected);
+    if (route != nullptr) {
+        // one wave per row while the per-wave arrays fit 32 KiB
+        const int64_t e4 = (num_experts + 3) & ~int64_t(3);
+        const int64_t per_wave = 2 * e4 * static_cast<int64_t>(sizeof(float));
+        const int waves = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(batch, 32768 / per_wave)));
+        const int j = plm_route_j(static_cast<int>(num_experts));
+        const size_t shmem =
+            static_cast<size_t>(per_wave * waves + (j == 4 ? batch * e4 * static_cast<int64_t>(sizeof(float)) : 0));
+        auto kern = j == 4 ? moe_route_plan_kernel<4> : (j == 16 ? moe_route_plan_kernel<16> : moe_route_plan_kernel<64>);
+        hipLaunchKernelGGL(kern, dim3(1), dim3(64 * waves), shmem, st, route->logits, route->bias,
+                           static_cast<int>(num_experts), static_cast<int>(batch), static_cast<int>(top_k),
+                           route->n_groups, route->topk_groups, route->scoring, route->route_scale, table,
+                           const_cast<int64_t*>(idx), const_cast<float*>(wts), plan, rejected);
+    } else {
+        hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(64), 0, st, table, num_experts, idx, wts,
+                           static_cast<int>(batch), static_cast<int>(top_k), plan, rejected);
+    }
     int code = plm::check_launch("moe plan kernel");
     if (code != 0) return code;
 
@@ -1707,6 +1876,24 @@ PLM_EXPORT int fp8_e4m3_block_moe_device_routed_bf16x_f32_noalloc(
     return device_routed_impl(expert_table, num_experts, route_indices, route_weights, top_k, shared_ptrs,
                               Act{nullptr, hidden_bf16}, out, out_shared, out_bf16, rejected, batch, inter, hid, gsc,
                               dsc, buf, kNoAllocScratchBytes);
+}
+
+PLM_EXPORT int fp8_e4m3_block_moe_from_logits_bf16x_f32(
+    const float* router_logits, const float* router_bias, int64_t n_groups, int64_t topk_groups, int scoring,
+    float route_scale, const uint64_t* expert_table, int64_t num_experts, int64_t top_k, const uint64_t* shared_ptrs,
+    const uint16_t* hidden_bf16, float* out, float* out_shared, uint16_t* out_bf16, int64_t* out_indices,
+    float* out_weights, int* rejected, int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
+    if (!router_logits || !expert_table || !hidden_bf16 || !out || (shared_ptrs && !out_shared) ||
+        ((out_indices == nullptr) != (out_weights == nullptr)))
+        return plm::fail(-1, "null pointer");
+    if (num_experts <= 0 || num_experts > 4096 || top_k <= 0 || top_k > num_experts || n_groups <= 0 ||
+        n_groups > 64 || num_experts % n_groups != 0 || (scoring != 0 && scoring != 1))
+        return plm::fail(-2, "bad routing dimensions");
+    const RouteFromLogits route = {router_logits, router_bias, static_cast<int>(n_groups),
+                                   static_cast<int>(topk_groups), scoring, route_scale};
+    return device_routed_impl(expert_table, num_experts, out_indices, out_weights, top_k, shared_ptrs,
+                              Act{nullptr, hidden_bf16}, out, out_shared, out_bf16, rejected, batch, inter, hid, gsc,
+                              dsc, nullptr, 0, &route);
 }
 
 // Used by the DeepSeek session entry points (ds_session.hip).

@@ -606,6 +606,62 @@ def fp8_e4m3_block_moe_device_routed_f32(table: FP8ExpertTable, hidden: torch.Te
     return DeviceRoutedMoE(out, out_shared, out_bf16, rejected)
 
 
+@dataclass
+class LogitsRoutedMoE(DeviceRoutedMoE):
+    """DeviceRoutedMoE plus the router's choices: indices int64 [M, k] and
+    weights fp32 [M, k] (bf16 values), as route_deepseek returns them."""
+    indices: torch.Tensor | None = None
+    weights: torch.Tensor | None = None
+
+
+def fp8_e4m3_block_moe_from_logits(table: FP8ExpertTable, hidden: torch.Tensor, router_logits: torch.Tensor,
+                                   shared=None, *, top_k: int = 8, n_groups: int = 8, topk_groups: int = 4,
+                                   scoring_func: str = "sigmoid", route_scale: float = 2.5,
+                                   bias: torch.Tensor | None = None) -> LogitsRoutedMoE:
+    """One DeepSeek-V3 MoE layer from the router's logits [M, E]: the routing
+    of route_deepseek (run_fp8_router, src/pcketlm/core/runtime/
+    fp8_source.py:1500-1566) and the plan in one launch, then the gate/up and
+    down launches of fp8_e4m3_block_moe_device_routed_f32 (run_fp8_moe,
+    1569-1884).  The same values as route_deepseek followed by that call.
+    bf16 activations only (the decode path's)."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_FP8_LINEAR", "Native FP8 logits-routed MoE")
+    if scoring_func not in ("sigmoid", "softmax"):
+        raise ValueError("scoring_func must be 'sigmoid' or 'softmax'")
+    dev = table.device
+    x = _on(hidden, dev, torch.bfloat16)
+    x = x.reshape(-1, int(x.shape[-1])).contiguous()
+    if int(x.shape[1]) != table.hid:
+        raise ValueError("hidden input size does not match FP8 MLP input size")
+    batch = int(x.shape[0])
+    lg = _on(router_logits, dev, torch.float32).reshape(batch, -1).contiguous()
+    if int(lg.shape[1]) != table.num_experts:
+        raise ValueError("router logits must have one column per expert of the table")
+    b = None if bias is None else _on(bias, dev, torch.float32).reshape(-1).contiguous()
+    k = int(top_k)
+    shared_arr = None
+    keep = []
+    if shared is not None:
+        sh = _Experts([shared], torch.zeros((1, 1)), dev, check_hidden=False)
+        if (sh.inter, sh.hid) != (table.inter, table.hid):
+            raise ValueError("the shared expert must have the routed experts' shapes")
+        keep.append(sh)
+        shared_arr = (ctypes.c_uint64 * 6)(*[int(t.data_ptr()) for t in sh.prepared[0]])
+    out = torch.empty((batch, table.hid), dtype=torch.float32, device=dev)
+    out_shared = torch.empty_like(out) if shared is not None else None
+    out_bf16 = torch.empty((batch, table.hid), dtype=torch.bfloat16, device=dev)
+    idx = torch.empty((batch, k), dtype=torch.int64, device=dev)
+    w = torch.empty((batch, k), dtype=torch.float32, device=dev)
+    rejected = torch.zeros((1,), dtype=torch.int32, device=dev)
+    with _launch(lib, dev):
+        code = lib.fp8_e4m3_block_moe_from_logits_bf16x_f32(
+            _p(lg), _p(b), int(n_groups), int(topk_groups), 0 if scoring_func == "sigmoid" else 1, float(route_scale),
+            _p(table.table), table.num_experts, k, None if shared_arr is None else ctypes.cast(shared_arr, ctypes.c_void_p),
+            _p(x), _p(out), _p(out_shared), _p(out_bf16), _p(idx), _p(w), _p(rejected), batch, table.inter, table.hid,
+            table.gsc, table.dsc)
+    _check("fp8_e4m3_block_moe_from_logits_bf16x_f32", code)
+    return LogitsRoutedMoE(out, out_shared, out_bf16, rejected, idx, w)
+
+
 def fp8_e4m3_block_mlp_many_weighted_avx512_f32(items, hidden, route_weights) -> torch.Tensor:
     """src/pcketlm/native/__init__.py:3951-4022 (same device kernel as the scalar name)."""
     return _weighted("fp8_e4m3_block_mlp_many_weighted_avx512_f32", "PCKETLM_DISABLE_NATIVE_FP8_AVX512",

@@ -236,3 +236,68 @@ def test_router_and_device_routed_moe_replay_in_a_hip_graph(nat):
         assert torch.equal(captured.shared, eager.shared), trial
         assert torch.equal(captured.output.view(torch.int16), eager.output.view(torch.int16)), trial
         assert int(captured.rejected.item()) == 0
+
+
+def _from_logits_case(nat, table, experts, shared, logits, **kw):
+    """fp8_e4m3_block_moe_from_logits equals route_deepseek followed by the
+    device-routed MoE, bit for bit, indices and weights included."""
+    x = kw.pop("x")
+    got = nat.fp8_e4m3_block_moe_from_logits(table, x, logits, shared, **kw)
+    idx, w = nat.route_deepseek(logits, weights_dtype=torch.float32, **kw)
+    want = nat.fp8_e4m3_block_moe_device_routed_f32(table, x, idx, w, shared)
+    torch.cuda.synchronize()
+    assert torch.equal(got.indices, idx)
+    assert torch.equal(got.weights, w)
+    assert torch.equal(got.routed, want.routed)
+    if shared is not None:
+        assert torch.equal(got.shared, want.shared)
+    assert torch.equal(got.output.view(torch.int16), want.output.view(torch.int16))
+    assert int(got.rejected.item()) == int(want.rejected.item())
+    return got
+
+
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_moe_from_logits_equals_router_then_device_routed(nat, m):
+    """256 resident experts (hidden 512, moe_inter 256), DeepSeek-V3 routing
+    (sigmoid, 8 groups keep 4, top 8, x2.5) with and without a correction
+    bias, softmax scoring, and flat top-8."""
+    hid, inter, n = 512, 256, 256
+    experts = {e: _expert(inter, hid, 3000 + 3 * e) for e in range(n)}
+    shared = _expert(inter, hid, 2999)
+    table = nat.FP8ExpertTable(experts, n)
+    g = torch.Generator().manual_seed(40 + m)
+    logits = torch.randn((m, n), generator=g).cuda()
+    x = _x(m, hid, 50 + m, torch.bfloat16)
+    bias = (torch.randn((n,), generator=g) * 0.1).cuda()
+    _from_logits_case(nat, table, experts, shared, logits, x=x)
+    _from_logits_case(nat, table, experts, shared, logits, x=x, bias=bias)
+    _from_logits_case(nat, table, experts, None, logits, x=x, scoring_func="softmax", top_k=4)
+    _from_logits_case(nat, table, experts, shared, logits, x=x, n_groups=1, topk_groups=1)
+
+
+def test_moe_from_logits_deepseek_shapes_and_nan_logits(nat):
+    """DeepSeek-V3 experts over 16 resident slots (2 per group); a NaN logit
+    sends that row through the rounds path of the router."""
+    experts = {e: _expert(2048, 7168, 4000 + 3 * e) for e in range(16)}
+    shared = _expert(2048, 7168, 3990)
+    table = nat.FP8ExpertTable(experts, 16)
+    g = torch.Generator().manual_seed(77)
+    logits = torch.randn((2, 16), generator=g)
+    logits[1, 5] = float("nan")
+    x = _x(2, 7168, 78, torch.bfloat16)
+    _from_logits_case(nat, table, experts, shared, logits.cuda(), x=x)
+
+
+@pytest.mark.parametrize("n,resident", [(384, 48), (2048, 16)])
+def test_moe_from_logits_wide_tables(nat, n, resident):
+    """Tables wider than 256 experts (no table copy in LDS; 16 and 64 experts
+    per router lane), most ids without weights (null addresses: those picks
+    contribute nothing), batches of 1 and 6 rows."""
+    hid, inter = 256, 128
+    experts = {e: _expert(inter, hid, 5000 + 3 * e) for e in range(0, n, n // resident)}
+    table = nat.FP8ExpertTable(experts, n)
+    g = torch.Generator().manual_seed(n)
+    for m in (1, 6):
+        logits = torch.randn((m, n), generator=g).cuda()
+        x = _x(m, hid, 60 + m, torch.bfloat16)
+        _from_logits_case(nat, table, experts, None, logits, x=x)

@@ -265,6 +265,33 @@ def test_deepseek_route_kat_and_random(nat, golden, oracle_mod):
         assert np.allclose(host(w.float()), ow, rtol=8e-3)
 
 
+@pytest.mark.parametrize("experts,groups,kept,top_k", [
+    (16, 8, 4, 8),       # two experts per group
+    (90, 3, 2, 6),       # a count that is not a multiple of 4 (scalar loads)
+    (160, 1, 1, 6),      # DeepSeek-V2 width, flat top-k
+    (384, 8, 4, 8),      # 16 experts per lane
+    (1024, 16, 8, 12),
+    (2048, 8, 4, 8),     # 64 experts per lane
+    (4096, 64, 16, 32),
+])
+def test_deepseek_route_widths_against_oracle(nat, oracle_mod, experts, groups, kept, top_k):
+    """Every lane width of the one-wave router (4, 16, 64 experts per lane),
+    with and without a correction bias, sigmoid and softmax scoring, batches
+    of 1 and 5 rows: the oracle's indices, its weights to bf16 rounding."""
+    rng = np.random.default_rng(experts)
+    for rows in (1, 5):
+        logits = rng.standard_normal((rows, experts)).astype(np.float32)
+        bias = (rng.standard_normal(experts) * 0.1).astype(np.float32)
+        for b in (None, bias):
+            for scoring in ("sigmoid", "softmax"):
+                idx, w = nat.route_deepseek(dev(logits), top_k=top_k, n_groups=groups, topk_groups=kept,
+                                            scoring_func=scoring, bias=None if b is None else dev(b))
+                oi, ow = oracle_mod.deepseek_route(logits, top_k=top_k, n_groups=groups, topk_groups=kept, bias=b,
+                                                   scoring=scoring)
+                assert host(idx).tolist() == oi.tolist(), (rows, b is None, scoring)
+                assert np.allclose(host(w.float()), ow, rtol=8e-3), (rows, b is None, scoring)
+
+
 def _route_in_order(logits, top_k, n_groups, topk_groups, bias, scale):
     """The routing as one in-order scan per step (strict > keeps the first
     of equal values; a NaN is kept only when it is where a scan starts)."""
