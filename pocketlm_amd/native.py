@@ -27,7 +27,6 @@ from __future__ import annotations
 
 import ctypes
 import os
-from collections import OrderedDict
 from contextlib import contextmanager
 from dataclasses import dataclass
 from pathlib import Path
@@ -802,11 +801,68 @@ def q4_moe_selected_forward_u16(hidden: torch.Tensor, experts, route_weights: to
 
 
 # --------------------------------------------------------------------------- row8
-# Pack cache: src/pcketlm/native/__init__.py:2108-2193.
 
-_PACKED_GEMV_CACHE: "OrderedDict[str, torch.Tensor]" = OrderedDict()
-_PACKED_GEMV_CACHE_BYTES = 0
-_PACKED_GEMV_CACHE_STATS = {"hits": 0, "misses": 0, "stores": 0, "evictions": 0}
+
+class _Row8PackCache:
+    """Packed row8 weights kept resident in HBM between calls, keyed by the
+    caller's cache key (the reference's cached_pack_weight_rows8,
+    src/pcketlm/native/__init__.py:2108-2193: same switches, budget and
+    statistics).  The budget, PCKETLM_PACKED_GEMV_CACHE_MB, counts device
+    bytes and is read on every call; when a new pack does not fit, the
+    entries used longest ago go first.  A pack larger than the whole budget
+    is returned without being kept."""
+
+    COUNTERS = ("hits", "misses", "stores", "evictions")
+
+    def __init__(self) -> None:
+        self._entries: dict[str, tuple[torch.Tensor, int, int]] = {}  # key -> (pack, bytes, last use)
+        self._clock = 0
+        self._bytes = 0
+        self.counts = dict.fromkeys(self.COUNTERS, 0)
+
+    @staticmethod
+    def budget() -> int:
+        text = os.environ.get("PCKETLM_PACKED_GEMV_CACHE_MB", "").strip()
+        try:
+            return max(0, int(text)) << 20 if text else 0
+        except ValueError:
+            return 0
+
+    def clear(self) -> None:
+        self._entries = {}
+        self._bytes = 0
+        self.counts = dict.fromkeys(self.COUNTERS, 0)
+
+    def stats(self) -> dict[str, int | float]:
+        return {**self.counts, "resident_count": len(self._entries), "resident_bytes": self._bytes,
+                "resident_mb": round(self._bytes / (1 << 20), 4), "budget_bytes": self.budget()}
+
+    def get(self, key: str, make) -> torch.Tensor:
+        self._clock += 1
+        limit = 0 if _flag("PCKETLM_DISABLE_PACKED_GEMV_CACHE") else self.budget()
+        found = self._entries.get(key) if limit > 0 else None
+        if found is not None:
+            self._entries[key] = (found[0], found[1], self._clock)
+            self.counts["hits"] += 1
+            return found[0]
+        self.counts["misses"] += 1
+        pack = make()
+        if limit <= 0:
+            return pack
+        size = pack.numel() * pack.element_size()
+        if size > limit:
+            return pack
+        while self._entries and self._bytes + size > limit:
+            oldest = min(self._entries, key=lambda k: self._entries[k][2])
+            self._bytes -= self._entries.pop(oldest)[1]
+            self.counts["evictions"] += 1
+        self._entries[key] = (pack, size, self._clock)
+        self._bytes += size
+        self.counts["stores"] += 1
+        return pack
+
+
+_ROW8_PACKS = _Row8PackCache()
 
 
 def _u16_storage_dtype_code(dtype: torch.dtype) -> int:
@@ -817,37 +873,14 @@ def _u16_storage_dtype_code(dtype: torch.dtype) -> int:
     raise TypeError("native KV kernels require torch.float16 or torch.bfloat16 tensors")
 
 
-def _packed_gemv_cache_disabled() -> bool:
-    return _flag("PCKETLM_DISABLE_PACKED_GEMV_CACHE")
-
-
-def _packed_gemv_cache_budget_bytes() -> int:
-    raw = os.environ.get("PCKETLM_PACKED_GEMV_CACHE_MB", "").strip()
-    if not raw:
-        return 0
-    try:
-        mb = int(raw)
-    except ValueError:
-        return 0
-    return max(0, mb) * 1024 * 1024
-
-
 def reset_packed_gemv_cache() -> None:
-    global _PACKED_GEMV_CACHE_BYTES
-    _PACKED_GEMV_CACHE.clear()
-    _PACKED_GEMV_CACHE_BYTES = 0
-    for key in _PACKED_GEMV_CACHE_STATS:
-        _PACKED_GEMV_CACHE_STATS[key] = 0
+    """Drops every resident pack and zeroes the counters."""
+    _ROW8_PACKS.clear()
 
 
 def packed_gemv_cache_stats() -> dict[str, int | float]:
-    return {
-        **_PACKED_GEMV_CACHE_STATS,
-        "resident_count": len(_PACKED_GEMV_CACHE),
-        "resident_bytes": _PACKED_GEMV_CACHE_BYTES,
-        "resident_mb": round(_PACKED_GEMV_CACHE_BYTES / 1024 / 1024, 4),
-        "budget_bytes": _packed_gemv_cache_budget_bytes(),
-    }
+    """hits, misses, stores, evictions, resident_count / _bytes / _mb, budget_bytes."""
+    return _ROW8_PACKS.stats()
 
 
 def pack_weight_rows8(weight: torch.Tensor) -> torch.Tensor:
@@ -869,34 +902,9 @@ def pack_weight_rows8(weight: torch.Tensor) -> torch.Tensor:
 
 
 def cached_pack_weight_rows8(cache_key: str, weight: torch.Tensor) -> torch.Tensor:
-    """src/pcketlm/native/__init__.py:2166-2193 (LRU bounded by PCKETLM_PACKED_GEMV_CACHE_MB)."""
-    global _PACKED_GEMV_CACHE_BYTES
-    if _packed_gemv_cache_disabled():
-        _PACKED_GEMV_CACHE_STATS["misses"] += 1
-        return pack_weight_rows8(weight)
-    budget = _packed_gemv_cache_budget_bytes()
-    if budget <= 0:
-        _PACKED_GEMV_CACHE_STATS["misses"] += 1
-        return pack_weight_rows8(weight)
-    key = str(cache_key)
-    cached = _PACKED_GEMV_CACHE.get(key)
-    if cached is not None:
-        _PACKED_GEMV_CACHE.move_to_end(key)
-        _PACKED_GEMV_CACHE_STATS["hits"] += 1
-        return cached
-    _PACKED_GEMV_CACHE_STATS["misses"] += 1
-    packed = pack_weight_rows8(weight)
-    nbytes = int(packed.numel() * packed.element_size())
-    if nbytes > budget:
-        return packed
-    while _PACKED_GEMV_CACHE and _PACKED_GEMV_CACHE_BYTES + nbytes > budget:
-        _old, old = _PACKED_GEMV_CACHE.popitem(last=False)
-        _PACKED_GEMV_CACHE_BYTES -= int(old.numel() * old.element_size())
-        _PACKED_GEMV_CACHE_STATS["evictions"] += 1
-    _PACKED_GEMV_CACHE[key] = packed
-    _PACKED_GEMV_CACHE_BYTES += nbytes
-    _PACKED_GEMV_CACHE_STATS["stores"] += 1
-    return packed
+    """pack_weight_rows8 through the HBM-resident pack cache (the reference's
+    LRU bounded by PCKETLM_PACKED_GEMV_CACHE_MB, src/pcketlm/native/__init__.py:2166-2193)."""
+    return _ROW8_PACKS.get(str(cache_key), lambda: pack_weight_rows8(weight))
 
 
 def packed_gemv_rows8(hidden: torch.Tensor, packed_weight: torch.Tensor, *, rows: int, cols: int) -> torch.Tensor:

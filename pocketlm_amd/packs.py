@@ -147,9 +147,88 @@ def fp8_pack_available(model_dir: Path) -> bool:
     return fp8_pack_enabled() and (default_fp8_pack_dir(model_dir) / "pack_manifest.json").exists()
 
 
+@dataclass(frozen=True, slots=True)
+class _Extent:
+    """Where one tensor's bytes sit: pack file number, offset, length."""
+
+    file: int
+    offset: int
+    length: int
+
+    @property
+    def end(self) -> int:
+        return self.offset + self.length
+
+
+@dataclass(frozen=True, slots=True)
+class _Record:
+    """One manifest entry, parsed once."""
+
+    name: str
+    dtype: str
+    shape: tuple[int, ...]
+    at: _Extent
+    scale_name: str | None
+    scale_dtype: str | None
+    scale_shape: tuple[int, ...] | None
+    scale_at: _Extent | None
+    expert: int | None
+    companion: bool
+    order: int
+
+    @classmethod
+    def parse(cls, name: str, e: dict) -> "_Record":
+        scale_at = None
+        if e.get("scale_name") and e.get("scale_byte_length") is not None:
+            scale_at = _Extent(int(e["scale_pack_file_index"]), int(e["scale_byte_offset"]),
+                               int(e["scale_byte_length"]))
+        shape = e.get("scale_shape")
+        return cls(name, str(e["dtype"]), tuple(int(v) for v in e.get("shape", [])),
+                   _Extent(int(e["pack_file_index"]), int(e["byte_offset"]), int(e["byte_length"])),
+                   e.get("scale_name"), e.get("scale_dtype"), None if shape is None else tuple(int(v) for v in shape),
+                   scale_at, None if e.get("expert_index") is None else int(e["expert_index"]),
+                   e.get("tensor_role") == "scale_companion", int(e.get("pack_order", 0)))
+
+
+class _PackFiles:
+    """The pack files of one pack directory: read-only maps opened on first
+    use and kept, plus the numbers of files handed out by path."""
+
+    def __init__(self, pack_dir: Path):
+        self.pack_dir = pack_dir
+        self.maps: dict[int, tuple[object, mmap.mmap]] = {}
+        self.located: set[int] = set()
+
+    def path(self, file: int) -> Path:
+        return self.pack_dir / f"pack_{int(file):04d}.bin"
+
+    def view(self, x: _Extent) -> memoryview:
+        if x.file not in self.maps:
+            handle = self.path(x.file).open("rb")
+            self.maps[x.file] = (handle, mmap.mmap(handle.fileno(), 0, access=mmap.ACCESS_READ))
+        return memoryview(self.maps[x.file][1])[x.offset:x.end]
+
+    def release(self) -> None:
+        """Unmaps every file no live view still exports."""
+        for file, (handle, mapped) in list(self.maps.items()):
+            try:
+                mapped.close()
+            except BufferError:
+                continue
+            handle.close()
+            del self.maps[file]
+
+
 class FP8PackReader:
-    """An FP8 pack read through long-lived mmaps (fp8_pack.py:54-241), plus
-    load_to_device for the bytes' way into HBM."""
+    """An FP8 pack ("pcketlm-fp8-pack-v1") opened for decode.
+
+    The public calls are those of fp8_pack.py:54-241 (host views, slice and
+    span locations, layer experts, telemetry, close), with its error
+    messages.  The manifest is parsed once into typed records.  The way into
+    HBM is load_to_device: the requested tensors (and scale companions) are
+    grouped per pack file and sorted by offset, so each file is read front
+    to back by one native transfer that lands every range in its device
+    tensor."""
 
     def __init__(self, model_dir: Path):
         self.model_dir = Path(model_dir).resolve()
@@ -159,171 +238,142 @@ class FP8PackReader:
             raise FileNotFoundError(f"FP8 pack manifest not found: {self.manifest_path}")
         self.manifest = json.loads(self.manifest_path.read_text(encoding="utf-8"))
         self.tensors: dict[str, dict] = dict(self.manifest.get("tensors") or {})
-        self._files: dict[int, object] = {}
-        self._mmaps: dict[int, mmap.mmap] = {}
-        self._located: set[int] = set()  # pack files handed out as paths
-        self._stats = {"sequential_reads": 0, "scattered_reads": 0, "bytes_returned": 0, "device_bytes_loaded": 0}
+        self._records = {n: _Record.parse(n, e) for n, e in self.tensors.items()}
+        self._files = _PackFiles(self.pack_dir)
+        self._reads = 0
+        self._returned = 0
+        self._device_bytes = 0
 
-    # ----------------------------------------------------------------- host views
-    def get_tensor(self, name: str) -> PackedTensorView:
-        entry = self._entry(name)
-        raw = self._view(entry["pack_file_index"], entry["byte_offset"], entry["byte_length"])
-        scale = None
-        if entry.get("scale_name"):
-            scale = self._view(entry["scale_pack_file_index"], entry["scale_byte_offset"], entry["scale_byte_length"])
-        self._count(int(entry["byte_length"]) + int(entry.get("scale_byte_length") or 0))
-        return PackedTensorView(
-            name=str(name), dtype=str(entry["dtype"]), shape=[int(v) for v in entry.get("shape", [])],
-            fp8_bytes=raw, scale_bytes=scale, scale_name=entry.get("scale_name"),
-            scale_dtype=entry.get("scale_dtype"),
-            scale_shape=None if entry.get("scale_shape") is None else [int(v) for v in entry["scale_shape"]])
-
-    def get_tensor_bytes(self, name: str) -> memoryview:
-        return self.get_tensor_slice_bytes(name, 0, int(self._entry(name)["byte_length"]))
-
-    def get_tensor_slice_bytes(self, name: str, relative_offset: int, byte_length: int) -> memoryview:
-        entry = self._entry(name)
-        self._check_slice(name, entry, int(relative_offset), int(byte_length))
-        self._count(int(byte_length))
-        return self._view(entry["pack_file_index"], int(entry["byte_offset"]) + int(relative_offset), int(byte_length))
-
-    def get_tensor_slice_location(self, name: str, relative_offset: int, byte_length: int) -> PackedSliceLocation:
-        entry = self._entry(name)
-        self._check_slice(name, entry, int(relative_offset), int(byte_length))
-        index = int(entry["pack_file_index"])
-        self._located.add(index)
-        self._count(int(byte_length))
-        return PackedSliceLocation(self._pack_path(index), int(entry["byte_offset"]) + int(relative_offset),
-                                   int(byte_length))
-
-    def get_tensor_span_location(self, names: list[str]) -> PackedSpanLocation:
-        index, start, end, slices = self._span(names)
-        self._located.add(index)
-        self._count(end - start)
-        return PackedSpanLocation(self._pack_path(index), start, end - start, slices)
-
-    def get_tensor_span_bytes(self, names: list[str]) -> PackedSpanView:
-        index, start, end, slices = self._span(names)
-        self._count(end - start)
-        return PackedSpanView(bytes=self._view(index, start, end - start), tensor_slices=slices)
-
-    def get_layer_experts(self, layer_idx: int, expert_ids: list[int]) -> list[PackedTensorView]:
-        """The weights (not scale companions) of the given experts of one
-        layer, in pack order."""
-        wanted = {int(v) for v in expert_ids}
-        prefix = f"model.layers.{int(layer_idx)}.mlp.experts."
-        names = [n for n, e in self.tensors.items()
-                 if n.startswith(prefix) and e.get("expert_index") is not None
-                 and int(e["expert_index"]) in wanted and e.get("tensor_role") != "scale_companion"]
-        names.sort(key=lambda n: self._entry(n).get("pack_order", 0))
-        return [self.get_tensor(n) for n in names]
-
-    # ----------------------------------------------------------------- to the device
+    # ----------------------------------------------------------------- into HBM
     def load_to_device(self, names: list[str], device=None, *, with_scales: bool = True) -> dict[str, torch.Tensor]:
         """The named tensors as device tensors of their dtype and shape (FP8
         as uint8 bytes), plus each one's scale companion when with_scales,
-        keyed by name.  One native transfer per pack file."""
+        keyed by name."""
         dev = _device(device)
-        out: dict[str, torch.Tensor] = {}
-        by_file: dict[int, list[tuple[int, torch.Tensor]]] = {}
-
-        def add(name: str, dtype: str, shape, index: int, offset: int, length: int) -> None:
-            if name in out:
-                return
-            t = _empty_on(dtype, shape, length, dev)
-            out[name] = t
-            by_file.setdefault(int(index), []).append((int(offset), t.view(torch.uint8).reshape(-1)))
-
+        wanted: dict[str, tuple[str, tuple[int, ...], _Extent]] = {}
         for name in names:
-            entry = self._entry(name)
-            add(name, entry["dtype"], entry.get("shape", []), entry["pack_file_index"], entry["byte_offset"],
-                entry["byte_length"])
-            if with_scales and entry.get("scale_name") and entry.get("scale_byte_length") is not None:
-                add(entry["scale_name"], entry["scale_dtype"], entry.get("scale_shape") or [],
-                    entry["scale_pack_file_index"], entry["scale_byte_offset"], entry["scale_byte_length"])
-        for index, spans in sorted(by_file.items()):
-            native.file_spans_to_device(self._pack_path(index), spans)
-            self._stats["device_bytes_loaded"] += sum(t.numel() for _o, t in spans)
-        self._stats["sequential_reads"] += len(by_file)
+            rec = self._record(name)
+            wanted.setdefault(rec.name, (rec.dtype, rec.shape, rec.at))
+            if with_scales and rec.scale_at is not None:
+                wanted.setdefault(rec.scale_name, (rec.scale_dtype, rec.scale_shape or (), rec.scale_at))
+        out = {n: _empty_on(dtype, shape, at.length, dev) for n, (dtype, shape, at) in wanted.items()}
+        per_file: dict[int, list[tuple[int, torch.Tensor]]] = {}
+        for n, (_dtype, _shape, at) in wanted.items():
+            per_file.setdefault(at.file, []).append((at.offset, out[n].view(torch.uint8).reshape(-1)))
+        for file in sorted(per_file):
+            spans = sorted(per_file[file], key=lambda span: span[0])
+            native.file_spans_to_device(self._files.path(file), spans)
+            self._device_bytes += sum(t.numel() for _offset, t in spans)
+        self._reads += len(per_file)
         return out
 
     def load_layer_experts(self, layer_idx: int, expert_ids: list[int], device=None) -> dict[int, tuple]:
         """Each expert's (gate, gate_scale_inv, up, up_scale_inv, down,
         down_scale_inv) on the device, as the MoE entry points take them."""
-        prefix = f"model.layers.{int(layer_idx)}.mlp.experts."
-        names = [f"{prefix}{int(e)}.{proj}.weight" for e in expert_ids for proj in ("gate_proj", "up_proj", "down_proj")]
-        loaded = self.load_to_device(names, device)
+        base = f"model.layers.{int(layer_idx)}.mlp.experts."
+        weights = {int(e): [f"{base}{int(e)}.{p}.weight" for p in ("gate_proj", "up_proj", "down_proj")]
+                   for e in expert_ids}
+        loaded = self.load_to_device([w for ws in weights.values() for w in ws], device)
         experts = {}
-        for e in expert_ids:
-            parts = []
-            for proj in ("gate_proj", "up_proj", "down_proj"):
-                wname = f"{prefix}{int(e)}.{proj}.weight"
-                sname = self._entry(wname).get("scale_name")
-                if not sname:
-                    raise KeyError(f"Tensor {wname} has no scale companion in the FP8 pack.")
-                parts += [loaded[wname], loaded[sname]]
-            experts[int(e)] = tuple(parts)
+        for e, ws in weights.items():
+            parts: list[torch.Tensor] = []
+            for w in ws:
+                scale = self._record(w).scale_name
+                if not scale:
+                    raise KeyError(f"Tensor {w} has no scale companion in the FP8 pack.")
+                parts.extend((loaded[w], loaded[scale]))
+            experts[e] = tuple(parts)
         return experts
+
+    # ----------------------------------------------------------------- host views and locations
+    def get_tensor(self, name: str) -> PackedTensorView:
+        rec = self._record(name)
+        raw = self._files.view(rec.at)
+        scale = self._files.view(rec.scale_at) if rec.scale_name and rec.scale_at is not None else None
+        self._returned_bytes(rec.at.length + (rec.scale_at.length if rec.scale_at is not None else 0))
+        return PackedTensorView(name=rec.name, dtype=rec.dtype, shape=list(rec.shape), fp8_bytes=raw,
+                                scale_bytes=scale, scale_name=rec.scale_name, scale_dtype=rec.scale_dtype,
+                                scale_shape=None if rec.scale_shape is None else list(rec.scale_shape))
+
+    def get_tensor_bytes(self, name: str) -> memoryview:
+        return self.get_tensor_slice_bytes(name, 0, self._record(name).at.length)
+
+    def get_tensor_slice_bytes(self, name: str, relative_offset: int, byte_length: int) -> memoryview:
+        x = self._sub(name, int(relative_offset), int(byte_length))
+        self._returned_bytes(x.length)
+        return self._files.view(x)
+
+    def get_tensor_slice_location(self, name: str, relative_offset: int, byte_length: int) -> PackedSliceLocation:
+        x = self._sub(name, int(relative_offset), int(byte_length))
+        self._files.located.add(x.file)
+        self._returned_bytes(x.length)
+        return PackedSliceLocation(self._files.path(x.file), x.offset, x.length)
+
+    def get_tensor_span_location(self, names: list[str]) -> PackedSpanLocation:
+        x, slices = self._cover(names)
+        self._files.located.add(x.file)
+        self._returned_bytes(x.length)
+        return PackedSpanLocation(self._files.path(x.file), x.offset, x.length, slices)
+
+    def get_tensor_span_bytes(self, names: list[str]) -> PackedSpanView:
+        x, slices = self._cover(names)
+        self._returned_bytes(x.length)
+        return PackedSpanView(bytes=self._files.view(x), tensor_slices=slices)
+
+    def get_layer_experts(self, layer_idx: int, expert_ids: list[int]) -> list[PackedTensorView]:
+        """Views of the given experts' weights of one layer (scale companions
+        travel inside each view), in pack order."""
+        ids = {int(v) for v in expert_ids}
+        base = f"model.layers.{int(layer_idx)}.mlp.experts."
+        chosen = sorted((r for r in self._records.values()
+                         if r.name.startswith(base) and r.expert in ids and not r.companion),
+                        key=lambda r: r.order)
+        return [self.get_tensor(r.name) for r in chosen]
 
     # ----------------------------------------------------------------- bookkeeping
     def telemetry(self) -> dict:
-        mapped = sum(len(m) for m in self._mmaps.values())
-        return {**self._stats, "pack_files_open": len(self._files),
-                "pack_files_accessed": len(self._located | set(self._mmaps)), "mmap_bytes_mapped": mapped,
-                "mmap_bytes_resident": None if mapped else 0, "mmap_residency_measured": False}
+        mapped = sum(len(m) for _h, m in self._files.maps.values())
+        return {"sequential_reads": self._reads, "scattered_reads": 0, "bytes_returned": self._returned,
+                "device_bytes_loaded": self._device_bytes, "pack_files_open": len(self._files.maps),
+                "pack_files_accessed": len(self._files.located | set(self._files.maps)),
+                "mmap_bytes_mapped": mapped, "mmap_bytes_resident": None if mapped else 0,
+                "mmap_residency_measured": False}
 
     def close(self) -> None:
-        """Unmap every pack file whose views are no longer held."""
-        for index in list(self._mmaps):
-            try:
-                self._mmaps[index].close()
-            except BufferError:  # a live view still exports it
-                continue
-            del self._mmaps[index]
-            handle = self._files.pop(index, None)
-            if handle is not None:
-                handle.close()
+        """Unmaps every pack file whose views are no longer held."""
+        self._files.release()
 
-    def _count(self, nbytes: int) -> None:
-        self._stats["sequential_reads"] += 1
-        self._stats["bytes_returned"] += int(nbytes)
+    def _returned_bytes(self, n: int) -> None:
+        self._reads += 1
+        self._returned += int(n)
 
-    def _pack_path(self, index: int) -> Path:
-        return self.pack_dir / f"pack_{int(index):04d}.bin"
-
-    def _entry(self, name: str) -> dict:
-        entry = self.tensors.get(name)
-        if entry is None:
+    def _record(self, name: str) -> _Record:
+        rec = self._records.get(name)
+        if rec is None:
             raise KeyError(f"Tensor {name} is not present in FP8 pack manifest.")
-        return entry
+        return rec
 
-    @staticmethod
-    def _check_slice(name: str, entry: dict, offset: int, length: int) -> None:
+    def _sub(self, name: str, offset: int, length: int) -> _Extent:
+        """A byte range inside one tensor, checked against its length."""
+        at = self._record(name).at
         if offset < 0 or length < 0:
             raise ValueError("Packed tensor slice offset and length must be non-negative.")
-        if offset + length > int(entry["byte_length"]):
+        if offset + length > at.length:
             raise ValueError(f"Packed tensor slice exceeds tensor byte length for {name}.")
+        return _Extent(at.file, at.offset + offset, length)
 
-    def _span(self, names: list[str]) -> tuple[int, int, int, dict[str, tuple[int, int]]]:
+    def _cover(self, names: list[str]) -> tuple[_Extent, dict[str, tuple[int, int]]]:
+        """The smallest range of one pack file holding every named tensor,
+        and each tensor's (offset in it, length)."""
         if not names:
             raise ValueError("Packed tensor span requires at least one tensor name.")
-        entries = [(str(n), self._entry(str(n))) for n in names]
-        files = {int(e["pack_file_index"]) for _n, e in entries}
-        if len(files) != 1:
+        ats = {str(n): self._record(str(n)).at for n in names}
+        if len({x.file for x in ats.values()}) != 1:
             raise ValueError("Packed tensor span crosses pack files.")
-        start = min(int(e["byte_offset"]) for _n, e in entries)
-        end = max(int(e["byte_offset"]) + int(e["byte_length"]) for _n, e in entries)
-        return files.pop(), start, end, {n: (int(e["byte_offset"]) - start, int(e["byte_length"])) for n, e in entries}
-
-    def _view(self, index, offset, length) -> memoryview:
-        index = int(index)
-        mapped = self._mmaps.get(index)
-        if mapped is None:
-            handle = self._pack_path(index).open("rb")
-            mapped = mmap.mmap(handle.fileno(), 0, access=mmap.ACCESS_READ)
-            self._files[index] = handle
-            self._mmaps[index] = mapped
-        return memoryview(mapped)[int(offset):int(offset) + int(length)]
+        lo = min(x.offset for x in ats.values())
+        hi = max(x.end for x in ats.values())
+        file = next(iter(ats.values())).file
+        return _Extent(file, lo, hi - lo), {n: (x.offset - lo, x.length) for n, x in ats.items()}
 
 
 def _now() -> str:

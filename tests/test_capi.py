@@ -147,3 +147,26 @@ def test_packed_gemv_cache_lru(monkeypatch):
     native.cached_pack_weight_rows8("a", w)
     assert len(calls) == 2
     native.reset_packed_gemv_cache()
+
+
+def test_packed_gemv_cache_evicts_least_recently_used(monkeypatch):
+    """A 1 MiB budget holds two 400 KiB packs: a third evicts the one used
+    longest ago (a hit refreshes), and a pack above the budget is returned
+    without being kept."""
+    sizes = {"a": 200 << 10, "b": 200 << 10, "c": 200 << 10, "big": 600 << 10}  # uint16 elements
+    monkeypatch.setattr(native, "pack_weight_rows8", lambda w: torch.zeros(int(w.item()), dtype=torch.uint16))
+    monkeypatch.setenv("PCKETLM_PACKED_GEMV_CACHE_MB", "1")
+    native.reset_packed_gemv_cache()
+    pack = {k: native.cached_pack_weight_rows8(k, torch.tensor(n)) for k, n in (("a", sizes["a"]), ("b", sizes["b"]))}
+    assert native.cached_pack_weight_rows8("a", torch.tensor(1)) is pack["a"]  # hit: "a" is now the newest
+    native.cached_pack_weight_rows8("c", torch.tensor(sizes["c"]))                # evicts "b"
+    st = native.packed_gemv_cache_stats()
+    assert (st["hits"], st["misses"], st["stores"], st["evictions"]) == (1, 3, 3, 1)
+    assert st["resident_count"] == 2 and st["resident_bytes"] == 800 << 10 and st["budget_bytes"] == 1 << 20
+    assert native.cached_pack_weight_rows8("a", torch.tensor(1)) is pack["a"]
+    assert native.cached_pack_weight_rows8("b", torch.tensor(sizes["b"])) is not pack["b"]  # was evicted
+    native.cached_pack_weight_rows8("big", torch.tensor(sizes["big"]))
+    st = native.packed_gemv_cache_stats()
+    assert (st["stores"], st["evictions"], st["resident_count"], st["resident_bytes"]) == (4, 2, 2, 800 << 10)
+    native.reset_packed_gemv_cache()
+    assert native.packed_gemv_cache_stats()["resident_count"] == 0

@@ -219,3 +219,33 @@ def test_row8_mapped_file_gives_host_views(tmp_path):
         mapped.close()
     with pytest.raises(OSError):
         native.map_native_row8_file(tmp_path / "missing.bin")
+
+
+def _q4_golden_cases(golden):
+    g = golden("q4")
+    for i in range(int(g["count"])):
+        shape = tuple(int(v) for v in g[f"t{i}_shape"])
+        t = torch.from_numpy(g[f"t{i}_in"].view(np.int16).copy()).view(torch.float16).reshape(shape)
+        yield i, t, g[f"t{i}_packed"], g[f"t{i}_scales"]
+
+
+def test_product_q4_quantizer_matches_golden(golden):
+    """formats.quantize_tensor_to_q4 (the quantizer that builds Q4 artifacts
+    and the bench's Q4 weights) gives the golden nibbles and fp16 scales of
+    the reference's torch arithmetic (q4_quantize.py:48-71), bit for bit,
+    on the 102 tensors of tests/golden/q4.npz (0-d, 1-d, 3-d and odd sizes
+    included)."""
+    for i, t, want_packed, want_scales in _q4_golden_cases(golden):
+        packed, scales, meta = formats.quantize_tensor_to_q4(t)
+        assert np.array_equal(packed.numpy(), want_packed), i
+        assert np.array_equal(scales.view(torch.int16).numpy().view(np.uint16), want_scales), i
+        assert meta["shape"] == list(t.shape) and meta["numel"] == t.numel()
+
+
+@pytest.mark.gpu
+def test_product_q4_quantizer_matches_golden_on_device(golden):
+    """The same quantizer run on the GPU (as the bench runs it)."""
+    for i, t, want_packed, want_scales in _q4_golden_cases(golden):
+        packed, scales, _meta = formats.quantize_tensor_to_q4(t.cuda())
+        assert np.array_equal(packed.cpu().numpy(), want_packed), i
+        assert np.array_equal(scales.cpu().view(torch.int16).numpy().view(np.uint16), want_scales), i
