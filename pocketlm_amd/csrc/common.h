@@ -60,6 +60,19 @@ typedef float plm_float2 __attribute__((ext_vector_type(2)));
 
 // Decode four e4m3fn bytes (one dword, byte 0 first) with the hardware
 // converter; NaN bytes (0x7F / 0xFF) come out as NaN.
+// A load through the global address space.  Pointers the compiler cannot
+// prove global (read from memory, as the device-routed plan's are) would
+// otherwise become flat loads, which also count against lgkmcnt: the wait
+// for a later scalar load then waits for them too.
+typedef uint32_t plm_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 plm_gload16(const void* p) {
+    const plm_u32x4 v = *(const __attribute__((address_space(1))) plm_u32x4*)(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float plm_gload_f32(const void* p) {
+    return *(const __attribute__((address_space(1))) float*)(p);
+}
+
 __device__ __forceinline__ void plm_decode4_e4m3(uint32_t d, float* v) {
     const plm_float2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(d), false);
     const plm_float2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(d), true);

@@ -452,11 +452,11 @@ __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
 #pragma unroll
                 for (int r = 0; r < TR; ++r) {
                     const int64_t rr = row0 + r < rows ? row0 + r : rows - 1;
-                    q[i][r] = *reinterpret_cast<const uint4*>(W[i] + rr * a.K + col);
+                    q[i][r] = plm_gload16(W[i] + rr * a.K + col);
                 }
             float sc[NWT];
 #pragma unroll
-            for (int i = 0; i < NWT; ++i) sc[i] = S[i][srow + (col >> 7)];
+            for (int i = 0; i < NWT; ++i) sc[i] = plm_gload_f32(S[i] + srow + (col >> 7));
             if constexpr (M == 1) {
                 // one activation row: decode each weight row right before its
                 // dot, so a larger tile needs no more registers (same arithmetic)
@@ -616,9 +616,9 @@ __device__ __forceinline__ void combine_chunk(const CombineArgs& a, int g, int c
 #pragma unroll
     for (int r = 0; r < TR; ++r) {
         const int64_t rr = row0 + r < a.rows ? row0 + r : a.rows - 1;
-        q[r] = *reinterpret_cast<const uint4*>(W + rr * a.K + col);
+        q[r] = plm_gload16(W + rr * a.K + col);
     }
-    const float sc = S[(row0 >> 7) * a.scale_cols + (col >> 7)];
+    const float sc = plm_gload_f32(S + (row0 >> 7) * a.scale_cols + (col >> 7));
     if constexpr (M == 1) {
         // one activation row: decode each weight row right before its dot,
         // so a larger tile needs no more registers (same arithmetic)
@@ -713,14 +713,19 @@ __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
             if (lane == kSumLane) red[wave * V + r * M + m] = t;
         }
     if constexpr (FUSED) {
-        // the split-off group in the same registers (its items on the waves
-        // a tile of its own would give them)
+        // The split-off group in the same registers.  With fewer items than
+        // waves its items go, in order, to the last waves (those with the
+        // fewest routed items), one each: the wave sums then add the same
+        // values in the same order as a tile of its own (whose item c sits
+        // on wave c), the other waves adding exact zeros.
         if (a.split_last) {
 #pragma unroll
             for (int r = 0; r < TR; ++r)
 #pragma unroll
                 for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
-            for (int c = wave; c < a.cps; c += nw) combine_chunk<M, TR>(a, a.ngroups - 1, c, false, row0, lane, acc);
+            const int shift = nw > a.cps ? nw - a.cps : 0;
+            for (int c = wave - shift; c < a.cps; c += nw)
+                if (c >= 0) combine_chunk<M, TR>(a, a.ngroups - 1, c, false, row0, lane, acc);
 #pragma unroll
             for (int r = 0; r < TR; ++r)
 #pragma unroll
@@ -867,13 +872,15 @@ int waves_for(int64_t nchunks) {
 // chosen per launch: at one or two activation rows (where each weight row is
 // decoded right before its dot) 8 rows halve the activation reads per weight
 // byte, used when the grid still has at least kTileWaves waves; otherwise 4
-// for one weight, fewer when two weights or many activation rows would need
-// too many accumulators.
+// for one weight, and 2 for two (gate and up): measured on the DeepSeek-V3
+// gate/up launch (9 x 2 weights of 2048 x 7168, M = 1) at 45.4 us with 2-row
+// tiles against 47.3 us with 4-row ones (twice the workgroups, the same
+// bytes per wave).
 constexpr int64_t kTileWaves = 4096;
 
 template <int M>
 constexpr int rows_tile(int nwt) {
-    return nwt == 1 ? 4 : (M == 1 ? 4 : 2);
+    return nwt == 1 ? 4 : 2;
 }
 
 template <int M>

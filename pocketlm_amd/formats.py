@@ -64,8 +64,13 @@ def quantize_tensor_to_q4(tensor: torch.Tensor) -> tuple[torch.Tensor, torch.Ten
     work = tensor.detach().float()
     m = _rows_view(work)
     max_abs = m.abs().amax(dim=1)
-    scales = torch.where(max_abs > 0, max_abs / 7.0, torch.ones_like(max_abs))
-    q = torch.round(m / scales[:, None]).clamp(-7, 7).to(torch.int8)
+    # The two divisions are those of the reference's fp32 torch code on the
+    # CPU, correctly rounded.  A GPU's fp32 division need not be (one ulp
+    # moves a quotient across a .5 and changes the nibble), so they are done
+    # in fp64 and rounded to fp32: for fp32 operands that gives the correctly
+    # rounded fp32 quotient (53 >= 2 * 24 + 2 bits: no double-rounding error).
+    scales = torch.where(max_abs > 0, (max_abs.double() / 7.0).float(), torch.ones_like(max_abs))
+    q = torch.round((m.double() / scales.double()[:, None]).float()).clamp(-7, 7).to(torch.int8)
     packed = pack_int4(q.flatten())
     scale_tensor = scales.to(torch.float16).contiguous()
     meta = {
