@@ -255,6 +255,29 @@ int fp8_e4m3_block_mlp_many_pair_weighted_bf16x_f32(
     const float* pair_weights, float* out, int64_t expert_count, int64_t pair_count,
     int64_t batch, int64_t intermediate_rows, int64_t hidden_cols, int64_t gate_scale_cols,
     int64_t down_scale_cols);
+/* No counterpart in the reference: the pair-weighted MoE above (fp32 or
+ * bf16 activations) without the host read-back of the pair indices, for
+ * callers that must not wait on the stream (HIP graph capture, the verifier
+ * batch).  Pairs with an index out of range are left out, and their number
+ * is written to *bad_pairs (device memory) instead of returning -4; the
+ * route weights are summed per (expert, row) in pair order, as above.
+ * Codes -1 null, -2 bad dims, -3 workspace. */
+int fp8_e4m3_block_mlp_many_pair_weighted_nosync_f32(
+    const uint64_t* gate_weight_ptrs, const uint64_t* gate_scale_ptrs,
+    const uint64_t* up_weight_ptrs, const uint64_t* up_scale_ptrs,
+    const uint64_t* down_weight_ptrs, const uint64_t* down_scale_ptrs, const float* hidden,
+    const int64_t* pair_item_indices, const int64_t* pair_row_indices,
+    const float* pair_weights, float* out, int* bad_pairs, int64_t expert_count, int64_t pair_count,
+    int64_t batch, int64_t intermediate_rows, int64_t hidden_cols, int64_t gate_scale_cols,
+    int64_t down_scale_cols);
+int fp8_e4m3_block_mlp_many_pair_weighted_nosync_bf16x_f32(
+    const uint64_t* gate_weight_ptrs, const uint64_t* gate_scale_ptrs,
+    const uint64_t* up_weight_ptrs, const uint64_t* up_scale_ptrs,
+    const uint64_t* down_weight_ptrs, const uint64_t* down_scale_ptrs, const uint16_t* hidden_bf16,
+    const int64_t* pair_item_indices, const int64_t* pair_row_indices,
+    const float* pair_weights, float* out, int* bad_pairs, int64_t expert_count, int64_t pair_count,
+    int64_t batch, int64_t intermediate_rows, int64_t hidden_cols, int64_t gate_scale_cols,
+    int64_t down_scale_cols);
 
 /* --------------------------------------------------------------------- Q4 */
 /* Per-row symmetric Q4 (src/pcketlm/core/model_import/q4_quantize.py:48-71):
@@ -403,6 +426,15 @@ int ds_forward_verify_f32(void* handle, const int64_t* candidate_token_ids, int6
 int ds_router_topk_u16(const uint16_t* hidden_u16, const uint16_t* router_weights_u16,
                        int64_t hidden_dim, int64_t num_experts, int64_t k, int64_t dtype_code,
                        int64_t* output_expert_ids, float* output_weights);
+/* No counterpart in the reference: ds_router_topk_u16 without the status
+ * read-back (for callers that must not wait on the stream, e.g. under HIP
+ * graph capture).  The status the synchronous call would return (0, or 3 / 4
+ * for a degenerate softmax sum) is written to *status (device memory); the
+ * return value covers only the argument checks (1 null, 2 bad dims) and the
+ * launch. */
+int ds_router_topk_u16_nosync(const uint16_t* hidden_u16, const uint16_t* router_weights_u16, int64_t hidden_dim,
+                              int64_t num_experts, int64_t k, int64_t dtype_code, int64_t* output_expert_ids,
+                              float* output_weights, int* status);
 
 /* New export for DeepSeek-V3 routing, the torch code of run_fp8_router
  * (src/pcketlm/core/runtime/fp8_source.py:1527-1547) with the group mask of

@@ -96,6 +96,8 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "fp8_e4m3_block_mlp_many_weighted_avx512_f32": (_i32, [_vp] * 9 + [_i64] * 6),
     "fp8_e4m3_block_mlp_many_row_weighted_f32": (_i32, [_vp] * 9 + [_i64] * 6),
     "fp8_e4m3_block_mlp_many_pair_weighted_f32": (_i32, [_vp] * 11 + [_i64] * 7),
+    "fp8_e4m3_block_mlp_many_pair_weighted_nosync_f32": (_i32, [_vp] * 12 + [_i64] * 7),
+    "fp8_e4m3_block_mlp_many_pair_weighted_nosync_bf16x_f32": (_i32, [_vp] * 12 + [_i64] * 7),
     "q4_dequant_to_fp16": (None, [_vp, _vp, _vp, _i64, _i64]),
     "q4_dequant_many_to_fp16": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64]),
     "q4_moe_selected_forward_u16": (_i32, [_vp] * 9 + [_i64] * 3),
@@ -119,6 +121,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ds_moe_layer_forward_f32": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "ds_moe_layer_forward_fp8_f32": (_i32, [_vp] * 9 + [_i64] * 6 + [_vp]),
     "ds_router_topk_u16": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "ds_router_topk_u16_nosync": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
     "ds_route_topk_f32": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _f32, _vp, _vp]),
     "ds_attention_layer_forward_f32": (_i32, [_vp, _i64, _vp, _i64, _i64, DS_ATTENTION_CALLBACK, _vp]),
     "ds_forward_decode_f32": (_i32, [_vp, _i64, DS_DECODE_CALLBACK, _vp, _i64]),

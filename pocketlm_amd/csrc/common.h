@@ -33,15 +33,17 @@ int hip_fail(hipError_t err, const char* where);
 // Check the last launch; returns 0 or the HIP failure code.
 int check_launch(const char* where);
 
-// Device scratch owned by the library, one arena per (device, stream).  The
-// returned block stays valid until the next workspace() call on the same
-// stream; growing waits for the stream before releasing the old block.
-// Returns nullptr on allocation failure (after recording the error).
+// Device scratch owned by the library, one arena per (device, stream, host
+// thread).  The returned block is the arena's until a larger request
+// replaces it; replaced blocks are kept, never freed, so launches already
+// queued and graphs captured earlier stay valid.  No stream synchronisation,
+// so it may run under stream capture.  Returns nullptr on allocation failure
+// (after recording the error).
 void* workspace(size_t bytes);
-// Device words private to the kernels of one (device, stream), zero when
-// first handed out and kept until the process ends (nothing else writes
-// them), for records that must survive other calls' use of the workspace.
-// Returns nullptr on allocation failure.
+// Device words private to the kernels of one (device, stream, host thread),
+// zeroed by a kernel on the stream when first handed out and kept until the
+// process ends (nothing else writes them), for records that must survive
+// other calls' use of the workspace.  Returns nullptr on allocation failure.
 constexpr int kStreamWords = 64;
 unsigned* stream_words();
 

@@ -333,6 +333,24 @@ PLM_EXPORT int ds_router_topk_u16(const uint16_t* hidden_u16, const uint16_t* ro
     return host_status;
 }
 
+// ds_router_topk_u16 without the status read-back: the kernel's status (0,
+// or 3 / 4 for a degenerate softmax sum, as the reference returns) goes to
+// *status in device memory and the call returns at once.  No counterpart in
+// the reference; for callers that must not wait on the stream.
+PLM_EXPORT int ds_router_topk_u16_nosync(const uint16_t* hidden_u16, const uint16_t* router_weights_u16,
+                                         int64_t hidden_dim, int64_t num_experts, int64_t k, int64_t dtype_code,
+                                         int64_t* output_expert_ids, float* output_weights, int* status) {
+    if (!hidden_u16 || !router_weights_u16 || !output_expert_ids || !output_weights || !status)
+        return plm::fail(1, "null pointer");
+    if (hidden_dim <= 0 || num_experts <= 0 || k <= 0 || k > num_experts) return plm::fail(2, "bad dimensions");
+    hipStream_t st = plm::current_stream();
+    float* ws = static_cast<float*>(plm::workspace(static_cast<size_t>(num_experts) * sizeof(float)));
+    if (ws == nullptr) return plm::fail(2, "workspace");
+    hipLaunchKernelGGL(softmax_router_kernel, dim3(1), dim3(256), 0, st, hidden_u16, router_weights_u16, hidden_dim,
+                       num_experts, k, dtype_code, ws, output_expert_ids, output_weights, status);
+    return plm::check_launch("softmax router kernel");
+}
+
 PLM_EXPORT int ds_route_topk_f32(const float* logits, const float* bias, int64_t batch, int64_t num_experts,
                                  int64_t top_k, int64_t n_groups, int64_t topk_groups, int scoring, float route_scale,
                                  int64_t* out_indices, float* out_weights) {

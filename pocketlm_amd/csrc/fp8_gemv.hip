@@ -853,12 +853,33 @@ __global__ void fill_f32_kernel(float* p, float v, int64_t n) {
     if (i < n) p[i] = v;
 }
 
-// Scatter sparse (item, row, weight) pairs into a dense [E, M] route matrix,
-// in pair order (one thread: pair lists are a few dozen entries).
-__global__ void scatter_pairs_kernel(const int64_t* items, const int64_t* rows, const float* w,
-                                     int64_t pairs, int64_t batch, float* route) {
-    if (blockIdx.x != 0 || threadIdx.x != 0) return;
-    for (int64_t p = 0; p < pairs; ++p) route[items[p] * batch + rows[p]] += w[p];
+// The dense route matrix [E, M] of sparse (item, row, weight) pairs: one
+// thread per cell adds the weights of its pairs in pair order (as the
+// reference's sequential scatter does), so no zero fill and no atomics.
+// Pairs with an index out of range match no cell; with bad set, workgroup 0
+// also counts them into *bad (one writer).
+__global__ __launch_bounds__(256) void scatter_pairs_kernel(const int64_t* items, const int64_t* rows, const float* w,
+                                                            int64_t pairs, int64_t experts, int64_t batch,
+                                                            float* route, int* bad) {
+    const int64_t cell = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (cell < experts * batch) {
+        const int64_t e = cell / batch, r = cell - e * batch;
+        float v = 0.0f;
+        for (int64_t p = 0; p < pairs; ++p)
+            if (items[p] == e && rows[p] == r) v += w[p];
+        route[cell] = v;
+    }
+    if (bad != nullptr && blockIdx.x == 0) {
+        __shared__ int count;
+        if (threadIdx.x == 0) count = 0;
+        __syncthreads();
+        int n = 0;
+        for (int64_t p = threadIdx.x; p < pairs; p += blockDim.x)
+            n += items[p] < 0 || items[p] >= experts || rows[p] < 0 || rows[p] >= batch;
+        if (n) atomicAdd(&count, n);
+        __syncthreads();
+        if (threadIdx.x == 0) *bad = count;
+    }
 }
 
 
@@ -1362,36 +1383,52 @@ int mlp_impl(const uint8_t* gate_weight, const float* gate_scale_inv, const uint
     return run_combine(c, st);
 }
 
+// bad_pairs null: the reference's contract, indices checked on the host
+// (read back, so the call synchronises its stream) and -4 for one out of
+// range.  bad_pairs set: no host read-back; pairs out of range are left out
+// and counted into *bad_pairs (device memory), so the call never waits.
 int pair_weighted_impl(const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp,
                        const uint64_t* dp, const uint64_t* dsp, Act hidden, const int64_t* pair_item_indices,
                        const int64_t* pair_row_indices, const float* pair_weights, float* out, int64_t expert_count,
-                       int64_t pair_count, int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
+                       int64_t pair_count, int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc,
+                       int* bad_pairs = nullptr) {
     if (pair_count < 0 || moe_dims_bad(expert_count, batch, inter, hid, gsc, dsc))
         return plm::fail(-2, "bad dimensions");
     hipStream_t st = plm::current_stream();
     int code = fill_f32(out, 0.0f, batch * hid, st);
-    if (code != 0 || pair_count == 0) return code;
-    // The index check needs the values on the host: read them back.
-    std::vector<int64_t> items(static_cast<size_t>(pair_count)), rows(static_cast<size_t>(pair_count));
-    hipError_t err = hipMemcpyAsync(items.data(), pair_item_indices, sizeof(int64_t) * pair_count,
-                                    hipMemcpyDeviceToHost, st);
-    if (err == hipSuccess)
-        err = hipMemcpyAsync(rows.data(), pair_row_indices, sizeof(int64_t) * pair_count, hipMemcpyDeviceToHost, st);
-    if (err == hipSuccess) err = hipStreamSynchronize(st);
-    if (err != hipSuccess) return plm::hip_fail(err, "pair index read-back");
-    for (int64_t p = 0; p < pair_count; ++p) {
-        if (items[p] < 0 || items[p] >= expert_count || rows[p] < 0 || rows[p] >= batch)
-            return plm::fail(-4, "pair %lld out of range", static_cast<long long>(p));
+    if (code != 0) return code;
+    if (pair_count == 0) {
+        if (bad_pairs != nullptr) {
+            hipLaunchKernelGGL(scatter_pairs_kernel, dim3(1), dim3(256), 0, st, pair_item_indices, pair_row_indices,
+                               pair_weights, int64_t(0), int64_t(0), batch, static_cast<float*>(nullptr), bad_pairs);
+            return plm::check_launch("scatter pairs");
+        }
+        return 0;
+    }
+    if (bad_pairs == nullptr) {
+        // The index check needs the values on the host: read them back.
+        std::vector<int64_t> items(static_cast<size_t>(pair_count)), rows(static_cast<size_t>(pair_count));
+        hipError_t err = hipMemcpyAsync(items.data(), pair_item_indices, sizeof(int64_t) * pair_count,
+                                        hipMemcpyDeviceToHost, st);
+        if (err == hipSuccess)
+            err = hipMemcpyAsync(rows.data(), pair_row_indices, sizeof(int64_t) * pair_count, hipMemcpyDeviceToHost,
+                                 st);
+        if (err == hipSuccess) err = hipStreamSynchronize(st);
+        if (err != hipSuccess) return plm::hip_fail(err, "pair index read-back");
+        for (int64_t p = 0; p < pair_count; ++p) {
+            if (items[p] < 0 || items[p] >= expert_count || rows[p] < 0 || rows[p] >= batch)
+                return plm::fail(-4, "pair %lld out of range", static_cast<long long>(p));
+        }
     }
     // Dense route matrix [E, batch] after the activations in the workspace.
     const size_t act_elems = static_cast<size_t>(expert_count * batch * inter);
     float* ws = static_cast<float*>(plm::workspace((act_elems + static_cast<size_t>(expert_count * batch)) * sizeof(float)));
     if (ws == nullptr) return -3;
     float* route = ws + act_elems;
-    code = fill_f32(route, 0.0f, expert_count * batch, st);
-    if (code != 0) return code;
-    hipLaunchKernelGGL(scatter_pairs_kernel, dim3(1), dim3(1), 0, st, pair_item_indices, pair_row_indices,
-                       pair_weights, pair_count, batch, route);
+    const int64_t cells = std::max<int64_t>(expert_count * batch, 1);
+    hipLaunchKernelGGL(scatter_pairs_kernel, dim3(static_cast<unsigned>(plm::ceil_div(cells, 256))), dim3(256), 0, st,
+                       pair_item_indices, pair_row_indices, pair_weights, pair_count, expert_count, batch, route,
+                       bad_pairs);
     code = plm::check_launch("scatter pairs");
     if (code != 0) return code;
     // weighted_moe asks for the same workspace size prefix, so act stays at ws.
@@ -1844,6 +1881,35 @@ PLM_EXPORT int fp8_e4m3_block_mlp_many_pair_weighted_bf16x_f32(
     return pair_weighted_impl(gp, gsp, up, usp, dp, dsp, Act{nullptr, hidden_bf16}, pair_item_indices,
                               pair_row_indices, pair_weights, out, expert_count, pair_count, batch, inter, hid, gsc,
                               dsc);
+}
+
+// The pair-weighted MoE without the host read-back: pairs out of range are
+// left out and counted into *bad_pairs (device memory).  No counterpart in
+// the reference; for callers that must not wait on the stream (graph
+// capture, the verifier batch).
+PLM_EXPORT int fp8_e4m3_block_mlp_many_pair_weighted_nosync_f32(
+    const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp, const uint64_t* dp,
+    const uint64_t* dsp, const float* hidden, const int64_t* pair_item_indices, const int64_t* pair_row_indices,
+    const float* pair_weights, float* out, int* bad_pairs, int64_t expert_count, int64_t pair_count, int64_t batch,
+    int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
+    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden || !pair_item_indices || !pair_row_indices ||
+        !pair_weights || !out || !bad_pairs)
+        return plm::fail(-1, "null pointer");
+    return pair_weighted_impl(gp, gsp, up, usp, dp, dsp, Act{hidden, nullptr}, pair_item_indices, pair_row_indices,
+                              pair_weights, out, expert_count, pair_count, batch, inter, hid, gsc, dsc, bad_pairs);
+}
+
+PLM_EXPORT int fp8_e4m3_block_mlp_many_pair_weighted_nosync_bf16x_f32(
+    const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, const uint64_t* usp, const uint64_t* dp,
+    const uint64_t* dsp, const uint16_t* hidden_bf16, const int64_t* pair_item_indices,
+    const int64_t* pair_row_indices, const float* pair_weights, float* out, int* bad_pairs, int64_t expert_count,
+    int64_t pair_count, int64_t batch, int64_t inter, int64_t hid, int64_t gsc, int64_t dsc) {
+    if (!gp || !gsp || !up || !usp || !dp || !dsp || !hidden_bf16 || !pair_item_indices || !pair_row_indices ||
+        !pair_weights || !out || !bad_pairs)
+        return plm::fail(-1, "null pointer");
+    return pair_weighted_impl(gp, gsp, up, usp, dp, dsp, Act{nullptr, hidden_bf16}, pair_item_indices,
+                              pair_row_indices, pair_weights, out, expert_count, pair_count, batch, inter, hid, gsc,
+                              dsc, bad_pairs);
 }
 
 PLM_EXPORT int fp8_e4m3_block_moe_device_routed_f32(const uint64_t* expert_table, int64_t num_experts,

@@ -236,13 +236,20 @@ __device__ __forceinline__ plm_half8 q4_mfma_c8_inplace() {
 // plane 0 is hi = fp16(v') and plane 1 is lo = fp16((v' - hi) * 2^11), so
 // hi + lo * 2^-11 carries 22 significant bits (the split follows the /16, so
 // no bits are lost to it).  A value that fp16 cannot hold (|v| >= 65504, inf,
-// NaN) records the call's sequence number in a word private to the stream
-// (zero at first), and that call's down phase reads the fp32 activations
-// instead.  Calls on one stream are ordered, and each stream has its own
-// word, so concurrent calls cannot overwrite each other's record; the word
-// only ever holds an earlier call's number, which selects nothing.
-__device__ __forceinline__ void q4_store_planes(uint4* base, int64_t k, float v, unsigned seq, unsigned* record) {
-    if (!(fabsf(v) < 65504.0f)) atomicExch(record, seq);
+// NaN) records the call's number in a word private to the stream and host
+// thread, and that call's down phase reads the fp32 activations instead.
+// The call's number is one more than an epoch word kept in device memory
+// beside the record: the down phase's last workgroup advances the epoch, so
+// each call (and each replay of a captured graph) gets a new number without
+// the host, and the record only ever holds an earlier call's number
+// otherwise, which selects nothing.  Words: [0] epoch, [1] record,
+// [2] the down phase's finished-workgroup count.
+constexpr int kQ4Epoch = 0, kQ4Record = 1, kQ4Done = 2;
+
+__device__ __forceinline__ void q4_store_planes(uint4* base, int64_t k, float v, unsigned* words) {
+    if (!(fabsf(v) < 65504.0f))
+        atomicExch(words + kQ4Record,
+                   __hip_atomic_load(words + kQ4Epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u);
     const int64_t s = k >> 9;
     const int p = static_cast<int>((k >> 5) & 15), j = static_cast<int>((k >> 3) & 3), n = static_cast<int>(k & 7);
     const float vs = (n & 1) ? v * 0.0625f : v;
@@ -265,8 +272,7 @@ struct Q4RowsArgs {
     int tiles_per_group;
     uint4* planes;        // SILU only: also write the fp16 B planes (nullptr: no)
     int64_t planes_stride;  // uint4 per group
-    unsigned seq;         // call sequence number for the overflow record
-    unsigned* overflow;   // the overflow record (with planes)
+    unsigned* words;      // epoch and overflow record (with planes)
 };
 
 // Position of value k of an fp32 activation vector stored in "step order":
@@ -379,7 +385,7 @@ __global__ __launch_bounds__(NWS * 64, q4_rows_min_waves<NWS>()) void q4_rows_ke
             if constexpr (SILU) {
                 const float act = plm_silu_mul(v[0], v[1]);
                 a.out[o] = act;
-                if (a.planes != nullptr) q4_store_planes(a.planes + g * a.planes_stride, row, act, a.seq, a.overflow);
+                if (a.planes != nullptr) q4_store_planes(a.planes + g * a.planes_stride, row, act, a.words);
             } else {
                 a.out[o] = v[0];
             }
@@ -394,8 +400,7 @@ struct Q4CombineArgs {
     int64_t act_stride;
     const uint4* planes;  // [ngroups][planes_stride] fp16 B planes, or nullptr
     int64_t planes_stride;
-    unsigned seq;
-    unsigned* overflow;   // the overflow record (with planes)
+    unsigned* words;      // epoch, overflow record, finished count (with planes)
     const float* route;   // [ngroups]
     uint16_t* out_f16;    // [rows]
     int64_t rows;
@@ -468,9 +473,12 @@ __global__ __launch_bounds__(NWS * 64) void q4_down_kernel(const Q4CombineArgs a
     // Both paths read the same weights: the first item's go out right after
     // the overflow record's read, which hides that read's latency.
     const unsigned flagged =
-        a.planes != nullptr ? __hip_atomic_load(a.overflow, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+        a.planes != nullptr ? __hip_atomic_load(a.words + kQ4Record, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+    const unsigned epoch =
+        a.planes != nullptr ? __hip_atomic_load(a.words + kQ4Epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
     load_w(g < ng ? s : steps - 1);
-    const bool use_planes = a.planes != nullptr && __builtin_amdgcn_readfirstlane(flagged) != a.seq;
+    const bool use_planes =
+        a.planes != nullptr && __builtin_amdgcn_readfirstlane(flagged) != __builtin_amdgcn_readfirstlane(epoch) + 1u;
 
     if (use_planes) {
         plm_f4 ah[TR], al[TR], ch = {0.0f, 0.0f, 0.0f, 0.0f}, cl = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -603,6 +611,16 @@ __global__ __launch_bounds__(NWS * 64) void q4_down_kernel(const Q4CombineArgs a
 #pragma unroll
             for (int w = 0; w < NWS; ++w) v += red[w][threadIdx.x];
             a.out_f16[row] = f16_from_bits(f2u(v), false);
+        }
+    }
+    // The last workgroup to finish advances the epoch (every workgroup has
+    // read the record and the epoch before it counts itself finished).
+    if (a.planes != nullptr && threadIdx.x == 0) {
+        const unsigned done =
+            __hip_atomic_fetch_add(a.words + kQ4Done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        if (done == gridDim.x - 1) {
+            __hip_atomic_store(a.words + kQ4Done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(a.words + kQ4Epoch, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -761,18 +779,15 @@ PLM_EXPORT int q4_moe_selected_forward_u16(const uint16_t* hidden, const uint8_t
     // vector, after it in the workspace).
     const bool planes = fast1 && fast2;
     const int64_t planes_stride = stride / 4;  // uint4 per expert
-    // The overflow record lives in the stream's private words (zero until a
-    // call records into it, written by nothing else); the workspace, which
-    // other entry points on the stream reuse, holds [fp32 act][planes].
-    unsigned* overflow = plm::stream_words();
-    if (overflow == nullptr) return 2;
+    // The epoch and overflow record live in the stream's private words
+    // (written by nothing else); the workspace, which other entry points on
+    // the stream reuse, holds [fp32 act][planes].
+    unsigned* words = plm::stream_words();
+    if (words == nullptr) return 2;
     char* ws = static_cast<char*>(plm::workspace(static_cast<size_t>(S * stride) * sizeof(float) * (planes ? 2 : 1)));
     if (ws == nullptr) return 2;
     float* act = reinterpret_cast<float*>(ws);
     uint4* bplanes = planes ? reinterpret_cast<uint4*>(act + S * stride) : nullptr;
-    static std::atomic<unsigned> call_seq{0};
-    unsigned seq = ++call_seq;
-    if (seq == 0) seq = ++call_seq;  // 0 is the record's initial value
     // Phase 1, groups of up to kMaxGroups experts.
     for (int64_t g0 = 0; g0 < S; g0 += kMaxGroups) {
         const int ng = static_cast<int>(std::min<int64_t>(kMaxGroups, S - g0));
@@ -792,8 +807,7 @@ PLM_EXPORT int q4_moe_selected_forward_u16(const uint16_t* hidden, const uint8_t
         a.out_steps = fast2 ? 1 : 0;
         a.planes = planes ? bplanes + g0 * planes_stride : nullptr;
         a.planes_stride = planes_stride;
-        a.seq = seq;
-        a.overflow = overflow;
+        a.words = words;
         if (fast1) {
             launch_q4_rows<2, 2, 4, true>(a, ng, st);
         } else {
@@ -815,8 +829,7 @@ PLM_EXPORT int q4_moe_selected_forward_u16(const uint16_t* hidden, const uint8_t
     c.act_stride = stride;
     c.planes = bplanes;
     c.planes_stride = planes_stride;
-    c.seq = seq;
-    c.overflow = overflow;
+    c.words = words;
     c.route = route_weights;
     c.out_f16 = out_fp16;
     c.rows = H;

@@ -1,11 +1,12 @@
 // Runtime plumbing of libpocketlm_hip.so: per-thread stream, error text,
-// device probes and the per-(device, stream) scratch arena.
+// device probes and the per-(device, stream, host thread) scratch arena.
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 #include "common.h"
 
@@ -16,14 +17,44 @@ namespace {
 thread_local hipStream_t t_stream = nullptr;
 thread_local char t_error[512] = {0};
 
+// Scratch of one (device, stream) for the calling host thread.  Blocks are
+// never freed while the process runs: a launch already queued, or a HIP
+// graph captured earlier, may still read a block that a larger request has
+// since replaced, so growth allocates a new block and keeps the old one.
+// Capacity grows at least twofold, which bounds the retired blocks to the
+// size of the current one.  Per thread: two host threads enqueueing on one
+// stream interleave their launches, and must not share intermediates.
 struct Arena {
     void* ptr = nullptr;
     size_t size = 0;
 };
 
-std::mutex g_arena_mu;
-std::map<std::pair<int, hipStream_t>, Arena> g_arenas;
-std::map<std::pair<int, hipStream_t>, unsigned*> g_words;
+struct ThreadScratch {
+    std::map<std::pair<int, hipStream_t>, Arena> arenas;
+    std::map<std::pair<int, hipStream_t>, unsigned*> words;
+};
+
+thread_local ThreadScratch t_scratch;
+
+std::mutex g_retired_mu;
+std::vector<void*> g_retired;  // replaced blocks, kept until the process ends
+
+// hipMalloc with the calling thread's stream-capture mode relaxed for the
+// call: under a capture in the global mode the runtime refuses allocations
+// (and invalidates the capture), although the block is an ordinary
+// allocation that outlives the graph, which is what the arena needs.
+hipError_t malloc_relaxed(void** p, size_t bytes) {
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    const hipError_t xe = hipThreadExchangeStreamCaptureMode(&mode);
+    const hipError_t err = hipMalloc(p, bytes);
+    if (xe == hipSuccess) hipThreadExchangeStreamCaptureMode(&mode);
+    return err;
+}
+
+__global__ void zero_words_kernel(unsigned* w, int n) {
+    const int i = static_cast<int>(threadIdx.x);
+    if (i < n) w[i] = 0u;
+}
 
 }  // namespace
 
@@ -59,31 +90,23 @@ void* workspace(size_t bytes) {
         return nullptr;
     }
     if (bytes == 0) bytes = 256;
-    std::lock_guard<std::mutex> lock(g_arena_mu);
-    Arena& a = g_arenas[{dev, t_stream}];
-    if (a.size >= bytes) {
-        return a.ptr;
-    }
-    if (a.ptr != nullptr) {
-        // Work already queued on this stream may still use the old block.
-        err = hipStreamSynchronize(t_stream);
-        if (err != hipSuccess) {
-            hip_fail(err, "hipStreamSynchronize(workspace)");
-            return nullptr;
-        }
-        hipFree(a.ptr);
-        a.ptr = nullptr;
-        a.size = 0;
-    }
-    // Round up to 1 MiB so that small growth does not reallocate each call.
-    const size_t rounded = (bytes + (1u << 20) - 1) & ~static_cast<size_t>((1u << 20) - 1);
-    err = hipMalloc(&a.ptr, rounded);
+    Arena& a = t_scratch.arenas[{dev, t_stream}];
+    if (a.size >= bytes) return a.ptr;
+    // Round up to 1 MiB, and at least double, so that growth is rare.
+    size_t want = (bytes + (1u << 20) - 1) & ~static_cast<size_t>((1u << 20) - 1);
+    if (want < 2 * a.size) want = 2 * a.size;
+    void* p = nullptr;
+    err = malloc_relaxed(&p, want);
     if (err != hipSuccess) {
-        a.ptr = nullptr;
         hip_fail(err, "hipMalloc(workspace)");
         return nullptr;
     }
-    a.size = rounded;
+    if (a.ptr != nullptr) {
+        std::lock_guard<std::mutex> lock(g_retired_mu);
+        g_retired.push_back(a.ptr);
+    }
+    a.ptr = p;
+    a.size = want;
     return a.ptr;
 }
 
@@ -94,14 +117,21 @@ unsigned* stream_words() {
         hip_fail(err, "hipGetDevice");
         return nullptr;
     }
-    std::lock_guard<std::mutex> lock(g_arena_mu);
-    unsigned*& w = g_words[{dev, t_stream}];
+    unsigned*& w = t_scratch.words[{dev, t_stream}];
     if (w == nullptr) {
         void* p = nullptr;
-        err = hipMalloc(&p, kStreamWords * sizeof(unsigned));
-        if (err == hipSuccess) err = hipMemsetAsync(p, 0, kStreamWords * sizeof(unsigned), t_stream);
+        err = malloc_relaxed(&p, kStreamWords * sizeof(unsigned));
         if (err != hipSuccess) {
-            if (p != nullptr) hipFree(p);
+            hip_fail(err, "stream words");
+            return nullptr;
+        }
+        // zeroed by a kernel on the stream (a captured graph then zeroes them
+        // on each replay, before its first use of them)
+        hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(kStreamWords), 0, t_stream, static_cast<unsigned*>(p),
+                           kStreamWords);
+        err = hipGetLastError();
+        if (err != hipSuccess) {
+            hipFree(p);
             hip_fail(err, "stream words");
             return nullptr;
         }

@@ -104,7 +104,9 @@ def run_fp8_moe(hidden: torch.Tensor, route_indices: torch.Tensor, route_weights
         pair_items = torch.cat([torch.full_like(rows, item) for item, (_e, rows, _t) in enumerate(jobs)])
         pair_rows = torch.cat([rows for _e, rows, _t in jobs])
         pair_w = torch.cat([weights[rows, tops] for _e, rows, tops in jobs])
-        y = native.fp8_e4m3_block_mlp_many_pair_weighted_f32(items, x, pair_items, pair_rows, pair_w)
+        # The pairs come from the validated jobs, so the no-sync form (no host
+        # read-back of the indices; same sums) is used.
+        y, _bad = native.fp8_e4m3_block_mlp_many_pair_weighted_nosync(items, x, pair_items, pair_rows, pair_w)
         out += y.to(dtype)
         path = "pair_weighted"
     elif jobs and m > 1 and _enabled("PCKETLM_ENABLE_FP8_MOE_ROW_WEIGHTED_MANY") \

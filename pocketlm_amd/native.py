@@ -694,6 +694,32 @@ def fp8_e4m3_block_mlp_many_pair_weighted_f32(items, hidden, pair_item_indices, 
     return _home(out, hidden)
 
 
+def fp8_e4m3_block_mlp_many_pair_weighted_nosync(items, hidden, pair_item_indices, pair_row_indices,
+                                                pair_weights) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp8_e4m3_block_mlp_many_pair_weighted_f32 without the host read-back
+    of the pair indices (no stream synchronisation; capturable in a HIP
+    graph).  Returns (out fp32 [M, H], bad_pairs int32 [1] on the device):
+    pairs with an index out of range are left out and counted instead of
+    raising."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_FP8_LINEAR", "Native FP8 pair-weighted many-MLP")
+    dev = _target_device(hidden, *(items[0] if items else ()))
+    ex = _Experts(items, hidden, dev, bf16_ok=True)
+    pi = _on(pair_item_indices, dev, torch.int64).reshape(-1)
+    pr = _on(pair_row_indices, dev, torch.int64).reshape(-1)
+    pw = _on(pair_weights, dev, torch.float32).reshape(-1)
+    if int(pi.numel()) != int(pr.numel()) or int(pi.numel()) != int(pw.numel()):
+        raise ValueError("pair index and weight tensors must have matching length")
+    batch = int(ex.x.shape[0])
+    out = torch.empty((batch, ex.hid), dtype=torch.float32, device=dev)
+    bad = torch.empty((1,), dtype=torch.int32, device=dev)
+    with _launch(lib, dev):
+        code = getattr(lib, _twin("fp8_e4m3_block_mlp_many_pair_weighted_nosync_f32", ex.bf16))(
+            *ex.table_args(), _p(ex.x), _p(pi), _p(pr), _p(pw), _p(out), _p(bad), ex.count, int(pi.numel()), batch,
+            ex.inter, ex.hid, ex.gsc, ex.dsc)
+    _check("fp8_e4m3_block_mlp_many_pair_weighted_nosync_f32", code)
+    return _home(out, hidden), bad
+
+
 # --------------------------------------------------------------------------- Q4
 
 def q4_dequant_to_fp16(packed: torch.Tensor, scales: torch.Tensor, num_channels: int, channel_size: int) -> torch.Tensor:
@@ -1135,6 +1161,28 @@ def ds_router_topk(hidden: torch.Tensor, router_weights: torch.Tensor, *, k: int
                                       _p(weights))
     _check("ds_router_topk_u16", code)
     return _home(ids, hidden), _home(weights, hidden)
+
+
+def ds_router_topk_nosync(hidden: torch.Tensor, router_weights: torch.Tensor, *,
+                          k: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """ds_router_topk without waiting on the stream: (ids, weights, status),
+    status int32 [1] on the device (0, or 3 / 4 where ds_router_topk would
+    raise for a degenerate softmax sum)."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_DS_ROUTER", "Native DeepSeek router")
+    dtype_code = _u16_storage_dtype_code(router_weights.dtype)
+    dev = _target_device(hidden, router_weights)
+    r = _on(router_weights, dev)
+    h = _on(hidden, dev, r.dtype).reshape(-1)
+    if r.ndim != 2 or int(r.shape[1]) != int(h.numel()):
+        raise ValueError("router weights must be [num_experts, hidden_dim] matching hidden")
+    ids = torch.empty((int(k),), dtype=torch.int64, device=dev)
+    weights = torch.empty((int(k),), dtype=torch.float32, device=dev)
+    status = torch.empty((1,), dtype=torch.int32, device=dev)
+    with _launch(lib, dev):
+        code = lib.ds_router_topk_u16_nosync(_p(h), _p(r), int(r.shape[1]), int(r.shape[0]), int(k), dtype_code,
+                                             _p(ids), _p(weights), _p(status))
+    _check("ds_router_topk_u16_nosync", code)
+    return ids, weights, status
 
 
 def route_deepseek(logits: torch.Tensor, *, top_k: int = 8, n_groups: int = 8, topk_groups: int = 4,

@@ -250,6 +250,24 @@ def test_softmax_router_golden(nat, golden):
         assert np.allclose(host(w), g["softmax_weights"][i], atol=1e-6, rtol=1e-6)
 
 
+def test_softmax_router_nosync_equals_checked_call(nat, golden):
+    """ds_router_topk_u16_nosync: the same ids and weights, the status in
+    device memory (0 here; 3 for a softmax whose sum is not positive, where
+    the checked call raises)."""
+    g = golden("router")
+    router = dev(g["softmax_router"]).view(torch.float16)
+    for h in g["softmax_hidden"]:
+        hx = dev(h).view(torch.float16)
+        ids, w = nat.ds_router_topk(hx, router, k=4)
+        ids2, w2, status = nat.ds_router_topk_nosync(hx, router, k=4)
+        assert torch.equal(ids, ids2) and torch.equal(w, w2) and int(status.item()) == 0
+    bad = torch.full_like(hx, float("nan"))
+    _ids, _w, status = nat.ds_router_topk_nosync(bad, router, k=4)
+    assert int(status.item()) == 3
+    with pytest.raises(RuntimeError):
+        nat.ds_router_topk(bad, router, k=4)
+
+
 def test_deepseek_route_kat_and_random(nat, golden, oracle_mod):
     g = golden("router")
     idx, w = nat.route_deepseek(dev(g["ds_kat_logits"]), top_k=1, n_groups=1, topk_groups=1, route_scale=2.5,
