@@ -35,10 +35,8 @@ constexpr int kAttnThreads = 256;
 constexpr int kAttnWaves = kAttnThreads / plm::kWave;
 constexpr int kMaxGroup = 16;     // query heads per kv head
 constexpr int kMaxHeadDim = 256;
-constexpr int kMaxSplitLen = 256; // tokens per attention workgroup
-constexpr int kTokUnroll = 4;      // tokens whose loads a wave issues together
 constexpr int kMergeThreads = 1024;
-constexpr int kMaxSplits = 4096;   // splits per head the merge stages in LDS
+constexpr int kMaxSplits = 65535;  // the split launch's grid height
 
 __device__ __forceinline__ float rd16(uint16_t v, bool bf16) {
     if (bf16) return __uint_as_float(static_cast<uint32_t>(v) << 16);
@@ -61,10 +59,15 @@ __device__ __forceinline__ float wave_sum_all(float v) {
     return v;
 }
 
-__device__ __forceinline__ float wave_max_all(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
+// A DPP lane swap within each 16-lane row (xor 1, xor 2, half-row mirror,
+// row mirror), and one row's value read from its first lane: the pieces of
+// the score and softmax reductions, with no LDS round trips.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float rows_f32(float v, int row) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16 * row));
 }
 
 // Sum over the workgroup (kNormThreads threads), returned to every thread.
@@ -139,87 +142,259 @@ __global__ __launch_bounds__(64) void qk_rope_append_kernel(const float* __restr
             v_row[static_cast<int64_t>(kvh) * hd + d] = wr16(v[static_cast<int64_t>(kvh) * hd + d], BF16);
 }
 
-// Flash-decode partials.  Block (kvh, sp) takes tokens [sp*L, min(T, sp*L+L))
-// of kv head kvh for its `group` query heads: scores q.k * scale into LDS,
-// per-head max m and sum l of exp(score - m), and acc = sum exp(score - m) v.
-// Waves take tokens, lanes take head dimensions.
-// G bounds the query heads per kv head (group <= G), DPL the head dimensions
-// per lane (hd <= 64 * DPL): the unrolled body stays small enough for the
-// instruction cache.
-template <bool BF16, int G, int DPL>
+// Flash-decode partials.  Workgroup (kvh, sp) takes the TOK tokens
+// [sp * TOK, ...) of kv head kvh for its `group` query heads and writes, per
+// head, the partial sum acc = sum_t exp(s_t - m) v_t, the max m of its scores
+// s_t = (q . k_t) * scale and l = sum_t exp(s_t - m).
+//   scores: lanes form groups of HS = min(G, 4) head slices times four
+//           quarters of the head dimensions (16-byte K loads; adjacent lanes
+//           read adjacent bytes); a lane dots its quarter of TPL tokens with
+//           the heads of its slice, reading each query piece once for all of
+//           them, then two lane swaps add the quarters;
+//   softmax: TOK lanes per head, 256 / TOK heads at a time;
+//   values: waves take every fourth token, lanes take VD adjacent head
+//           dimensions (V rows read 64 lanes wide), accumulating all heads;
+//   the four waves' sums meet in LDS behind one barrier and every thread
+//   adds ((w0 + w2) + (w1 + w3)) for a few outputs.
+// G bounds the query heads per kv head (group <= G), VD the head dimensions
+// per lane in the value pass (hd <= 64 * VD).  TOK (16, 32 or 64) is chosen
+// per launch so that short contexts still spread over the CUs.
+constexpr int kMaxSplitTokens = 64;
+constexpr int kMinSplitTokens = 16;
+constexpr int kAttnTargetGroups = 1024;  // four workgroups per CU of an MI355X
+
+// Max / sum over aligned segments of W lanes (16, 32 or 64), the result in
+// every lane of the segment: DPP swaps within each 16-lane row, then the
+// rows' results read from lanes 0, 16, 32 and 48.
+template <int W>
+__device__ __forceinline__ float seg_max(float v, int lane) {
+    v = fmaxf(v, dpp_f32<0xB1>(v));
+    v = fmaxf(v, dpp_f32<0x4E>(v));
+    v = fmaxf(v, dpp_f32<0x141>(v));
+    v = fmaxf(v, dpp_f32<0x140>(v));
+    if constexpr (W == 16) return v;
+    const float r0 = rows_f32(v, 0), r1 = rows_f32(v, 1), r2 = rows_f32(v, 2), r3 = rows_f32(v, 3);
+    if constexpr (W == 32) return lane < 32 ? fmaxf(r0, r1) : fmaxf(r2, r3);
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+template <int W>
+__device__ __forceinline__ float seg_sum(float v, int lane) {
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x141>(v);
+    v += dpp_f32<0x140>(v);
+    if constexpr (W == 16) return v;
+    const float r0 = rows_f32(v, 0), r1 = rows_f32(v, 1), r2 = rows_f32(v, 2), r3 = rows_f32(v, 3);
+    if constexpr (W == 32) return lane < 32 ? r0 + r1 : r2 + r3;
+    return (r0 + r1) + (r2 + r3);
+}
+
+// VD adjacent 16-bit values as raw words (one 32-bit word per two values),
+// loaded with one instruction when vec, else value by value (valid of them).
+template <int VD>
+struct VRaw {
+    uint32_t w[(VD + 1) / 2];
+};
+
+template <int VD>
+__device__ __forceinline__ VRaw<VD> load_vraw(const uint16_t* p, bool vec, int valid) {
+    VRaw<VD> r;
+    if (vec && valid == VD) {
+        if constexpr (VD == 1) {
+            r.w[0] = p[0];
+        } else if constexpr (VD == 2) {
+            r.w[0] = *reinterpret_cast<const uint32_t*>(p);
+        } else {
+            const uint2 v = *reinterpret_cast<const uint2*>(p);
+            r.w[0] = v.x;
+            r.w[1] = v.y;
+        }
+        return r;
+    }
+#pragma unroll
+    for (int i = 0; i < (VD + 1) / 2; ++i) r.w[i] = 0;
+#pragma unroll
+    for (int v = 0; v < VD; ++v)
+        if (v < valid) r.w[v >> 1] |= static_cast<uint32_t>(p[v]) << (16 * (v & 1));
+    return r;
+}
+
+template <int VD>
+__device__ __forceinline__ void unpack_vraw(const VRaw<VD>& r, bool bf16, float* out) {
+#pragma unroll
+    for (int v = 0; v < VD; ++v) out[v] = rd16(static_cast<uint16_t>(r.w[v >> 1] >> (16 * (v & 1))), bf16);
+}
+
+// LDS of the split kernel, in floats: q (rows of hd + pad, padded when
+// head slices read several rows at once) shares its space with `slots` (4,
+// or 2 where four would pass 64 KB) of the waves' sums, then the [TOK][G]
+// scores.
+constexpr int kAttnLdsFloats = 16384;
+__host__ __device__ constexpr int split_q_stride(int hd, int hs) { return hd + (hs > 1 ? 16 : 0); }
+__host__ __device__ constexpr int split_sum_floats(int hd, int group, int hs, int slots) {
+    return ((group * split_q_stride(hd, hs) > slots * group * hd ? group * split_q_stride(hd, hs) : slots * group * hd) +
+            3) &
+           ~3;
+}
+
+template <bool BF16, int G, int VD, int TOK>
 __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(
     const float* __restrict__ q_rot, const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ v_cache,
-    int64_t kv_width, int hd, int group, int64_t T, int L, float scale, float* __restrict__ part,
+    int64_t kv_width, int hd, int group, int64_t T, float scale, int vec, int slots, float* __restrict__ part,
     float* __restrict__ ml) {
-    extern __shared__ float sm[];
-    float* q_s = sm;                   // [group][hd], later the cross-wave sum
-    float* p_s = sm + group * hd;      // [group][L]
+    constexpr int HS = G < 4 ? G : 4;         // head slices
+    constexpr int HPL = G / HS;               // heads per lane in the score pass
+    constexpr int NTG = kAttnThreads / (4 * HS);  // token groups in the score pass
+    constexpr int TPL = TOK / NTG;            // tokens per lane in the score pass
+    constexpr int NV = TOK / kAttnWaves;      // value-pass tokens per wave
+    constexpr int NP = 2 * VD;                // 16-byte K pieces per quarter: hd / 32 <= 2 * VD
+    static_assert(TPL >= 1 && TPL * NTG == TOK, "whole tokens per lane");
+    static_assert(TPL * NP <= 16, "K pieces held in registers");
+    extern __shared__ float4 sm4[];
+    const int qs = split_q_stride(hd, HS);
+    float* q_s = reinterpret_cast<float*>(sm4);               // [group][qs], dead after the scores
+    float* buf = q_s;                                         // [slots][group][hd]: the waves' sums
+    float* p_t = q_s + split_sum_floats(hd, group, HS, slots);  // [TOK][G]: scores, then weights
     const int kvh = blockIdx.x, sp = blockIdx.y, nsplit = gridDim.y;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t t0 = static_cast<int64_t>(sp) * L;
-    const int n = static_cast<int>(min(static_cast<int64_t>(L), T - t0));
-    for (int i = threadIdx.x; i < group * hd; i += kAttnThreads)
-        q_s[i] = q_rot[static_cast<int64_t>(kvh) * group * hd + i];
-    __syncthreads();
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t t0 = static_cast<int64_t>(sp) * TOK;
+    const int n = static_cast<int>(min(static_cast<int64_t>(TOK), T - t0));
 
-    // Scores: a wave loads the rows of kTokUnroll tokens before using any;
-    // the V rows of its first tokens are loaded at the same time (vpre) so
-    // that the value pass does not start with a full memory latency.
-    float vpre[kTokUnroll][DPL];
-    for (int i0 = wave; i0 < n; i0 += kAttnWaves * kTokUnroll) {
-        float kv[kTokUnroll][DPL];
+    // Every global load is issued before the first wait: this thread's K
+    // pieces, its wave's V values, then the query heads into LDS.
+    // score-pass lane: tokens tg, tg + NTG, ..., head slice hs, quarter qd
+    const int tg = tid / (4 * HS), hs = (tid >> 2) % HS, qd = tid & 3;
+    const uint16_t* kbase = k_cache + t0 * kv_width + static_cast<int64_t>(kvh) * hd;
+    uint4 kraw[TPL][NP];
+    if (vec) {
 #pragma unroll
-        for (int u = 0; u < kTokUnroll; ++u) {
-            const int i = min(i0 + u * kAttnWaves, n - 1);
-            const uint16_t* kr = k_cache + (t0 + i) * kv_width + static_cast<int64_t>(kvh) * hd;
-            const uint16_t* vr = v_cache + (t0 + i) * kv_width + static_cast<int64_t>(kvh) * hd;
+        for (int j = 0; j < TPL; ++j) {
+            const uint16_t* kr = kbase + min(tg + NTG * j, n - 1) * kv_width;
 #pragma unroll
-            for (int j = 0; j < DPL; ++j) {
-                const int d = lane + 64 * j;
-                kv[u][j] = d < hd ? rd16(kr[d], BF16) : 0.0f;
-                if (i0 == wave) vpre[u][j] = d < hd ? rd16(vr[d], BF16) : 0.0f;
+            for (int it = 0; it < NP; ++it) {
+                const int pc = qd + 4 * it;
+                kraw[j][it] = 8 * pc < hd ? *reinterpret_cast<const uint4*>(kr + 8 * pc) : make_uint4(0, 0, 0, 0);
             }
         }
+    }
+    const int d0 = lane * VD;
+    const int valid = max(0, min(VD, hd - d0));
+    VRaw<VD> vraw[NV];
 #pragma unroll
-        for (int u = 0; u < kTokUnroll; ++u) {
-            const int i = i0 + u * kAttnWaves;
-            if (i >= n) break;
-            float acc[G];
+    for (int u = 0; u < NV; ++u) {
+        const int i = min(wave + u * kAttnWaves, n - 1);
+        vraw[u] = load_vraw<VD>(v_cache + (t0 + i) * kv_width + static_cast<int64_t>(kvh) * hd + d0, vec != 0, valid);
+    }
+    {
+        // the query heads: float4 pieces, all loaded before the first is stored
+        const float* qsrc = q_rot + static_cast<int64_t>(kvh) * group * hd;
+        if (vec) {  // hd % 8 == 0: rows of hd / 4 float4, 16-byte aligned at every kv head
+            constexpr int QV = (kMaxGroup * kMaxHeadDim / 4 + kAttnThreads - 1) / kAttnThreads;
+            const int hq = hd >> 2, nq = group * hq;
+            float4 qv[QV];  // loaded unconditionally (clamped index), so it stays in registers
 #pragma unroll
-            for (int h = 0; h < G; ++h) acc[h] = 0.0f;
+            for (int r = 0; r < QV; ++r) qv[r] = reinterpret_cast<const float4*>(qsrc)[min(tid + r * kAttnThreads, nq - 1)];
 #pragma unroll
-            for (int j = 0; j < DPL; ++j) {
-                const int d = lane + 64 * j;
-                if (d < hd) {
-#pragma unroll
-                    for (int h = 0; h < G; ++h)
-                        if (h < group) acc[h] = fmaf(q_s[h * hd + d], kv[u][j], acc[h]);
+            for (int r = 0; r < QV; ++r) {
+                const int i = tid + r * kAttnThreads;
+                if (i < nq) {
+                    const int row = i / hq;
+                    reinterpret_cast<float4*>(q_s)[row * (qs >> 2) + i - row * hq] = qv[r];
                 }
             }
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                if (h < group) {
-                    const float sum = plm_wave_sum(acc[h]);
-                    if (lane == kSumLane) p_s[h * L + i] = sum * scale;
-                }
+        } else {
+            for (int i = tid; i < group * hd; i += kAttnThreads) {
+                const int row = i / hd;
+                q_s[row * qs + i - row * hd] = qsrc[i];
             }
         }
     }
     __syncthreads();
 
-    for (int h = wave; h < group; h += kAttnWaves) {
-        float m = -INFINITY;
-        for (int i = lane; i < n; i += 64) m = fmaxf(m, p_s[h * L + i]);
-        m = wave_max_all(m);
-        float l = 0.0f;
-        for (int i = lane; i < n; i += 64) {
-            const float e = expf(p_s[h * L + i] - m);
-            p_s[h * L + i] = e;
-            l += e;
+    // Scores.  Quarter qd takes the 16-byte pieces qd, qd + 4, ... of the
+    // head (8 values each), or with vec unset (head dimensions not a
+    // multiple of 8) the single values qd, qd + 4, ...; head slice hs takes
+    // heads hs, hs + HS, ...  Heads past `group` repeat the last one and are
+    // dropped: no branch between the LDS reads, so they issue back to back.
+    {
+        float acc[TPL][HPL];
+#pragma unroll
+        for (int j = 0; j < TPL; ++j)
+#pragma unroll
+            for (int h = 0; h < HPL; ++h) acc[j][h] = 0.0f;
+        int qrow[HPL];
+#pragma unroll
+        for (int h = 0; h < HPL; ++h) qrow[h] = min(hs + HS * h, group - 1) * qs;
+        if (vec) {
+            const float4* q4 = reinterpret_cast<const float4*>(q_s);  // qs % 4 == 0: rows stay 16-byte aligned
+#pragma unroll
+            for (int it = 0; it < NP; ++it) {
+                const int pc = qd + 4 * it;
+                if (8 * pc < hd) {
+                    float4 qa[HPL], qb[HPL];
+#pragma unroll
+                    for (int h = 0; h < HPL; ++h) {
+                        qa[h] = q4[(qrow[h] + 8 * pc) >> 2];
+                        qb[h] = q4[((qrow[h] + 8 * pc) >> 2) + 1];
+                    }
+#pragma unroll
+                    for (int j = 0; j < TPL; ++j) {
+                        const uint32_t wv[4] = {kraw[j][it].x, kraw[j][it].y, kraw[j][it].z, kraw[j][it].w};
+                        float kf[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            kf[e] = rd16(static_cast<uint16_t>(wv[e >> 1] >> (16 * (e & 1))), BF16);
+#pragma unroll
+                        for (int h = 0; h < HPL; ++h) {
+                            const float qv[8] = {qa[h].x, qa[h].y, qa[h].z, qa[h].w,
+                                                 qb[h].x, qb[h].y, qb[h].z, qb[h].w};
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) acc[j][h] = fmaf(qv[e], kf[e], acc[j][h]);
+                        }
+                    }
+                }
+            }
+        } else {
+            for (int d = qd; d < hd; d += 4) {
+                float qv[HPL];
+#pragma unroll
+                for (int h = 0; h < HPL; ++h) qv[h] = q_s[qrow[h] + d];
+#pragma unroll
+                for (int j = 0; j < TPL; ++j) {
+                    const float kv = rd16(kbase[min(tg + NTG * j, n - 1) * kv_width + d], BF16);
+#pragma unroll
+                    for (int h = 0; h < HPL; ++h) acc[j][h] = fmaf(qv[h], kv, acc[j][h]);
+                }
+            }
         }
-        l = wave_sum_all(l);
-        if (lane == 0) {
+#pragma unroll
+        for (int j = 0; j < TPL; ++j)
+#pragma unroll
+            for (int h = 0; h < HPL; ++h) {
+                acc[j][h] += dpp_f32<0xB1>(acc[j][h]);  // + the xor-1 lane's quarter
+                acc[j][h] += dpp_f32<0x4E>(acc[j][h]);  // + the xor-2 lanes' pair
+            }
+        if (qd == 0) {
+#pragma unroll
+            for (int j = 0; j < TPL; ++j) {
+                const int t = tg + NTG * j;
+#pragma unroll
+                for (int h = 0; h < HPL; ++h) p_t[t * G + hs + HS * h] = t < n ? acc[j][h] * scale : -INFINITY;
+            }
+        }
+    }
+    __syncthreads();
+
+    // Softmax: lane tt of a TOK-lane segment holds token tt of head h.
+    for (int h = tid / TOK; h < group; h += kAttnThreads / TOK) {
+        const int tt = tid % TOK;
+        const float sc = tt < n ? p_t[tt * G + h] : -INFINITY;
+        const float m = seg_max<TOK>(sc, lane);
+        const float e = tt < n ? expf(sc - m) : 0.0f;
+        const float l = seg_sum<TOK>(e, lane);
+        p_t[tt * G + h] = e;
+        if (tt == 0) {
             const int64_t slot = (static_cast<int64_t>(kvh) * nsplit + sp) * group + h;
             ml[slot * 2] = m;
             ml[slot * 2 + 1] = l;
@@ -227,141 +402,257 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(
     }
     __syncthreads();
 
-    float acc[G][DPL];
+    // Values: this wave's tokens wave, wave + 4, ... (already loaded); the
+    // weights of all G heads of a token are one contiguous LDS read.
+    float acc[G][VD];
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) acc[h][j] = 0.0f;
-    for (int i0 = wave; i0 < n; i0 += kAttnWaves * kTokUnroll) {
-        float vv[kTokUnroll][DPL];
+        for (int v = 0; v < VD; ++v) acc[h][v] = 0.0f;
 #pragma unroll
-        for (int u = 0; u < kTokUnroll; ++u) {
-            const int i = min(i0 + u * kAttnWaves, n - 1);
-            const uint16_t* vr = v_cache + (t0 + i) * kv_width + static_cast<int64_t>(kvh) * hd;
+    for (int u = 0; u < NV; ++u) {
+        const int i = wave + u * kAttnWaves;
+        if (i >= n) break;
+        float vv[VD];
+        unpack_vraw<VD>(vraw[u], BF16, vv);
+        float pw[G];
+        if constexpr (G % 4 == 0) {
 #pragma unroll
-            for (int j = 0; j < DPL; ++j) {
-                const int d = lane + 64 * j;
-                vv[u][j] = i0 == wave ? vpre[u][j] : (d < hd ? rd16(vr[d], BF16) : 0.0f);
+            for (int h4 = 0; h4 < G / 4; ++h4) {
+                const float4 w4 = reinterpret_cast<const float4*>(p_t + i * G)[h4];
+                pw[4 * h4] = w4.x;
+                pw[4 * h4 + 1] = w4.y;
+                pw[4 * h4 + 2] = w4.z;
+                pw[4 * h4 + 3] = w4.w;
             }
+        } else {
+#pragma unroll
+            for (int h = 0; h < G; ++h) pw[h] = p_t[i * G + h];
         }
 #pragma unroll
-        for (int u = 0; u < kTokUnroll; ++u) {
-            const int i = i0 + u * kAttnWaves;
-            if (i >= n) break;
+        for (int h = 0; h < G; ++h)
 #pragma unroll
-            for (int j = 0; j < DPL; ++j) {
-                if (lane + 64 * j < hd) {
-#pragma unroll
-                    for (int h = 0; h < G; ++h)
-                        if (h < group) acc[h][j] = fmaf(p_s[h * L + i], vv[u][j], acc[h][j]);
-                }
-            }
-        }
+            for (int v = 0; v < VD; ++v) acc[h][v] = fmaf(pw[h], vv[v], acc[h][v]);
     }
-    // Waves add their sums into q_s (free again) one after another.
-    for (int w = 0; w < kAttnWaves; ++w) {
-        if (wave == w) {
+    // The waves' sums go to LDS (over q, read by no wave any more).  With
+    // four slots, one barrier, then each thread adds ((w0 + w2) + (w1 + w3))
+    // for outputs tid, tid + 256, ..., stored 256 lanes wide.  With two,
+    // waves 2 and 3 hand over first and waves 0 and 1 leave w0 + w2 and
+    // w1 + w3 in their slots: the same sums, one barrier more.
+    const int gh = group * hd;
+    float* dst = part + (static_cast<int64_t>(kvh) * nsplit + sp) * gh;
+    if (slots == 4) {
+        if (valid > 0) {
 #pragma unroll
-            for (int h = 0; h < G; ++h) {
+            for (int h = 0; h < G; ++h)
+                if (h < group)
 #pragma unroll
-                for (int j = 0; j < DPL; ++j) {
-                    const int d = lane + 64 * j;
-                    if (h < group && d < hd) q_s[h * hd + d] = (w == 0 ? 0.0f : q_s[h * hd + d]) + acc[h][j];
-                }
-            }
+                    for (int v = 0; v < VD; ++v)
+                        if (v < valid) buf[wave * gh + h * hd + d0 + v] = acc[h][v];
         }
         __syncthreads();
+        for (int i = tid; i < gh; i += kAttnThreads)
+            dst[i] = (buf[i] + buf[2 * gh + i]) + (buf[gh + i] + buf[3 * gh + i]);
+        return;
     }
-    float* dst = part + (static_cast<int64_t>(kvh) * nsplit + sp) * group * hd;
-    for (int i = threadIdx.x; i < group * hd; i += kAttnThreads) dst[i] = q_s[i];
+    const int slot = wave & 1;
+    if (wave >= 2 && valid > 0) {
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+            if (h < group)
+#pragma unroll
+                for (int v = 0; v < VD; ++v)
+                    if (v < valid) buf[slot * gh + h * hd + d0 + v] = acc[h][v];
+    }
+    __syncthreads();
+    if (wave < 2 && valid > 0) {
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+            if (h < group)
+#pragma unroll
+                for (int v = 0; v < VD; ++v)
+                    if (v < valid) {
+                        float* b = buf + slot * gh + h * hd + d0 + v;
+                        *b = acc[h][v] + *b;
+                    }
+    }
+    __syncthreads();
+    for (int i = tid; i < gh; i += kAttnThreads) dst[i] = buf[i] + buf[gh + i];
+}
+
+// The launchers return false for a shape no kernel instance covers.
+template <bool BF16, int G, int TOK>
+bool launch_split_t(int vd, dim3 grid, size_t lds, hipStream_t st, const float* q_rot, const uint16_t* kc,
+                    const uint16_t* vc, int64_t kvw, int hd, int group, int64_t T, float scale, int vec, int slots,
+                    float* part, float* ml) {
+    if (vd <= 1) {
+        hipLaunchKernelGGL((attention_split_kernel<BF16, G, 1, TOK>), grid, dim3(kAttnThreads), lds, st, q_rot, kc, vc,
+                           kvw, hd, group, T, scale, vec, slots, part, ml);
+        return true;
+    }
+    if (vd == 2) {
+        hipLaunchKernelGGL((attention_split_kernel<BF16, G, 2, TOK>), grid, dim3(kAttnThreads), lds, st, q_rot, kc, vc,
+                           kvw, hd, group, T, scale, vec, slots, part, ml);
+        return true;
+    }
+    if constexpr (8 * (TOK * (G < 4 ? G : 4) / 64) <= 16) {  // K pieces per lane: 2 * VD per token
+        hipLaunchKernelGGL((attention_split_kernel<BF16, G, 4, TOK>), grid, dim3(kAttnThreads), lds, st, q_rot, kc, vc,
+                           kvw, hd, group, T, scale, vec, slots, part, ml);
+        return true;
+    }
+    return false;
 }
 
 template <bool BF16, int G>
-void launch_split_g(int dpl, dim3 grid, size_t lds, hipStream_t st, const float* q_rot, const uint16_t* kc,
-                    const uint16_t* vc, int64_t kvw, int hd, int group, int64_t T, int L, float scale, float* part,
-                    float* ml) {
-    if (dpl <= 1) {
-        hipLaunchKernelGGL((attention_split_kernel<BF16, G, 1>), grid, dim3(kAttnThreads), lds, st, q_rot, kc, vc, kvw,
-                           hd, group, T, L, scale, part, ml);
-    } else if (dpl == 2) {
-        hipLaunchKernelGGL((attention_split_kernel<BF16, G, 2>), grid, dim3(kAttnThreads), lds, st, q_rot, kc, vc, kvw,
-                           hd, group, T, L, scale, part, ml);
-    } else {
-        hipLaunchKernelGGL((attention_split_kernel<BF16, G, 4>), grid, dim3(kAttnThreads), lds, st, q_rot, kc, vc, kvw,
-                           hd, group, T, L, scale, part, ml);
+bool launch_split_g(int tok, int vd, dim3 grid, size_t lds, hipStream_t st, const float* q_rot, const uint16_t* kc,
+                    const uint16_t* vc, int64_t kvw, int hd, int group, int64_t T, float scale, int vec, int slots,
+                    float* part, float* ml) {
+    if constexpr (G >= 4) {
+        if (tok == 16)
+            return launch_split_t<BF16, G, 16>(vd, grid, lds, st, q_rot, kc, vc, kvw, hd, group, T, scale, vec, slots,
+                                               part, ml);
     }
+    if constexpr (G >= 2) {
+        if (tok == 32)
+            return launch_split_t<BF16, G, 32>(vd, grid, lds, st, q_rot, kc, vc, kvw, hd, group, T, scale, vec, slots,
+                                               part, ml);
+    }
+    if (tok != 64) return false;
+    return launch_split_t<BF16, G, 64>(vd, grid, lds, st, q_rot, kc, vc, kvw, hd, group, T, scale, vec, slots, part,
+                                       ml);
+}
+
+// Heads per kv head rounded up to the kernels' G.
+int split_g(int group) { return group <= 1 ? 1 : (group <= 2 ? 2 : (group <= 4 ? 4 : (group <= 8 ? 8 : kMaxGroup))); }
+
+int split_hs(int g) { return g < 4 ? g : 4; }
+int split_vd(int hd) { return hd <= 64 ? 1 : (hd <= 128 ? 2 : 4); }
+
+// Tokens per split: 64 (32 where four tokens per lane of 256-dimension heads
+// would not fit the registers), halved while the launch has fewer than
+// kAttnTargetGroups workgroups, down to 16 and to no fewer than the score
+// pass's token groups (64 / min(G, 4)).  The work per workgroup is a chain
+// of short dependent steps, so several workgroups per CU hide each other's
+// latencies; the merge's cost grows only slowly with the split count.
+int split_tokens(int64_t nkv, int64_t T, int g, int hd) {
+    const int hs = split_hs(g);
+    int tok = split_vd(hd) == 4 && hs == 4 ? kMaxSplitTokens / 2 : kMaxSplitTokens;
+    while (tok > kMinSplitTokens && tok / 2 >= kMaxSplitTokens / hs && nkv * ((T + tok - 1) / tok) < kAttnTargetGroups)
+        tok /= 2;
+    return tok;
+}
+
+// Slots for the waves' sums: four unless that passes kAttnLdsFloats.
+int split_slots(int hd, int group, int tok) {
+    return split_sum_floats(hd, group, split_hs(split_g(group)), 4) + split_g(group) * tok <= kAttnLdsFloats ? 4 : 2;
+}
+
+size_t split_lds_bytes(int hd, int group, int tok, int slots) {
+    return static_cast<size_t>(split_sum_floats(hd, group, split_hs(split_g(group)), slots) + split_g(group) * tok) *
+           sizeof(float);
 }
 
 template <bool BF16>
-void launch_split(dim3 grid, size_t lds, hipStream_t st, const float* q_rot, const uint16_t* kc, const uint16_t* vc,
-                  int64_t kvw, int hd, int group, int64_t T, int L, float scale, float* part, float* ml) {
-    const int dpl = (hd + 63) / 64;
-    if (group <= 1) {
-        launch_split_g<BF16, 1>(dpl, grid, lds, st, q_rot, kc, vc, kvw, hd, group, T, L, scale, part, ml);
-    } else if (group <= 2) {
-        launch_split_g<BF16, 2>(dpl, grid, lds, st, q_rot, kc, vc, kvw, hd, group, T, L, scale, part, ml);
-    } else if (group <= 4) {
-        launch_split_g<BF16, 4>(dpl, grid, lds, st, q_rot, kc, vc, kvw, hd, group, T, L, scale, part, ml);
-    } else if (group <= 8) {
-        launch_split_g<BF16, 8>(dpl, grid, lds, st, q_rot, kc, vc, kvw, hd, group, T, L, scale, part, ml);
-    } else {
-        launch_split_g<BF16, kMaxGroup>(dpl, grid, lds, st, q_rot, kc, vc, kvw, hd, group, T, L, scale, part, ml);
+bool launch_split(int tok, dim3 grid, size_t lds, hipStream_t st, const float* q_rot, const uint16_t* kc,
+                  const uint16_t* vc, int64_t kvw, int hd, int group, int64_t T, float scale, int vec, int slots,
+                  float* part, float* ml) {
+    const int vd = split_vd(hd);
+    switch (split_g(group)) {
+        case 1:
+            return launch_split_g<BF16, 1>(tok, vd, grid, lds, st, q_rot, kc, vc, kvw, hd, group, T, scale, vec, slots,
+                                           part, ml);
+        case 2:
+            return launch_split_g<BF16, 2>(tok, vd, grid, lds, st, q_rot, kc, vc, kvw, hd, group, T, scale, vec, slots,
+                                           part, ml);
+        case 4:
+            return launch_split_g<BF16, 4>(tok, vd, grid, lds, st, q_rot, kc, vc, kvw, hd, group, T, scale, vec, slots,
+                                           part, ml);
+        case 8:
+            return launch_split_g<BF16, 8>(tok, vd, grid, lds, st, q_rot, kc, vc, kvw, hd, group, T, scale, vec, slots,
+                                           part, ml);
+        default:
+            return launch_split_g<BF16, kMaxGroup>(tok, vd, grid, lds, st, q_rot, kc, vc, kvw, hd, group, T, scale, vec,
+                                                   slots, part, ml);
     }
 }
 
 // context[h][d] = sum_s exp(m_s - M) acc_s[d] / sum_s exp(m_s - M) l_s.
-// One workgroup per query head: the split factors exp(m_s - M) go to LDS,
-// then thread (c, d) sums splits c, c + C, ... of dimension d with several
-// loads in flight, and the C partial sums are added in LDS.
+// Workgroup (head, 64-dimension slice); lane = dimension, wave w takes the
+// splits w, w + 16, ...  A wave issues its first kMergeBatch partials (and,
+// lane u, the max of its u-th split) before anything waits, then works out M
+// and the denominator itself (lanes over the splits, no barrier), so the
+// partials' round trip and the (m, l) one overlap.  Lane u's exp(m_s - M)
+// reaches the other lanes by readlane: one exp per lane and batch.  The 16
+// waves' sums meet in LDS, added in wave order.
+constexpr int kMergeBatch = 20;  // splits per wave in flight: 320 per pass
+
 __global__ __launch_bounds__(kMergeThreads) void attention_merge_kernel(const float* __restrict__ part,
                                                                        const float* __restrict__ ml,
                                                                        float* __restrict__ context, int hd, int group,
                                                                        int nsplit) {
-    __shared__ float f_s[kMaxSplits];
-    __shared__ float red[kMergeThreads / 64];
-    __shared__ float sums[kMergeThreads];
+    constexpr int W = kMergeThreads / 64;
+    constexpr int KM = 4;  // (m, l) pairs per lane kept in registers
+    __shared__ float sums[W][64];
     const int head = blockIdx.x;
     const int kvh = head / group, hl = head - kvh * group;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int d = blockIdx.y * 64 + lane;
+    const int dc = min(d, hd - 1);  // lanes past the head's end read a valid column and store nothing
     const int64_t base = static_cast<int64_t>(kvh) * nsplit * group + hl;  // slot of split s: base + s * group
-    float m = -INFINITY;
-    for (int sp = tid; sp < nsplit; sp += kMergeThreads) m = fmaxf(m, ml[(base + static_cast<int64_t>(sp) * group) * 2]);
-    m = wave_max_all(m);
-    if (lane == 0) red[wave] = m;
-    __syncthreads();
-    m = red[0];
-    for (int w = 1; w < kMergeThreads / 64; ++w) m = fmaxf(m, red[w]);
-    __syncthreads();
-    float den = 0.0f;
-    for (int sp = tid; sp < nsplit; sp += kMergeThreads) {
-        const int64_t slot = base + static_cast<int64_t>(sp) * group;
-        const float f = expf(ml[slot * 2] - m);
-        f_s[sp] = f;
-        den += f * ml[slot * 2 + 1];
-    }
-    den = block_sum(den, red);  // its barriers also publish f_s
-    const int C = kMergeThreads / hd;  // split lanes per dimension (hd <= kMergeThreads)
-    const int c = tid / hd, d = tid - c * hd;
-    float num = 0.0f;
-    if (c < C) {
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        int sp = c;
-        for (; sp + 3 * C < nsplit; sp += 4 * C) {
+
+    float pv[kMergeBatch], mlane;
+    auto load_batch = [&](int s0) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int64_t slot = base + static_cast<int64_t>(sp + u * C) * group;
-                acc[u] = fmaf(f_s[sp + u * C], part[slot * hd + d], acc[u]);
-            }
+        for (int u = 0; u < kMergeBatch; ++u) {
+            const int s = min(s0 + W * u, nsplit - 1);
+            pv[u] = part[(base + static_cast<int64_t>(s) * group) * hd + dc];
         }
-        for (; sp < nsplit; sp += C) acc[0] = fmaf(f_s[sp], part[(base + static_cast<int64_t>(sp) * group) * hd + d], acc[0]);
-        num = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        mlane = ml[(base + static_cast<int64_t>(min(s0 + W * lane, nsplit - 1)) * group) * 2];
+    };
+    load_batch(wave);
+
+    float ms[KM], ls[KM];
+#pragma unroll
+    for (int k = 0; k < KM; ++k) {
+        const int s = min(lane + 64 * k, nsplit - 1);
+        const int64_t slot = base + static_cast<int64_t>(s) * group;
+        ms[k] = ml[slot * 2];
+        ls[k] = ml[slot * 2 + 1];
     }
-    sums[tid] = num;
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < KM; ++k)
+        if (lane + 64 * k < nsplit) m = fmaxf(m, ms[k]);
+    for (int s = lane + 64 * KM; s < nsplit; s += 64) m = fmaxf(m, ml[(base + static_cast<int64_t>(s) * group) * 2]);
+    m = seg_max<64>(m, lane);
+    float den = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KM; ++k)
+        if (lane + 64 * k < nsplit) den += expf(ms[k] - m) * ls[k];
+    for (int s = lane + 64 * KM; s < nsplit; s += 64) {
+        const int64_t slot = base + static_cast<int64_t>(s) * group;
+        den += expf(ml[slot * 2] - m) * ml[slot * 2 + 1];
+    }
+    den = seg_sum<64>(den, lane);
+
+    float acc = 0.0f;
+    for (int s0 = wave;; s0 += W * kMergeBatch) {
+        const float fl = expf(mlane - m);
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u)
+            if (s0 + W * u < nsplit)
+                acc = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(fl), u)), pv[u], acc);
+        if (s0 + W * kMergeBatch >= nsplit) break;
+        load_batch(s0 + W * kMergeBatch);
+    }
+    sums[wave][lane] = acc;
     __syncthreads();
-    if (tid < hd) {
+    if (wave == 0 && d < hd) {
         float t = 0.0f;
-        for (int k = 0; k < C; ++k) t += sums[k * hd + tid];
-        context[static_cast<int64_t>(head) * hd + tid] = t / den;
+#pragma unroll
+        for (int w = 0; w < W; ++w) t += sums[w][lane];
+        context[static_cast<int64_t>(head) * hd + d] = t / den;
     }
 }
 
@@ -467,15 +758,6 @@ struct DenseArgs {
     float eps, theta;
 };
 
-// Attention split length: about eight workgroups per CU over (kv head, split),
-// at least 16 tokens each, at most kMaxSplitLen.
-int split_len_for(int64_t T, int64_t nkv) {
-    const int64_t target = std::max<int64_t>(1, 8 * plm::cu_count() / std::max<int64_t>(1, nkv));
-    int64_t L = (T + target - 1) / target;
-    L = ((L + 15) / 16) * 16;
-    return static_cast<int>(std::min<int64_t>(std::max<int64_t>(L, 16), kMaxSplitLen));
-}
-
 template <bool BF16>
 int dense_decode(KvSession* s, int64_t layer, const DenseArgs& a) {
     // Attention-stage checks keep the reference's codes, offset by 100.
@@ -496,8 +778,8 @@ int dense_decode(KvSession* s, int64_t layer, const DenseArgs& a) {
     if (hipGetDevice(&dev) != hipSuccess || dev != s->device) return plm::fail(107, "session lives on another device");
 
     const int64_t H = a.hidden_size, I = a.inter, T = pos + 1;
-    const int L = split_len_for(T, a.nkv);
-    const int64_t nsplit = (T + L - 1) / L;
+    const int tok = split_tokens(a.nkv, T, split_g(static_cast<int>(group)), static_cast<int>(hd));
+    const int64_t nsplit = (T + tok - 1) / tok;
     if (nsplit > kMaxSplits) return plm::fail(106, "context too long for one attention launch");
     // workspace: q f32[H] | k, v f32[kvw] | q_rot f32[H] | part | ml | ctx f32[H] | proj f32[H] | resid f32[H]
     //            | post u16[H] | gate, up f32[I]
@@ -545,13 +827,21 @@ int dense_decode(KvSession* s, int64_t layer, const DenseArgs& a) {
     if ((code = plm::check_launch("q/k rope and cache append")) != 0) return code;
     st.tentative += 1;  // the row is in the cache once the stream reaches here
 
-    const size_t lds = static_cast<size_t>(group) * (hd + L) * sizeof(float);
+    const int slots = split_slots(static_cast<int>(hd), static_cast<int>(group), tok);
+    const size_t lds = split_lds_bytes(static_cast<int>(hd), static_cast<int>(group), tok, slots);
     const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
-    launch_split<BF16>(dim3(static_cast<unsigned>(a.nkv), static_cast<unsigned>(nsplit)), lds, stream, q_rot,
-                       s->k_rows(layer), s->v_rows(layer), kvw, static_cast<int>(hd), static_cast<int>(group), T, L,
-                       scale, part, ml);
+    // 16-byte K pieces need head dimensions in multiples of 8 and rows that
+    // keep them aligned; the value pass's wider loads then also stay aligned
+    const int vec = hd % 8 == 0 && kvw % 8 == 0 && plm::aligned16(s->k_rows(layer)) &&
+                    plm::aligned16(s->v_rows(layer));
+    if (!launch_split<BF16>(tok, dim3(static_cast<unsigned>(a.nkv), static_cast<unsigned>(nsplit)), lds, stream,
+                            q_rot, s->k_rows(layer), s->v_rows(layer), kvw, static_cast<int>(hd),
+                            static_cast<int>(group), T, scale, vec, slots, part, ml))
+        return plm::fail(106, "no attention kernel for %d-token splits of head_dim %lld", tok,
+                         static_cast<long long>(hd));
     if ((code = plm::check_launch("attention split")) != 0) return code;
-    hipLaunchKernelGGL(attention_merge_kernel, dim3(static_cast<unsigned>(a.nh)), dim3(kMergeThreads), 0, stream,
+    hipLaunchKernelGGL(attention_merge_kernel, dim3(static_cast<unsigned>(a.nh), static_cast<unsigned>((hd + 63) / 64)),
+                       dim3(kMergeThreads), 0, stream,
                        part, ml, ctx,
                        static_cast<int>(hd), static_cast<int>(group), static_cast<int>(nsplit));
     if ((code = plm::check_launch("attention merge")) != 0) return code;

@@ -95,13 +95,19 @@ def _rel(a, b):
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
 
 
-@pytest.mark.parametrize("dtype,extras,shape", [
-    (torch.float16, False, (8, 16, 2, 1)),        # the reference test's layer
-    (torch.bfloat16, True, (256, 512, 8, 2)),     # biases, q/k norm, head_dim 32
-    (torch.float16, True, (512, 384, 4, 4)),      # head_dim 128, no grouping
-    (torch.bfloat16, False, (960, 640, 15, 5)),   # 3 query heads per kv head, head_dim 64
+@pytest.mark.parametrize("dtype,extras,shape,ctx", [
+    (torch.float16, False, (8, 16, 2, 1), 30),        # the reference test's layer
+    (torch.bfloat16, True, (256, 512, 8, 2), 30),     # biases, q/k norm, head_dim 32
+    (torch.float16, True, (512, 384, 4, 4), 30),      # head_dim 128, no grouping
+    (torch.bfloat16, False, (960, 640, 15, 5), 30),   # 3 query heads per kv head, head_dim 64
+    (torch.float16, False, (480, 256, 12, 4), 200),   # head_dim 40: some lanes without a K piece
+    (torch.bfloat16, False, (432, 256, 12, 4), 200),  # head_dim 36: scalar K reads
+    (torch.bfloat16, False, (1728, 512, 9, 1), 150),  # 9 query heads per kv head, head_dim 192
+    (torch.float16, True, (4096, 512, 16, 1), 300),   # 16 query heads per kv head, head_dim 256: two sum slots
+    (torch.bfloat16, False, (960, 640, 15, 5), 1700),  # 32-token splits
+    (torch.float16, False, (1024, 256, 32, 8), 2040),  # 64-token splits with 4 query heads per kv head
 ])
-def test_decode_steps_match_the_oracle(nat, dtype, extras, shape):
+def test_decode_steps_match_the_oracle(nat, dtype, extras, shape, ctx):
     H, I, nh, nkv = shape
     dc = 1 if dtype == torch.bfloat16 else 0
     kvw = H // nh * nkv
@@ -111,10 +117,10 @@ def test_decode_steps_match_the_oracle(nat, dtype, extras, shape):
     # by 4.9e-3 in bf16.
     w, norms, extra, rng = _layer(H + I, H, I, nh, nkv, dc, extras, scale=0.1 if H <= 8 else 0.02)
     dev_w, opt = _device_layer(nat, w, norms, extra, dtype)
-    ours = nat.NativeKvSession(layer_count=2, max_seq_len=64, kv_width=kvw, dtype=dtype)
-    ora = kvo.KvSessionOracle(2, 64, kvw, dc)
-    pre = kvo.f32_to_u16(rng.standard_normal((2, 30, kvw)).astype(np.float32), dc)
-    ours.append_committed(1, _t(pre[0], dtype), _t(pre[1], dtype), count=30)
+    ours = nat.NativeKvSession(layer_count=2, max_seq_len=ctx + 34, kv_width=kvw, dtype=dtype)
+    ora = kvo.KvSessionOracle(2, ctx + 34, kvw, dc)
+    pre = kvo.f32_to_u16(rng.standard_normal((2, ctx, kvw)).astype(np.float32), dc)
+    ours.append_committed(1, _t(pre[0], dtype), _t(pre[1], dtype), count=ctx)
     ora.append(1, pre[0], pre[1], tentative=False)
     kw = dict(num_heads=nh, num_kv_heads=nkv, rms_eps=1e-6, rope_theta=10000.0)
     for step in range(7):
@@ -134,8 +140,14 @@ def test_decode_steps_match_the_oracle(nat, dtype, extras, shape):
     k, v = ours.copy_layer(1)
     kw_, vw_ = ora.copy_layer(1)
     for a, b in ((k, kw_), (v, vw_)):
-        a = _bits(a).astype(np.int32)
-        assert a.shape == b.shape and np.abs(a - b.astype(np.int32)).max() <= 1
+        a = _bits(a)
+        assert a.shape == b.shape
+        # within one unit in the last place, or (where RoPE cancels, leaving a
+        # value far below the row's scale) within 1e-3 of the cache's largest value
+        close_bits = np.abs(a.astype(np.int32) - b.astype(np.int32)) <= 1
+        af, bf = kvo.u16_to_f32(a, dc), kvo.u16_to_f32(b, dc)
+        close_abs = np.abs(af - bf) <= 1e-3 * np.abs(bf).max()
+        assert np.all(close_bits | close_abs)
     assert ours.committed_length(0) == 0
     ours.close()
 
