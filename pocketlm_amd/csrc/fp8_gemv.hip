@@ -35,6 +35,7 @@
 #include <cstdint>
 #include <cstring>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "common.h"
@@ -71,9 +72,12 @@ struct RowsArgs {
     int64_t K;
     int64_t scale_cols;
     int tiles_per_group;
-    int nchunks;
+    int nblocks;          // 128-column blocks per row: ceil(K / 128)
     int m_total;
     int m0;
+    int mc;               // activation rows of this launch (m0 .. m0 + mc - 1), at most kMaxM
+    uint16_t* hhi;        // SiLU epilogue: the bf16 hi / lo planes of silu(gate) * up, element (g, m, row)
+    uint16_t* hlo;        //   at ((g * m_total + m) * out_ld + row)
     // Groups of different row counts (the many-linear entry point, one weight
     // per group): group g owns tiles [vtile[g], vtile[g+1]) of the grid and
     // writes its vrows[g] rows to vout[g] as [m_total][vrows[g]].  nvar = 0:
@@ -93,7 +97,8 @@ struct RowsArgs {
 struct CombineArgs {
     const uint8_t* w[kMaxGroups];
     const float* s[kMaxGroups];
-    const float* act;     // activations of group g: act + ((g_base+g)*m_total + m) * K
+    const uint16_t* act_hi;  // activations of group g, bf16 hi / lo planes of the SiLU intermediate:
+    const uint16_t* act_lo;  //   element ((g_base+g)*m_total + m) * K + col
     const float* route;   // route of (g, m): route[(g_base+g)*route_sg + m*route_sm], or null (= 1)
     float* out;
     int64_t rows;
@@ -103,7 +108,7 @@ struct CombineArgs {
     int64_t route_sm;
     int ngroups;
     int g_base;
-    int cps;              // chunks per group segment
+    int nbe;              // 128-column blocks per group segment
     int tiles_per_group;  // per_group_out only
     int per_group_out;    // 1: out[(g_base+g)*m_total + m][row]; 0: out[m][row] summed over groups
     int split_last;       // (summed mode) the last group is not summed: its own tiles write it, with
@@ -113,42 +118,12 @@ struct CombineArgs {
     int zero_skip;        // skip (g, m) whose route is exactly 0
     int m_total;
     int m0;
+    int mc;               // activation rows of this launch
     const MoePlan* plan;  // as in RowsArgs (tab rows 4-5 for the down matrices)
     int ndev;
     int fused;            // split_last computed inside the routed tiles (fp8_combine_kernel FUSED)
     uint16_t* out_bf16;   // fused only: bf16(bf16(out) + bf16(out_last)), or null
 };
-
-__device__ __forceinline__ float dot16(const float* w, const float* x) {
-    float p = w[0] * x[0];
-#pragma unroll
-    for (int j = 1; j < 16; ++j) p = fmaf(w[j], x[j], p);
-    return p;
-}
-
-__device__ __forceinline__ void decode16(const uint4& q, float* w) {
-    plm_decode4_e4m3(q.x, w);
-    plm_decode4_e4m3(q.y, w + 4);
-    plm_decode4_e4m3(q.z, w + 8);
-    plm_decode4_e4m3(q.w, w + 12);
-}
-
-__device__ __forceinline__ void zero_nans16(float* w) {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) w[j] = (w[j] != w[j]) ? 0.0f : w[j];
-}
-
-__device__ __forceinline__ void load_x16(const float* p, float* x) {
-    const float4* p4 = reinterpret_cast<const float4*>(p);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float4 v = p4[i];
-        x[4 * i + 0] = v.x;
-        x[4 * i + 1] = v.y;
-        x[4 * i + 2] = v.z;
-        x[4 * i + 3] = v.w;
-    }
-}
 
 static_assert(kMaxGroups == 64, "the plan maps one lane of the first wave to each group");
 struct PlanShared {
@@ -365,29 +340,333 @@ __global__ __launch_bounds__(512) void moe_route_plan_kernel(const float* __rest
     }
 }
 
-// 16 activations of row m at column col, from the fp32 or (XB) the bf16
-// copy; both give the same fp32 values.
-template <bool XB>
-__device__ __forceinline__ void load_row_x16(const RowsArgs& a, int m, int64_t col, float* x) {
-    const int64_t off = static_cast<int64_t>(a.m0 + m) * a.x_stride + col;
-    if constexpr (XB) {
-        const uint4* p = reinterpret_cast<const uint4*>(a.xb + off);
-        const uint4 h0 = p[0], h1 = p[1];
-        const uint32_t h[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+// ------------------------------------------------------------------ matrix-core tiles
+//
+// A tile is 8 weight rows by one 128-column block (one block of the scale
+// grid).  The 16 rows of the A operand of v_mfma_f32_16x16x32_bf16 are the
+// pairs (weight row r, half h) = (i & 7, i >> 3): lane l (i = l & 15,
+// quarter q = l >> 4) loads the 16 bytes at columns 64h + 16q of row r, so
+// one load instruction reads 8 whole 128-byte lines.  The 16 columns of the
+// B operand are the pairs (activation row m, half h') = (n & 7, n >> 3) and
+// hold the same columns of activation row m, so D[(r, h)][(m, h')] is the
+// dot of weight row r with activation row m over half h of the block when
+// h == h' (the other half of D is not used).  The lane's 16 bytes are two
+// MFMAs' worth (8 bf16 each); e4m3 -> bf16 is exact.  Each block's D is
+// scaled into the accumulators, acc = fma(D, scale, acc), and the two halves
+// are added after the last block, acc(h = 0) + acc(h = 1).
+//
+// Activation rows are MFMA columns: a column's result depends only on that
+// column's inputs, so an M-row call returns, row for row, the bits of M
+// one-row calls.  bf16 activations are one B operand; fp32 activations are
+// split into hi (the upper 16 bits) + lo (the remainder rounded to bf16),
+// two more MFMAs, within 2^-17 relative of the fp32 value.
+//
+// NaN weight bytes count as 0 (fp8_linear.cpp:31-33).  The hot loop decodes
+// them as NaN; a wave whose accumulators come out NaN runs its blocks again
+// with NaN bytes zeroed and infinite or NaN activations split exactly (hi =
+// the value, lo = 0).  Rows and activations without such values give the
+// same bits in both passes.
+
+typedef __bf16 plm_bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 plm_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float plm_f32x4 __attribute__((ext_vector_type(4)));
+
+// Weight bytes are read once per call: nontemporal loads keep them from
+// displacing the activations and scales in the caches.
+__device__ __forceinline__ plm_u32x4 wload16(const void* p) {
+    return __builtin_nontemporal_load((const __attribute__((address_space(1))) plm_u32x4*)(p));
+}
+
+__device__ __forceinline__ plm_u32x4 xload16(const void* p) {
+    return *(const __attribute__((address_space(1))) plm_u32x4*)(p);
+}
+
+template <bool HI>
+__device__ __forceinline__ uint32_t e4m3_pair_to_bf16(uint32_t v) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v, 1.0f, HI));
+}
+
+// 16 e4m3 bytes -> the two A operands (bytes 0-7, 8-15)
+__device__ __forceinline__ void weights_to_bf16(const plm_u32x4 q, plm_bf16x8& a0, plm_bf16x8& a1) {
+    const plm_u32x4 t0 = {e4m3_pair_to_bf16<false>(q.x), e4m3_pair_to_bf16<true>(q.x),
+                          e4m3_pair_to_bf16<false>(q.y), e4m3_pair_to_bf16<true>(q.y)};
+    const plm_u32x4 t1 = {e4m3_pair_to_bf16<false>(q.z), e4m3_pair_to_bf16<true>(q.z),
+                          e4m3_pair_to_bf16<false>(q.w), e4m3_pair_to_bf16<true>(q.w)};
+    a0 = __builtin_bit_cast(plm_bf16x8, t0);
+    a1 = __builtin_bit_cast(plm_bf16x8, t1);
+}
+
+// NaN bytes (0x7F, 0xFF) -> 0
+__device__ __forceinline__ plm_u32x4 zero_nan_bytes(plm_u32x4 q) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            x[2 * j] = __uint_as_float(h[j] << 16);
-            x[2 * j + 1] = __uint_as_float(h[j] & 0xFFFF0000u);
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t w = q[k];
+        const uint32_t nan = ((w & 0x7F7F7F7Fu) + 0x01010101u) & 0x80808080u;  // 0x80 where the low 7 bits are all 1
+        q[k] = w & ~((nan >> 7) * 0xFFu);
+    }
+    return q;
+}
+
+// hi / lo bf16 halves of one fp32 value.  EXACT: infinities and NaNs go to hi
+// whole (a quiet NaN for every NaN) with lo = 0.
+template <bool EXACT>
+__device__ __forceinline__ void split_f32(uint32_t x, uint32_t& hi, uint32_t& lo) {
+    hi = x >> 16;
+    const float rem = __uint_as_float(x) - __uint_as_float(x & 0xFFFF0000u);
+    lo = __builtin_bit_cast(uint16_t, static_cast<__bf16>(rem));
+    if constexpr (EXACT) {
+        if ((x & 0x7F800000u) == 0x7F800000u) {
+            hi = (x & 0x007FFFFFu) != 0 ? 0x7FC0u : hi;
+            lo = 0;
         }
-    } else {
-        load_x16(a.x + off, x);
     }
 }
 
-template <int M, int TR, int NWT, bool SILU, bool XB>
+// 8 fp32 activations (two loads) -> hi and lo B operands
+template <bool EXACT>
+__device__ __forceinline__ void split8(const plm_u32x4 v0, const plm_u32x4 v1, plm_bf16x8& hi, plm_bf16x8& lo) {
+    const uint32_t x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    plm_u32x4 h, l;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        if constexpr (EXACT) {
+            uint32_t h0, l0, h1, l1;
+            split_f32<true>(x[2 * p], h0, l0);
+            split_f32<true>(x[2 * p + 1], h1, l1);
+            h[p] = h0 | (h1 << 16);
+            l[p] = l0 | (l1 << 16);
+        } else {
+            h[p] = __builtin_amdgcn_perm(x[2 * p + 1], x[2 * p], 0x07060302u);
+            const float r0 = __uint_as_float(x[2 * p]) - __uint_as_float(x[2 * p] & 0xFFFF0000u);
+            const float r1 = __uint_as_float(x[2 * p + 1]) - __uint_as_float(x[2 * p + 1] & 0xFFFF0000u);
+            const plm_float2 rr = {r0, r1};
+            l[p] = __builtin_bit_cast(uint32_t, __builtin_convertvector(rr, plm_bf16x2));
+        }
+    }
+    hi = __builtin_bit_cast(plm_bf16x8, h);
+    lo = __builtin_bit_cast(plm_bf16x8, l);
+}
+
+__device__ __forceinline__ plm_f32x4 mfma_bf16(plm_bf16x8 a, plm_bf16x8 b, plm_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// The activations of one block for the lane's B column: two bf16 loads, or
+// four fp32 loads (split into hi and lo later).
+template <bool XB>
+struct XPiece {
+    plm_u32x4 v[XB ? 2 : 4];
+};
+
+template <bool XB>
+__device__ __forceinline__ XPiece<XB> load_xpiece(const void* p, bool live) {
+    XPiece<XB> r;
+    const char* c = static_cast<const char*>(p);
+#pragma unroll
+    for (int k = 0; k < (XB ? 2 : 4); ++k) r.v[k] = live ? xload16(c + 16 * k) : plm_u32x4{0, 0, 0, 0};
+    return r;
+}
+
+// D of one tile and block: the A operands from the weights q against the
+// activation piece x.
+template <bool XB, bool SAN>
+struct BOperands {
+    plm_bf16x8 h0, h1, l0, l1;
+    __device__ __forceinline__ explicit BOperands(const XPiece<XB>& x) {
+        if constexpr (XB) {
+            h0 = __builtin_bit_cast(plm_bf16x8, x.v[0]);
+            h1 = __builtin_bit_cast(plm_bf16x8, x.v[1]);
+        } else {
+            split8<SAN>(x.v[0], x.v[1], h0, l0);
+            split8<SAN>(x.v[2], x.v[3], h1, l1);
+        }
+    }
+};
+
+template <bool XB, bool SAN>
+__device__ __forceinline__ plm_f32x4 tile_block(plm_u32x4 q, const BOperands<XB, SAN>& b) {
+    plm_bf16x8 a0, a1;
+    weights_to_bf16(SAN ? zero_nan_bytes(q) : q, a0, a1);
+    plm_f32x4 d = mfma_bf16(a0, b.h0, plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+    d = mfma_bf16(a1, b.h1, d);
+    if constexpr (!XB) {
+        d = mfma_bf16(a0, b.l0, d);
+        d = mfma_bf16(a1, b.l1, d);
+    }
+    return d;
+}
+
+template <int NT>
+__device__ __forceinline__ bool any_nan(const plm_f32x4 (&acc)[NT]) {
+    bool bad = false;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bad = bad || acc[t][j] != acc[t][j];
+    return __any(bad);
+}
+
+// Adds the two halves and leaves tile t's sums of this wave in LDS:
+// red[(slot * NT + t) * 64 + r * 8 + m] for weight row r, activation row m.
+template <int NT>
+__device__ __forceinline__ void halves_to_lds(const plm_f32x4 (&acc)[NT], float* red, int slot, int lane) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float v = acc[t][j] + __shfl(acc[t][j], (lane + 40) & 63);
+            if (lane < 24 && (lane & 15) < 8) red[(slot * NT + t) * 64 + (4 * (lane >> 4) + j) * 8 + (lane & 7)] = v;
+        }
+}
+
+// The SiLU intermediate silu(gate) * up as the down phase reads it: bf16
+// hi / lo planes (exact for infinities and NaNs).
+__device__ __forceinline__ void store_hplanes(uint16_t* hi, uint16_t* lo, int64_t o, float v) {
+    uint32_t h, l;
+    split_f32<true>(__float_as_uint(v), h, l);
+    hi[o] = static_cast<uint16_t>(h);
+    lo[o] = static_cast<uint16_t>(l);
+}
+
+__device__ __forceinline__ float lane_value(float v, int k) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), k));
+}
+
+// Runs nk steps through P register slots, pipelined: P steps are in
+// flight and step k + P is issued into the slot step k leaves; the steps
+// beyond a multiple of P run first, unpipelined.
+template <int P, class Issue, class Compute>
+__device__ __forceinline__ void run_pipelined(int nk, Issue& issue, Compute& compute) {
+    const int r = nk % P;
+    for (int k = 0; k < r; ++k) {
+        issue(0, k);
+        compute(0, k);
+    }
+    if (nk > r) {
+#pragma unroll
+        for (int u = 0; u < P; ++u) issue(u, r + u);
+        for (int k0 = r; k0 + P < nk; k0 += P) {
+#pragma unroll
+            for (int u = 0; u < P; ++u) {
+                compute(u, k0 + u);
+                issue(u, k0 + u + P);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < P; ++u) compute(u, nk - P + u);
+    }
+}
+
+// The burst schedule of a rows-kernel wave (the MoE's gate/up launches):
+// the loads of U blocks b = b0, b0 + nw, ... are issued together, then the
+// U blocks are consumed.  Activations are loaded by the lanes of live rows
+// only and scales per block.
+template <int TT, int U, int NWT, bool XB, bool SAN>
+__device__ __forceinline__ void rows_pass_burst(const RowsArgs& a, const uint8_t* const (&wrow)[NWT * TT],
+                                                const float* const (&sp)[NWT], const char* xrow, bool xlive,
+                                                int64_t lane_col, int wave, int nw, plm_f32x4 (&acc)[NWT * TT]) {
+    constexpr int NT = NWT * TT;
+    constexpr int XE = XB ? 2 : 4;  // bytes per activation
+    const int64_t nb = a.nblocks;
+    for (int64_t b0 = wave; b0 < nb; b0 += static_cast<int64_t>(U) * nw) {
+        plm_u32x4 q[U][NT];
+        XPiece<XB> x[U];
+        float sc[U][NWT];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t b = b0 + static_cast<int64_t>(u) * nw;
+            const int64_t off = b * 128 + lane_col;
+            const bool in = b < nb && off < a.K;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) q[u][t] = in ? wload16(wrow[t] + off) : plm_u32x4{0, 0, 0, 0};
+            x[u] = load_xpiece<XB>(xrow + off * XE, xlive && in);
+#pragma unroll
+            for (int n = 0; n < NWT; ++n) sc[u][n] = b < nb ? plm_gload_f32(sp[n] + b) : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const BOperands<XB, SAN> bo(x[u]);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const plm_f32x4 d = tile_block<XB, SAN>(q[u][t], bo);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[t][j] = fmaf(d[j], sc[u][t / TT], acc[t][j]);
+            }
+        }
+    }
+}
+
+// One pass of a rows-kernel wave over its blocks b = wave + k nw, k = 0,
+// 1, ...  Software-pipelined: P blocks are in flight, and block k + P is
+// issued into the slot block k leaves.  No load sits behind a branch (a
+// conditional load makes the compiler wait for every outstanding load
+// before the next use): loads past the end of a row read its last 16
+// bytes and are masked when used, activation rows past the batch read row
+// 0 into B columns whose results are dropped, and the blocks beyond a
+// multiple of P run first, unpipelined.  The wave's scales come first, one
+// load for up to 64 blocks (lane k holds block k's), read with v_readlane.
+template <int TT, int P, int NWT, bool XB, bool SAN>
+__device__ __forceinline__ void rows_pass(const RowsArgs& a, const uint8_t* const (&wrow)[NWT * TT],
+                                          const float* const (&sp)[NWT], const char* xrow, int64_t lane_col,
+                                          int wave, int nw, int lane, plm_f32x4 (&acc)[NWT * TT]) {
+    constexpr int NT = NWT * TT;
+    constexpr int XE = XB ? 2 : 4;  // bytes per activation
+    const int64_t K = a.K;
+    const bool ragged = (K & 127) != 0;
+    const int64_t nb = a.nblocks;
+    const int nk_all = wave < nb ? static_cast<int>((nb - 1 - wave) / nw) + 1 : 0;
+    for (int kb = 0; kb < nk_all; kb += 64) {
+        const int nk = min(nk_all - kb, 64);
+        float sv[NWT];
+        const int64_t sblk = wave + static_cast<int64_t>(kb + min(lane, nk - 1)) * nw;
+#pragma unroll
+        for (int n = 0; n < NWT; ++n) sv[n] = plm_gload_f32(sp[n] + sblk);
+        plm_u32x4 q[P][NT];
+        XPiece<XB> x[P];
+        auto issue = [&](int slot, int k) {
+            const int64_t off = min((wave + static_cast<int64_t>(kb + k) * nw) * 128 + lane_col, K - 16);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) q[slot][t] = wload16(wrow[t] + off);
+            x[slot] = load_xpiece<XB>(xrow + off * XE, true);
+        };
+        auto compute = [&](int slot, int k) {
+            float sc[NWT];
+#pragma unroll
+            for (int n = 0; n < NWT; ++n) sc[n] = lane_value(sv[n], k);
+            XPiece<XB> xv = x[slot];
+            plm_u32x4 qv[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) qv[t] = q[slot][t];
+            if (ragged) {
+                // the row's last block: columns past K add nothing
+                const bool in = (wave + static_cast<int64_t>(kb + k) * nw) * 128 + lane_col < K;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) qv[t] = in ? qv[t] : plm_u32x4{0, 0, 0, 0};
+#pragma unroll
+                for (int i = 0; i < (XB ? 2 : 4); ++i) xv.v[i] = in ? xv.v[i] : plm_u32x4{0, 0, 0, 0};
+            }
+            const BOperands<XB, SAN> bo(xv);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const plm_f32x4 d = tile_block<XB, SAN>(qv[t], bo);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[t][j] = fmaf(d[j], sc[t / TT], acc[t][j]);
+            }
+        };
+        run_pipelined<P>(nk, issue, compute);
+    }
+}
+
+// Rows of one or more weights sharing the activations (linear, dual, the
+// gate/up phase with its SiLU epilogue, weights of different row counts in
+// one grid).  A workgroup owns TT tiles (8 TT rows) of each of its NWT
+// weights; its nw waves split the K blocks (block b on wave b % nw), and nw
+// depends only on K.  TT and U (blocks in flight per wave) change the grid
+// and the schedule, never a row's arithmetic.
+template <int TT, int U, bool BURST, int NWT, bool SILU, bool XB>
 __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
-    constexpr int V = NWT * TR * M;
-    __shared__ float red[kMaxWaves * V];
+    constexpr int NT = NWT * TT;
+    __shared__ float red[kMaxWaves * NT * 64];
     const int nw = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63;
@@ -397,11 +676,11 @@ __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
         g = 0;
         for (int i = 1; i < a.nvar; ++i)
             if (static_cast<int>(blockIdx.x) >= a.vtile[i]) g = i;
-        row0 = static_cast<int64_t>(blockIdx.x - a.vtile[g]) * TR;
+        row0 = static_cast<int64_t>(blockIdx.x - a.vtile[g]) * 8 * TT;
         rows = a.vrows[g];
     } else {
         g = blockIdx.x / a.tiles_per_group;
-        row0 = static_cast<int64_t>(blockIdx.x - g * a.tiles_per_group) * TR;
+        row0 = static_cast<int64_t>(blockIdx.x - g * a.tiles_per_group) * 8 * TT;
     }
 
     const uint8_t* W[NWT];
@@ -430,133 +709,60 @@ __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
 #pragma unroll
     for (int i = 0; i < NWT; ++i) live = live && W[i] != nullptr && S[i] != nullptr;
 
-    float acc[NWT][TR][M];
+    const int li = lane & 15;
+    const int64_t lane_col = 64 * (li >> 3) + 16 * (lane >> 4);
+    const int xm = li & 7;  // activation row of this lane's B column
+    const bool xlive = xm < a.mc;
+    plm_f32x4 acc[NT];
 #pragma unroll
-    for (int i = 0; i < NWT; ++i)
-#pragma unroll
-        for (int r = 0; r < TR; ++r)
-#pragma unroll
-            for (int m = 0; m < M; ++m) acc[i][r][m] = 0.0f;
+    for (int t = 0; t < NT; ++t) acc[t] = plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     if (live) {
-        const int64_t srow = (row0 >> 7) * a.scale_cols;
-        for (int c = wave; c < a.nchunks; c += nw) {
-            const int64_t col = static_cast<int64_t>(c) * plm::kChunkBytes + lane * 16;
-            if (col >= a.K) continue;
-            // Loads are unconditional (rows past the end are clamped to the last
-            // row and their results dropped) so that all of them issue before
-            // the first wait.
-            uint4 q[NWT][TR];
+        const uint8_t* wrow[NT];
+        const float* sp[NWT];
 #pragma unroll
-            for (int i = 0; i < NWT; ++i)
+        for (int i = 0; i < NWT; ++i) {
+            sp[i] = S[i] + (row0 >> 7) * a.scale_cols;
 #pragma unroll
-                for (int r = 0; r < TR; ++r) {
-                    const int64_t rr = row0 + r < rows ? row0 + r : rows - 1;
-                    q[i][r] = plm_gload16(W[i] + rr * a.K + col);
-                }
-            float sc[NWT];
-#pragma unroll
-            for (int i = 0; i < NWT; ++i) sc[i] = plm_gload_f32(S[i] + srow + (col >> 7));
-            if constexpr (M == 1) {
-                // one activation row: decode each weight row right before its
-                // dot, so a larger tile needs no more registers (same arithmetic)
-                float xv[16];
-                load_row_x16<XB>(a, 0, col, xv);
-#pragma unroll
-                for (int i = 0; i < NWT; ++i)
-#pragma unroll
-                    for (int r = 0; r < TR; ++r) {
-                        float w16[16];
-                        decode16(q[i][r], w16);
-                        float p = dot16(w16, xv);
-                        if (p != p) {
-                            zero_nans16(w16);
-                            p = dot16(w16, xv);
-                        }
-                        acc[i][r][0] = fmaf(p, sc[i], acc[i][r][0]);
-                    }
-                continue;
-            }
-            if constexpr (TR >= 8) {
-                // wide tiles with several activation rows: each weight row is
-                // decoded again for every activation row (registers for one
-                // decoded row only), halving the activation reads per weight
-                // byte; a NaN span is redone with NaN bytes as 0, which equals
-                // using the sanitised row for every activation row.
-#pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    float xv[16];
-                    load_row_x16<XB>(a, m, col, xv);
-#pragma unroll
-                    for (int i = 0; i < NWT; ++i)
-#pragma unroll
-                        for (int r = 0; r < TR; ++r) {
-                            // opaque copy: the compiler would otherwise keep
-                            // every decoded row live across the activation rows
-                            uint4 qq = q[i][r];
-                            asm volatile("" : "+v"(qq.x), "+v"(qq.y), "+v"(qq.z), "+v"(qq.w));
-                            float w16[16];
-                            decode16(qq, w16);
-                            float p = dot16(w16, xv);
-                            if (p != p) {
-                                zero_nans16(w16);
-                                p = dot16(w16, xv);
-                            }
-                            acc[i][r][m] = fmaf(p, sc[i], acc[i][r][m]);
-                        }
-                }
-                continue;
-            }
-            float wv[NWT][TR][16];
-#pragma unroll
-            for (int i = 0; i < NWT; ++i)
-#pragma unroll
-                for (int r = 0; r < TR; ++r) decode16(q[i][r], wv[i][r]);
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                float xv[16];
-                load_row_x16<XB>(a, m, col, xv);
-#pragma unroll
-                for (int i = 0; i < NWT; ++i)
-#pragma unroll
-                    for (int r = 0; r < TR; ++r) {
-                        float p = dot16(wv[i][r], xv);
-                        if (m == 0 && p != p) {
-                            zero_nans16(wv[i][r]);
-                            p = dot16(wv[i][r], xv);
-                        }
-                        acc[i][r][m] = fmaf(p, sc[i], acc[i][r][m]);
-                    }
+            for (int t = 0; t < TT; ++t) {
+                // rows past the end read the last row; their results are dropped
+                const int64_t r = min(row0 + 8 * t + (li & 7), rows - 1);
+                wrow[i * TT + t] = W[i] + r * a.K;
             }
         }
+        const int64_t xo = static_cast<int64_t>(a.m0 + (xlive ? xm : 0)) * a.x_stride;
+        const char* xrow = XB ? reinterpret_cast<const char*>(a.xb + xo) : reinterpret_cast<const char*>(a.x + xo);
+        auto pass = [&](auto san) {
+            constexpr bool SAN = decltype(san)::value;
+            if constexpr (BURST)
+                rows_pass_burst<TT, U, NWT, XB, SAN>(a, wrow, sp, xrow, xlive, lane_col, wave, nw, acc);
+            else
+                rows_pass<TT, U, NWT, XB, SAN>(a, wrow, sp, xrow, lane_col, wave, nw, lane, acc);
+        };
+        pass(std::false_type{});
+        if (any_nan(acc)) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[t] = plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            pass(std::true_type{});
+        }
     }
-
-#pragma unroll
-    for (int i = 0; i < NWT; ++i)
-#pragma unroll
-        for (int r = 0; r < TR; ++r)
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                const float t = plm_wave_sum(acc[i][r][m]);
-                if (lane == kSumLane) red[wave * V + (i * TR + r) * M + m] = t;
-            }
+    halves_to_lds(acc, red, wave, lane);
     __syncthreads();
 
-    for (int t = threadIdx.x; t < TR * M; t += blockDim.x) {
-        const int r = t / M;
-        const int m = t - r * M;
-        const int64_t row = row0 + r;
-        if (row >= rows) continue;
+    for (int t = threadIdx.x; t < TT * 64; t += blockDim.x) {
+        const int tt = t >> 6, r = (t >> 3) & 7, m = t & 7;
+        const int64_t row = row0 + 8 * tt + r;
+        if (m >= a.mc || row >= rows) continue;
         float v[NWT];
 #pragma unroll
         for (int i = 0; i < NWT; ++i) {
             float s = 0.0f;
-            for (int w = 0; w < nw; ++w) s += red[w * V + (i * TR + r) * M + m];
+            for (int w = 0; w < nw; ++w) s += red[(w * NT + i * TT + tt) * 64 + r * 8 + m];
             v[i] = s;
         }
         const int64_t o = (static_cast<int64_t>(g) * a.m_total + a.m0 + m) * a.out_ld + row;
         if constexpr (SILU) {
-            a.out[0][o] = plm_silu_mul(v[0], v[1]);
+            store_hplanes(a.hhi, a.hlo, o, plm_silu_mul(v[0], v[1]));
         } else {
             if (a.nvar > 0) {
                 a.vout[g][static_cast<int64_t>(a.m0 + m) * rows + row] = v[0];
@@ -586,88 +792,126 @@ __device__ __forceinline__ uint16_t moe_bf16_tail(float routed, float shared, bo
     return static_cast<uint16_t>(v != v ? 0x7FC0u : bf16_rne_bits(v));
 }
 
-// One (group g, chunk cc) item of the down phase for a tile of TR rows:
-// acc[r][m] += route(g, m) * scale * (D_g[row0 + r, chunk] . act_g,m[chunk]).
-template <int M, int TR>
-__device__ __forceinline__ void combine_chunk(const CombineArgs& a, int g, int cc, bool weighted, int64_t row0,
-                                              int lane, float (&acc)[TR][M]) {
-    const int64_t col = static_cast<int64_t>(cc) * plm::kChunkBytes + lane * 16;
-    const uint8_t* W;
-    const float* S;
-    if (g < a.ndev) {
-        W = reinterpret_cast<const uint8_t*>(a.plan->tab[4][g]);
-        S = reinterpret_cast<const float*>(a.plan->tab[5][g]);
-    } else {
-        W = a.w[g - a.ndev];
-        S = a.s[g - a.ndev];
-    }
-    if (W == nullptr || S == nullptr) return;
-    float rw[M];
-    bool any = false;
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-        rw[m] = a.route && weighted ? a.route[static_cast<int64_t>(a.g_base + g) * a.route_sg +
-                                              static_cast<int64_t>(a.m0 + m) * a.route_sm]
-                                    : 1.0f;
-        any = any || !(a.zero_skip && rw[m] == 0.0f);
-    }
-    if (!any || col >= a.K) return;
-    uint4 q[TR];
-#pragma unroll
-    for (int r = 0; r < TR; ++r) {
-        const int64_t rr = row0 + r < a.rows ? row0 + r : a.rows - 1;
-        q[r] = plm_gload16(W + rr * a.K + col);
-    }
-    const float sc = plm_gload_f32(S + (row0 >> 7) * a.scale_cols + (col >> 7));
-    if constexpr (M == 1) {
-        // one activation row: decode each weight row right before its dot,
-        // so a larger tile needs no more registers (same arithmetic)
-        if (a.zero_skip && rw[0] == 0.0f) return;
-        float xv[16];
-        load_x16(a.act + (static_cast<int64_t>(a.g_base + g) * a.m_total + a.m0) * a.K + col, xv);
-#pragma unroll
-        for (int r = 0; r < TR; ++r) {
-            float w16[16];
-            decode16(q[r], w16);
-            float p = dot16(w16, xv);
-            if (p != p) {
-                zero_nans16(w16);
-                p = dot16(w16, xv);
+// What every item of a group needs, staged in LDS by the whole workgroup
+// before its waves start: the down matrix, its scales and the route weight
+// of each activation row.  (Read per item from global memory, the route and
+// a plan's pointers were two dependent round trips before every item's
+// weight loads.)
+struct GroupInfo {
+    const uint8_t* w;
+    const float* s;
+    float rw[kMaxM];
+};
+
+// Every thread calls it (it synchronises the workgroup).
+__device__ __forceinline__ void stage_groups(const CombineArgs& a, GroupInfo* gi) {
+    for (int t = threadIdx.x; t < a.ngroups * kMaxM; t += blockDim.x) {
+        const int g = t / kMaxM, m = t - g * kMaxM;
+        if (m == 0) {
+            if (g < a.ndev) {
+                gi[g].w = reinterpret_cast<const uint8_t*>(a.plan->tab[4][g]);
+                gi[g].s = reinterpret_cast<const float*>(a.plan->tab[5][g]);
+            } else {
+                gi[g].w = a.w[g - a.ndev];
+                gi[g].s = a.s[g - a.ndev];
             }
-            acc[r][0] = fmaf(p * sc, rw[0], acc[r][0]);
         }
-        return;
+        gi[g].rw[m] = (a.route != nullptr && m < a.mc) ? a.route[static_cast<int64_t>(a.g_base + g) * a.route_sg +
+                                                                 static_cast<int64_t>(a.m0 + m) * a.route_sm]
+                                                       : 1.0f;
     }
-    float wv[TR][16];
+    __syncthreads();
+}
+
+// One pass of a combine-kernel wave over items [first, end) of the groups
+// from g_lo (item c: group g_lo + c / nbe, block c % nbe), items first,
+// first + nw, ..., U items' loads issued together.  acc += route(g, m) *
+// scale * D_g(block) . act_g,m; with zero_skip, an (item, activation row)
+// whose route is exactly 0 adds nothing (fp8_linear.cpp:630-747), and an
+// item no live row keeps is not loaded.
+template <int TT, int U, bool SAN>
+__device__ __forceinline__ void combine_pass(const CombineArgs& a, const GroupInfo* gi, int g_lo, int first, int end,
+                                             bool weighted, int64_t row0, int lane, int nw, plm_f32x4 (&acc)[TT]) {
+    const int li = lane & 15;
+    const int64_t lane_col = 64 * (li >> 3) + 16 * (lane >> 4);
+    const int xm = li & 7;
+    const bool xlive = xm < a.mc;
+    int64_t roff[TT];
 #pragma unroll
-    for (int r = 0; r < TR; ++r) decode16(q[r], wv[r]);
-    bool fixed = false;
+    for (int t = 0; t < TT; ++t) roff[t] = min(row0 + 8 * t + (li & 7), a.rows - 1) * a.K + lane_col;
+    const int64_t srow = (row0 >> 7) * a.scale_cols;
+    for (int c0 = first; c0 < end; c0 += U * nw) {
+        plm_u32x4 q[U][TT];
+        XPiece<true> xh[U], xl[U];
+        float f[U];
+        bool keep[U];
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-        if (a.zero_skip && rw[m] == 0.0f) continue;
-        float xv[16];
-        load_x16(a.act + (static_cast<int64_t>(a.g_base + g) * a.m_total + a.m0 + m) * a.K + col, xv);
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + u * nw;
+            const int gl = c < end ? c / a.nbe : 0;
+            const int g = g_lo + gl;
+            const int64_t blk = c - gl * a.nbe;
+            const int64_t col = blk * 128;
+            const uint8_t* W = gi[g].w;
+            const float* S = gi[g].s;
+            const float rw = weighted ? gi[g].rw[xm] : 1.0f;
+            keep[u] = !(a.zero_skip && rw == 0.0f);
+            // the whole wave skips an item no live row keeps, or a group without weights
+            const bool item = c < end && W != nullptr && S != nullptr && __any(xlive && keep[u]);
+            const bool in = item && col + lane_col < a.K;
 #pragma unroll
-        for (int r = 0; r < TR; ++r) {
-            float p = dot16(wv[r], xv);
-            if (!fixed && p != p) {
-                zero_nans16(wv[r]);
-                p = dot16(wv[r], xv);
-            }
-            acc[r][m] = fmaf(p * sc, rw[m], acc[r][m]);
+            for (int t = 0; t < TT; ++t) q[u][t] = in ? wload16(W + roff[t] + col) : plm_u32x4{0, 0, 0, 0};
+            const int64_t xo = (static_cast<int64_t>(a.g_base + g) * a.m_total + a.m0 + (xlive ? xm : 0)) * a.K +
+                               col + lane_col;
+            xh[u] = load_xpiece<true>(a.act_hi + xo, xlive && in);
+            xl[u] = load_xpiece<true>(a.act_lo + xo, xlive && in);
+            f[u] = item ? plm_gload_f32(S + srow + blk) * rw : 0.0f;
+            keep[u] = keep[u] && item;
         }
-        fixed = true;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const BOperands<true, SAN> bh(xh[u]), bl(xl[u]);
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                plm_bf16x8 a0, a1;
+                weights_to_bf16(SAN ? zero_nan_bytes(q[u][t]) : q[u][t], a0, a1);
+                plm_f32x4 d = mfma_bf16(a0, bh.h0, plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+                d = mfma_bf16(a1, bh.h1, d);
+                d = mfma_bf16(a0, bl.h0, d);
+                d = mfma_bf16(a1, bl.h1, d);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[t][j] = keep[u] ? fmaf(d[j], f[u], acc[t][j]) : acc[t][j];
+            }
+        }
     }
 }
 
-// FUSED (the device-routed MoE): one workgroup computes both the routed sum
-// and the split-off last group (the shared expert) of its rows, each with
-// the item-to-wave assignment of the split tiles, and also writes the bf16
-// tail of the two when out_bf16 is set.
-template <int M, int TR, bool FUSED>
+// A combine pass with its NaN redo.
+template <int TT, int U>
+__device__ __forceinline__ void combine_items(const CombineArgs& a, const GroupInfo* gi, int g_lo, int first, int end,
+                                              bool weighted, int64_t row0, int lane, int nw, plm_f32x4 (&acc)[TT]) {
+#pragma unroll
+    for (int t = 0; t < TT; ++t) acc[t] = plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    combine_pass<TT, U, false>(a, gi, g_lo, first, end, weighted, row0, lane, nw, acc);
+    if (any_nan(acc)) {
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[t] = plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        combine_pass<TT, U, true>(a, gi, g_lo, first, end, weighted, row0, lane, nw, acc);
+    }
+}
+
+// Down phase of every MLP / MoE entry point: rows whose K range is the
+// concatenation of several groups' down matrices, each with its own
+// activations (the bf16 hi / lo planes of the SiLU intermediate) and route
+// weight.  Items (group, block) go to waves round robin; nw depends only on
+// the number of items.  FUSED (the device-routed MoE): one workgroup
+// computes both the routed sum and the split-off last group (the shared
+// expert) of its rows, each with the item-to-wave assignment of the split
+// tiles, and also writes the bf16 tail of the two when out_bf16 is set.
+template <int TT, int U, bool FUSED>
 __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
-    constexpr int V = TR * M;
-    __shared__ float red[(FUSED ? 2 : 1) * kMaxWaves * V];
+    __shared__ float red[(FUSED ? 2 : 1) * kMaxWaves * TT * 64];
+    __shared__ GroupInfo gi[kMaxGroups + 1];  // the device-routed MoE: up to 64 chosen + the shared expert
     const int nw = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63;
@@ -688,30 +932,16 @@ __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
             last = true;
         }
     }
-    const int64_t row0 = static_cast<int64_t>(tile) * TR;
+    const int64_t row0 = static_cast<int64_t>(tile) * 8 * TT;
     // Device-chosen groups past the router's count are left out.  The items
     // before them keep their wave assignment (item c goes to wave c % nw), so
     // the sums are those of a call given just the chosen groups.
     if (a.ndev > 0 && !last) g_hi = min(g_hi, a.plan->count);
+    stage_groups(a, gi);
 
-    float acc[TR][M];
-#pragma unroll
-    for (int r = 0; r < TR; ++r)
-#pragma unroll
-        for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
-
-    const int nchunks = (g_hi - g_lo) * a.cps;
-    for (int c = wave; c < nchunks; c += nw) {
-        const int gi = c / a.cps;
-        combine_chunk<M, TR>(a, g_lo + gi, c - gi * a.cps, !last, row0, lane, acc);
-    }
-#pragma unroll
-    for (int r = 0; r < TR; ++r)
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            const float t = plm_wave_sum(acc[r][m]);
-            if (lane == kSumLane) red[wave * V + r * M + m] = t;
-        }
+    plm_f32x4 acc[TT];
+    combine_items<TT, U>(a, gi, g_lo, wave, (g_hi - g_lo) * a.nbe, !last, row0, lane, nw, acc);
+    halves_to_lds(acc, red, wave, lane);
     if constexpr (FUSED) {
         // The split-off group in the same registers.  With fewer items than
         // waves its items go, in order, to the last waves (those with the
@@ -719,36 +949,31 @@ __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
         // values in the same order as a tile of its own (whose item c sits
         // on wave c), the other waves adding exact zeros.
         if (a.split_last) {
+            const int shift = nw > a.nbe ? nw - a.nbe : 0;
+            const int first = wave - shift;
+            if (first >= 0) {
+                combine_items<TT, U>(a, gi, a.ngroups - 1, first, a.nbe, false, row0, lane, nw, acc);
+            } else {
 #pragma unroll
-            for (int r = 0; r < TR; ++r)
-#pragma unroll
-                for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
-            const int shift = nw > a.cps ? nw - a.cps : 0;
-            for (int c = wave - shift; c < a.cps; c += nw)
-                if (c >= 0) combine_chunk<M, TR>(a, a.ngroups - 1, c, false, row0, lane, acc);
-#pragma unroll
-            for (int r = 0; r < TR; ++r)
-#pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    const float t = plm_wave_sum(acc[r][m]);
-                    if (lane == kSumLane) red[(kMaxWaves + wave) * V + r * M + m] = t;
-                }
+                for (int t = 0; t < TT; ++t) acc[t] = plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+            halves_to_lds(acc, red, kMaxWaves + wave, lane);
         }
     }
     __syncthreads();
 
-    for (int t = threadIdx.x; t < V; t += blockDim.x) {
-        const int r = t / M;
-        const int m = t - r * M;
-        const int64_t row = row0 + r;
-        if (row >= a.rows) continue;
+    for (int t = threadIdx.x; t < TT * 64; t += blockDim.x) {
+        const int tt = t >> 6, r = (t >> 3) & 7, m = t & 7;
+        const int64_t row = row0 + 8 * tt + r;
+        if (m >= a.mc || row >= a.rows) continue;
+        const int cell = tt * 64 + r * 8 + m;
         float v = 0.0f;
-        for (int w = 0; w < nw; ++w) v += red[w * V + t];
+        for (int w = 0; w < nw; ++w) v += red[w * TT * 64 + cell];
         int64_t o = static_cast<int64_t>(a.m0 + m) * a.rows + row;
         if constexpr (FUSED) {
             float v2 = 0.0f;
             if (a.split_last) {
-                for (int w = 0; w < nw; ++w) v2 += red[(kMaxWaves + w) * V + t];
+                for (int w = 0; w < nw; ++w) v2 += red[(kMaxWaves + w) * TT * 64 + cell];
                 a.out_last[o] = v2;
             }
             a.out[o] = v;
@@ -787,6 +1012,25 @@ __device__ float scalar_row_dot(const uint8_t* w, const float* s, const float* x
     return acc;
 }
 
+// The same over the hi / lo planes of the SiLU intermediate (hi + lo is
+// exact in fp32).
+__device__ float scalar_plane_dot(const uint8_t* w, const float* s, const uint16_t* hi, const uint16_t* lo,
+                                  int64_t K) {
+    float acc = 0.0f;
+    for (int64_t c0 = 0; c0 < K; c0 += 128) {
+        const int64_t c1 = c0 + 128 < K ? c0 + 128 : K;
+        float blk = 0.0f;
+        for (int64_t c = c0; c < c1; ++c) {
+            float v[4];
+            plm_decode4_e4m3(static_cast<uint32_t>(w[c]), v);
+            const float wv = (v[0] != v[0]) ? 0.0f : v[0];
+            blk = fmaf(bf16_bits_to_f32(hi[c]) + bf16_bits_to_f32(lo[c]), wv, blk);
+        }
+        acc = fmaf(blk, s[c0 >> 7], acc);
+    }
+    return acc;
+}
+
 template <bool SILU, int NWT>
 __global__ void fp8_rows_scalar_kernel(const RowsArgs a, int mcount, int ngroups) {
     const int64_t id = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -811,7 +1055,7 @@ __global__ void fp8_rows_scalar_kernel(const RowsArgs a, int mcount, int ngroups
     for (int i = 0; i < NWT; ++i) live = live && a.w[i][g] != nullptr && a.s[i][g] != nullptr;
     const int64_t o = (static_cast<int64_t>(g) * a.m_total + a.m0 + m) * a.out_ld + row;
     if constexpr (SILU) {
-        a.out[0][o] = live ? plm_silu_mul(v[0], v[1]) : 0.0f;
+        store_hplanes(a.hhi, a.hlo, o, live ? plm_silu_mul(v[0], v[1]) : 0.0f);
     } else {
         for (int i = 0; i < NWT; ++i) a.out[i][o] = v[i];
     }
@@ -837,9 +1081,9 @@ __global__ void fp8_combine_scalar_kernel(const CombineArgs a, int mcount) {
                                                     static_cast<int64_t>(a.m0 + m) * a.route_sm]
                                           : 1.0f;
         if (a.zero_skip && rw == 0.0f) continue;
-        const float e = scalar_row_dot(W + row * a.K, S + (row >> 7) * a.scale_cols,
-                                       a.act + (static_cast<int64_t>(a.g_base + g) * a.m_total + a.m0 + m) * a.K,
-                                       a.K);
+        const int64_t xo = (static_cast<int64_t>(a.g_base + g) * a.m_total + a.m0 + m) * a.K;
+        const float e = scalar_plane_dot(W + row * a.K, S + (row >> 7) * a.scale_cols, a.act_hi + xo, a.act_lo + xo,
+                                         a.K);
         v = fmaf(e, rw, v);
     }
     int64_t o = static_cast<int64_t>(a.m0 + m) * a.rows + row;
@@ -885,107 +1129,110 @@ __global__ __launch_bounds__(256) void scatter_pairs_kernel(const int64_t* items
 
 // ------------------------------------------------------------------ dispatch
 
-int waves_for(int64_t nchunks) {
-    return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(nchunks, kMaxWaves)));
+// Waves per workgroup.  They split a row's K blocks (or the combine's
+// items) round robin and their sums are added in wave order, so the count
+// depends only on K (on the items), never on the batch: it is part of the
+// per-row arithmetic.
+int waves_for(int64_t items) {
+    return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(items, kMaxWaves)));
 }
 
-// Rows per tile.  The per-row arithmetic does not depend on it, so it is
-// chosen per launch: at one or two activation rows (where each weight row is
-// decoded right before its dot) 8 rows halve the activation reads per weight
-// byte, used when the grid still has at least kTileWaves waves; otherwise 4
-// for one weight, and 2 for two (gate and up): measured on the DeepSeek-V3
-// gate/up launch (9 x 2 weights of 2048 x 7168, M = 1) at 45.4 us with 2-row
-// tiles against 47.3 us with 4-row ones (twice the workgroups, the same
-// bytes per wave).
-constexpr int64_t kTileWaves = 4096;
-
-template <int M>
-constexpr int rows_tile(int nwt) {
-    return nwt == 1 ? 4 : 2;
+// The rows kernel's waves for nb K blocks: preferably a count that gives
+// every wave the same even number of blocks, which the pipelined loop runs
+// with no unpipelined remainder (7168 columns: 56 blocks, 7 waves of 8).
+int waves_for_blocks(int64_t nb) {
+    if (nb <= kMaxWaves) return waves_for(nb);
+    for (int w = kMaxWaves; w >= 4; --w)
+        if (nb % w == 0 && (nb / w) % 2 == 0) return w;
+    return kMaxWaves;
 }
 
-template <int M>
-constexpr int combine_tile() {
-    return 4;
+// Waves of a rows launch.  Each family of entry points keeps one rule for
+// every batch size (it fixes the per-row arithmetic): the linear family
+// (linear, dual, many) spreads K evenly for the pipelined loop, the SiLU
+// gate/up phase of the MLP / MoE family takes min(8, blocks).
+template <bool SILU>
+int rows_waves(int64_t nb) {
+    return SILU ? waves_for(nb) : waves_for_blocks(nb);
 }
 
-bool wide_tile_fits(int64_t rows, int64_t groups, int nw) {
-    return plm::ceil_div(rows, 8) * groups * nw >= kTileWaves;
-}
+// Tiles per wave (TT, 8 rows each) and blocks in flight per wave (U) only
+// shape the grid and the schedule, so they are chosen per launch.  Measured
+// on the DeepSeek-V3 shapes (us, one MI355X): at one activation row 1 tile
+// with 2 blocks in flight (o 7168x16384 25.5, 2048x7168 6.3), and 1 tile
+// with 4 blocks for the gate/up pair (9 experts' gate/up 41.5 against 43.9
+// with 2 tiles and 1 block); with several rows, wider tiles share each
+// activation load among more weight rows while the grid keeps enough
+// workgroups (o at 8 rows: 4 tiles 29.5, 2 tiles 32.9, 1 tile 45.0).
+constexpr int64_t kMinTiles = 192;
 
-// With one weight, halving the tile to 2 rows pays when 4-row tiles would
-// leave CUs idle (fewer tiles than CUs) or load them unevenly (the busiest
-// CU's share of ceil(tiles / CUs) is above the mean by more than it would be
-// with twice the tiles): 1536 rows give 384 tiles of 4, 1.5 per CU, against
-// 768 of 2, 3 per CU.  Where both divide evenly (2048, 3072 rows) the
-// 4-row tile reads the activations half as often and stays.
-bool narrow_tile_balances(int64_t tiles4) {
-    const int64_t cus = plm::cu_count();
-    const int64_t tiles2 = 2 * tiles4;
-    return tiles4 < cus || plm::ceil_div(tiles2, cus) * tiles4 < plm::ceil_div(tiles4, cus) * tiles2;
-}
-
-template <int M, int TR, int NWT, bool SILU>
-void launch_rows_tr(const RowsArgs& a, int ngroups, hipStream_t st) {
+template <int TT, int P, bool BURST, int NWT, bool SILU>
+void launch_rows_cfg(const RowsArgs& a, int ngroups, hipStream_t st) {
     RowsArgs b = a;
-    b.tiles_per_group = static_cast<int>(plm::ceil_div(a.rows, TR));
-    const int nw = waves_for(a.nchunks);
+    b.tiles_per_group = static_cast<int>(plm::ceil_div(a.rows, 8 * TT));
+    const int nw = rows_waves<SILU>(a.nblocks);
     int64_t grid = static_cast<int64_t>(b.tiles_per_group) * ngroups;
     if (a.nvar > 0) {
         b.vtile[0] = 0;
         for (int i = 0; i < a.nvar; ++i)
-            b.vtile[i + 1] = b.vtile[i] + static_cast<int>(plm::ceil_div(a.vrows[i], TR));
+            b.vtile[i + 1] = b.vtile[i] + static_cast<int>(plm::ceil_div(a.vrows[i], 8 * TT));
         grid = b.vtile[a.nvar];
     }
     if (a.xb != nullptr) {
-        hipLaunchKernelGGL((fp8_rows_kernel<M, TR, NWT, SILU, true>), dim3(static_cast<unsigned>(grid)),
+        hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, true>), dim3(static_cast<unsigned>(grid)),
                            dim3(nw * plm::kWave), 0, st, b);
     } else {
-        hipLaunchKernelGGL((fp8_rows_kernel<M, TR, NWT, SILU, false>), dim3(static_cast<unsigned>(grid)),
+        hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, false>), dim3(static_cast<unsigned>(grid)),
                            dim3(nw * plm::kWave), 0, st, b);
     }
 }
 
-template <int M, int NWT, bool SILU>
-void launch_rows_m(const RowsArgs& a, int ngroups, hipStream_t st) {
-    if constexpr (NWT == 1) {
-        int64_t all_rows = a.rows;
-        int64_t tiles4 = plm::ceil_div(a.rows, 4) * ngroups;
-        if (a.nvar > 0) {
-            all_rows = 0;
-            tiles4 = 0;
-            for (int i = 0; i < a.nvar; ++i) {
-                all_rows += a.vrows[i];
-                tiles4 += plm::ceil_div(a.vrows[i], 4);
-            }
-        }
-        // (at three or more activation rows the wide tile's re-decoding and
-        // registers cost more than the activation reads it saves)
-        if constexpr (M <= 2) {
-            if (wide_tile_fits(all_rows, a.nvar > 0 ? 1 : ngroups, waves_for(a.nchunks))) {
-                launch_rows_tr<M, 8, 1, SILU>(a, ngroups, st);
-                return;
-            }
-        }
-        if (narrow_tile_balances(tiles4)) {
-            launch_rows_tr<M, 2, 1, SILU>(a, ngroups, st);
-            return;
-        }
-    }
-    launch_rows_tr<M, rows_tile<M>(NWT), NWT, SILU>(a, ngroups, st);
+// Workgroups of a rows launch at TT tiles per wave.
+int64_t rows_tiles(const RowsArgs& a, int ngroups, int tt) {
+    if (a.nvar == 0) return plm::ceil_div(a.rows, 8 * tt) * ngroups;
+    int64_t n = 0;
+    for (int i = 0; i < a.nvar; ++i) n += plm::ceil_div(a.vrows[i], 8 * tt);
+    return n;
+}
+
+// Blocks per wave of a rows launch.
+template <bool SILU>
+int64_t rows_blocks_per_wave(const RowsArgs& a) {
+    return plm::ceil_div(a.nblocks, rows_waves<SILU>(a.nblocks));
 }
 
 template <int NWT, bool SILU>
 void launch_rows(const RowsArgs& a, int mcount, int ngroups, hipStream_t st) {
-    switch (mcount) {
-        case 1: launch_rows_m<1, NWT, SILU>(a, ngroups, st); break;
-        case 2: launch_rows_m<2, NWT, SILU>(a, ngroups, st); break;
-        case 3: launch_rows_m<3, NWT, SILU>(a, ngroups, st); break;
-        case 4: launch_rows_m<4, NWT, SILU>(a, ngroups, st); break;
-        case 5: launch_rows_m<5, NWT, SILU>(a, ngroups, st); break;
-        case 6: launch_rows_m<6, NWT, SILU>(a, ngroups, st); break;
-        case 7: launch_rows_m<7, NWT, SILU>(a, ngroups, st); break;
-        default: launch_rows_m<8, NWT, SILU>(a, ngroups, st); break;
+    RowsArgs b = a;
+    b.mc = mcount;
+    if constexpr (SILU) {
+        // the MoE's gate/up: bursts of blocks
+        if (mcount == 1 || rows_tiles(b, ngroups, 2) < kMinTiles)
+            launch_rows_cfg<1, 4, true, NWT, SILU>(b, ngroups, st);
+        else
+            launch_rows_cfg<2, 1, true, NWT, SILU>(b, ngroups, st);
+        return;
+    }
+    const bool few = rows_blocks_per_wave<SILU>(b) <= 4;  // a 4-deep pipeline would leave them unpipelined
+    if (mcount == 1) {
+        if (few)
+            launch_rows_cfg<1, 2, false, NWT, SILU>(b, ngroups, st);
+        else
+            launch_rows_cfg<1, 4, false, NWT, SILU>(b, ngroups, st);
+        return;
+    }
+    if constexpr (NWT == 1) {
+        if (rows_tiles(b, ngroups, 4) >= kMinTiles) {
+            launch_rows_cfg<4, 2, false, NWT, SILU>(b, ngroups, st);
+            return;
+        }
+    }
+    if (rows_tiles(b, ngroups, 2) >= kMinTiles) {
+        launch_rows_cfg<2, 2, false, NWT, SILU>(b, ngroups, st);
+    } else if (few) {
+        launch_rows_cfg<1, 2, false, NWT, SILU>(b, ngroups, st);
+    } else {
+        launch_rows_cfg<1, 4, false, NWT, SILU>(b, ngroups, st);
     }
 }
 
@@ -1000,46 +1247,28 @@ int combine_outputs(const CombineArgs& a) {
     return a.per_group_out ? a.ngroups : (a.split_last && !a.fused ? 2 : 1);
 }
 
-template <int M, int TR>
-void launch_combine_tr(const CombineArgs& a, hipStream_t st) {
+template <int TT, int U>
+void launch_combine_cfg(const CombineArgs& a, hipStream_t st) {
     CombineArgs b = a;
-    const int tiles = static_cast<int>(plm::ceil_div(a.rows, TR));
+    const int tiles = static_cast<int>(plm::ceil_div(a.rows, 8 * TT));
     b.tiles_per_group = tiles;
-    const int nw = waves_for(combine_segments(a) * a.cps);
+    const int nw = waves_for(static_cast<int64_t>(combine_segments(a)) * a.nbe);
     const int64_t grid = static_cast<int64_t>(tiles) * combine_outputs(a);
     if (a.fused) {
-        hipLaunchKernelGGL((fp8_combine_kernel<M, TR, true>), dim3(static_cast<unsigned>(grid)),
+        hipLaunchKernelGGL((fp8_combine_kernel<TT, U, true>), dim3(static_cast<unsigned>(grid)),
                            dim3(nw * plm::kWave), 0, st, b);
     } else {
-        hipLaunchKernelGGL((fp8_combine_kernel<M, TR, false>), dim3(static_cast<unsigned>(grid)),
+        hipLaunchKernelGGL((fp8_combine_kernel<TT, U, false>), dim3(static_cast<unsigned>(grid)),
                            dim3(nw * plm::kWave), 0, st, b);
     }
 }
 
-template <int M>
-void launch_combine_m(const CombineArgs& a, hipStream_t st) {
-    if constexpr (M == 1) {
-        // (fused tiles also carry the split-off group: 4-row tiles keep the
-        // grid at several workgroups per CU)
-        if (wide_tile_fits(a.rows, combine_outputs(a), waves_for(combine_segments(a) * a.cps))) {
-            launch_combine_tr<1, 8>(a, st);
-            return;
-        }
-    }
-    launch_combine_tr<M, combine_tile<M>()>(a, st);
-}
-
+// The down phase: 2 tiles per wave, 1 block in flight (the 9-expert
+// DeepSeek-V3 down phase: 30.5 us against 42.0 with 1 tile at one row).
 void launch_combine(const CombineArgs& a, int mcount, hipStream_t st) {
-    switch (mcount) {
-        case 1: launch_combine_m<1>(a, st); break;
-        case 2: launch_combine_m<2>(a, st); break;
-        case 3: launch_combine_m<3>(a, st); break;
-        case 4: launch_combine_m<4>(a, st); break;
-        case 5: launch_combine_m<5>(a, st); break;
-        case 6: launch_combine_m<6>(a, st); break;
-        case 7: launch_combine_m<7>(a, st); break;
-        default: launch_combine_m<8>(a, st); break;
-    }
+    CombineArgs b = a;
+    b.mc = mcount;
+    launch_combine_cfg<2, 1>(b, st);
 }
 
 // A GEMV problem over groups that share the activations.
@@ -1093,14 +1322,20 @@ int run_rows(const RowsProblem& p, hipStream_t st) {
         a.x_stride = p.x_stride;
         // Output offsets of this group batch: element (g, m, row) lives at
         // ((g0 + g) * batch + m) * out_ld + row.
-        for (int i = 0; i < p.nwt; ++i) {
-            a.out[i] = p.out[i] ? p.out[i] + static_cast<int64_t>(g0) * p.batch * p.out_ld : nullptr;
+        const int64_t goff = static_cast<int64_t>(g0) * p.batch * p.out_ld;
+        if (p.silu) {
+            // the SiLU intermediate as two bf16 planes in the caller's fp32-sized buffer
+            uint16_t* planes = reinterpret_cast<uint16_t*>(p.out[0]);
+            a.hhi = planes + goff;
+            a.hlo = planes + static_cast<int64_t>(p.ngroups) * p.batch * p.out_ld + goff;
+        } else {
+            for (int i = 0; i < p.nwt; ++i) a.out[i] = p.out[i] ? p.out[i] + goff : nullptr;
         }
         a.out_ld = p.out_ld;
         a.rows = p.rows;
         a.K = p.K;
         a.scale_cols = p.scale_cols;
-        a.nchunks = static_cast<int>(plm::ceil_div(p.K, plm::kChunkBytes));
+        a.nblocks = static_cast<int>(plm::ceil_div(p.K, 128));
         a.m_total = static_cast<int>(p.batch);
         a.nvar = p.nvar;
         for (int i = 0; i < p.nvar; ++i) {
@@ -1110,6 +1345,7 @@ int run_rows(const RowsProblem& p, hipStream_t st) {
         for (int64_t m0 = 0; m0 < p.batch; m0 += kMaxM) {
             const int mc = static_cast<int>(std::min<int64_t>(kMaxM, p.batch - m0));
             a.m0 = static_cast<int>(m0);
+            a.mc = mc;
             if (fast) {
                 if (p.nwt == 1) {
                     launch_rows<1, false>(a, mc, ng, st);
@@ -1169,7 +1405,8 @@ int run_combine(const CombineProblem& p, hipStream_t st) {
             a.w[g] = p.w[g0 + g];
             a.s[g] = p.s[g0 + g];
         }
-        a.act = p.act;
+        a.act_hi = reinterpret_cast<const uint16_t*>(p.act);
+        a.act_lo = a.act_hi + static_cast<int64_t>(p.ngroups) * p.batch * p.K;
         a.route = p.route;
         a.route_sg = p.route_sg;
         a.route_sm = p.route_sm;
@@ -1179,7 +1416,7 @@ int run_combine(const CombineProblem& p, hipStream_t st) {
         a.scale_cols = p.scale_cols;
         a.ngroups = ng;
         a.g_base = g0;
-        a.cps = static_cast<int>(plm::ceil_div(p.K, plm::kChunkBytes));
+        a.nbe = static_cast<int>(plm::ceil_div(p.K, 128));
         a.per_group_out = p.per_group_out ? 1 : 0;
         a.split_last = p.out_last != nullptr ? 1 : 0;
         a.out_last = p.out_last;
@@ -1189,6 +1426,7 @@ int run_combine(const CombineProblem& p, hipStream_t st) {
         for (int64_t m0 = 0; m0 < p.batch; m0 += kMaxM) {
             const int mc = static_cast<int>(std::min<int64_t>(kMaxM, p.batch - m0));
             a.m0 = static_cast<int>(m0);
+            a.mc = mc;
             if (fast) {
                 launch_combine(a, mc, st);
             } else {
@@ -1539,12 +1777,13 @@ int device_routed_impl(const uint64_t* table, int64_t num_experts, const int64_t
     a.x = hidden.f32;
     a.xb = hidden.bf16;
     a.x_stride = hid;
-    a.out[0] = act;
+    a.hhi = reinterpret_cast<uint16_t*>(act);
+    a.hlo = a.hhi + static_cast<int64_t>(groups) * batch * inter;
     a.out_ld = inter;
     a.rows = inter;
     a.K = hid;
     a.scale_cols = gsc;
-    a.nchunks = static_cast<int>(plm::ceil_div(hid, plm::kChunkBytes));
+    a.nblocks = static_cast<int>(plm::ceil_div(hid, 128));
     a.m_total = static_cast<int>(batch);
     a.plan = plan;
     a.ndev = ndev;
@@ -1558,7 +1797,8 @@ int device_routed_impl(const uint64_t* table, int64_t num_experts, const int64_t
         c.w[0] = reinterpret_cast<const uint8_t*>(static_cast<uintptr_t>(shared[4]));
         c.s[0] = reinterpret_cast<const float*>(static_cast<uintptr_t>(shared[5]));
     }
-    c.act = act;
+    c.act_hi = reinterpret_cast<const uint16_t*>(act);
+    c.act_lo = c.act_hi + static_cast<int64_t>(groups) * batch * inter;
     c.route = reinterpret_cast<const float*>(reinterpret_cast<const char*>(plan) + offsetof(MoePlan, route));
     c.route_sg = batch;
     c.route_sm = 1;
@@ -1570,7 +1810,7 @@ int device_routed_impl(const uint64_t* table, int64_t num_experts, const int64_t
     c.K = inter;
     c.scale_cols = dsc;
     c.ngroups = groups;
-    c.cps = static_cast<int>(plm::ceil_div(inter, plm::kChunkBytes));
+    c.nbe = static_cast<int>(plm::ceil_div(inter, 128));
     c.m_total = static_cast<int>(batch);
     c.plan = plan;
     c.ndev = ndev;
