@@ -45,6 +45,7 @@ namespace {
 
 constexpr int kMaxGroups = 64;  // experts per launch (pointer tables travel as kernel arguments)
 constexpr int kMaxWaves = 8;
+constexpr int kCombineWaves = 8;  // waves of a down-phase workgroup (at most)
 constexpr int kMaxM = 8;        // activation rows per launch; larger batches are split
 constexpr int kMaxVar = 8;      // matrices of different row counts per many-linear launch
 
@@ -236,12 +237,11 @@ __global__ __launch_bounds__(64) void moe_plan_kernel(const uint64_t* __restrict
 // are then numbered by a prefix count over the lanes (the lanes hold
 // ascending experts).  Wider tables go through plan_from_choices.
 template <int J>
-__global__ __launch_bounds__(512) void moe_route_plan_kernel(const float* __restrict__ logits,
-                                                            const float* __restrict__ bias, int experts, int batch,
-                                                            int top_k, int n_groups, int topk_groups, int scoring,
-                                                            float route_scale, const uint64_t* __restrict__ table,
-                                                            int64_t* idx_out, float* w_out,
-                                                            MoePlan* __restrict__ plan, int* __restrict__ rejected) {
+__device__ __forceinline__ void route_plan_body(const float* __restrict__ logits, const float* __restrict__ bias,
+                                                int experts, int batch, int top_k, int n_groups, int topk_groups,
+                                                int scoring, float route_scale, const uint64_t* __restrict__ table,
+                                                int64_t* idx_out, float* w_out, MoePlan* __restrict__ plan,
+                                                int* __restrict__ rejected) {
     extern __shared__ float4 sh4[];
     const int waves = static_cast<int>(blockDim.x >> 6);
     const int wave = static_cast<int>(threadIdx.x >> 6);
@@ -338,6 +338,17 @@ __global__ __launch_bounds__(512) void moe_route_plan_kernel(const float* __rest
             }
         plan_from_choices(table, experts, kidx, kwt, batch, top_k, plan, rejected, ps);
     }
+}
+
+template <int J>
+__global__ __launch_bounds__(512) void moe_route_plan_kernel(const float* __restrict__ logits,
+                                                            const float* __restrict__ bias, int experts, int batch,
+                                                            int top_k, int n_groups, int topk_groups, int scoring,
+                                                            float route_scale, const uint64_t* __restrict__ table,
+                                                            int64_t* idx_out, float* w_out,
+                                                            MoePlan* __restrict__ plan, int* __restrict__ rejected) {
+    route_plan_body<J>(logits, bias, experts, batch, top_k, n_groups, topk_groups, scoring, route_scale, table,
+                       idx_out, w_out, plan, rejected);
 }
 
 // ------------------------------------------------------------------ matrix-core tiles
@@ -664,7 +675,7 @@ __device__ __forceinline__ void rows_pass(const RowsArgs& a, const uint8_t* cons
 // depends only on K.  TT and U (blocks in flight per wave) change the grid
 // and the schedule, never a row's arithmetic.
 template <int TT, int U, bool BURST, int NWT, bool SILU, bool XB>
-__global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
+__device__ __forceinline__ void rows_tile(const RowsArgs& a, const int block) {
     constexpr int NT = NWT * TT;
     __shared__ float red[kMaxWaves * NT * 64];
     const int nw = blockDim.x >> 6;
@@ -675,12 +686,12 @@ __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
     if (a.nvar > 0) {
         g = 0;
         for (int i = 1; i < a.nvar; ++i)
-            if (static_cast<int>(blockIdx.x) >= a.vtile[i]) g = i;
-        row0 = static_cast<int64_t>(blockIdx.x - a.vtile[g]) * 8 * TT;
+            if (block >= a.vtile[i]) g = i;
+        row0 = static_cast<int64_t>(block - a.vtile[g]) * 8 * TT;
         rows = a.vrows[g];
     } else {
-        g = blockIdx.x / a.tiles_per_group;
-        row0 = static_cast<int64_t>(blockIdx.x - g * a.tiles_per_group) * 8 * TT;
+        g = block / a.tiles_per_group;
+        row0 = static_cast<int64_t>(block - g * a.tiles_per_group) * 8 * TT;
     }
 
     const uint8_t* W[NWT];
@@ -774,6 +785,12 @@ __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
     }
 }
 
+template <int TT, int U, bool BURST, int NWT, bool SILU, bool XB>
+__global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
+    rows_tile<TT, U, BURST, NWT, SILU, XB>(a, static_cast<int>(blockIdx.x));
+}
+
+
 // bf16 bits of v rounded to nearest even (finite and infinite v).
 __device__ __forceinline__ uint32_t bf16_rne_bits(float v) {
     const uint32_t b = __float_as_uint(v);
@@ -829,8 +846,8 @@ __device__ __forceinline__ void stage_groups(const CombineArgs& a, GroupInfo* gi
 // scale * D_g(block) . act_g,m; with zero_skip, an (item, activation row)
 // whose route is exactly 0 adds nothing (fp8_linear.cpp:630-747), and an
 // item no live row keeps is not loaded.
-template <int TT, int U, bool SAN>
-__device__ __forceinline__ void combine_pass(const CombineArgs& a, const GroupInfo* gi, int g_lo, int first, int end,
+template <int TT, int U, bool SAN, class Groups>
+__device__ __forceinline__ void combine_pass(const CombineArgs& a, const Groups& gi, int g_lo, int first, int end,
                                              bool weighted, int64_t row0, int lane, int nw, plm_f32x4 (&acc)[TT]) {
     const int li = lane & 15;
     const int64_t lane_col = 64 * (li >> 3) + 16 * (lane >> 4);
@@ -887,8 +904,8 @@ __device__ __forceinline__ void combine_pass(const CombineArgs& a, const GroupIn
 }
 
 // A combine pass with its NaN redo.
-template <int TT, int U>
-__device__ __forceinline__ void combine_items(const CombineArgs& a, const GroupInfo* gi, int g_lo, int first, int end,
+template <int TT, int U, class Groups>
+__device__ __forceinline__ void combine_items(const CombineArgs& a, const Groups& gi, int g_lo, int first, int end,
                                               bool weighted, int64_t row0, int lane, int nw, plm_f32x4 (&acc)[TT]) {
 #pragma unroll
     for (int t = 0; t < TT; ++t) acc[t] = plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -909,8 +926,8 @@ __device__ __forceinline__ void combine_items(const CombineArgs& a, const GroupI
 // expert) of its rows, each with the item-to-wave assignment of the split
 // tiles, and also writes the bf16 tail of the two when out_bf16 is set.
 template <int TT, int U, bool FUSED>
-__global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
-    __shared__ float red[(FUSED ? 2 : 1) * kMaxWaves * TT * 64];
+__global__ __launch_bounds__(64 * kCombineWaves) void fp8_combine_kernel(const CombineArgs a) {
+    __shared__ float red[(FUSED ? 2 : 1) * kCombineWaves * TT * 64];
     __shared__ GroupInfo gi[kMaxGroups + 1];  // the device-routed MoE: up to 64 chosen + the shared expert
     const int nw = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -957,7 +974,7 @@ __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
 #pragma unroll
                 for (int t = 0; t < TT; ++t) acc[t] = plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             }
-            halves_to_lds(acc, red, kMaxWaves + wave, lane);
+            halves_to_lds(acc, red, kCombineWaves + wave, lane);
         }
     }
     __syncthreads();
@@ -973,7 +990,7 @@ __global__ __launch_bounds__(512) void fp8_combine_kernel(const CombineArgs a) {
         if constexpr (FUSED) {
             float v2 = 0.0f;
             if (a.split_last) {
-                for (int w = 0; w < nw; ++w) v2 += red[(kMaxWaves + w) * TT * 64 + cell];
+                for (int w = 0; w < nw; ++w) v2 += red[(kCombineWaves + w) * TT * 64 + cell];
                 a.out_last[o] = v2;
             }
             a.out[o] = v;
@@ -1213,10 +1230,16 @@ void launch_rows(const RowsArgs& a, int mcount, int ngroups, hipStream_t st) {
             launch_rows_cfg<2, 1, true, NWT, SILU>(b, ngroups, st);
         return;
     }
-    const bool few = rows_blocks_per_wave<SILU>(b) <= 4;  // a 4-deep pipeline would leave them unpipelined
+    // Pipeline depth at one row: every block of a wave in flight up to 8
+    // (7168 columns: q_a 1536 rows 6.0 us, 576 rows 5.8, 2048 rows 6.1),
+    // 4 deep beyond (16384 columns: 28.0 us against 32.2 at 8 deep).
+    const int64_t per_wave = rows_blocks_per_wave<SILU>(b);
+    const bool few = per_wave <= 4;  // a 4-deep pipeline would leave them unpipelined
     if (mcount == 1) {
         if (few)
             launch_rows_cfg<1, 2, false, NWT, SILU>(b, ngroups, st);
+        else if (per_wave <= 8)
+            launch_rows_cfg<1, 8, false, NWT, SILU>(b, ngroups, st);
         else
             launch_rows_cfg<1, 4, false, NWT, SILU>(b, ngroups, st);
         return;
@@ -1252,7 +1275,8 @@ void launch_combine_cfg(const CombineArgs& a, hipStream_t st) {
     CombineArgs b = a;
     const int tiles = static_cast<int>(plm::ceil_div(a.rows, 8 * TT));
     b.tiles_per_group = tiles;
-    const int nw = waves_for(static_cast<int64_t>(combine_segments(a)) * a.nbe);
+    const int nw = static_cast<int>(
+        std::max<int64_t>(1, std::min<int64_t>(static_cast<int64_t>(combine_segments(a)) * a.nbe, kCombineWaves)));
     const int64_t grid = static_cast<int64_t>(tiles) * combine_outputs(a);
     if (a.fused) {
         hipLaunchKernelGGL((fp8_combine_kernel<TT, U, true>), dim3(static_cast<unsigned>(grid)),
@@ -1746,6 +1770,25 @@ int device_routed_impl(const uint64_t* table, int64_t num_experts, const int64_t
     }
     float* act = reinterpret_cast<float*>(ws);
     MoePlan* plan = reinterpret_cast<MoePlan*>(ws + act_bytes);
+    uint16_t* hhi = reinterpret_cast<uint16_t*>(act);
+    uint16_t* hlo = hhi + static_cast<int64_t>(groups) * batch * inter;
+
+    RowsArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.x = hidden.f32;
+    a.xb = hidden.bf16;
+    a.x_stride = hid;
+    a.hhi = hhi;
+    a.hlo = hlo;
+    a.out_ld = inter;
+    a.rows = inter;
+    a.K = hid;
+    a.scale_cols = gsc;
+    a.nblocks = static_cast<int>(plm::ceil_div(hid, 128));
+    a.m_total = static_cast<int>(batch);
+    a.mc = static_cast<int>(batch);
+
+    int code = 0;
     if (route != nullptr) {
         // one wave per row while the per-wave arrays fit 32 KiB
         const int64_t e4 = (num_experts + 3) & ~int64_t(3);
@@ -1759,32 +1802,20 @@ int device_routed_impl(const uint64_t* table, int64_t num_experts, const int64_t
                            static_cast<int>(num_experts), static_cast<int>(batch), static_cast<int>(top_k),
                            route->n_groups, route->topk_groups, route->scoring, route->route_scale, table,
                            const_cast<int64_t*>(idx), const_cast<float*>(wts), plan, rejected);
+        code = plm::check_launch("moe route + plan kernel");
     } else {
         hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(64), 0, st, table, num_experts, idx, wts,
                            static_cast<int>(batch), static_cast<int>(top_k), plan, rejected);
+        code = plm::check_launch("moe plan kernel");
     }
-    int code = plm::check_launch("moe plan kernel");
     if (code != 0) return code;
 
-    RowsArgs a;
-    std::memset(&a, 0, sizeof(a));
     if (shared != nullptr) {
         a.w[0][0] = reinterpret_cast<const uint8_t*>(static_cast<uintptr_t>(shared[0]));
         a.s[0][0] = reinterpret_cast<const float*>(static_cast<uintptr_t>(shared[1]));
         a.w[1][0] = reinterpret_cast<const uint8_t*>(static_cast<uintptr_t>(shared[2]));
         a.s[1][0] = reinterpret_cast<const float*>(static_cast<uintptr_t>(shared[3]));
     }
-    a.x = hidden.f32;
-    a.xb = hidden.bf16;
-    a.x_stride = hid;
-    a.hhi = reinterpret_cast<uint16_t*>(act);
-    a.hlo = a.hhi + static_cast<int64_t>(groups) * batch * inter;
-    a.out_ld = inter;
-    a.rows = inter;
-    a.K = hid;
-    a.scale_cols = gsc;
-    a.nblocks = static_cast<int>(plm::ceil_div(hid, 128));
-    a.m_total = static_cast<int>(batch);
     a.plan = plan;
     a.ndev = ndev;
     launch_rows<2, true>(a, static_cast<int>(batch), groups, st);
