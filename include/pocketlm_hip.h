@@ -419,6 +419,30 @@ int ds_forward_verify_f32(void* handle, const int64_t* candidate_token_ids, int6
                           pocketlm_ds_verify_callback verify_callback, float* output_logits_per_position,
                           int64_t vocab_size);
 
+/* ds_forward.cpp:517-597: MLA attention of one decode token over the latent
+ * cache (device fp32): q_nope [H][nope], q_pe [H][rope], kv_cache [L][R],
+ * pe_cache [L][rope], wkv_b [H][nope + v][R] -> output_heads [H][v].
+ * Codes: 1 null pointer, 2 bad dimensions (also R > 1024 or rope > 256, the
+ * device kernel's limits), -3 workspace. */
+int ds_mla_attention_flash_forward(const float* q_nope, const float* q_pe, const float* kv_cache,
+                                   const float* pe_cache, const float* wkv_b, float* output_heads,
+                                   int64_t num_heads, int64_t cache_len, int64_t qk_nope_dim, int64_t qk_rope_dim,
+                                   int64_t kv_lora_rank, int64_t v_head_dim, float softmax_scale);
+
+/* ds_forward.cpp:647-782: one-token DeepSeek attention block (device fp32
+ * weights and caches): q_a -> RMSNorm -> q_b -> RoPE, kv_a -> RMSNorm /
+ * RoPE into row previous_len of next_kv_cache / next_pe_cache (after the
+ * previous rows, copied unless the buffers are the same), the MLA above,
+ * then o.  Codes: 1 null pointer or handle, 2 bad dimensions, 3 null
+ * previous caches with previous_len > 0, 100 + the MLA call's code. */
+int ds_attention_block_forward_f32(
+    void* handle, const float* hidden_in, const float* q_a_weight, const float* q_b_weight, const float* kv_a_weight,
+    const float* kv_b_weight, const float* o_weight, const float* q_norm_weight, const float* kv_norm_weight,
+    const float* previous_kv_cache, const float* previous_pe_cache, const float* rope_cos, const float* rope_sin,
+    float* next_kv_cache, float* next_pe_cache, float* hidden_out, int64_t hidden_dim, int64_t q_lora_rank,
+    int64_t kv_lora_rank, int64_t num_heads, int64_t qk_nope_dim, int64_t qk_rope_dim, int64_t v_head_dim,
+    int64_t previous_len, float rms_eps, float softmax_scale);
+
 /* ds_forward.cpp:879-955: softmax top-k router over u16 (fp16/bf16) hidden
  * [hidden_dim] and router weights [num_experts, hidden_dim] (device);
  * output_expert_ids int64 [k] and output_weights fp32 [k] (device).

@@ -118,6 +118,18 @@ __global__ __launch_bounds__(64) void ds_route_kernel(const float* __restrict__ 
 
 }  // namespace
 
+// Counters of one fused attention block call (ds_forward.cpp:775-779), for
+// ds_attention_block_forward_f32 (mla.hip).  Returns 1 on a null handle.
+int plm_ds_session_note_fused_attention(void* handle) {
+    Session* s = static_cast<Session*>(handle);
+    if (s == nullptr) return 1;
+    s->monolithic_calls += 1;
+    s->attention_invocations += 1;
+    s->fused_attention_invocations += 1;
+    return 0;
+}
+
+
 PLM_EXPORT void* ds_session_create(int64_t num_layers, int64_t hidden_dim, int64_t num_experts, int64_t top_k,
                                    void* fp8_pack_callback, void* kv_session_handle) {
     if (num_layers <= 0 || hidden_dim <= 0 || num_experts < 0 || top_k < 0) return nullptr;

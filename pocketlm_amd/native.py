@@ -1219,6 +1219,111 @@ def route_deepseek(logits: torch.Tensor, *, top_k: int = 8, n_groups: int = 8, t
 
 # --------------------------------------------------------------------------- lm_head
 
+# --------------------------------------------------------------------------- MLA attention
+
+def native_flash_mla_available() -> bool:
+    """src/pcketlm/native/__init__.py:837-842."""
+    return _available("PCKETLM_DISABLE_NATIVE_FLASH_MLA")
+
+
+def native_fused_ds_attention_available() -> bool:
+    """src/pcketlm/native/__init__.py:845-850."""
+    return _available("PCKETLM_DISABLE_FUSED_DS_ATTENTION")
+
+
+def ds_mla_attention_flash_forward(q_nope: torch.Tensor, q_pe: torch.Tensor, kv_cache: torch.Tensor,
+                                   pe_cache: torch.Tensor, wkv_b: torch.Tensor, *, softmax_scale: float) -> torch.Tensor:
+    """src/pcketlm/native/__init__.py:878-939 -> ds_forward.cpp:517-597: MLA
+    attention of one token over the latent cache; returns [heads, v_head_dim]
+    fp32 where q_nope lives."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_FLASH_MLA", "Native flash MLA")
+    dev = _target_device(q_nope, q_pe, kv_cache, pe_cache, wkv_b)
+    qn, qp, kv, pe, wkv = (_on(t, dev, torch.float32) for t in (q_nope, q_pe, kv_cache, pe_cache, wkv_b))
+    if qn.ndim != 2 or qp.ndim != 2:
+        raise ValueError("q_nope and q_pe must be [heads, dim]")
+    if kv.ndim != 2 or pe.ndim != 2:
+        raise ValueError("kv_cache and pe_cache must be [cache_len, dim]")
+    if wkv.ndim != 3:
+        raise ValueError("wkv_b must be [heads, qk_nope + v_head_dim, kv_lora_rank]")
+    heads, nope = int(qn.shape[0]), int(qn.shape[1])
+    rope, cache_len, rank = int(qp.shape[1]), int(kv.shape[0]), int(kv.shape[1])
+    if int(qp.shape[0]) != heads or int(wkv.shape[0]) != heads:
+        raise ValueError("head count mismatch")
+    if int(pe.shape[0]) != cache_len or int(pe.shape[1]) != rope:
+        raise ValueError("pe_cache shape mismatch")
+    if int(wkv.shape[2]) != rank or int(wkv.shape[1]) <= nope:
+        raise ValueError("wkv_b shape mismatch")
+    v_dim = int(wkv.shape[1]) - nope
+    out = torch.empty((heads, v_dim), dtype=torch.float32, device=dev)
+    with _launch(lib, dev):
+        code = lib.ds_mla_attention_flash_forward(_p(qn), _p(qp), _p(kv), _p(pe), _p(wkv), _p(out), heads, cache_len,
+                                                  nope, rope, rank, v_dim, float(softmax_scale))
+    _check("ds_mla_attention_flash_forward", code)
+    return _home(out, q_nope)
+
+
+def ds_attention_block_forward(session: "DeepSeekNativeSession", hidden: torch.Tensor, q_a_weight: torch.Tensor,
+                               q_b_weight: torch.Tensor, kv_a_weight: torch.Tensor, kv_b_weight: torch.Tensor,
+                               o_weight: torch.Tensor, q_norm_weight: torch.Tensor, kv_norm_weight: torch.Tensor, *,
+                               previous_kv_cache: torch.Tensor | None, previous_pe_cache: torch.Tensor | None,
+                               rope_cos: torch.Tensor, rope_sin: torch.Tensor, q_lora_rank: int, kv_lora_rank: int,
+                               num_heads: int, qk_nope_dim: int, qk_rope_dim: int, v_head_dim: int, rms_eps: float,
+                               softmax_scale: float):
+    """src/pcketlm/native/__init__.py:942-1068 -> ds_forward.cpp:647-782: a
+    one-token DeepSeek attention block as one native call.  Returns
+    (hidden_out [hidden_dim], (next_kv_cache, next_pe_cache)) where hidden
+    lives."""
+    lib = _require("PCKETLM_DISABLE_FUSED_DS_ATTENTION", "Native fused DeepSeek attention")
+    dev = _target_device(hidden, q_a_weight, q_b_weight, kv_a_weight, kv_b_weight, o_weight)
+    x = _on(hidden, dev, torch.float32).reshape(-1)
+    if int(x.numel()) <= 0:
+        raise ValueError("hidden must not be empty")
+    hidden_dim = int(x.numel())
+    q_a, q_b, kv_a, kv_b, o = (_on(t, dev, torch.float32) for t in (q_a_weight, q_b_weight, kv_a_weight, kv_b_weight,
+                                                                    o_weight))
+    q_norm = _on(q_norm_weight, dev, torch.float32).reshape(-1)
+    kv_norm = _on(kv_norm_weight, dev, torch.float32).reshape(-1)
+    cos = _on(rope_cos, dev, torch.float32).reshape(-1)
+    sin = _on(rope_sin, dev, torch.float32).reshape(-1)
+    q_rank, kv_rank, heads = int(q_lora_rank), int(kv_lora_rank), int(num_heads)
+    nope, rope, v_dim = int(qk_nope_dim), int(qk_rope_dim), int(v_head_dim)
+    if tuple(q_a.shape) != (q_rank, hidden_dim):
+        raise ValueError("q_a_weight must be [q_lora_rank, hidden_dim]")
+    if tuple(q_b.shape) != (heads * (nope + rope), q_rank):
+        raise ValueError("q_b_weight shape does not match DeepSeek attention config")
+    if tuple(kv_a.shape) != (kv_rank + rope, hidden_dim):
+        raise ValueError("kv_a_weight shape does not match DeepSeek attention config")
+    if tuple(kv_b.shape) != (heads * (nope + v_dim), kv_rank):
+        raise ValueError("kv_b_weight shape does not match DeepSeek attention config")
+    if tuple(o.shape) != (hidden_dim, heads * v_dim):
+        raise ValueError("o_weight shape does not match DeepSeek attention config")
+    if int(q_norm.numel()) != q_rank or int(kv_norm.numel()) != kv_rank:
+        raise ValueError("norm weight sizes do not match ranks")
+    if int(cos.numel()) != max(0, rope // 2) or int(sin.numel()) != max(0, rope // 2):
+        raise ValueError("rope cos/sin sizes must be qk_rope_dim / 2")
+    prev_kv = (torch.empty((0, kv_rank), dtype=torch.float32, device=dev) if previous_kv_cache is None
+               else _on(previous_kv_cache, dev, torch.float32).reshape(-1, kv_rank))
+    prev_pe = (torch.empty((0, rope), dtype=torch.float32, device=dev) if previous_pe_cache is None
+               else _on(previous_pe_cache, dev, torch.float32).reshape(-1, rope))
+    previous_len = int(prev_kv.shape[0])
+    if int(prev_pe.shape[0]) != previous_len:
+        raise ValueError("previous KV and PE cache lengths must match")
+    next_kv = torch.empty((previous_len + 1, kv_rank), dtype=torch.float32, device=dev)
+    next_pe = torch.empty((previous_len + 1, rope), dtype=torch.float32, device=dev)
+    out = torch.empty((hidden_dim,), dtype=torch.float32, device=dev)
+    prev_kv_p = _p(None) if previous_len == 0 else _p(prev_kv)
+    prev_pe_p = _p(None) if previous_len == 0 else _p(prev_pe)
+    with _launch(lib, dev):
+        code = lib.ds_attention_block_forward_f32(
+            session._handle, _p(x), _p(q_a), _p(q_b), _p(kv_a), _p(kv_b), _p(o), _p(q_norm), _p(kv_norm), prev_kv_p,
+            prev_pe_p, _p(cos), _p(sin), _p(next_kv), _p(next_pe), _p(out), hidden_dim, q_rank, kv_rank, heads, nope,
+            rope, v_dim, previous_len, float(rms_eps), float(softmax_scale))
+    _check("ds_attention_block_forward_f32", code)
+    # (no keep-alive list: the launches are ordered on torch's stream, so its
+    # allocator reuses these buffers only after them)
+    return _home(out, hidden), (_home(next_kv, hidden), _home(next_pe, hidden))
+
+
 def native_lm_head_topk_available() -> bool:
     return _available("PCKETLM_DISABLE_NATIVE_MATMUL")
 

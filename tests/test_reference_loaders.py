@@ -101,6 +101,8 @@ REFERENCE_OPTIONAL = [
     ("fp8_e4m3_block_mlp_many_weighted_f32", 15), ("fp8_e4m3_block_mlp_many_row_weighted_f32", 15),
     ("fp8_e4m3_block_mlp_many_pair_weighted_f32", 18), ("fp8_e4m3_block_mlp_avx512_f32", 13),
     ("ds_fused_attention_invocation_count", 1), ("kv_dense_layer_decode_u16_ext_packed_rows8", 24),
+    # bound behind hasattr by _load_ds_forward_lib (native/__init__.py:672-718)
+    ("ds_mla_attention_flash_forward", 13), ("ds_attention_block_forward_f32", 26),
 ]
 
 
