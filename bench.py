@@ -1172,6 +1172,60 @@ def table(args):
         dense_layer(1024)
         dense_layer(8192)
 
+    def mla_flash(cache_len):
+        # DeepSeek-V3 MLA attention of one token: 128 heads, nope 128, rope 64,
+        # latent rank 512, v 128; fp32 wkv_b [128, 256, 512] (67 MB) in two
+        # copies, a cache_len-row latent cache (fp32, as the reference keeps it)
+        H, nope, rope, R, v = 128, 128, 64, 512, 128
+        qn = torch.randn((H, nope), generator=gen, device="cuda") * 0.05
+        qp = torch.randn((H, rope), generator=gen, device="cuda") * 0.05
+        kvc = torch.randn((cache_len, R), generator=gen, device="cuda")
+        pec = torch.randn((cache_len, rope), generator=gen, device="cuda")
+        ws = [torch.randn((H, nope + v, R), generator=gen, device="cuda") * 0.02 for _ in range(2)]
+        out = torch.empty((H, v), device="cuda")
+        lib.pocketlm_set_stream(_stream_ptr(torch))
+        p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        calls = [lambda w=w: lib.ds_mla_attention_flash_forward(p(qn), p(qp), p(kvc), p(pec), p(w), p(out), H, cache_len,
+                                                                nope, rope, R, v, 1.0 / math.sqrt(192.0)) for w in ws]
+        nbytes = H * (nope + v) * R * 4 + cache_len * (R + rope) * 4 + H * (nope + rope) * 4 + H * v * 4
+        measure(f"mla attention DeepSeek-V3, {cache_len}-row latent cache (fp32)", 1, lambda: calls, nbytes)
+        del ws
+        torch.cuda.empty_cache()
+
+    if want("mla attention"):
+        mla_flash(1024)
+        mla_flash(4096)
+
+    def mla_block(prev_len):
+        # DeepSeek-V3 attention block of one token with fp32 weights (the
+        # reference's ds_attention_block_forward_f32): q_a 1536x7168, q_b
+        # 24576x1536, kv_a 576x7168, kv_b 32768x512, o 7168x16384 (750 MB)
+        hid, qr, R, H, nope, rope, v = 7168, 1536, 512, 128, 128, 64, 128
+        w = [torch.randn(s, generator=gen, device="cuda") * 0.02
+             for s in ((qr, hid), (H * (nope + rope), qr), (R + rope, hid), (H * (nope + v), R), (hid, H * v))]
+        norms = [torch.ones(qr, device="cuda"), torch.ones(R, device="cuda")]
+        x = torch.randn(hid, generator=gen, device="cuda")
+        kvb = torch.randn((prev_len + 1, R), generator=gen, device="cuda")
+        peb = torch.randn((prev_len + 1, rope), generator=gen, device="cuda")
+        cs = [torch.ones(rope // 2, device="cuda"), torch.zeros(rope // 2, device="cuda")]
+        out = torch.empty(hid, device="cuda")
+        sess = lib.ds_session_create(1, hid, 0, 0, None, None)
+        lib.pocketlm_set_stream(_stream_ptr(torch))
+        p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        call = lambda: lib.ds_attention_block_forward_f32(sess, p(x), *[p(t) for t in w], *[p(t) for t in norms],  # noqa: E731
+                                                          p(kvb), p(peb), *[p(t) for t in cs], p(kvb), p(peb), p(out),
+                                                          hid, qr, R, H, nope, rope, v, prev_len, 1e-6,
+                                                          1.0 / math.sqrt(192.0))
+        nbytes = sum(t.numel() for t in w) * 4 + (prev_len + 1) * (R + rope) * 4 + 2 * hid * 4
+        measure(f"ds-v3 attention block, {prev_len}-row latent cache (fp32 weights)", 1, lambda: [call], nbytes)
+        torch.cuda.synchronize()
+        lib.ds_session_destroy(sess)
+        del w
+        torch.cuda.empty_cache()
+
+    if want("attention block"):
+        mla_block(4096)
+
     transfers = []
     if want("fp8 pack -> HBM"):
         transfers.append(pack_transfer(torch))

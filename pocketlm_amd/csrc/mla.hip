@@ -54,8 +54,15 @@ __global__ __launch_bounds__(kThreads) void mla_qabs_kernel(const float* __restr
     const float* qh = q_nope + h * nope;
     const float* wh = wkv_b + h * (nope + v) * R;
     float acc = 0.0f;
-    if (r < R)
-        for (int64_t d = wave; d < nope; d += 4) acc = fmaf(qh[d], wh[d * R + r], acc);
+    if (r < R) {
+        for (int64_t d0 = wave; d0 < nope; d0 += 4 * 8) {
+            float vals[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) vals[u] = wh[min(d0 + 4 * u, nope - 1) * R + r];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = fmaf(d0 + 4 * u < nope ? qh[d0 + 4 * u] : 0.0f, vals[u], acc);
+        }
+    }
     part[wave][lane] = acc;
     __syncthreads();
     if (wave == 0 && r < R) q_abs[h * R + r] = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
@@ -73,7 +80,7 @@ __global__ __launch_bounds__(kThreads) void mla_qabs_kernel(const float* __restr
 constexpr int kChunks = 16;
 
 __host__ __device__ constexpr int64_t split_lds_floats(int cpt, int ppt) {
-    return static_cast<int64_t>(kTileTokens) * kChunks * ((cpt + 1) + (ppt + 1));
+    return static_cast<int64_t>(kTileTokens) * kChunks * ((cpt + 4) + (ppt + 4)) + kHeadsPerGroup * kTileTokens;
 }
 
 size_t split_lds_bytes(int cpt, int ppt) { return static_cast<size_t>(split_lds_floats(cpt, ppt)) * sizeof(float); }
@@ -85,19 +92,20 @@ __global__ __launch_bounds__(kThreads) void mla_split_kernel(const float* __rest
                                                             float* __restrict__ part, float* __restrict__ ml,
                                                             int64_t H, int64_t L, int64_t R, int64_t rope, float scale,
                                                             int64_t per_split) {
-    extern __shared__ float sm[];
-    constexpr int CS = CPT + 1, PS = PPT + 1;
+    extern __shared__ float4 sm4[];
+    float* sm = reinterpret_cast<float*>(sm4);
+    constexpr int CS = CPT + 4, PS = PPT + 4;  // 16-byte aligned chunks, staggered over the banks
+    static_assert(CPT % 4 == 0 && PPT % 4 == 0, "chunks of whole float4s");
     float* kv_t = sm;                                // [16 rows][16 chunks][CS]
     float* pe_t = kv_t + kTileTokens * kChunks * CS;  // [16 rows][16 chunks][PS]
+    float* pw = pe_t + kTileTokens * kChunks * PS;    // [16 heads][16 rows]: scores, then weights
     const int tid = threadIdx.x;
     const int hh = tid >> 4, cq = tid & 15;
     const int64_t h = static_cast<int64_t>(blockIdx.y) * kHeadsPerGroup + hh;
     const bool live = h < H;
     const int64_t t_begin = static_cast<int64_t>(blockIdx.x) * per_split;
     const int64_t t_end = min(L, t_begin + per_split);
-
-    // columns past R / rope stay zero in every tile
-    for (int64_t i = tid; i < split_lds_floats(CPT, PPT); i += kThreads) sm[i] = 0.0f;
+    const bool vec4 = CPT % 4 == 0 && (R & 3) == 0 && (reinterpret_cast<uintptr_t>(kv) & 15) == 0;
     float q[CPT], qr[PPT], acc[CPT];
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
@@ -114,56 +122,104 @@ __global__ __launch_bounds__(kThreads) void mla_split_kernel(const float* __rest
 
     for (int64_t t0 = t_begin; t0 < t_end; t0 += kTileTokens) {
         const int n = static_cast<int>(min(static_cast<int64_t>(kTileTokens), t_end - t0));
-        __syncthreads();  // the previous tile's readers are done
-        for (int64_t i = tid; i < kTileTokens * R; i += kThreads) {
-            const int64_t t = i / R, c = i - t * R;
-            kv_t[(t * kChunks + c / CPT) * CS + c % CPT] = t < n ? kv[(t0 + t) * R + c] : 0.0f;
-        }
-        for (int64_t i = tid; i < kTileTokens * rope; i += kThreads) {
-            const int64_t t = i / rope, c = i - t * rope;
-            pe_t[(t * kChunks + c / PPT) * PS + c % PPT] = t < n ? pe[(t0 + t) * rope + c] : 0.0f;
+        // thread (row tid / 16, chunk tid % 16) stages that chunk of the row:
+        // every load is issued before the first store
+        {
+            const int sr = tid >> 4, sc0 = tid & 15;
+            const bool row_in = sr < n;
+            const int64_t row = t0 + (row_in ? sr : 0);
+            const float* src = kv + row * R + static_cast<int64_t>(sc0) * CPT;
+            const int64_t left = R - static_cast<int64_t>(sc0) * CPT;  // columns of this chunk inside R
+            float vals[CPT];
+            if (vec4 && left >= CPT) {
+#pragma unroll
+                for (int i = 0; i < CPT / 4; ++i) {
+                    const float4 f = reinterpret_cast<const float4*>(src)[i];
+                    vals[4 * i] = f.x;
+                    vals[4 * i + 1] = f.y;
+                    vals[4 * i + 2] = f.z;
+                    vals[4 * i + 3] = f.w;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < CPT; ++i) vals[i] = i < left ? src[i] : 0.0f;
+            }
+            float pvals[PPT];
+            const float* psrc = pe + row * rope + static_cast<int64_t>(sc0) * PPT;
+            const int64_t pleft = rope - static_cast<int64_t>(sc0) * PPT;
+#pragma unroll
+            for (int i = 0; i < PPT; ++i) pvals[i] = i < pleft ? psrc[i] : 0.0f;
+            __syncthreads();  // the previous tile's readers are done
+            float4* dst = reinterpret_cast<float4*>(kv_t + (sr * kChunks + sc0) * CS);
+#pragma unroll
+            for (int i = 0; i < CPT / 4; ++i)
+                dst[i] = row_in ? make_float4(vals[4 * i], vals[4 * i + 1], vals[4 * i + 2], vals[4 * i + 3])
+                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            float4* pdst = reinterpret_cast<float4*>(pe_t + (sr * kChunks + sc0) * PS);
+#pragma unroll
+            for (int i = 0; i < PPT / 4; ++i)
+                pdst[i] = row_in ? make_float4(pvals[4 * i], pvals[4 * i + 1], pvals[4 * i + 2], pvals[4 * i + 3])
+                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
         __syncthreads();
-        // partial scores of the chunk: latent part, then rope part
-        float sc[kTileTokens];
-#pragma unroll
-        for (int t = 0; t < kTileTokens; ++t) {
-            const float* k = kv_t + (t * kChunks + cq) * CS;
-            const float* kr = pe_t + (t * kChunks + cq) * PS;
+        // scores, one token at a time: the chunk's partial dot (latent, then
+        // rope part), added over the head's 16 lanes; lane 0 of the head
+        // keeps it in pw
+        for (int t = 0; t < n; ++t) {
+            const float4* k = reinterpret_cast<const float4*>(kv_t + (t * kChunks + cq) * CS);
+            const float4* kr = reinterpret_cast<const float4*>(pe_t + (t * kChunks + cq) * PS);
             float d = 0.0f, dr = 0.0f;
 #pragma unroll
-            for (int i = 0; i < CPT; ++i) d = fmaf(q[i], k[i], d);
+            for (int i = 0; i < CPT / 4; ++i) {
+                const float4 kk = k[i];
+                d = fmaf(q[4 * i], kk.x, d);
+                d = fmaf(q[4 * i + 1], kk.y, d);
+                d = fmaf(q[4 * i + 2], kk.z, d);
+                d = fmaf(q[4 * i + 3], kk.w, d);
+            }
 #pragma unroll
-            for (int i = 0; i < PPT; ++i) dr = fmaf(qr[i], kr[i], dr);
-            sc[t] = d + dr;
+            for (int i = 0; i < PPT / 4; ++i) {
+                const float4 kk = kr[i];
+                dr = fmaf(qr[4 * i], kk.x, dr);
+                dr = fmaf(qr[4 * i + 1], kk.y, dr);
+                dr = fmaf(qr[4 * i + 2], kk.z, dr);
+                dr = fmaf(qr[4 * i + 3], kk.w, dr);
+            }
+            float sc = d + dr;
+#pragma unroll
+            for (int off = 8; off >= 1; off >>= 1) sc += __shfl_xor(sc, off);
+            if (cq == 0) pw[hh * kTileTokens + t] = sc * scale;
         }
+        __syncthreads();
+        // softmax step, lane cq of a head taking token cq
+        const float st = cq < n ? pw[hh * kTileTokens + cq] : -INFINITY;
+        float mt = st;
 #pragma unroll
-        for (int off = 8; off >= 1; off >>= 1)
-#pragma unroll
-            for (int t = 0; t < kTileTokens; ++t) sc[t] += __shfl_xor(sc[t], off);
-        float mt = -INFINITY;
-#pragma unroll
-        for (int t = 0; t < kTileTokens; ++t) {
-            sc[t] = t < n ? sc[t] * scale : -INFINITY;
-            mt = fmaxf(mt, sc[t]);
-        }
+        for (int off = 8; off >= 1; off >>= 1) mt = fmaxf(mt, __shfl_xor(mt, off));
         const float m_new = fmaxf(m_run, mt);
         const float corr = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
-        float lt = 0.0f;
+        const float pt = st == -INFINITY ? 0.0f : expf(st - m_new);
+        float lt = pt;
 #pragma unroll
-        for (int t = 0; t < kTileTokens; ++t) {
-            sc[t] = sc[t] == -INFINITY ? 0.0f : expf(sc[t] - m_new);
-            lt += sc[t];
-        }
+        for (int off = 8; off >= 1; off >>= 1) lt += __shfl_xor(lt, off);
         l_run = l_run * corr + lt;
         m_run = m_new;
+        __syncthreads();  // every score read before the weights replace them
+        pw[hh * kTileTokens + cq] = pt;
+        __syncthreads();
 #pragma unroll
         for (int i = 0; i < CPT; ++i) acc[i] *= corr;
+        for (int t = 0; t < n; ++t) {
+            const float w = pw[hh * kTileTokens + t];
+            const float4* k = reinterpret_cast<const float4*>(kv_t + (t * kChunks + cq) * CS);
 #pragma unroll
-        for (int t = 0; t < kTileTokens; ++t) {
-            const float* k = kv_t + (t * kChunks + cq) * CS;
-#pragma unroll
-            for (int i = 0; i < CPT; ++i) acc[i] = fmaf(sc[t], k[i], acc[i]);
+            for (int i = 0; i < CPT / 4; ++i) {
+                const float4 kk = k[i];
+                acc[4 * i] = fmaf(w, kk.x, acc[4 * i]);
+                acc[4 * i + 1] = fmaf(w, kk.y, acc[4 * i + 1]);
+                acc[4 * i + 2] = fmaf(w, kk.z, acc[4 * i + 2]);
+                acc[4 * i + 3] = fmaf(w, kk.w, acc[4 * i + 3]);
+            }
         }
     }
     if (!live) return;
@@ -191,25 +247,35 @@ __global__ __launch_bounds__(kThreads) void mla_merge_out_kernel(const float* __
     extern __shared__ float lat[];  // [R]
     __shared__ float w[kMaxSplits];
     __shared__ float inv_s;
+    static_assert(kMaxSplits == 64, "the split weights are one wave's lanes");
     const int64_t h = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid == 0) {
-        float M = -INFINITY;
-        for (int64_t s = 0; s < nsplit; ++s) M = fmaxf(M, ml[(s * H + h) * 2]);
-        float denom = 0.0f;
-        for (int64_t s = 0; s < nsplit; ++s) {
-            const float m = ml[(s * H + h) * 2];
-            const float ws = m == -INFINITY ? 0.0f : expf(m - M);
-            w[s] = ws;
-            denom = fmaf(ws, ml[(s * H + h) * 2 + 1], denom);
-        }
-        inv_s = denom > 0.0f ? 1.0f / denom : 0.0f;
+    if (wave == 0) {
+        // lane s: split s (a fixed DPP tree for the sum)
+        const bool has = lane < nsplit;
+        const float m = has ? ml[(static_cast<int64_t>(lane) * H + h) * 2] : -INFINITY;
+        const float l = has ? ml[(static_cast<int64_t>(lane) * H + h) * 2 + 1] : 0.0f;
+        float M = m;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+        const float ws = m == -INFINITY ? 0.0f : expf(m - M);
+        w[lane] = ws;
+        const float denom = plm_wave_sum(ws * l);
+        if (lane == kSumLane) inv_s = denom > 0.0f ? 1.0f / denom : 0.0f;
     }
     __syncthreads();
     const float inv = inv_s;
+    // (loads past the last split read the last one again; their weight is 0)
     for (int64_t c = tid; c < R; c += kThreads) {
+        const float* src = part + h * R + c;
         float a = 0.0f;
-        for (int64_t s = 0; s < nsplit; ++s) a = fmaf(w[s], part[(s * H + h) * R + c], a);
+        for (int64_t s0 = 0; s0 < nsplit; s0 += 16) {
+            float vals[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) vals[u] = src[min(s0 + u, nsplit - 1) * H * R];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) a = fmaf(w[min(s0 + u, static_cast<int64_t>(kMaxSplits) - 1)], vals[u], a);
+        }
         lat[c] = a * inv;
     }
     __syncthreads();
@@ -218,7 +284,13 @@ __global__ __launch_bounds__(kThreads) void mla_merge_out_kernel(const float* __
     for (int64_t j = static_cast<int64_t>(blockIdx.y) * 32 + wave; j < j_end; j += 4) {
         const float* row = wv + j * R;
         float a = 0.0f;
-        for (int64_t c = lane; c < R; c += 64) a = fmaf(lat[c], row[c], a);
+        for (int64_t c0 = lane; c0 < R; c0 += 64 * 8) {
+            float vals[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) vals[u] = row[min(c0 + 64 * u, R - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) a = fmaf(c0 + 64 * u < R ? lat[c0 + 64 * u] : 0.0f, vals[u], a);
+        }
         a = plm_wave_sum(a);
         if (lane == kSumLane) out[h * v + j] = a;
     }
