@@ -12,13 +12,15 @@
 //                         split nope, their partial sums added in wave order.
 //   mla_split_kernel      flash-decode partials: workgroup (split, 16 heads)
 //                         walks its tokens in tiles of 16 rows staged in LDS
-//                         (each latent row is read once for 16 heads); a
-//                         thread owns one head's 1/16 of the latent columns,
-//                         with a running max / sum per head.
-//   mla_merge_out_kernel  rescales the splits to the global max, divides by
-//                         the sum (1 / sum, 0 when the sum is not positive, as
-//                         the reference does), and applies the value rows of
-//                         kv_b to the latent: workgroup (head, 32 outputs).
+//                         (each latent row is read once for 16 heads); the
+//                         scores and the weighted rows are 16 x 16 products
+//                         on the matrix cores (fp32), with a running max /
+//                         sum per head.
+//   mla_merge_kernel      rescales the splits to the global max and divides
+//                         by the sum (1 / sum, 0 when the sum is not positive,
+//                         as the reference does): latent [H][R].
+//   mla_value_kernel      the value rows of kv_b applied to the latent, four
+//                         rows per wave.
 //
 // The block: fp32 GEMVs (one wave per row, float4 loads, a fixed DPP sum),
 // RMSNorm and RoPE kernels, the new cache row appended after the previous
@@ -37,8 +39,8 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kHeadsPerGroup = 16;  // heads of one split workgroup
 constexpr int kTileTokens = 16;     // latent rows staged per step
-constexpr int64_t kMaxRank = 1024;  // 16 chunks of at most 64 columns
-constexpr int64_t kMaxRope = 256;   // 16 chunks of at most 16
+constexpr int64_t kMaxRank = 1024;  // the split kernel's largest instance: 16 column tiles per wave,
+constexpr int64_t kMaxRope = 256;   // 20 chunks of 16 columns per wave
 constexpr int kMaxSplits = 64;
 
 // ------------------------------------------------------------------ q_abs
@@ -68,183 +70,258 @@ __global__ __launch_bounds__(kThreads) void mla_qabs_kernel(const float* __restr
     if (wave == 0 && r < R) q_abs[h * R + r] = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
 }
 
-// ------------------------------------------------------------------ split
-// Thread (head tid / 16 of the group, column chunk tid % 16): it holds the
-// CPT query values of its chunk in registers (and PPT of the rope part), dots
-// them with each staged row's chunk, and the 16 chunks' partial dots are
-// added across the head's 16 lanes (xor shuffles), so every lane of a head
-// sees all 16 scores of the tile.  The same thread then accumulates its
-// chunk of the head's latent with those weights.  LDS holds the tile's rows
-// chunk by chunk, each chunk padded by one float (no bank conflicts between
-// the 16 chunks).
-constexpr int kChunks = 16;
-
-__host__ __device__ constexpr int64_t split_lds_floats(int cpt, int ppt) {
-    return static_cast<int64_t>(kTileTokens) * kChunks * ((cpt + 4) + (ppt + 4)) + kHeadsPerGroup * kTileTokens;
+// The same with float4 columns (R % 4 == 0, aligned): grid (H, ceil(R / 256)),
+// lane l of every wave takes columns 4 l .. 4 l + 3 of the workgroup's 256.
+__global__ __launch_bounds__(kThreads) void mla_qabs4_kernel(const float* __restrict__ q_nope,
+                                                            const float* __restrict__ wkv_b, float* __restrict__ q_abs,
+                                                            int64_t nope, int64_t R, int64_t v) {
+    __shared__ float4 part[4][64];
+    const int64_t h = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t c = static_cast<int64_t>(blockIdx.y) * 256 + 4 * lane;
+    const float* qh = q_nope + h * nope;
+    const float* wh = wkv_b + h * (nope + v) * R;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (c < R) {
+        for (int64_t d0 = wave; d0 < nope; d0 += 4 * 8) {
+            float4 vals[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) vals[u] = *reinterpret_cast<const float4*>(wh + min(d0 + 4 * u, nope - 1) * R + c);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float qd = d0 + 4 * u < nope ? qh[d0 + 4 * u] : 0.0f;
+                acc.x = fmaf(qd, vals[u].x, acc.x);
+                acc.y = fmaf(qd, vals[u].y, acc.y);
+                acc.z = fmaf(qd, vals[u].z, acc.z);
+                acc.w = fmaf(qd, vals[u].w, acc.w);
+            }
+        }
+    }
+    part[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && c < R) {
+        const float4 p0 = part[0][lane], p1 = part[1][lane], p2 = part[2][lane], p3 = part[3][lane];
+        *reinterpret_cast<float4*>(q_abs + h * R + c) =
+            make_float4(((p0.x + p1.x) + p2.x) + p3.x, ((p0.y + p1.y) + p2.y) + p3.y, ((p0.z + p1.z) + p2.z) + p3.z,
+                        ((p0.w + p1.w) + p2.w) + p3.w);
+    }
 }
 
-size_t split_lds_bytes(int cpt, int ppt) { return static_cast<size_t>(split_lds_floats(cpt, ppt)) * sizeof(float); }
+// ------------------------------------------------------------------ split
+// Flash-decode partials on the matrix cores, v_mfma_f32_16x16x4_f32 (fp32
+// products and sums; A[i][k] in lane i + 16 k, B[k][j] in lane j + 16 k,
+// D[i][j] in lane j + 16 (i / 4), register i % 4).  Workgroup (split, 16
+// heads), four waves.  A tile of 16 cache rows is staged in LDS as
+// [row][RS]: the latent columns padded with zeros to R16 (a multiple of 16),
+// then the rope columns padded to P16; rows past the split are zeros.
+//
+//  scores  S^T[row][head] = sum_c row[c] * qfull[head][c] (qfull = q_abs then
+//          q_pe, padded alike).  The K dimension goes in chunks of 16
+//          columns, chunk j to wave j % 4; in a chunk, lane group g = lane /
+//          16 takes columns 16 j + 4 g .. 16 j + 4 g + 3 over the four steps,
+//          so each lane reads one float4 of the row (LDS) and one of the query
+//          (registers, loaded once).  The four waves' partial tiles are added
+//          in LDS in wave order: every wave then holds the same scores, lane
+//          (head l % 16) registers r = rows 4 g + r.
+//  softmax running max / sum per head; the rows of a head are spread over
+//          4 registers and 4 lane groups (two cross-group shuffles).
+//  values  Lat^T[col][head] += sum_row kv[row][col] * p[row][head], column
+//          tiles of 16 dealt out to the waves.  Step s takes row 4 g + s in
+//          lane group g: register s of the score tile is already the B
+//          operand, and the accumulator of lane l is head l % 16's, so the
+//          rescale by exp(m_old - m_new) is a per-lane multiply.
+// QC: chunks (and staging float4s) per lane at most; NT: column tiles per
+// wave at most.
+typedef float mla_f32x4 __attribute__((ext_vector_type(4)));
 
-template <int CPT, int PPT>
+struct SplitShape {
+    int64_t R16, P16, K16, RS, nct;
+};
+
+__host__ __device__ inline SplitShape split_shape(int64_t R, int64_t rope) {
+    SplitShape s;
+    s.R16 = (R + 15) & ~int64_t(15);
+    s.P16 = (rope + 15) & ~int64_t(15);
+    s.K16 = s.R16 + s.P16;
+    s.RS = ((s.K16 + 31) & ~int64_t(31)) + 4;  // rows 4 banks apart
+    s.nct = s.R16 / 16;
+    return s;
+}
+
+size_t split_lds_bytes(int64_t R, int64_t rope) {
+    return static_cast<size_t>(kTileTokens * split_shape(R, rope).RS + 4 * 64 * 4) * sizeof(float);
+}
+
+__device__ __forceinline__ mla_f32x4 mfma_f32(float a, float b, mla_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Columns c0 .. c0 + 3 of a padded [latent | rope] row, zeros outside the
+// two parts or when !ok.  VEC: R and rope are multiples of 4 and the rows
+// 16-byte aligned; the load is always issued, from krow when the columns are
+// padding, and masked afterwards (bitwise, so the zeros are exact).
+template <bool VEC>
+__device__ __forceinline__ float4 padded4(const float* krow, const float* prow, int c0, int R, int R16, int rope,
+                                          bool ok) {
+    if constexpr (VEC) {
+        const bool in_k = c0 < R, in_p = !in_k && c0 >= R16 && c0 < R16 + rope;
+        const float* base = in_p ? prow : krow;
+        const int off = in_k ? c0 : (in_p ? c0 - R16 : 0);
+        const uint4 x = *reinterpret_cast<const uint4*>(base + off);
+        const uint32_t m = ok && (in_k || in_p) ? ~0u : 0u;
+        return make_float4(__uint_as_float(x.x & m), __uint_as_float(x.y & m), __uint_as_float(x.z & m),
+                           __uint_as_float(x.w & m));
+    } else {
+        float e[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = c0 + i;
+            e[i] = !ok ? 0.0f : (c < R ? krow[c] : (c >= R16 && c < R16 + rope ? prow[c - R16] : 0.0f));
+        }
+        return make_float4(e[0], e[1], e[2], e[3]);
+    }
+}
+
+template <int QC, int NT, bool VEC>
 __global__ __launch_bounds__(kThreads) void mla_split_kernel(const float* __restrict__ q_abs,
                                                             const float* __restrict__ q_pe,
                                                             const float* __restrict__ kv, const float* __restrict__ pe,
                                                             float* __restrict__ part, float* __restrict__ ml,
-                                                            int64_t H, int64_t L, int64_t R, int64_t rope, float scale,
-                                                            int64_t per_split) {
+                                                            int64_t H, int64_t L, int64_t R64, int64_t rope64,
+                                                            float scale, int64_t per_split) {
     extern __shared__ float4 sm4[];
-    float* sm = reinterpret_cast<float*>(sm4);
-    constexpr int CS = CPT + 4, PS = PPT + 4;  // 16-byte aligned chunks, staggered over the banks
-    static_assert(CPT % 4 == 0 && PPT % 4 == 0, "chunks of whole float4s");
-    float* kv_t = sm;                                // [16 rows][16 chunks][CS]
-    float* pe_t = kv_t + kTileTokens * kChunks * CS;  // [16 rows][16 chunks][PS]
-    float* pw = pe_t + kTileTokens * kChunks * PS;    // [16 heads][16 rows]: scores, then weights
-    const int tid = threadIdx.x;
-    const int hh = tid >> 4, cq = tid & 15;
-    const int64_t h = static_cast<int64_t>(blockIdx.y) * kHeadsPerGroup + hh;
+    float* tile = reinterpret_cast<float*>(sm4);  // [16][RS]
+    const SplitShape sh = split_shape(R64, rope64);
+    const int R = static_cast<int>(R64), rope = static_cast<int>(rope64);
+    const int R16 = static_cast<int>(sh.R16), K16 = static_cast<int>(sh.K16), RS = static_cast<int>(sh.RS);
+    const int nct = R16 / 16;
+    mla_f32x4* red = reinterpret_cast<mla_f32x4*>(tile + kTileTokens * RS);  // [4 waves][64 lanes]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hl = lane & 15, g = lane >> 4;
+    const int64_t h = static_cast<int64_t>(blockIdx.y) * kHeadsPerGroup + hl;
     const bool live = h < H;
+    // the row padding [K16, RS) is zero for good: chunks past K16 read it
+    for (int i = tid; i < kTileTokens * (RS - K16); i += kThreads) {
+        const int r = i / (RS - K16);
+        tile[r * RS + K16 + (i - r * (RS - K16))] = 0.0f;
+    }
     const int64_t t_begin = static_cast<int64_t>(blockIdx.x) * per_split;
     const int64_t t_end = min(L, t_begin + per_split);
-    const bool vec4 = CPT % 4 == 0 && (R & 3) == 0 && (reinterpret_cast<uintptr_t>(kv) & 15) == 0;
-    float q[CPT], qr[PPT], acc[CPT];
+
+    // the query chunks of this wave, for head hl (a dead head reads head 0, weighted 0)
+    float4 q[QC];
+    {
+        const int64_t hq = live ? h : 0;
+        const float* qrow = q_abs + hq * R;
+        const float* prow = q_pe + hq * rope;
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-        const int64_t c = static_cast<int64_t>(cq) * CPT + i;
-        q[i] = live && c < R ? q_abs[h * R + c] : 0.0f;
-        acc[i] = 0.0f;
+        for (int jj = 0; jj < QC; ++jj) {
+            const int c0 = 16 * (wave + 4 * jj) + 4 * g;
+            q[jj] = padded4<VEC>(qrow, prow, c0, R, R16, rope, live);
+        }
     }
+    // staging: thread (row tid / 16) takes float4 columns tid % 16 + 16 k of the row
+    const int sr = tid >> 4, sq = tid & 15;
+    float4 st[QC];
+    auto fetch = [&](int64_t t0, int n) {
+        const int64_t t = t0 + (sr < n ? sr : 0);
+        const float* krow = kv + t * R;
+        const float* prow = pe + t * rope;
 #pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-        const int64_t c = static_cast<int64_t>(cq) * PPT + i;
-        qr[i] = live && c < rope ? q_pe[h * rope + c] : 0.0f;
-    }
+        for (int k = 0; k < QC; ++k) st[k] = padded4<VEC>(krow, prow, 4 * sq + 64 * k, R, R16, rope, sr < n);
+    };
+    mla_f32x4 acc[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) acc[i] = mla_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -INFINITY, l_run = 0.0f;
 
+    int n = static_cast<int>(min(static_cast<int64_t>(kTileTokens), t_end - t_begin));
+    fetch(t_begin, n);
     for (int64_t t0 = t_begin; t0 < t_end; t0 += kTileTokens) {
-        const int n = static_cast<int>(min(static_cast<int64_t>(kTileTokens), t_end - t0));
-        // thread (row tid / 16, chunk tid % 16) stages that chunk of the row:
-        // every load is issued before the first store
-        {
-            const int sr = tid >> 4, sc0 = tid & 15;
-            const bool row_in = sr < n;
-            const int64_t row = t0 + (row_in ? sr : 0);
-            const float* src = kv + row * R + static_cast<int64_t>(sc0) * CPT;
-            const int64_t left = R - static_cast<int64_t>(sc0) * CPT;  // columns of this chunk inside R
-            float vals[CPT];
-            if (vec4 && left >= CPT) {
+        __syncthreads();  // the previous tile's readers are done
 #pragma unroll
-                for (int i = 0; i < CPT / 4; ++i) {
-                    const float4 f = reinterpret_cast<const float4*>(src)[i];
-                    vals[4 * i] = f.x;
-                    vals[4 * i + 1] = f.y;
-                    vals[4 * i + 2] = f.z;
-                    vals[4 * i + 3] = f.w;
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < CPT; ++i) vals[i] = i < left ? src[i] : 0.0f;
-            }
-            float pvals[PPT];
-            const float* psrc = pe + row * rope + static_cast<int64_t>(sc0) * PPT;
-            const int64_t pleft = rope - static_cast<int64_t>(sc0) * PPT;
-#pragma unroll
-            for (int i = 0; i < PPT; ++i) pvals[i] = i < pleft ? psrc[i] : 0.0f;
-            __syncthreads();  // the previous tile's readers are done
-            float4* dst = reinterpret_cast<float4*>(kv_t + (sr * kChunks + sc0) * CS);
-#pragma unroll
-            for (int i = 0; i < CPT / 4; ++i)
-                dst[i] = row_in ? make_float4(vals[4 * i], vals[4 * i + 1], vals[4 * i + 2], vals[4 * i + 3])
-                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            float4* pdst = reinterpret_cast<float4*>(pe_t + (sr * kChunks + sc0) * PS);
-#pragma unroll
-            for (int i = 0; i < PPT / 4; ++i)
-                pdst[i] = row_in ? make_float4(pvals[4 * i], pvals[4 * i + 1], pvals[4 * i + 2], pvals[4 * i + 3])
-                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
+        for (int k = 0; k < QC; ++k)  // columns past K16 land in the row's padding
+            *reinterpret_cast<float4*>(tile + sr * RS + min(4 * sq + 64 * k, K16)) = st[k];
         __syncthreads();
-        // scores, one token at a time: the chunk's partial dot (latent, then
-        // rope part), added over the head's 16 lanes; lane 0 of the head
-        // keeps it in pw
-        for (int t = 0; t < n; ++t) {
-            const float4* k = reinterpret_cast<const float4*>(kv_t + (t * kChunks + cq) * CS);
-            const float4* kr = reinterpret_cast<const float4*>(pe_t + (t * kChunks + cq) * PS);
-            float d = 0.0f, dr = 0.0f;
+        const int64_t t1 = t0 + kTileTokens;
+        const int n_next = static_cast<int>(min(static_cast<int64_t>(kTileTokens), t_end - t1));
+        if (n_next > 0) fetch(t1, n_next);  // in flight during this tile's work
+
+        // scores: this wave's chunks (past Kc: zero rows times a zero query)
+        mla_f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+        float4 a[QC];
 #pragma unroll
-            for (int i = 0; i < CPT / 4; ++i) {
-                const float4 kk = k[i];
-                d = fmaf(q[4 * i], kk.x, d);
-                d = fmaf(q[4 * i + 1], kk.y, d);
-                d = fmaf(q[4 * i + 2], kk.z, d);
-                d = fmaf(q[4 * i + 3], kk.w, d);
-            }
+        for (int jj = 0; jj < QC; ++jj)
+            a[jj] = *reinterpret_cast<const float4*>(tile + hl * RS + min(16 * (wave + 4 * jj) + 4 * g, K16));
 #pragma unroll
-            for (int i = 0; i < PPT / 4; ++i) {
-                const float4 kk = kr[i];
-                dr = fmaf(qr[4 * i], kk.x, dr);
-                dr = fmaf(qr[4 * i + 1], kk.y, dr);
-                dr = fmaf(qr[4 * i + 2], kk.z, dr);
-                dr = fmaf(qr[4 * i + 3], kk.w, dr);
-            }
-            float sc = d + dr;
-#pragma unroll
-            for (int off = 8; off >= 1; off >>= 1) sc += __shfl_xor(sc, off);
-            if (cq == 0) pw[hh * kTileTokens + t] = sc * scale;
+        for (int jj = 0; jj < QC; ++jj) {
+            s = mfma_f32(a[jj].x, q[jj].x, s);
+            s = mfma_f32(a[jj].y, q[jj].y, s);
+            s = mfma_f32(a[jj].z, q[jj].z, s);
+            s = mfma_f32(a[jj].w, q[jj].w, s);
         }
+        red[wave * 64 + lane] = s;
         __syncthreads();
-        // softmax step, lane cq of a head taking token cq
-        const float st = cq < n ? pw[hh * kTileTokens + cq] : -INFINITY;
-        float mt = st;
+        s = ((red[lane] + red[64 + lane]) + red[128 + lane]) + red[192 + lane];
+
+        // softmax step: lane (head hl, rows 4 g + r)
+        float p[4];
+        float mt = -INFINITY;
 #pragma unroll
-        for (int off = 8; off >= 1; off >>= 1) mt = fmaxf(mt, __shfl_xor(mt, off));
+        for (int r = 0; r < 4; ++r) {
+            p[r] = 4 * g + r < n ? s[r] * scale : -INFINITY;
+            mt = fmaxf(mt, p[r]);
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
         const float m_new = fmaxf(m_run, mt);
         const float corr = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
-        const float pt = st == -INFINITY ? 0.0f : expf(st - m_new);
-        float lt = pt;
+        float lt = 0.0f;
 #pragma unroll
-        for (int off = 8; off >= 1; off >>= 1) lt += __shfl_xor(lt, off);
+        for (int r = 0; r < 4; ++r) {
+            p[r] = p[r] == -INFINITY ? 0.0f : expf(p[r] - m_new);
+            lt += p[r];
+        }
+        lt += __shfl_xor(lt, 16);
+        lt += __shfl_xor(lt, 32);
         l_run = l_run * corr + lt;
         m_run = m_new;
-        __syncthreads();  // every score read before the weights replace them
-        pw[hh * kTileTokens + cq] = pt;
-        __syncthreads();
+
+        // values: this wave's column tiles (past nct: the last tile again, never stored)
+        const float* vrow = tile + 4 * g * RS + hl;
 #pragma unroll
-        for (int i = 0; i < CPT; ++i) acc[i] *= corr;
-        for (int t = 0; t < n; ++t) {
-            const float w = pw[hh * kTileTokens + t];
-            const float4* k = reinterpret_cast<const float4*>(kv_t + (t * kChunks + cq) * CS);
+        for (int i = 0; i < NT; ++i) {
+            const int col = 16 * min(wave + 4 * i, nct - 1);
+            acc[i] *= corr;
 #pragma unroll
-            for (int i = 0; i < CPT / 4; ++i) {
-                const float4 kk = k[i];
-                acc[4 * i] = fmaf(w, kk.x, acc[4 * i]);
-                acc[4 * i + 1] = fmaf(w, kk.y, acc[4 * i + 1]);
-                acc[4 * i + 2] = fmaf(w, kk.z, acc[4 * i + 2]);
-                acc[4 * i + 3] = fmaf(w, kk.w, acc[4 * i + 3]);
-            }
+            for (int r = 0; r < 4; ++r) acc[i] = mfma_f32(vrow[r * RS + col], p[r], acc[i]);
         }
+        n = n_next;
     }
     if (!live) return;
     const int64_t s_idx = blockIdx.x;
-    float* dst = part + (s_idx * H + h) * R;
+    float* dst = part + (s_idx * H + h) * R16;
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-        const int64_t c = static_cast<int64_t>(cq) * CPT + i;
-        if (c < R) dst[c] = acc[i];
+    for (int i = 0; i < NT; ++i) {
+        const int ct = wave + 4 * i;
+        if (ct < nct)
+            *reinterpret_cast<float4*>(dst + 16 * ct + 4 * g) = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
     }
-    if (cq == 0) {
+    if (wave == 0 && g == 0) {
         ml[(s_idx * H + h) * 2] = m_run;
         ml[(s_idx * H + h) * 2 + 1] = l_run;
     }
 }
 
-// ------------------------------------------------------------------ merge + value rows
-// Workgroup (head h, outputs 32 j0 .. 32 j0 + 31): latent = sum_s w_s part_s /
-// sum_s w_s l_s with w_s = exp(m_s - M), then out[h][j] = latent . wkv_b[h][nope + j].
-__global__ __launch_bounds__(kThreads) void mla_merge_out_kernel(const float* __restrict__ part,
-                                                                const float* __restrict__ ml,
-                                                                const float* __restrict__ wkv_b,
-                                                                float* __restrict__ out, int64_t H, int64_t nsplit,
-                                                                int64_t nope, int64_t R, int64_t v) {
-    extern __shared__ float lat[];  // [R]
+// ------------------------------------------------------------------ merge
+// Workgroup (head h, latent columns 256 y ..): latent = sum_s w_s part_s /
+// sum_s w_s l_s with w_s = exp(m_s - M) (1 / sum, 0 when the sum is not
+// positive, as the reference does).  Each partial is read once; the
+// partials are rows of RP (R rounded up to 16) floats.
+__global__ __launch_bounds__(kThreads) void mla_merge_kernel(const float* __restrict__ part,
+                                                            const float* __restrict__ ml, float* __restrict__ lat,
+                                                            int64_t H, int64_t nsplit, int64_t R, int64_t RP) {
     __shared__ float w[kMaxSplits];
     __shared__ float inv_s;
     static_assert(kMaxSplits == 64, "the split weights are one wave's lanes");
@@ -264,35 +341,64 @@ __global__ __launch_bounds__(kThreads) void mla_merge_out_kernel(const float* __
         if (lane == kSumLane) inv_s = denom > 0.0f ? 1.0f / denom : 0.0f;
     }
     __syncthreads();
-    const float inv = inv_s;
+    const int64_t c = static_cast<int64_t>(blockIdx.y) * kThreads + tid;
+    if (c >= R) return;
     // (loads past the last split read the last one again; their weight is 0)
-    for (int64_t c = tid; c < R; c += kThreads) {
-        const float* src = part + h * R + c;
-        float a = 0.0f;
-        for (int64_t s0 = 0; s0 < nsplit; s0 += 16) {
-            float vals[16];
+    const float* src = part + h * RP + c;
+    float a = 0.0f;
+    for (int64_t s0 = 0; s0 < nsplit; s0 += 16) {
+        float vals[16];
 #pragma unroll
-            for (int u = 0; u < 16; ++u) vals[u] = src[min(s0 + u, nsplit - 1) * H * R];
+        for (int u = 0; u < 16; ++u) vals[u] = src[min(s0 + u, nsplit - 1) * H * RP];
 #pragma unroll
-            for (int u = 0; u < 16; ++u) a = fmaf(w[min(s0 + u, static_cast<int64_t>(kMaxSplits) - 1)], vals[u], a);
-        }
-        lat[c] = a * inv;
+        for (int u = 0; u < 16; ++u) a = fmaf(w[min(s0 + u, static_cast<int64_t>(kMaxSplits) - 1)], vals[u], a);
     }
-    __syncthreads();
-    const float* wv = wkv_b + (h * (nope + v) + nope) * R;
-    const int64_t j_end = min(v, static_cast<int64_t>(blockIdx.y) * 32 + 32);
-    for (int64_t j = static_cast<int64_t>(blockIdx.y) * 32 + wave; j < j_end; j += 4) {
-        const float* row = wv + j * R;
-        float a = 0.0f;
-        for (int64_t c0 = lane; c0 < R; c0 += 64 * 8) {
-            float vals[8];
+    lat[h * R + c] = a * inv_s;
+}
+
+// ------------------------------------------------------------------ value rows
+// out[h][j] = latent[h] . wkv_b[h][nope + j]: grid (ceil(v / 16), H), four
+// rows per wave, every row's loads issued before the sums (VEC: float4 loads,
+// R % 4 == 0 and aligned).
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void mla_value_kernel(const float* __restrict__ wkv_b,
+                                                            const float* __restrict__ lat, float* __restrict__ out,
+                                                            int64_t nope, int64_t R, int64_t v) {
+    constexpr int kRows = 4;
+    const int lane = threadIdx.x & 63;
+    const int64_t h = blockIdx.y;
+    const int64_t j0 = (static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6)) * kRows;
+    if (j0 >= v) return;
+    const float* x = lat + h * R;
+    const float* w0 = wkv_b + (h * (nope + v) + nope) * R;
+    float acc[kRows] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (VEC) {
+        const int64_t R4 = R / 4;
+        for (int64_t k = lane; k < R4; k += 64) {
+            const float4 xv = reinterpret_cast<const float4*>(x)[k];
+            float4 wv[kRows];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) vals[u] = row[min(c0 + 64 * u, R - 1)];
+            for (int i = 0; i < kRows; ++i)
+                wv[i] = reinterpret_cast<const float4*>(w0 + min(j0 + i, v - 1) * R)[k];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) a = fmaf(c0 + 64 * u < R ? lat[c0 + 64 * u] : 0.0f, vals[u], a);
+            for (int i = 0; i < kRows; ++i) {
+                acc[i] = fmaf(wv[i].x, xv.x, acc[i]);
+                acc[i] = fmaf(wv[i].y, xv.y, acc[i]);
+                acc[i] = fmaf(wv[i].z, xv.z, acc[i]);
+                acc[i] = fmaf(wv[i].w, xv.w, acc[i]);
+            }
         }
-        a = plm_wave_sum(a);
-        if (lane == kSumLane) out[h * v + j] = a;
+    } else {
+        for (int64_t k = lane; k < R; k += 64) {
+            const float xv = x[k];
+#pragma unroll
+            for (int i = 0; i < kRows; ++i) acc[i] = fmaf(w0[min(j0 + i, v - 1) * R + k], xv, acc[i]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+        const float t = plm_wave_sum(acc[i]);
+        if (lane == kSumLane && j0 + i < v) out[h * v + j0 + i] = t;
     }
 }
 
@@ -397,58 +503,99 @@ int gemv(const float* W, const float* x, float* y, int64_t N, int64_t K, hipStre
     return plm::check_launch("f32 gemv");
 }
 
-// Query columns per chunk thread of the split kernel (its instances).
-int split_cpt(int64_t R) { return R <= 4 * kChunks ? 4 : (R <= 32 * kChunks ? 32 : 64); }
-int split_ppt(int64_t rope) { return rope <= 4 * kChunks ? 4 : 16; }
-
 // Tokens per split: a multiple of 16, at most kMaxSplits splits.
 int64_t tokens_per_split(int64_t L) {
     return plm::ceil_div(plm::ceil_div(L, kMaxSplits), kTileTokens) * kTileTokens;
 }
 
-size_t flash_workspace_bytes(int64_t H, int64_t L, int64_t R) {
-    const int64_t nsplit = plm::ceil_div(L, tokens_per_split(L));
-    return static_cast<size_t>(H * R + nsplit * H * R + nsplit * H * 2) * sizeof(float);
+// The flash workspace, in floats, every array 16-byte aligned: q_abs [H][R],
+// the partials [nsplit][H][R16], (max, sum) [nsplit][H][2], latent [H][R].
+struct FlashLayout {
+    int64_t per, nsplit, part, ml, lat, total;
+};
+
+FlashLayout flash_layout(int64_t H, int64_t L, int64_t R) {
+    auto align4 = [](int64_t n) { return (n + 3) & ~int64_t(3); };
+    FlashLayout f;
+    f.per = tokens_per_split(L);
+    f.nsplit = plm::ceil_div(L, f.per);
+    f.part = align4(H * R);
+    f.ml = f.part + f.nsplit * H * split_shape(R, 0).R16;
+    f.lat = align4(f.ml + f.nsplit * H * 2);
+    f.total = f.lat + H * R;
+    return f;
 }
 
-// The three MLA launches; ws holds flash_workspace_bytes.
+size_t flash_workspace_bytes(int64_t H, int64_t L, int64_t R) {
+    return static_cast<size_t>(flash_layout(H, L, R).total) * sizeof(float);
+}
+
+// The split kernel's instances: <QC, NT> with QC >= ceil(K16 / 64) and
+// NT >= ceil(R16 / 64).
+template <int QC, int NT>
+int launch_split(dim3 grid, size_t lds, hipStream_t st, bool vec, const float* q_abs, const float* q_pe, const float* kv,
+                 const float* pe, float* part, float* ml, int64_t H, int64_t L, int64_t R, int64_t rope, float scale,
+                 int64_t per) {
+    if (lds > 64 * 1024) {
+        static bool raised[2] = {false, false};  // per instance and VEC
+        if (!raised[vec]) {
+            const void* fn = vec ? reinterpret_cast<const void*>(&mla_split_kernel<QC, NT, true>)
+                                 : reinterpret_cast<const void*>(&mla_split_kernel<QC, NT, false>);
+            if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+                return plm::fail(-1, "mla split kernel: LDS attribute refused");
+            raised[vec] = true;
+        }
+    }
+    if (vec)
+        hipLaunchKernelGGL((mla_split_kernel<QC, NT, true>), grid, dim3(kThreads), lds, st, q_abs, q_pe, kv, pe, part,
+                           ml, H, L, R, rope, scale, per);
+    else
+        hipLaunchKernelGGL((mla_split_kernel<QC, NT, false>), grid, dim3(kThreads), lds, st, q_abs, q_pe, kv, pe, part,
+                           ml, H, L, R, rope, scale, per);
+    return plm::check_launch("mla split kernel");
+}
+
+// The MLA launches; ws holds flash_workspace_bytes.
 int flash(const float* q_nope, const float* q_pe, const float* kv, const float* pe, const float* wkv_b, float* out,
           int64_t H, int64_t L, int64_t nope, int64_t rope, int64_t R, int64_t v, float scale, float* ws,
           hipStream_t st) {
-    const int64_t per = tokens_per_split(L);
-    const int64_t nsplit = plm::ceil_div(L, per);
+    const FlashLayout f = flash_layout(H, L, R);
+    const int64_t per = f.per, nsplit = f.nsplit;
+    const SplitShape sh = split_shape(R, rope);
     float* q_abs = ws;
-    float* part = q_abs + H * R;
-    float* ml = part + nsplit * H * R;
-    hipLaunchKernelGGL(mla_qabs_kernel, dim3(static_cast<unsigned>(H), static_cast<unsigned>(plm::ceil_div(R, 64))),
-                       dim3(kThreads), 0, st, q_nope, wkv_b, q_abs, nope, R, v);
+    float* part = ws + f.part;
+    float* ml = ws + f.ml;
+    float* lat = ws + f.lat;
+    if (R % 4 == 0 && plm::aligned16(wkv_b))
+        hipLaunchKernelGGL(mla_qabs4_kernel, dim3(static_cast<unsigned>(H), static_cast<unsigned>(plm::ceil_div(R, 256))),
+                           dim3(kThreads), 0, st, q_nope, wkv_b, q_abs, nope, R, v);
+    else
+        hipLaunchKernelGGL(mla_qabs_kernel, dim3(static_cast<unsigned>(H), static_cast<unsigned>(plm::ceil_div(R, 64))),
+                           dim3(kThreads), 0, st, q_nope, wkv_b, q_abs, nope, R, v);
     int code = plm::check_launch("mla q_abs kernel");
     if (code != 0) return code;
     const dim3 sgrid(static_cast<unsigned>(nsplit), static_cast<unsigned>(plm::ceil_div(H, kHeadsPerGroup)));
     // q_pe / pe are not read when rope is 0 (the reference still requires them)
-#define PLM_MLA_SPLIT(C, P)                                                                                    \
-    hipLaunchKernelGGL((mla_split_kernel<C, P>), sgrid, dim3(kThreads), split_lds_bytes(C, P), st, q_abs, q_pe, kv, \
-                       pe, part, ml, H, L, R, rope, scale, per)
-    const int cpt = split_cpt(R), ppt = split_ppt(rope);
-    if (cpt == 4 && ppt == 4)
-        PLM_MLA_SPLIT(4, 4);
-    else if (cpt == 32 && ppt == 4)
-        PLM_MLA_SPLIT(32, 4);
-    else if (cpt == 32 && ppt == 16)
-        PLM_MLA_SPLIT(32, 16);
-    else if (cpt == 4 && ppt == 16)
-        PLM_MLA_SPLIT(4, 16);
-    else if (cpt == 64 && ppt == 4)
-        PLM_MLA_SPLIT(64, 4);
+    const bool vec = R % 4 == 0 && rope % 4 == 0 && plm::aligned16(q_abs) && plm::aligned16(kv) &&
+                     (rope == 0 || (plm::aligned16(q_pe) && plm::aligned16(pe)));
+    const int64_t qc = plm::ceil_div(sh.K16, 64), nt = plm::ceil_div(sh.R16, 64);
+    const size_t lds = split_lds_bytes(R, rope);
+    if (qc <= 3 && nt <= 2)
+        code = launch_split<3, 2>(sgrid, lds, st, vec, q_abs, q_pe, kv, pe, part, ml, H, L, R, rope, scale, per);
+    else if (qc <= 9 && nt <= 8)
+        code = launch_split<9, 8>(sgrid, lds, st, vec, q_abs, q_pe, kv, pe, part, ml, H, L, R, rope, scale, per);
     else
-        PLM_MLA_SPLIT(64, 16);
-#undef PLM_MLA_SPLIT
-    code = plm::check_launch("mla split kernel");
+        code = launch_split<20, 16>(sgrid, lds, st, vec, q_abs, q_pe, kv, pe, part, ml, H, L, R, rope, scale, per);
     if (code != 0) return code;
-    hipLaunchKernelGGL(mla_merge_out_kernel, dim3(static_cast<unsigned>(H), static_cast<unsigned>(plm::ceil_div(v, 32))),
-                       dim3(kThreads), static_cast<size_t>(R) * sizeof(float), st, part, ml, wkv_b, out, H, nsplit,
-                       nope, R, v);
-    return plm::check_launch("mla merge kernel");
+    hipLaunchKernelGGL(mla_merge_kernel, dim3(static_cast<unsigned>(H), static_cast<unsigned>(plm::ceil_div(R, kThreads))),
+                       dim3(kThreads), 0, st, part, ml, lat, H, nsplit, R, sh.R16);
+    if ((code = plm::check_launch("mla merge kernel")) != 0) return code;
+    const dim3 vgrid(static_cast<unsigned>(plm::ceil_div(v, 16)), static_cast<unsigned>(H));
+    if (R % 4 == 0 && plm::aligned16(wkv_b) && plm::aligned16(lat))
+        hipLaunchKernelGGL(mla_value_kernel<true>, vgrid, dim3(kThreads), 0, st, wkv_b, lat, out, nope, R, v);
+    else
+        hipLaunchKernelGGL(mla_value_kernel<false>, vgrid, dim3(kThreads), 0, st, wkv_b, lat, out, nope, R, v);
+    return plm::check_launch("mla value kernel");
 }
 
 bool device_limits_ok(int64_t R, int64_t rope) { return R <= kMaxRank && rope <= kMaxRope; }

@@ -66,6 +66,21 @@ def test_deepseek_v3_dimensions(nat, cache_len):
     assert rel(got, mla.mla_flash_closed_form(*args, scale)) < 1e-5
 
 
+@pytest.mark.parametrize("heads,cache_len,nope,rope,rank,v", [
+    (20, 100, 32, 256, 1024, 48),  # the largest instance, 4 heads of a second group
+    (17, 45, 24, 62, 510, 40),     # rank and rope not multiples of 4 (element loads)
+    (3, 33, 8, 6, 200, 8),         # one chunk of rope columns
+])
+def test_kernel_instances(nat, heads, cache_len, nope, rope, rank, v):
+    print("mla instance", heads, cache_len, nope, rope, rank, v, flush=True)
+    rng = np.random.default_rng(heads * 1000 + rank)
+    args = [rng.standard_normal(s).astype(np.float32) * 0.1 for s in
+            ((heads, nope), (heads, rope), (cache_len, rank), (cache_len, rope), (heads, nope + v, rank))]
+    scale = 1.0 / np.sqrt(nope + rope)
+    got = host(nat.ds_mla_attention_flash_forward(*(dev(a) for a in args), softmax_scale=scale))
+    assert rel(got, mla.mla_flash_closed_form(*args, scale)) < 1e-5
+
+
 def test_peaked_scores(nat):
     """Large scores: a few rows dominate each head, so the running max moves
     across tiles and splits."""
