@@ -156,6 +156,16 @@ __device__ __forceinline__ mla_f32x4 mfma_f32(float a, float b, mla_f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// op over lanes l, l ^ 16, l ^ 32, l ^ 48, as (lower row, upper row) pairs
+// at each step, so all four lanes get the same bits.
+template <typename Op>
+__device__ __forceinline__ float cross_groups(float v, Op op) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return op(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 // Columns c0 .. c0 + 3 of a padded [latent | rope] row, zeros outside the
 // two parts or when !ok.  VEC: R and rope are multiples of 4 and the rows
 // 16-byte aligned; the load is always issued, from krow when the columns are
@@ -265,7 +275,8 @@ __global__ __launch_bounds__(kThreads) void mla_split_kernel(const float* __rest
         __syncthreads();
         s = ((red[lane] + red[64 + lane]) + red[128 + lane]) + red[192 + lane];
 
-        // softmax step: lane (head hl, rows 4 g + r)
+        // softmax step: lane (head hl, rows 4 g + r); the other lane groups
+        // of the head are lanes l ^ 16, l ^ 32, l ^ 48 (permlane swaps)
         float p[4];
         float mt = -INFINITY;
 #pragma unroll
@@ -273,8 +284,7 @@ __global__ __launch_bounds__(kThreads) void mla_split_kernel(const float* __rest
             p[r] = 4 * g + r < n ? s[r] * scale : -INFINITY;
             mt = fmaxf(mt, p[r]);
         }
-        mt = fmaxf(mt, __shfl_xor(mt, 16));
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        mt = cross_groups(mt, [](float x, float y) { return fmaxf(x, y); });
         const float m_new = fmaxf(m_run, mt);
         const float corr = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
         float lt = 0.0f;
@@ -283,8 +293,7 @@ __global__ __launch_bounds__(kThreads) void mla_split_kernel(const float* __rest
             p[r] = p[r] == -INFINITY ? 0.0f : expf(p[r] - m_new);
             lt += p[r];
         }
-        lt += __shfl_xor(lt, 16);
-        lt += __shfl_xor(lt, 32);
+        lt = cross_groups(lt, [](float x, float y) { return x + y; });
         l_run = l_run * corr + lt;
         m_run = m_new;
 
@@ -503,9 +512,11 @@ int gemv(const float* W, const float* x, float* y, int64_t N, int64_t K, hipStre
     return plm::check_launch("f32 gemv");
 }
 
-// Tokens per split: a multiple of 16, at most kMaxSplits splits.
+// Tokens per split: a multiple of 16, at least two tiles (the next tile's
+// loads overlap the current one's work), at most kMaxSplits splits.
 int64_t tokens_per_split(int64_t L) {
-    return plm::ceil_div(plm::ceil_div(L, kMaxSplits), kTileTokens) * kTileTokens;
+    return std::max<int64_t>(2 * kTileTokens,
+                             plm::ceil_div(plm::ceil_div(L, kMaxSplits), kTileTokens) * kTileTokens);
 }
 
 // The flash workspace, in floats, every array 16-byte aligned: q_abs [H][R],

@@ -120,6 +120,7 @@ def test_error_codes(nat):
     assert lib.ds_mla_attention_flash_forward(p, p, p, p, p, p, 0, 1, 1, 1, 1, 1, 1.0) == 2
     assert lib.ds_mla_attention_flash_forward(p, p, p, p, p, p, 1, 1, 1, 1, 1, 0, 1.0) == 2
     assert lib.ds_mla_attention_flash_forward(p, p, p, p, p, p, 1, 1, 1, 1, 2048, 1, 1.0) == 2  # rank limit
+    assert lib.ds_mla_attention_flash_forward(p, p, p, p, p, p, 1, 1, 1, 512, 8, 1, 1.0) == 2  # rope limit
     handle = lib.ds_session_create(1, 8, 0, 0, None, None)
     try:
         args = [p] * 15
