@@ -239,11 +239,13 @@ __device__ __forceinline__ plm_half8 q4_mfma_c8_inplace() {
 // NaN) records the call's number in a word private to the stream and host
 // thread, and that call's down phase reads the fp32 activations instead.
 // The call's number is one more than an epoch word kept in device memory
-// beside the record: the down phase's last workgroup advances the epoch, so
-// each call (and each replay of a captured graph) gets a new number without
-// the host, and the record only ever holds an earlier call's number
-// otherwise, which selects nothing.  Words: [0] epoch, [1] record,
-// [2] the down phase's finished-workgroup count.
+// beside the record: after a call that recorded its number, the down phase's
+// last workgroup advances the epoch, so the next call (or replay of a
+// captured graph) has a new number without the host, and at the start of
+// every call the record is at most the epoch, which selects nothing.  Calls
+// that record nothing touch neither word (no atomics on the common path).
+// Words: [0] epoch, [1] record, [2] the down phase's finished-workgroup
+// count.
 constexpr int kQ4Epoch = 0, kQ4Record = 1, kQ4Done = 2;
 
 __device__ __forceinline__ void q4_store_planes(uint4* base, int64_t k, float v, unsigned* words) {
@@ -613,14 +615,18 @@ __global__ __launch_bounds__(NWS * 64) void q4_down_kernel(const Q4CombineArgs a
             a.out_f16[row] = f16_from_bits(f2u(v), false);
         }
     }
-    // The last workgroup to finish advances the epoch (every workgroup has
-    // read the record and the epoch before it counts itself finished).
-    if (a.planes != nullptr && threadIdx.x == 0) {
+    // After a flagged call the last workgroup to finish advances the epoch,
+    // so the record (this call's number) never matches a later call.  Every
+    // workgroup read the record and the epoch (the values decide this
+    // branch) before it counts itself; a call that flagged nothing leaves
+    // both words as they are, the record staying at most the epoch.  The
+    // kernel's end makes the new epoch visible to the next call.
+    if (a.planes != nullptr && !use_planes && threadIdx.x == 0) {
         const unsigned done =
-            __hip_atomic_fetch_add(a.words + kQ4Done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(a.words + kQ4Done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (done == gridDim.x - 1) {
             __hip_atomic_store(a.words + kQ4Done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_fetch_add(a.words + kQ4Epoch, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(a.words + kQ4Epoch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
