@@ -1223,8 +1223,48 @@ def table(args):
         del w
         torch.cuda.empty_cache()
 
+    def mla_fp8_block(prev_len):
+        # The FP8 model's one-token attention (fp8_source.py:6337-6454) at
+        # DeepSeek-V3 shapes: FP8 q_a 1536x7168, q_b 24576x1536, kv_a 576x7168,
+        # o 7168x16384 (170 MB with scales), kv_b dequantized fp32 32768x512
+        # (67 MB), bf16 hidden state; two weight sets rotated
+        hid, qr, R, H, nope, rope, v = 7168, 1536, 512, 128, 128, 64, 128
+        shapes = {"q_a": (qr, hid), "q_b": (H * (nope + rope), qr), "kv_a": (R + rope, hid), "o": (hid, H * v)}
+        sets = []
+        for _ in range(2):
+            fp8 = {}
+            for k, (rows, cols) in shapes.items():
+                w = torch.randn((rows, cols), generator=gen, device="cuda").mul_(0.02).to(torch.float8_e4m3fn)
+                s = torch.rand((math.ceil(rows / 128), math.ceil(cols / 128)), generator=gen, device="cuda") + 0.5
+                fp8[k] = (w.view(torch.uint8), s)
+            kvb = torch.randn((H * (nope + v), R), generator=gen, device="cuda") * 0.02
+            sets.append((fp8, kvb))
+        norms = [torch.ones(qr, device="cuda"), torch.ones(R, device="cuda")]
+        x = torch.randn(hid, generator=gen, device="cuda").to(torch.bfloat16)
+        kvc = torch.randn((prev_len + 1, R), generator=gen, device="cuda")
+        pec = torch.randn((prev_len + 1, rope), generator=gen, device="cuda")
+        cs = [torch.ones(rope // 2, device="cuda"), torch.zeros(rope // 2, device="cuda")]
+        out = torch.empty(hid, device="cuda")
+        lib.pocketlm_set_stream(_stream_ptr(torch))
+        p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+
+        def call(fp8, kvb):
+            return lib.ds_fp8_attention_block_bf16x_f32(
+                p(x), *[p(t) for k in ("q_a", "q_b", "kv_a") for t in fp8[k]], p(kvb), *[p(t) for t in fp8["o"]],
+                *[p(t) for t in norms], p(kvc), p(pec), *[p(t) for t in cs], p(kvc), p(pec), p(out), hid, qr, R, H,
+                nope, rope, v, prev_len, 1e-6, 1.0 / math.sqrt(192.0))
+
+        calls = [lambda st=st: call(*st) for st in sets]
+        fp8_bytes = sum(r * c + 4 * math.ceil(r / 128) * math.ceil(c / 128) for r, c in shapes.values())
+        nbytes = fp8_bytes + H * (nope + v) * R * 4 + (prev_len + 1) * (R + rope) * 4 + 2 * hid + 4 * hid
+        measure(f"ds-v3 attention block, {prev_len}-row latent cache (FP8 weights, fp32 kv_b)", 1, lambda: calls,
+                nbytes)
+        del sets
+        torch.cuda.empty_cache()
+
     if want("attention block"):
         mla_block(4096)
+        mla_fp8_block(4096)
 
     transfers = []
     if want("fp8 pack -> HBM"):

@@ -443,6 +443,27 @@ int ds_attention_block_forward_f32(
     int64_t kv_lora_rank, int64_t num_heads, int64_t qk_nope_dim, int64_t qk_rope_dim, int64_t v_head_dim,
     int64_t previous_len, float rms_eps, float softmax_scale);
 
+/* No single reference counterpart: the FP8 model's one-token attention,
+ * fp8_source.py:6337-6454 (`_run_fp8_single_token_attention_native_linear`
+ * at one token), which the reference runs as native FP8 linears plus torch.
+ * The steps and arguments of ds_attention_block_forward_f32 (without the
+ * session handle), with the projections FP8 block-scaled: q_a [q_rank,
+ * hidden] and kv_a [R + rope, hidden] on the bf16 hidden state in one launch,
+ * q_b [H (nope + rope), q_rank] and o [hidden, H v] on fp32 activations (the
+ * reference's FP8 linear takes fp32), each with its scale_inv grid
+ * [ceil(rows/128)][ceil(cols/128)]; kv_b fp32 [H (nope + v), R] (the
+ * reference dequantizes it to fp32 before the attention).  hidden_out fp32
+ * [hidden].  Codes as ds_attention_block_forward_f32, and -1 / -2 from an FP8
+ * linear. */
+int ds_fp8_attention_block_bf16x_f32(
+    const uint16_t* hidden_bf16, const uint8_t* q_a_weight, const float* q_a_scale_inv, const uint8_t* q_b_weight,
+    const float* q_b_scale_inv, const uint8_t* kv_a_weight, const float* kv_a_scale_inv, const float* kv_b_weight,
+    const uint8_t* o_weight, const float* o_scale_inv, const float* q_norm_weight, const float* kv_norm_weight,
+    const float* previous_kv_cache, const float* previous_pe_cache, const float* rope_cos, const float* rope_sin,
+    float* next_kv_cache, float* next_pe_cache, float* hidden_out, int64_t hidden_dim, int64_t q_lora_rank,
+    int64_t kv_lora_rank, int64_t num_heads, int64_t qk_nope_dim, int64_t qk_rope_dim, int64_t v_head_dim,
+    int64_t previous_len, float rms_eps, float softmax_scale);
+
 /* ds_forward.cpp:879-955: softmax top-k router over u16 (fp16/bf16) hidden
  * [hidden_dim] and router weights [num_experts, hidden_dim] (device);
  * output_expert_ids int64 [k] and output_weights fp32 [k] (device).

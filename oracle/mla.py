@@ -19,6 +19,16 @@ numpy's float32 summation, not the reference's 8-lane AVX2 order.
 same attention (native/__init__.py:857-876: einsum, softmax, einsum) in
 float64: the value the float32 computations approximate.
 
+``fp8_attention_block`` follows the FP8 model's one-token attention
+(core/runtime/fp8_source.py:6337-6454): the native FP8 linear (the C
+oracle's ``fp8_linear``, pinned to the reference's fp8_linear.cpp) for q_a
+(6373), q_b (6384) and kv_a (6393) on fp32 activations, RMSNorm
+(``_rms_norm_any``, 5311-5317: x * rsqrt(mean(x^2) + eps) * w), RoPE on
+pairs (``_apply_rope_real``, 5191-5209), the latent and pe rows appended
+after the previous rows (6422-6428), kv_b as fp32 (dequantized, 6399-6402),
+the absorbed-query attention (6429-6451: one query row, so no causal mask)
+and o as an FP8 linear (6452-6458).
+
 ``attention_block`` follows ds_attention_block_forward_f32
 (ds_forward.cpp:647-782): q_a (698), RMSNorm (699; 610-619), q_b split into
 nope / pe (701-713), RoPE on the pe parts (714-716; 621-645: an odd rope
@@ -129,3 +139,36 @@ def attention_block(hidden, q_a, q_b, kv_a, kv_b, o, q_norm, kv_norm, prev_kv, p
     heads = np.asarray(flash(q_nope, q_pe, next_kv, next_pe, np.asarray(kv_b, f32).reshape(H, nope + v, R),
                              softmax_scale), f32).reshape(-1)
     return (np.asarray(o, f32) @ heads).astype(f32), next_kv, next_pe
+
+
+def rms_norm_rsqrt(x, w, eps):
+    """fp8_source.py:5311-5317 in float32: x * rsqrt(mean(x^2) + eps) * w."""
+    x = np.asarray(x, f32)
+    var = f32(np.mean(x.astype(np.float64) ** 2))
+    return (x * f32(1.0 / np.sqrt(np.float64(var) + np.float64(eps))) * np.asarray(w, f32)).astype(f32)
+
+
+def fp8_attention_block(hidden, fp8, kv_b, q_norm, kv_norm, prev_kv, prev_pe, cos, sin, *, num_heads, qk_nope_dim,
+                        qk_rope_dim, v_head_dim, kv_lora_rank, rms_eps, softmax_scale, flash=mla_flash_online):
+    """fp8_source.py:6337-6454 at one token.  fp8: {"q_a"|"q_b"|"kv_a"|"o":
+    (e4m3 bytes [N, K], scale_inv [ceil(N/128), ceil(K/128)])}; kv_b fp32
+    [H (nope + v), R].  Returns (hidden_out fp32, next_kv, next_pe)."""
+    import oracle  # the C oracle (fp8_linear pinned to the reference build)
+
+    H, nope, rp, v, R = num_heads, qk_nope_dim, qk_rope_dim, v_head_dim, kv_lora_rank
+    x = np.asarray(hidden, f32).reshape(1, -1)
+    q_low = rms_norm_rsqrt(oracle.fp8_linear(*fp8["q_a"], x).reshape(-1), q_norm, rms_eps)
+    q = oracle.fp8_linear(*fp8["q_b"], q_low.reshape(1, -1)).reshape(H, nope + rp)
+    kv_raw = oracle.fp8_linear(*fp8["kv_a"], x).reshape(-1)
+    q_nope = q[:, :nope]
+    q_pe = np.stack([rope(q[h, nope:], cos, sin) for h in range(H)]) if rp else np.zeros((H, 0), f32)
+    new_kv = rms_norm_rsqrt(kv_raw[:R], kv_norm, rms_eps)
+    new_pe = rope(kv_raw[R:], cos, sin)
+    prev_kv = np.zeros((0, R), f32) if prev_kv is None else np.asarray(prev_kv, f32).reshape(-1, R)
+    prev_pe = np.zeros((0, rp), f32) if prev_pe is None else np.asarray(prev_pe, f32).reshape(-1, rp)
+    next_kv = np.concatenate([prev_kv, new_kv[None]], axis=0)
+    next_pe = np.concatenate([prev_pe, new_pe[None]], axis=0)
+    heads = np.asarray(flash(q_nope, q_pe, next_kv, next_pe, np.asarray(kv_b, f32).reshape(H, nope + v, R),
+                             softmax_scale), f32).reshape(1, -1)
+    return oracle.fp8_linear(*fp8["o"], heads).reshape(-1), next_kv, next_pe
+

@@ -129,6 +129,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ds_forward_verify_f32": (_i32, [_vp, _vp, _i64, DS_VERIFY_CALLBACK, _vp, _i64]),
     "ds_mla_attention_flash_forward": (_i32, [_vp] * 6 + [_i64] * 6 + [_f32]),
     "ds_attention_block_forward_f32": (_i32, [_vp] * 16 + [_i64] * 8 + [_f32, _f32]),
+    "ds_fp8_attention_block_bf16x_f32": (_i32, [_vp] * 19 + [_i64] * 8 + [_f32, _f32]),
     "kv_attention_decode_fp16": (_i32, [_vp, _i64] + [_vp] * 6 + [_i64] * 3 + [_f32]),
     "kv_attention_decode_u16_ext": (_i32, [_vp, _i64] + [_vp] * 11 + [_i64] * 3 + [_f32, _f32]),
     "kv_dense_layer_decode_fp16": (_i32, [_vp, _i64] + [_vp] * 11 + [_i64] * 4 + [_f32, _f32]),

@@ -31,6 +31,7 @@
 #include <cstring>
 
 #include "common.h"
+#include "pocketlm_hip.h"
 
 int plm_ds_session_note_fused_attention(void* handle);
 
@@ -633,6 +634,71 @@ PLM_EXPORT int ds_mla_attention_flash_forward(const float* q_nope, const float* 
                  qk_rope_dim, kv_lora_rank, v_head_dim, softmax_scale, ws, plm::current_stream());
 }
 
+namespace {
+
+// The attention block after its projections are chosen (ds_forward.cpp:647-782):
+// project_a fills q_low [q_rank] and kvraw [R + rope] from the hidden state,
+// project_qb fills q [H (nope + rope)] from the normalised q_low, project_o
+// fills the output from heads [H v].  ws: block_workspace_floats floats.
+struct BlockDims {
+    int64_t hidden, q_rank, R, H, nope, rope, v, prev;
+};
+
+int64_t block_scratch_floats(const BlockDims& d) {
+    const int64_t scratch = d.q_rank + d.H * (d.nope + d.rope) + d.H * d.nope + d.H * d.rope + (d.R + d.rope) + d.H * d.v;
+    return (scratch + 63) & ~int64_t(63);
+}
+
+size_t block_workspace_bytes(const BlockDims& d) {
+    return static_cast<size_t>(block_scratch_floats(d)) * sizeof(float) + flash_workspace_bytes(d.H, d.prev + 1, d.R);
+}
+
+template <class ProjectA, class ProjectQb, class ProjectO>
+int attention_block(const BlockDims& d, ProjectA&& project_a, ProjectQb&& project_qb, ProjectO&& project_o,
+                    const float* kv_b_weight, const float* q_norm_weight, const float* kv_norm_weight,
+                    const float* previous_kv_cache, const float* previous_pe_cache, const float* rope_cos,
+                    const float* rope_sin, float* next_kv_cache, float* next_pe_cache, float rms_eps,
+                    float softmax_scale, float* ws, hipStream_t st) {
+    const int64_t H = d.H, nope = d.nope, rope = d.rope, R = d.R, v = d.v, qw = nope + rope, L = d.prev + 1;
+    float* q_low = ws;
+    float* q = q_low + d.q_rank;
+    float* qn = q + H * qw;
+    float* qp = qn + H * nope;
+    float* kvraw = qp + H * rope;
+    float* heads = kvraw + R + rope;
+    float* fws = ws + block_scratch_floats(d);
+
+    int code = project_a(q_low, kvraw);
+    if (code != 0) return code;
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(1), dim3(kThreads), 0, st, q_low, q_norm_weight, d.q_rank, rms_eps);
+    if ((code = plm::check_launch("rms norm")) != 0) return code;
+    if ((code = project_qb(q_low, q)) != 0) return code;
+    const int64_t qn_threads = std::max(H * nope, H * rope);
+    hipLaunchKernelGGL(mla_q_split_kernel, dim3(static_cast<unsigned>(plm::ceil_div(std::max<int64_t>(qn_threads, 1), kThreads))),
+                       dim3(kThreads), 0, st, q, qn, qp, rope_cos, rope_sin, H, nope, rope);
+    if ((code = plm::check_launch("mla q split")) != 0) return code;
+    // the previous rows, then the new one (ds_forward.cpp:716-744)
+    if (d.prev > 0) {
+        hipError_t err = hipSuccess;
+        if (next_kv_cache != previous_kv_cache)
+            err = hipMemcpyAsync(next_kv_cache, previous_kv_cache,
+                                 static_cast<size_t>(d.prev * R) * sizeof(float), hipMemcpyDeviceToDevice, st);
+        if (err == hipSuccess && rope > 0 && next_pe_cache != previous_pe_cache)
+            err = hipMemcpyAsync(next_pe_cache, previous_pe_cache,
+                                 static_cast<size_t>(d.prev * rope) * sizeof(float), hipMemcpyDeviceToDevice, st);
+        if (err != hipSuccess) return plm::hip_fail(err, "previous cache copy");
+    }
+    hipLaunchKernelGGL(mla_kv_row_kernel, dim3(1), dim3(kThreads), 0, st, kvraw, kv_norm_weight,
+                       next_kv_cache + d.prev * R, next_pe_cache + d.prev * rope, rope_cos, rope_sin, R, rope, rms_eps);
+    if ((code = plm::check_launch("mla kv row")) != 0) return code;
+    code = flash(qn, qp, next_kv_cache, next_pe_cache, kv_b_weight, heads, H, L, nope, rope, R, v, softmax_scale, fws,
+                 st);
+    if (code != 0) return code > 0 ? 100 + code : code;
+    return project_o(heads);
+}
+
+}  // namespace
+
 PLM_EXPORT int ds_attention_block_forward_f32(
     void* handle, const float* hidden_in, const float* q_a_weight, const float* q_b_weight, const float* kv_a_weight,
     const float* kv_b_weight, const float* o_weight, const float* q_norm_weight, const float* kv_norm_weight,
@@ -649,51 +715,74 @@ PLM_EXPORT int ds_attention_block_forward_f32(
     if (previous_len > 0 && (!previous_kv_cache || !previous_pe_cache))
         return plm::fail(3, "previous caches are null with previous_len %lld", static_cast<long long>(previous_len));
     if (!device_limits_ok(kv_lora_rank, qk_rope_dim)) return 102;  // the flash call's dimension code, offset by 100
-    const int64_t H = num_heads, nope = qk_nope_dim, rope = qk_rope_dim, R = kv_lora_rank, v = v_head_dim;
-    const int64_t qw = nope + rope, L = previous_len + 1;
+    const BlockDims d{hidden_dim, q_lora_rank, kv_lora_rank, num_heads, qk_nope_dim, qk_rope_dim, v_head_dim,
+                      previous_len};
     hipStream_t st = plm::current_stream();
-    // scratch: q_low, q, q_nope, q_pe, kvraw, heads, then the flash workspace
-    const int64_t scratch = q_lora_rank + H * qw + H * nope + H * rope + (R + rope) + H * v;
-    const int64_t pad = (scratch + 63) & ~int64_t(63);
-    float* ws = static_cast<float*>(
-        plm::workspace(static_cast<size_t>(pad) * sizeof(float) + flash_workspace_bytes(H, L, R)));
+    float* ws = static_cast<float*>(plm::workspace(block_workspace_bytes(d)));
     if (ws == nullptr) return -3;
-    float* q_low = ws;
-    float* q = q_low + q_lora_rank;
-    float* qn = q + H * qw;
-    float* qp = qn + H * nope;
-    float* kvraw = qp + H * rope;
-    float* heads = kvraw + R + rope;
-    float* fws = ws + pad;
-
-    int code = gemv(q_a_weight, hidden_in, q_low, q_lora_rank, hidden_dim, st);
+    const int64_t qw = qk_nope_dim + qk_rope_dim;
+    auto project_a = [&](float* q_low, float* kvraw) {
+        const int code = gemv(q_a_weight, hidden_in, q_low, q_lora_rank, hidden_dim, st);
+        return code != 0 ? code : gemv(kv_a_weight, hidden_in, kvraw, kv_lora_rank + qk_rope_dim, hidden_dim, st);
+    };
+    auto project_qb = [&](const float* q_low, float* q) {
+        return gemv(q_b_weight, q_low, q, num_heads * qw, q_lora_rank, st);
+    };
+    auto project_o = [&](const float* heads) {
+        return gemv(o_weight, heads, hidden_out, hidden_dim, num_heads * v_head_dim, st);
+    };
+    const int code = attention_block(d, project_a, project_qb, project_o, kv_b_weight, q_norm_weight, kv_norm_weight,
+                                     previous_kv_cache, previous_pe_cache, rope_cos, rope_sin, next_kv_cache,
+                                     next_pe_cache, rms_eps, softmax_scale, ws, st);
     if (code != 0) return code;
-    hipLaunchKernelGGL(rms_norm_kernel, dim3(1), dim3(kThreads), 0, st, q_low, q_norm_weight, q_lora_rank, rms_eps);
-    if ((code = plm::check_launch("rms norm")) != 0) return code;
-    if ((code = gemv(q_b_weight, q_low, q, H * qw, q_lora_rank, st)) != 0) return code;
-    const int64_t qn_threads = std::max(H * nope, H * rope);
-    hipLaunchKernelGGL(mla_q_split_kernel, dim3(static_cast<unsigned>(plm::ceil_div(std::max<int64_t>(qn_threads, 1), kThreads))),
-                       dim3(kThreads), 0, st, q, qn, qp, rope_cos, rope_sin, H, nope, rope);
-    if ((code = plm::check_launch("mla q split")) != 0) return code;
-    // the previous rows, then the new one (ds_forward.cpp:716-744)
-    if (previous_len > 0) {
-        hipError_t err = hipSuccess;
-        if (next_kv_cache != previous_kv_cache)
-            err = hipMemcpyAsync(next_kv_cache, previous_kv_cache,
-                                 static_cast<size_t>(previous_len * R) * sizeof(float), hipMemcpyDeviceToDevice, st);
-        if (err == hipSuccess && rope > 0 && next_pe_cache != previous_pe_cache)
-            err = hipMemcpyAsync(next_pe_cache, previous_pe_cache,
-                                 static_cast<size_t>(previous_len * rope) * sizeof(float), hipMemcpyDeviceToDevice, st);
-        if (err != hipSuccess) return plm::hip_fail(err, "previous cache copy");
-    }
-    if ((code = gemv(kv_a_weight, hidden_in, kvraw, R + rope, hidden_dim, st)) != 0) return code;
-    hipLaunchKernelGGL(mla_kv_row_kernel, dim3(1), dim3(kThreads), 0, st, kvraw, kv_norm_weight,
-                       next_kv_cache + previous_len * R, next_pe_cache + previous_len * rope, rope_cos, rope_sin, R,
-                       rope, rms_eps);
-    if ((code = plm::check_launch("mla kv row")) != 0) return code;
-    code = flash(qn, qp, next_kv_cache, next_pe_cache, kv_b_weight, heads, H, L, nope, rope, R, v, softmax_scale, fws,
-                 st);
-    if (code != 0) return code > 0 ? 100 + code : code;
-    if ((code = gemv(o_weight, heads, hidden_out, hidden_dim, H * v, st)) != 0) return code;
     return plm_ds_session_note_fused_attention(handle);
+}
+
+// The FP8 attention of one decode token (fp8_source.py:6337-6454 at one
+// token): q_a and kv_a in one FP8 launch on the bf16 hidden state, q_b and o
+// as FP8 linears on fp32 activations (the reference's native FP8 linear takes
+// fp32), kv_b dequantized to fp32 beforehand as the reference loads it.
+PLM_EXPORT int ds_fp8_attention_block_bf16x_f32(
+    const uint16_t* hidden_bf16, const uint8_t* q_a_weight, const float* q_a_scale_inv, const uint8_t* q_b_weight,
+    const float* q_b_scale_inv, const uint8_t* kv_a_weight, const float* kv_a_scale_inv, const float* kv_b_weight,
+    const uint8_t* o_weight, const float* o_scale_inv, const float* q_norm_weight, const float* kv_norm_weight,
+    const float* previous_kv_cache, const float* previous_pe_cache, const float* rope_cos, const float* rope_sin,
+    float* next_kv_cache, float* next_pe_cache, float* hidden_out, int64_t hidden_dim, int64_t q_lora_rank,
+    int64_t kv_lora_rank, int64_t num_heads, int64_t qk_nope_dim, int64_t qk_rope_dim, int64_t v_head_dim,
+    int64_t previous_len, float rms_eps, float softmax_scale) {
+    if (!hidden_bf16 || !q_a_weight || !q_a_scale_inv || !q_b_weight || !q_b_scale_inv || !kv_a_weight ||
+        !kv_a_scale_inv || !kv_b_weight || !o_weight || !o_scale_inv || !q_norm_weight || !kv_norm_weight ||
+        !rope_cos || !rope_sin || !next_kv_cache || !next_pe_cache || !hidden_out)
+        return plm::fail(1, "null pointer");
+    if (hidden_dim <= 0 || q_lora_rank <= 0 || kv_lora_rank <= 0 || num_heads <= 0 || qk_nope_dim < 0 ||
+        qk_rope_dim < 0 || v_head_dim <= 0 || previous_len < 0)
+        return plm::fail(2, "bad dimensions");
+    if (previous_len > 0 && (!previous_kv_cache || !previous_pe_cache))
+        return plm::fail(3, "previous caches are null with previous_len %lld", static_cast<long long>(previous_len));
+    if (!device_limits_ok(kv_lora_rank, qk_rope_dim)) return 102;
+    const BlockDims d{hidden_dim, q_lora_rank, kv_lora_rank, num_heads, qk_nope_dim, qk_rope_dim, v_head_dim,
+                      previous_len};
+    hipStream_t st = plm::current_stream();
+    float* ws = static_cast<float*>(plm::workspace(block_workspace_bytes(d)));
+    if (ws == nullptr) return -3;
+    const int64_t qw = qk_nope_dim + qk_rope_dim;
+    auto cols = [](int64_t k) { return plm::ceil_div(k, 128); };
+    auto project_a = [&](float* q_low, float* kvraw) {
+        const uint64_t w[2] = {reinterpret_cast<uint64_t>(q_a_weight), reinterpret_cast<uint64_t>(kv_a_weight)};
+        const uint64_t s[2] = {reinterpret_cast<uint64_t>(q_a_scale_inv), reinterpret_cast<uint64_t>(kv_a_scale_inv)};
+        const uint64_t o[2] = {reinterpret_cast<uint64_t>(q_low), reinterpret_cast<uint64_t>(kvraw)};
+        const int64_t rows[2] = {q_lora_rank, kv_lora_rank + qk_rope_dim};
+        return fp8_e4m3_block_linear_many_bf16x_f32(w, s, hidden_bf16, o, rows, 2, 1, hidden_dim, cols(hidden_dim));
+    };
+    auto project_qb = [&](const float* q_low, float* q) {
+        return fp8_e4m3_block_linear_f32(q_b_weight, q_b_scale_inv, q_low, q, 1, num_heads * qw, q_lora_rank,
+                                         cols(q_lora_rank));
+    };
+    auto project_o = [&](const float* heads) {
+        return fp8_e4m3_block_linear_f32(o_weight, o_scale_inv, heads, hidden_out, 1, hidden_dim,
+                                         num_heads * v_head_dim, cols(num_heads * v_head_dim));
+    };
+    return attention_block(d, project_a, project_qb, project_o, kv_b_weight, q_norm_weight, kv_norm_weight,
+                           previous_kv_cache, previous_pe_cache, rope_cos, rope_sin, next_kv_cache, next_pe_cache,
+                           rms_eps, softmax_scale, ws, st);
 }

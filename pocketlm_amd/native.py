@@ -1324,6 +1324,75 @@ def ds_attention_block_forward(session: "DeepSeekNativeSession", hidden: torch.T
     return _home(out, hidden), (_home(next_kv, hidden), _home(next_pe, hidden))
 
 
+def fp8_attention_block_forward(hidden: torch.Tensor, q_a_weight: torch.Tensor, q_a_scale_inv: torch.Tensor,
+                                q_b_weight: torch.Tensor, q_b_scale_inv: torch.Tensor, kv_a_weight: torch.Tensor,
+                                kv_a_scale_inv: torch.Tensor, kv_b_weight: torch.Tensor, o_weight: torch.Tensor,
+                                o_scale_inv: torch.Tensor, q_norm_weight: torch.Tensor, kv_norm_weight: torch.Tensor, *,
+                                previous_kv_cache: torch.Tensor | None, previous_pe_cache: torch.Tensor | None,
+                                rope_cos: torch.Tensor, rope_sin: torch.Tensor, q_lora_rank: int, kv_lora_rank: int,
+                                num_heads: int, qk_nope_dim: int, qk_rope_dim: int, v_head_dim: int, rms_eps: float,
+                                softmax_scale: float, dtype: torch.dtype = torch.float32):
+    """The FP8 model's one-token attention (src/pcketlm/core/runtime/
+    fp8_source.py:6337-6454 at one token) as one native call
+    (ds_fp8_attention_block_bf16x_f32): q_a / q_b / kv_a / o are FP8 e4m3
+    weights with their 128x128 scale_inv grids, kv_b is the fp32
+    dequantized weight (``dequantize_fp8_block_scaled(..., torch.float32)``,
+    as the reference loads it).  The hidden state is taken as bf16 (the
+    reference widens it to fp32 for its FP8 linears; the widening is exact).
+    Returns (hidden_out [hidden_dim] in ``dtype``, (next_kv_cache,
+    next_pe_cache)) on the weights' device."""
+    lib = _require("PCKETLM_DISABLE_FUSED_DS_ATTENTION", "Native fused DeepSeek attention")
+    dev = _target_device(hidden, q_a_weight, q_b_weight, kv_a_weight, kv_b_weight, o_weight)
+    x = _on(hidden, dev, torch.bfloat16).reshape(-1)
+    hidden_dim = int(x.numel())
+    if hidden_dim <= 0:
+        raise ValueError("hidden must not be empty")
+    q_rank, kv_rank, heads = int(q_lora_rank), int(kv_lora_rank), int(num_heads)
+    nope, rope, v_dim = int(qk_nope_dim), int(qk_rope_dim), int(v_head_dim)
+    fp8 = {}
+    for name, w, s, shape in (("q_a", q_a_weight, q_a_scale_inv, (q_rank, hidden_dim)),
+                              ("q_b", q_b_weight, q_b_scale_inv, (heads * (nope + rope), q_rank)),
+                              ("kv_a", kv_a_weight, kv_a_scale_inv, (kv_rank + rope, hidden_dim)),
+                              ("o", o_weight, o_scale_inv, (hidden_dim, heads * v_dim))):
+        wt = _fp8_bytes(w, dev)
+        if tuple(wt.shape) != shape:
+            raise ValueError(f"{name}_weight shape does not match DeepSeek attention config")
+        st = _on(s, dev, torch.float32)
+        if st.ndim != 2 or int(st.shape[0]) != -(-shape[0] // 128) or int(st.shape[1]) != -(-shape[1] // 128):
+            raise ValueError(f"{name}_scale_inv must be the 128x128 block layout of {name}_weight")
+        fp8[name] = (wt, st)
+    kv_b = _on(kv_b_weight, dev, torch.float32)
+    if tuple(kv_b.shape) != (heads * (nope + v_dim), kv_rank):
+        raise ValueError("kv_b_weight shape does not match DeepSeek attention config")
+    q_norm = _on(q_norm_weight, dev, torch.float32).reshape(-1)
+    kv_norm = _on(kv_norm_weight, dev, torch.float32).reshape(-1)
+    if int(q_norm.numel()) != q_rank or int(kv_norm.numel()) != kv_rank:
+        raise ValueError("norm weight sizes do not match ranks")
+    cos = _on(rope_cos, dev, torch.float32).reshape(-1)
+    sin = _on(rope_sin, dev, torch.float32).reshape(-1)
+    if int(cos.numel()) != max(0, rope // 2) or int(sin.numel()) != max(0, rope // 2):
+        raise ValueError("rope cos/sin sizes must be qk_rope_dim / 2")
+    prev_kv = (torch.empty((0, kv_rank), dtype=torch.float32, device=dev) if previous_kv_cache is None
+               else _on(previous_kv_cache, dev, torch.float32).reshape(-1, kv_rank))
+    prev_pe = (torch.empty((0, rope), dtype=torch.float32, device=dev) if previous_pe_cache is None
+               else _on(previous_pe_cache, dev, torch.float32).reshape(-1, rope))
+    previous_len = int(prev_kv.shape[0])
+    if int(prev_pe.shape[0]) != previous_len:
+        raise ValueError("previous KV and PE cache lengths must match")
+    next_kv = torch.empty((previous_len + 1, kv_rank), dtype=torch.float32, device=dev)
+    next_pe = torch.empty((previous_len + 1, rope), dtype=torch.float32, device=dev)
+    out = torch.empty((hidden_dim,), dtype=torch.float32, device=dev)
+    prev_kv_p = _p(None) if previous_len == 0 else _p(prev_kv)
+    prev_pe_p = _p(None) if previous_len == 0 else _p(prev_pe)
+    with _launch(lib, dev):
+        code = lib.ds_fp8_attention_block_bf16x_f32(
+            _p(x), *[_p(t) for name in ("q_a", "q_b", "kv_a") for t in fp8[name]], _p(kv_b), *[_p(t) for t in fp8["o"]],
+            _p(q_norm), _p(kv_norm), prev_kv_p, prev_pe_p, _p(cos), _p(sin), _p(next_kv), _p(next_pe), _p(out),
+            hidden_dim, q_rank, kv_rank, heads, nope, rope, v_dim, previous_len, float(rms_eps), float(softmax_scale))
+    _check("ds_fp8_attention_block_bf16x_f32", code)
+    return _home(out.to(dtype), hidden), (_home(next_kv, hidden), _home(next_pe, hidden))
+
+
 def native_lm_head_topk_available() -> bool:
     return _available("PCKETLM_DISABLE_NATIVE_MATMUL")
 

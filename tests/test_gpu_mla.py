@@ -17,7 +17,7 @@ import pytest
 import torch
 
 from oracle import mla
-from test_mla_oracle import REF_CASES, block_inputs, make_inputs, rel
+from test_mla_oracle import FP8_DIMS, REF_CASES, _fp8_block, block_inputs, fp8_attention_inputs, make_inputs, rel
 
 pytestmark = pytest.mark.gpu
 
@@ -202,3 +202,47 @@ def test_block_deepseek_like_dimensions_in_place_cache(nat):
     assert rel(host(out), want) < 1e-5
     assert np.array_equal(host(kv_buf)[:prev], prev_kv) and np.array_equal(host(pe_buf)[:prev], prev_pe)
     assert rel(host(kv_buf)[prev], want_kv[prev]) < 1e-6 and rel(host(pe_buf)[prev], want_pe[prev]) < 1e-6
+
+
+@pytest.mark.parametrize("dims", [FP8_DIMS, (7168, 1536, 512, 16, 128, 64, 128, 300)])
+def test_fp8_attention_block_matches_the_oracle(nat, dims):
+    """The FP8 model's one-token attention (fp8_source.py:6337-6454) through
+    ds_fp8_attention_block_bf16x_f32 against the oracle's restatement (C
+    oracle FP8 linears, float32 attention); the second case has DeepSeek-V3's
+    projection widths with 16 heads."""
+    print("fp8 attention", dims, flush=True)
+    hidden_dim, q_rank, kv_rank, heads, nope, rope, v, prev = dims
+    t = fp8_attention_inputs(*dims)
+    want, want_kv, want_pe = _fp8_block(t, dims)
+    import oracle
+
+    d = {k: (torch.from_numpy(w).cuda(), torch.from_numpy(s).cuda()) for k, (w, s) in t["fp8"].items()}
+    kv_b = torch.from_numpy(oracle.fp8_dequant(*t["kv_b"], "f32")).cuda()
+    hidden = torch.from_numpy(t["hidden"]).to(torch.bfloat16).cuda()
+    kw = dict(previous_kv_cache=dev(t["prev_kv"]), previous_pe_cache=dev(t["prev_pe"]), rope_cos=dev(t["cos"]),
+              rope_sin=dev(t["sin"]), q_lora_rank=q_rank, kv_lora_rank=kv_rank, num_heads=heads, qk_nope_dim=nope,
+              qk_rope_dim=rope, v_head_dim=v, rms_eps=1e-6, softmax_scale=float(1 / np.sqrt(nope + rope)))
+    got, (got_kv, got_pe) = nat.fp8_attention_block_forward(
+        hidden, *d["q_a"], *d["q_b"], *d["kv_a"], kv_b, *d["o"], dev(t["q_norm"]), dev(t["kv_norm"]), **kw)
+    assert rel(host(got), want) < 1e-5
+    assert rel(host(got_kv), want_kv) < 1e-6 and rel(host(got_pe), want_pe) < 1e-6
+    assert np.array_equal(host(got_kv)[:prev], t["prev_kv"]) and np.array_equal(host(got_pe)[:prev], t["prev_pe"])
+    got16, _ = nat.fp8_attention_block_forward(
+        hidden, *d["q_a"], *d["q_b"], *d["kv_a"], kv_b, *d["o"], dev(t["q_norm"]), dev(t["kv_norm"]),
+        dtype=torch.bfloat16, **kw)
+    assert got16.dtype == torch.bfloat16 and torch.equal(got16, got.to(torch.bfloat16))
+
+
+def test_fp8_attention_block_error_codes(nat):
+    from pocketlm_amd import _lib
+
+    lib = _lib.load()
+    a = torch.zeros(4096, device="cuda")
+    p = ctypes.c_void_p(a.data_ptr())
+    n = ctypes.c_void_p(0)
+    args = [p] * 19
+    assert lib.ds_fp8_attention_block_bf16x_f32(n, *args[1:], 128, 128, 4, 1, 2, 2, 2, 0, 1e-6, 1.0) == 1
+    assert lib.ds_fp8_attention_block_bf16x_f32(*args, 0, 128, 4, 1, 2, 2, 2, 0, 1e-6, 1.0) == 2
+    assert lib.ds_fp8_attention_block_bf16x_f32(*args, 128, 128, 2048, 1, 2, 2, 2, 0, 1e-6, 1.0) == 102
+    with_null_prev = [p] * 12 + [n, n] + [p] * 5
+    assert lib.ds_fp8_attention_block_bf16x_f32(*with_null_prev, 128, 128, 4, 1, 2, 2, 2, 3, 1e-6, 1.0) == 3

@@ -178,3 +178,72 @@ def test_rope_leaves_an_odd_width_alone():
     assert np.array_equal(mla.rope(x, np.ones(2, np.float32), np.zeros(2, np.float32)), x)
     y = mla.rope(np.array([1.0, 0.0], np.float32), np.array([0.0], np.float32), np.array([1.0], np.float32))
     assert np.allclose(y, [0.0, 1.0])  # a quarter turn
+
+
+def fp8_attention_inputs(hidden_dim, q_rank, kv_rank, heads, nope, rope, v, prev, seed=31):
+    """FP8 e4m3 weights (N(0, 0.05), cast as torch casts), scale_inv grids
+    ~U(0.5, 1.5), bf16-valued hidden state, fp32 norms, caches and rotations."""
+    g = torch.Generator().manual_seed(seed)
+
+    def fp8(rows, cols):
+        w = (torch.randn((rows, cols), generator=g) * 0.05).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        s = (torch.rand((-(-rows // 128), -(-cols // 128)), generator=g) + 0.5).numpy()
+        return w, s
+
+    weights = {"q_a": fp8(q_rank, hidden_dim), "q_b": fp8(heads * (nope + rope), q_rank),
+               "kv_a": fp8(kv_rank + rope, hidden_dim), "o": fp8(hidden_dim, heads * v)}
+    kv_b = fp8(heads * (nope + v), kv_rank)
+    hidden = torch.randn(hidden_dim, generator=g).to(torch.bfloat16).float().numpy()
+    q_norm = (1 + 0.1 * torch.randn(q_rank, generator=g)).numpy()
+    kv_norm = (1 + 0.1 * torch.randn(kv_rank, generator=g)).numpy()
+    prev_kv = torch.randn((prev, kv_rank), generator=g).numpy()
+    prev_pe = torch.randn((prev, rope), generator=g).numpy()
+    ang = np.arange(rope // 2, dtype=np.float32) * 0.37
+    return dict(hidden=hidden, fp8=weights, kv_b=kv_b, q_norm=q_norm, kv_norm=kv_norm, prev_kv=prev_kv,
+                prev_pe=prev_pe, cos=np.cos(ang).astype(np.float32), sin=np.sin(ang).astype(np.float32))
+
+
+FP8_DIMS = (256, 128, 64, 4, 16, 8, 16, 20)  # hidden, q rank, latent rank, heads, nope, rope, v, previous rows
+
+
+def _fp8_block(t, dims, fp8=None, flash=mla.mla_flash_online):
+    hidden_dim, q_rank, kv_rank, heads, nope, rope, v, prev = dims
+    import oracle
+
+    kv_b = oracle.fp8_dequant(*t["kv_b"], "f32")
+    return mla.fp8_attention_block(t["hidden"], fp8 or t["fp8"], kv_b, t["q_norm"], t["kv_norm"], t["prev_kv"],
+                                   t["prev_pe"], t["cos"], t["sin"], num_heads=heads, qk_nope_dim=nope,
+                                   qk_rope_dim=rope, v_head_dim=v, kv_lora_rank=kv_rank, rms_eps=1e-6,
+                                   softmax_scale=float(1 / np.sqrt(nope + rope)), flash=flash)
+
+
+def test_fp8_attention_matches_the_reference_formulation_on_dequantized_weights():
+    """fp8_source.py:6337-6454 restated with torch on the dequantized
+    weights (F.linear, _rms_norm_any, _apply_rope_real, the einsums): the
+    FP8 linears' block-sum-then-scale order differs only by rounding."""
+    import oracle
+
+    hidden_dim, q_rank, kv_rank, heads, nope, rope, v, prev = FP8_DIMS
+    t = fp8_attention_inputs(*FP8_DIMS)
+    got, got_kv, got_pe = _fp8_block(t, FP8_DIMS)
+    deq = {k: torch.from_numpy(oracle.fp8_dequant(*t["fp8"][k], "f32")) for k in t["fp8"]}
+    want, want_kv, want_pe = _torch_block(
+        torch.from_numpy(t["hidden"]), deq["q_a"], deq["q_b"], deq["kv_a"],
+        torch.from_numpy(oracle.fp8_dequant(*t["kv_b"], "f32")), deq["o"], torch.from_numpy(t["q_norm"]),
+        torch.from_numpy(t["kv_norm"]), torch.from_numpy(t["prev_kv"]), torch.from_numpy(t["prev_pe"]),
+        torch.from_numpy(t["cos"]), torch.from_numpy(t["sin"]), heads=heads, nope=nope, rope=rope, v=v, rank=kv_rank,
+        eps=1e-6, scale=float(1 / np.sqrt(nope + rope)))
+    assert rel(got, want.numpy()) < 1e-5
+    assert rel(got_kv, want_kv.numpy()) < 1e-6 and rel(got_pe, want_pe.numpy()) < 1e-6
+    assert got_kv.shape == (prev + 1, kv_rank)
+
+
+def test_fp8_attention_planted_mistakes_are_caught():
+    t = fp8_attention_inputs(*FP8_DIMS)
+    good = _fp8_block(t, FP8_DIMS)[0]
+    w, s = t["fp8"]["q_b"]
+    bad_scale = dict(t["fp8"], q_b=(w, s * np.float32(1.25)))
+    w, s = t["fp8"]["kv_a"]
+    swapped_rows = dict(t["fp8"], kv_a=(np.ascontiguousarray(w[::-1]), s))
+    for fp8 in (bad_scale, swapped_rows):
+        assert rel(_fp8_block(t, FP8_DIMS, fp8=fp8)[0], good) > 1e-3
