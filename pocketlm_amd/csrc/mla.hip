@@ -462,9 +462,6 @@ __device__ __forceinline__ void rope_pair(const float* in, float* out, int64_t p
     out[2 * pair + 1] = x0 * s + x1 * c;
 }
 
-__global__ __launch_bounds__(kThreads) void rms_norm_kernel(float* v, const float* w, int64_t dim, float eps) {
-    rms_norm_block(v, w, v, dim, eps);
-}
 
 // q [H][nope + rope] -> q_nope [H][nope], q_pe [H][rope] with RoPE.
 __global__ __launch_bounds__(kThreads) void mla_q_split_kernel(const float* __restrict__ q, float* __restrict__ q_nope,
@@ -488,13 +485,19 @@ __global__ __launch_bounds__(kThreads) void mla_q_split_kernel(const float* __re
     }
 }
 
-// The new cache row: RMSNorm of the latent part with kv_norm, RoPE of the
-// positional part (one workgroup).
-__global__ __launch_bounds__(kThreads) void mla_kv_row_kernel(const float* __restrict__ kvraw,
-                                                             const float* __restrict__ kv_norm, float* __restrict__ kv_row,
-                                                             float* __restrict__ pe_row, const float* __restrict__ cs,
-                                                             const float* __restrict__ sn, int64_t R, int64_t rope,
-                                                             float eps) {
+// The two norms after the q_a / kv_a projections, one workgroup each:
+// q_low in place (workgroup 0), and the new cache row (workgroup 1).
+__global__ __launch_bounds__(kThreads) void mla_norms_kernel(float* __restrict__ q_low,
+                                                            const float* __restrict__ q_norm, int64_t q_rank,
+                                                            const float* __restrict__ kvraw,
+                                                            const float* __restrict__ kv_norm, float* __restrict__ kv_row,
+                                                            float* __restrict__ pe_row, const float* __restrict__ cs,
+                                                            const float* __restrict__ sn, int64_t R, int64_t rope,
+                                                            float eps) {
+    if (blockIdx.x == 0) {
+        rms_norm_block(q_low, q_norm, q_low, q_rank, eps);
+        return;
+    }
     rms_norm_block(kvraw, kv_norm, kv_row, R, eps);
     if ((rope & 1) == 0) {
         for (int64_t p = threadIdx.x; p < rope / 2; p += kThreads) rope_pair(kvraw + R, pe_row, p, cs, sn);
@@ -670,8 +673,12 @@ int attention_block(const BlockDims& d, ProjectA&& project_a, ProjectQb&& projec
 
     int code = project_a(q_low, kvraw);
     if (code != 0) return code;
-    hipLaunchKernelGGL(rms_norm_kernel, dim3(1), dim3(kThreads), 0, st, q_low, q_norm_weight, d.q_rank, rms_eps);
-    if ((code = plm::check_launch("rms norm")) != 0) return code;
+    // the new row (RMSNorm of the latent, RoPE of the pe part) goes after
+    // the previous rows, which are copied below into other buffers only
+    hipLaunchKernelGGL(mla_norms_kernel, dim3(2), dim3(kThreads), 0, st, q_low, q_norm_weight, d.q_rank, kvraw,
+                       kv_norm_weight, next_kv_cache + d.prev * R, next_pe_cache + d.prev * rope, rope_cos, rope_sin, R,
+                       rope, rms_eps);
+    if ((code = plm::check_launch("mla norms")) != 0) return code;
     if ((code = project_qb(q_low, q)) != 0) return code;
     const int64_t qn_threads = std::max(H * nope, H * rope);
     hipLaunchKernelGGL(mla_q_split_kernel, dim3(static_cast<unsigned>(plm::ceil_div(std::max<int64_t>(qn_threads, 1), kThreads))),
@@ -688,9 +695,6 @@ int attention_block(const BlockDims& d, ProjectA&& project_a, ProjectQb&& projec
                                  static_cast<size_t>(d.prev * rope) * sizeof(float), hipMemcpyDeviceToDevice, st);
         if (err != hipSuccess) return plm::hip_fail(err, "previous cache copy");
     }
-    hipLaunchKernelGGL(mla_kv_row_kernel, dim3(1), dim3(kThreads), 0, st, kvraw, kv_norm_weight,
-                       next_kv_cache + d.prev * R, next_pe_cache + d.prev * rope, rope_cos, rope_sin, R, rope, rms_eps);
-    if ((code = plm::check_launch("mla kv row")) != 0) return code;
     code = flash(qn, qp, next_kv_cache, next_pe_cache, kv_b_weight, heads, H, L, nope, rope, R, v, softmax_scale, fws,
                  st);
     if (code != 0) return code > 0 ? 100 + code : code;
