@@ -683,6 +683,7 @@ def table(args):
               + (f"   cpu {cpu_us:10.1f} us {cpu_gbs:7.2f} GB/s" if cpu_us else ""), flush=True)
 
     import oracle
+    from oracle import mla as oracle_mla
 
     gen = torch.Generator(device="cuda").manual_seed(11)
 
@@ -1174,21 +1175,28 @@ def table(args):
 
     def mla_flash(cache_len):
         # DeepSeek-V3 MLA attention of one token: 128 heads, nope 128, rope 64,
-        # latent rank 512, v 128; fp32 wkv_b [128, 256, 512] (67 MB) in two
-        # copies, a cache_len-row latent cache (fp32, as the reference keeps it)
+        # latent rank 512, v 128; fp32 wkv_b [128, 256, 512] (67 MB) in six
+        # copies (402 MB, more than the memory-side cache holds), a
+        # cache_len-row latent cache (fp32, as the reference keeps it)
         H, nope, rope, R, v = 128, 128, 64, 512, 128
         qn = torch.randn((H, nope), generator=gen, device="cuda") * 0.05
         qp = torch.randn((H, rope), generator=gen, device="cuda") * 0.05
         kvc = torch.randn((cache_len, R), generator=gen, device="cuda")
         pec = torch.randn((cache_len, rope), generator=gen, device="cuda")
-        ws = [torch.randn((H, nope + v, R), generator=gen, device="cuda") * 0.02 for _ in range(2)]
+        ws = [torch.randn((H, nope + v, R), generator=gen, device="cuda") * 0.02 for _ in range(6)]
         out = torch.empty((H, v), device="cuda")
         lib.pocketlm_set_stream(_stream_ptr(torch))
         p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
         calls = [lambda w=w: lib.ds_mla_attention_flash_forward(p(qn), p(qp), p(kvc), p(pec), p(w), p(out), H, cache_len,
                                                                 nope, rope, R, v, 1.0 / math.sqrt(192.0)) for w in ws]
         nbytes = H * (nope + v) * R * 4 + cache_len * (R + rope) * 4 + H * (nope + rope) * 4 + H * v * 4
-        measure(f"mla attention DeepSeek-V3, {cache_len}-row latent cache (fp32)", 1, lambda: calls, nbytes)
+        host = [t.cpu().numpy() for t in (qn, qp, kvc, pec, ws[0])]
+
+        def cpu_mla():  # the reference's own formulation (native/__init__.py:857-876), numpy float64
+            oracle_mla.mla_flash_closed_form(*host, 1.0 / math.sqrt(192.0))
+
+        measure(f"mla attention DeepSeek-V3, {cache_len}-row latent cache (fp32)", 1, lambda: calls, nbytes,
+                cpu_fn=cpu_mla)
         del ws
         torch.cuda.empty_cache()
 
