@@ -19,7 +19,7 @@
 //   mla_merge_kernel      rescales the splits to the global max and divides
 //                         by the sum (1 / sum, 0 when the sum is not positive,
 //                         as the reference does): latent [H][R].
-//   mla_value_kernel      the value rows of kv_b applied to the latent, four
+//   mla_value_kernel      the value rows of kv_b applied to the latent, two
 //                         rows per wave.
 //
 // The block: fp32 GEMVs (one wave per row, float4 loads, a fixed DPP sum),
@@ -43,6 +43,7 @@ constexpr int kTileTokens = 16;     // latent rows staged per step
 constexpr int64_t kMaxRank = 1024;  // the split kernel's largest instance: 16 column tiles per wave,
 constexpr int64_t kMaxRope = 256;   // 20 chunks of 16 columns per wave
 constexpr int kMaxSplits = 64;
+constexpr int kQabsWaves = 16;  // waves of the absorbed-query kernel
 
 // ------------------------------------------------------------------ q_abs
 // q_abs[h][r] = sum_d q_nope[h][d] * wkv_b[h][d][r]; grid (H, ceil(R / 64)),
@@ -72,11 +73,14 @@ __global__ __launch_bounds__(kThreads) void mla_qabs_kernel(const float* __restr
 }
 
 // The same with float4 columns (R % 4 == 0, aligned): grid (H, ceil(R / 256)),
-// lane l of every wave takes columns 4 l .. 4 l + 3 of the workgroup's 256.
-__global__ __launch_bounds__(kThreads) void mla_qabs4_kernel(const float* __restrict__ q_nope,
-                                                            const float* __restrict__ wkv_b, float* __restrict__ q_abs,
-                                                            int64_t nope, int64_t R, int64_t v) {
-    __shared__ float4 part[4][64];
+// NW waves; lane l of every wave takes columns 4 l .. 4 l + 3 of the
+// workgroup's 256, wave w the rows d = w, w + NW, ... (8 in flight), and the
+// waves' sums are added in wave order.
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void mla_qabs4_kernel(const float* __restrict__ q_nope,
+                                                           const float* __restrict__ wkv_b, float* __restrict__ q_abs,
+                                                           int64_t nope, int64_t R, int64_t v) {
+    __shared__ float4 part[NW][64];
     const int64_t h = blockIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t c = static_cast<int64_t>(blockIdx.y) * 256 + 4 * lane;
@@ -84,13 +88,14 @@ __global__ __launch_bounds__(kThreads) void mla_qabs4_kernel(const float* __rest
     const float* wh = wkv_b + h * (nope + v) * R;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (c < R) {
-        for (int64_t d0 = wave; d0 < nope; d0 += 4 * 8) {
+        for (int64_t d0 = wave; d0 < nope; d0 += NW * 8) {
             float4 vals[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) vals[u] = *reinterpret_cast<const float4*>(wh + min(d0 + 4 * u, nope - 1) * R + c);
+            for (int u = 0; u < 8; ++u)
+                vals[u] = *reinterpret_cast<const float4*>(wh + min(d0 + NW * u, nope - 1) * R + c);
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const float qd = d0 + 4 * u < nope ? qh[d0 + 4 * u] : 0.0f;
+                const float qd = d0 + NW * u < nope ? qh[d0 + NW * u] : 0.0f;
                 acc.x = fmaf(qd, vals[u].x, acc.x);
                 acc.y = fmaf(qd, vals[u].y, acc.y);
                 acc.z = fmaf(qd, vals[u].z, acc.z);
@@ -101,10 +106,13 @@ __global__ __launch_bounds__(kThreads) void mla_qabs4_kernel(const float* __rest
     part[wave][lane] = acc;
     __syncthreads();
     if (wave == 0 && c < R) {
-        const float4 p0 = part[0][lane], p1 = part[1][lane], p2 = part[2][lane], p3 = part[3][lane];
-        *reinterpret_cast<float4*>(q_abs + h * R + c) =
-            make_float4(((p0.x + p1.x) + p2.x) + p3.x, ((p0.y + p1.y) + p2.y) + p3.y, ((p0.z + p1.z) + p2.z) + p3.z,
-                        ((p0.w + p1.w) + p2.w) + p3.w);
+        float4 t = part[0][lane];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            const float4 p = part[w][lane];
+            t = make_float4(t.x + p.x, t.y + p.y, t.z + p.z, t.w + p.w);
+        }
+        *reinterpret_cast<float4*>(q_abs + h * R + c) = t;
     }
 }
 
@@ -367,21 +375,21 @@ __global__ __launch_bounds__(kThreads) void mla_merge_kernel(const float* __rest
 }
 
 // ------------------------------------------------------------------ value rows
-// out[h][j] = latent[h] . wkv_b[h][nope + j]: grid (ceil(v / 16), H), four
+// out[h][j] = latent[h] . wkv_b[h][nope + j]: grid (ceil(v / 8), H), two
 // rows per wave, every row's loads issued before the sums (VEC: float4 loads,
 // R % 4 == 0 and aligned).
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void mla_value_kernel(const float* __restrict__ wkv_b,
                                                             const float* __restrict__ lat, float* __restrict__ out,
                                                             int64_t nope, int64_t R, int64_t v) {
-    constexpr int kRows = 4;
+    constexpr int kRows = 2;
     const int lane = threadIdx.x & 63;
     const int64_t h = blockIdx.y;
     const int64_t j0 = (static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6)) * kRows;
     if (j0 >= v) return;
     const float* x = lat + h * R;
     const float* w0 = wkv_b + (h * (nope + v) + nope) * R;
-    float acc[kRows] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float acc[kRows] = {};
     if constexpr (VEC) {
         const int64_t R4 = R / 4;
         for (int64_t k = lane; k < R4; k += 64) {
@@ -582,8 +590,9 @@ int flash(const float* q_nope, const float* q_pe, const float* kv, const float* 
     float* ml = ws + f.ml;
     float* lat = ws + f.lat;
     if (R % 4 == 0 && plm::aligned16(wkv_b))
-        hipLaunchKernelGGL(mla_qabs4_kernel, dim3(static_cast<unsigned>(H), static_cast<unsigned>(plm::ceil_div(R, 256))),
-                           dim3(kThreads), 0, st, q_nope, wkv_b, q_abs, nope, R, v);
+        hipLaunchKernelGGL(mla_qabs4_kernel<kQabsWaves>,
+                           dim3(static_cast<unsigned>(H), static_cast<unsigned>(plm::ceil_div(R, 256))),
+                           dim3(kQabsWaves * 64), 0, st, q_nope, wkv_b, q_abs, nope, R, v);
     else
         hipLaunchKernelGGL(mla_qabs_kernel, dim3(static_cast<unsigned>(H), static_cast<unsigned>(plm::ceil_div(R, 64))),
                            dim3(kThreads), 0, st, q_nope, wkv_b, q_abs, nope, R, v);
@@ -605,7 +614,7 @@ int flash(const float* q_nope, const float* q_pe, const float* kv, const float* 
     hipLaunchKernelGGL(mla_merge_kernel, dim3(static_cast<unsigned>(H), static_cast<unsigned>(plm::ceil_div(R, kThreads))),
                        dim3(kThreads), 0, st, part, ml, lat, H, nsplit, R, sh.R16);
     if ((code = plm::check_launch("mla merge kernel")) != 0) return code;
-    const dim3 vgrid(static_cast<unsigned>(plm::ceil_div(v, 16)), static_cast<unsigned>(H));
+    const dim3 vgrid(static_cast<unsigned>(plm::ceil_div(v, 8)), static_cast<unsigned>(H));
     if (R % 4 == 0 && plm::aligned16(wkv_b) && plm::aligned16(lat))
         hipLaunchKernelGGL(mla_value_kernel<true>, vgrid, dim3(kThreads), 0, st, wkv_b, lat, out, nope, R, v);
     else
