@@ -268,7 +268,9 @@ def bench_verifier(torch, lib, timer, pool, ms=(1, 8), reps=200):
     activations, through fp8_e4m3_block_linear_bf16x_f32.  The expert shapes
     rotate over the pool's 256 experts; q_a and kv_a over the first rows of
     the pool's gate matrices (row-major, so a prefix of rows is a weight of
-    its own); o over 9 copies of its own (1.06 GB)."""
+    its own); o over 9 copies of its own (1.06 GB), and o once more in 8-row
+    tiles (fp8_e4m3_pack_tiles8 / fp8_e4m3_block_linear_tiles8_bf16x_f32, the
+    same values)."""
     gen = torch.Generator(device="cuda").manual_seed(11)
     o_sets = []
     for _ in range(max(2, math.ceil(MALL_BYTES / (7168 * 16384)))):
@@ -285,17 +287,27 @@ def bench_verifier(torch, lib, timer, pool, ms=(1, 8), reps=200):
     }
     out = []
     lib.pocketlm_set_stream(_stream_ptr(torch))
-    for name, rows, cols in VERIFIER_SHAPES:
+    tiles = []
+    for w, s in o_sets:
+        t = torch.empty((lib.fp8_e4m3_tiles8_bytes(7168, 16384),), dtype=torch.uint8, device="cuda")
+        if lib.fp8_e4m3_pack_tiles8(_vp(w), _vp(t), 7168, 16384) != 0:
+            raise RuntimeError("fp8_e4m3_pack_tiles8 failed")
+        tiles.append((t, s))
+    sources["o (8-row tiles)"] = tiles
+    entry = {"o (8-row tiles)": "fp8_e4m3_block_linear_tiles8_bf16x_f32"}
+    for name, rows, cols in VERIFIER_SHAPES + (("o (8-row tiles)", 7168, 16384),):
         sets = sources[name]
+        fn_name = entry.get(name, "fp8_e4m3_block_linear_bf16x_f32")
+        fn = getattr(lib, fn_name)
         for m in ms:
             x = torch.randn((m, cols), generator=gen, device="cuda").to(torch.bfloat16)
             y = torch.empty((m, rows), device="cuda")
             sc = math.ceil(cols / 128)
 
-            def call(w, s, x=x, y=y, m=m, rows=rows, cols=cols, sc=sc):
-                code = lib.fp8_e4m3_block_linear_bf16x_f32(_vp(w), _vp(s), _vp(x), _vp(y), m, rows, cols, sc)
+            def call(w, s, x=x, y=y, m=m, rows=rows, cols=cols, sc=sc, fn=fn, fn_name=fn_name):
+                code = fn(_vp(w), _vp(s), _vp(x), _vp(y), m, rows, cols, sc)
                 if code != 0:
-                    raise RuntimeError(f"fp8_e4m3_block_linear_bf16x_f32 failed with code {code}")
+                    raise RuntimeError(f"{fn_name} failed with code {code}")
 
             for w, s in sets[:4]:
                 call(w, s)
@@ -307,7 +319,7 @@ def bench_verifier(torch, lib, timer, pool, ms=(1, 8), reps=200):
             gbs = nbytes / us / 1e3
             out.append({"shape": f"{name} {rows}x{cols}", "m": m, "us": round(us, 3), "bytes": nbytes,
                         "gb_s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)})
-    del o_sets
+    del o_sets, tiles, sources
     torch.cuda.empty_cache()
     return out
 
@@ -723,6 +735,36 @@ def table(args):
             measure(name, m, make, fp8_bytes(rows, cols, m),
                     lambda w=host_w, s=host_s, xh=xh: oracle.fp8_linear(w, s, xh, batch_reuse=True))
         del sets
+        torch.cuda.empty_cache()
+
+    # ---- the o projection with its weight in 8-row tiles (packed once; the
+    # same values as the row-major linear)
+    if want("fp8 o 7168x16384 (8-row tiles)"):
+        rows, cols = 7168, 16384
+        count = max(2, math.ceil(MALL_BYTES / (rows * cols)))
+        sets = fp8_sets(rows, cols, count)
+        host_w, host_s = sets[0][0].cpu().numpy(), sets[0][1].cpu().numpy()
+        packed = []
+        for w, s in sets:
+            t = torch.empty((lib.fp8_e4m3_tiles8_bytes(rows, cols),), dtype=torch.uint8, device="cuda")
+            if lib.fp8_e4m3_pack_tiles8(ctypes.c_void_p(w.data_ptr()), ctypes.c_void_p(t.data_ptr()), rows, cols):
+                raise RuntimeError("fp8_e4m3_pack_tiles8 failed")
+            packed.append((t, s))
+        del sets
+        for m in (1, 2, 4, 8):
+            x = torch.randn((m, cols), generator=gen, device="cuda").to(torch.bfloat16)
+            y = torch.empty((m, rows), device="cuda")
+            lib.pocketlm_set_stream(_stream_ptr(torch))
+
+            def make(x=x, y=y, m=m):
+                return [lambda t=t, s=s: lib.fp8_e4m3_block_linear_tiles8_bf16x_f32(
+                    ctypes.c_void_p(t.data_ptr()), ctypes.c_void_p(s.data_ptr()), ctypes.c_void_p(x.data_ptr()),
+                    ctypes.c_void_p(y.data_ptr()), m, rows, cols, cols // 128) for t, s in packed]
+
+            xh = x.float().cpu().numpy()
+            measure("fp8 o 7168x16384 (8-row tiles)", m, make, fp8_bytes(rows, cols, m),
+                    lambda w=host_w, s=host_s, xh=xh: oracle.fp8_linear(w, s, xh, batch_reuse=True))
+        del packed
         torch.cuda.empty_cache()
 
     # ---- q_a and kv_a from one hidden state in one launch (configuration 5's

@@ -211,6 +211,29 @@ int fp8_e4m3_block_linear_many_f32(const uint64_t* weight_ptrs, const uint64_t* 
 int fp8_e4m3_block_linear_bf16x_f32(const uint8_t* fp8_weight, const float* scale_inv,
                                     const uint16_t* hidden_bf16, float* out, int64_t batch,
                                     int64_t out_rows, int64_t in_cols, int64_t scale_cols);
+/* FP8 weights in 8-row tiles (no counterpart in the reference, whose FP8
+ * linears read the row-major [out_rows, in_cols] e4m3 matrix of
+ * fp8_linear.cpp:79-210; for callers that keep a weight resident and run it
+ * on batches of 2..8 rows, e.g. a speculative verifier).  The packed weight
+ * holds ceil(rows / 8) x ceil(cols / 128) tiles of 1 KB, tile (t, b) at
+ * (t * ceil(cols / 128) + b) * 1024, row r of the tile at r * 128 within it,
+ * columns b * 128 .. b * 128 + 127; rows and columns past the matrix are
+ * zero.  Every wave load of the linear then reads one contiguous KB.
+ * fp8_e4m3_tiles8_bytes returns the packed size (-2 for bad dimensions);
+ * fp8_e4m3_pack_tiles8 packs a row-major weight into a 16-byte aligned
+ * buffer of that size on the current stream.  The tiles8 linears return
+ * exactly the values of fp8_e4m3_block_linear_f32 / _bf16x_f32 for the
+ * row-major weight (same kernel, schedule and arithmetic; only the weight
+ * addresses differ); they need in_cols % 16 == 0 and 16-byte aligned
+ * activations (code -2 otherwise). */
+int64_t fp8_e4m3_tiles8_bytes(int64_t rows, int64_t cols);
+int fp8_e4m3_pack_tiles8(const uint8_t* fp8_weight, uint8_t* out_tiles, int64_t rows, int64_t cols);
+int fp8_e4m3_block_linear_tiles8_f32(const uint8_t* fp8_tiles, const float* scale_inv, const float* hidden,
+                                     float* out, int64_t batch, int64_t out_rows, int64_t in_cols,
+                                     int64_t scale_cols);
+int fp8_e4m3_block_linear_tiles8_bf16x_f32(const uint8_t* fp8_tiles, const float* scale_inv,
+                                           const uint16_t* hidden_bf16, float* out, int64_t batch,
+                                           int64_t out_rows, int64_t in_cols, int64_t scale_cols);
 int fp8_e4m3_block_linear_many_bf16x_f32(const uint64_t* weight_ptrs, const uint64_t* scale_ptrs,
                                          const uint16_t* hidden_bf16, const uint64_t* out_ptrs,
                                          const int64_t* out_rows, int64_t count, int64_t batch,

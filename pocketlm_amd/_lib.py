@@ -59,6 +59,10 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "fp8_e4m3_block_mlp_many_weighted_f32": (_i32, [_vp] * 9 + [_i64] * 6),
     "fp8_e4m3_block_mlp_many_weighted_shared_f32": (_i32, [_vp] * 10 + [_i64] * 6),
     "fp8_e4m3_block_linear_bf16x_f32": (_i32, [_vp] * 4 + [_i64] * 4),
+    "fp8_e4m3_tiles8_bytes": (_i64, [_i64, _i64]),
+    "fp8_e4m3_pack_tiles8": (_i32, [_vp] * 2 + [_i64] * 2),
+    "fp8_e4m3_block_linear_tiles8_f32": (_i32, [_vp] * 4 + [_i64] * 4),
+    "fp8_e4m3_block_linear_tiles8_bf16x_f32": (_i32, [_vp] * 4 + [_i64] * 4),
     "fp8_e4m3_block_linear_many_f32": (_i32, [_vp] * 5 + [_i64] * 4),
     "fp8_e4m3_block_linear_many_bf16x_f32": (_i32, [_vp] * 5 + [_i64] * 4),
     "fp8_e4m3_block_dual_linear_bf16x_f32": (_i32, [_vp] * 7 + [_i64] * 4),

@@ -93,7 +93,16 @@ struct RowsArgs {
     // g - ndev.  ndev = 0: all groups from the arguments.
     const MoePlan* plan;
     int ndev;
+    // Weights in 8-row tiles (fp8_e4m3_pack_tiles8): the byte of row r,
+    // column c sits at ((r / 8) * nblocks + c / 128) * 1024 + (r % 8) * 128
+    // + c % 128.  Only the weight addresses change.
+    int tiled;
 };
+
+// Byte offset of column offset off (a multiple of 16) from a weight row's
+// base: off itself in a row-major row, and off plus 896 bytes per 128-column
+// block in an 8-row tile row (each block of a tile row is 1 KB from the last).
+__device__ __forceinline__ int64_t tile_col(int64_t off, int tiled) { return off + (tiled ? (off >> 7) * 896 : 0); }
 
 struct CombineArgs {
     const uint8_t* w[kMaxGroups];
@@ -588,8 +597,9 @@ __device__ __forceinline__ void rows_pass_burst(const RowsArgs& a, const uint8_t
             const int64_t b = b0 + static_cast<int64_t>(u) * nw;
             const int64_t off = b * 128 + lane_col;
             const bool in = b < nb && off < a.K;
+            const int64_t woff = tile_col(off, a.tiled);
 #pragma unroll
-            for (int t = 0; t < NT; ++t) q[u][t] = in ? wload16(wrow[t] + off) : plm_u32x4{0, 0, 0, 0};
+            for (int t = 0; t < NT; ++t) q[u][t] = in ? wload16(wrow[t] + woff) : plm_u32x4{0, 0, 0, 0};
             x[u] = load_xpiece<XB>(xrow + off * XE, xlive && in);
 #pragma unroll
             for (int n = 0; n < NWT; ++n) sc[u][n] = b < nb ? plm_gload_f32(sp[n] + b) : 0.0f;
@@ -637,7 +647,7 @@ __device__ __forceinline__ void rows_pass(const RowsArgs& a, const uint8_t* cons
         auto issue = [&](int slot, int k) {
             const int64_t off = min((wave + static_cast<int64_t>(kb + k) * nw) * 128 + lane_col, K - 16);
 #pragma unroll
-            for (int t = 0; t < NT; ++t) q[slot][t] = wload16(wrow[t] + off);
+            for (int t = 0; t < NT; ++t) q[slot][t] = wload16(wrow[t] + tile_col(off, a.tiled));
             x[slot] = load_xpiece<XB>(xrow + off * XE, true);
         };
         auto compute = [&](int slot, int k) {
@@ -738,7 +748,7 @@ __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int block) {
             for (int t = 0; t < TT; ++t) {
                 // rows past the end read the last row; their results are dropped
                 const int64_t r = min(row0 + 8 * t + (li & 7), rows - 1);
-                wrow[i * TT + t] = W[i] + r * a.K;
+                wrow[i * TT + t] = a.tiled ? W[i] + ((r >> 3) * a.nblocks * 1024 + (r & 7) * 128) : W[i] + r * a.K;
             }
         }
         const int64_t xo = static_cast<int64_t>(a.m0 + (xlive ? xm : 0)) * a.x_stride;
@@ -1322,6 +1332,7 @@ struct RowsProblem {
     int nvar;             // > 0: ngroups single weights of vrows[g] rows each, written to vout[g]
     int64_t vrows[kMaxVar];
     float* vout[kMaxVar];
+    bool tiled;           // weights in 8-row tiles (RowsArgs::tiled)
 };
 
 bool rows_fast_ok(const RowsProblem& p) {
@@ -1338,6 +1349,8 @@ bool rows_fast_ok(const RowsProblem& p) {
 
 int run_rows(const RowsProblem& p, hipStream_t st) {
     const bool fast = rows_fast_ok(p);
+    if (p.tiled && (!fast || p.nvar > 0))
+        return plm::fail(-2, "8-row tile weights need K %% 16 == 0 and 16-byte aligned weights and activations");
     if (p.nvar > 0 && (!fast || p.nwt != 1 || p.ngroups != p.nvar || p.nvar > kMaxVar))
         return plm::fail(-2, "variable-row groups need the vector path and one weight per group");
     for (int g0 = 0; g0 < p.ngroups; g0 += kMaxGroups) {
@@ -1368,6 +1381,7 @@ int run_rows(const RowsProblem& p, hipStream_t st) {
         a.K = p.K;
         a.scale_cols = p.scale_cols;
         a.nblocks = static_cast<int>(plm::ceil_div(p.K, 128));
+        a.tiled = p.tiled ? 1 : 0;
         a.m_total = static_cast<int>(p.batch);
         a.nvar = p.nvar;
         for (int i = 0; i < p.nvar; ++i) {
@@ -1570,7 +1584,7 @@ int weighted_moe(const uint64_t* gp, const uint64_t* gsp, const uint64_t* up, co
 }
 
 int linear_impl(const uint8_t* fp8_weight, const float* scale_inv, Act hidden, float* out, int64_t batch,
-                int64_t out_rows, int64_t in_cols, int64_t scale_cols) {
+                int64_t out_rows, int64_t in_cols, int64_t scale_cols, bool tiled = false) {
     if (batch <= 0 || out_rows <= 0 || in_cols <= 0 || scale_cols < plm::ceil_div(in_cols, 128))
         return plm::fail(-2, "bad dimensions");
     const uint8_t* w[1] = {fp8_weight};
@@ -1590,7 +1604,38 @@ int linear_impl(const uint8_t* fp8_weight, const float* scale_inv, Act hidden, f
     p.rows = out_rows;
     p.K = in_cols;
     p.scale_cols = scale_cols;
+    p.tiled = tiled;
     return run_rows(p, plm::current_stream());
+}
+
+// Bytes of a rows x cols FP8 weight in 8-row tiles: ceil(rows / 8) tile rows
+// of ceil(cols / 128) tiles of 1 KB.
+int64_t tiles8_bytes(int64_t rows, int64_t cols) { return plm::ceil_div(rows, 8) * plm::ceil_div(cols, 128) * 1024; }
+
+// One thread per 16 output bytes: tile row t, block b, row r of the tile,
+// piece p (16 columns), output chunk ((t * nb + b) * 8 + r) * 8 + p.  Rows
+// past the matrix and columns past K are zero.
+__global__ __launch_bounds__(256) void fp8_pack_tiles8_kernel(const uint8_t* __restrict__ w, uint4* __restrict__ out,
+                                                              int64_t rows, int64_t cols, int64_t nb, int64_t chunks,
+                                                              int vec) {
+    const int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (q >= chunks) return;
+    const int64_t piece = q & 7, r = (q >> 3) & 7, tb = q >> 6;
+    const int64_t b = tb % nb, t = tb / nb;
+    const int64_t row = t * 8 + r, col = b * 128 + piece * 16;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (row < rows) {
+        const uint8_t* src = w + row * cols + col;
+        if (vec && col + 16 <= cols) {
+            v = *reinterpret_cast<const uint4*>(src);
+        } else {
+            uint32_t wd[4] = {0u, 0u, 0u, 0u};
+            for (int i = 0; i < 16; ++i)
+                if (col + i < cols) wd[i >> 2] |= static_cast<uint32_t>(src[i]) << (8 * (i & 3));
+            v = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+        }
+    }
+    out[q] = v;
 }
 
 int dual_linear_impl(const uint8_t* wa, const float* sa, const uint8_t* wb, const float* sb, Act hidden,
@@ -1951,6 +1996,39 @@ PLM_EXPORT int fp8_e4m3_block_linear_bf16x_f32(const uint8_t* fp8_weight, const 
                                                int64_t out_rows, int64_t in_cols, int64_t scale_cols) {
     if (!fp8_weight || !scale_inv || !hidden_bf16 || !out) return plm::fail(-1, "null pointer");
     return linear_impl(fp8_weight, scale_inv, Act{nullptr, hidden_bf16}, out, batch, out_rows, in_cols, scale_cols);
+}
+
+PLM_EXPORT int64_t fp8_e4m3_tiles8_bytes(int64_t rows, int64_t cols) {
+    if (rows <= 0 || cols <= 0 || rows > (int64_t{1} << 40) / cols) return plm::fail(-2, "bad dimensions");
+    return tiles8_bytes(rows, cols);
+}
+
+PLM_EXPORT int fp8_e4m3_pack_tiles8(const uint8_t* fp8_weight, uint8_t* out_tiles, int64_t rows, int64_t cols) {
+    if (!fp8_weight || !out_tiles) return plm::fail(-1, "null pointer");
+    if (rows <= 0 || cols <= 0 || rows > (int64_t{1} << 40) / cols) return plm::fail(-2, "bad dimensions");
+    if (!plm::aligned16(out_tiles)) return plm::fail(-2, "the tiles need a 16-byte aligned buffer");
+    const int64_t nb = plm::ceil_div(cols, 128);
+    const int64_t chunks = tiles8_bytes(rows, cols) / 16;
+    const int vec = cols % 16 == 0 && plm::aligned16(fp8_weight);
+    hipLaunchKernelGGL(fp8_pack_tiles8_kernel, dim3(static_cast<unsigned>(plm::ceil_div(chunks, 256))), dim3(256), 0,
+                       plm::current_stream(), fp8_weight, reinterpret_cast<uint4*>(out_tiles), rows, cols, nb, chunks,
+                       vec);
+    return plm::check_launch("fp8 pack tiles8 kernel");
+}
+
+PLM_EXPORT int fp8_e4m3_block_linear_tiles8_f32(const uint8_t* fp8_tiles, const float* scale_inv, const float* hidden,
+                                                float* out, int64_t batch, int64_t out_rows, int64_t in_cols,
+                                                int64_t scale_cols) {
+    if (!fp8_tiles || !scale_inv || !hidden || !out) return plm::fail(-1, "null pointer");
+    return linear_impl(fp8_tiles, scale_inv, Act{hidden, nullptr}, out, batch, out_rows, in_cols, scale_cols, true);
+}
+
+PLM_EXPORT int fp8_e4m3_block_linear_tiles8_bf16x_f32(const uint8_t* fp8_tiles, const float* scale_inv,
+                                                      const uint16_t* hidden_bf16, float* out, int64_t batch,
+                                                      int64_t out_rows, int64_t in_cols, int64_t scale_cols) {
+    if (!fp8_tiles || !scale_inv || !hidden_bf16 || !out) return plm::fail(-1, "null pointer");
+    return linear_impl(fp8_tiles, scale_inv, Act{nullptr, hidden_bf16}, out, batch, out_rows, in_cols, scale_cols,
+                       true);
 }
 
 PLM_EXPORT int fp8_e4m3_block_linear_many_f32(const uint64_t* weight_ptrs, const uint64_t* scale_ptrs,

@@ -30,6 +30,7 @@ import os
 from contextlib import contextmanager
 from dataclasses import dataclass
 from pathlib import Path
+from typing import NamedTuple
 
 import torch
 
@@ -276,6 +277,56 @@ def fp8_e4m3_block_linear_f32(fp8_weight: torch.Tensor, scale_inv: torch.Tensor,
         code = getattr(lib, _twin("fp8_e4m3_block_linear_f32", bf16))(_p(w), _p(s), _p(x), _p(out), int(x.shape[0]),
                                                                     out_rows, in_cols, (in_cols + 127) // 128)
     _check("fp8_e4m3_block_linear_f32", code)
+    return _home(out, hidden)
+
+
+class Fp8Tiles8(NamedTuple):
+    """A row-major [rows, cols] FP8 e4m3 weight packed in 8-row tiles
+    (fp8_e4m3_pack_tiles8): 1 KB tiles of 8 rows x 128 columns, zero-padded.
+    No counterpart in the reference."""
+    tiles: torch.Tensor  # uint8, fp8_e4m3_tiles8_bytes(rows, cols) bytes
+    rows: int
+    cols: int
+
+
+def pack_fp8_tiles8(fp8_weight: torch.Tensor) -> Fp8Tiles8:
+    """Packs a row-major FP8 weight into 8-row tiles on its device (no
+    counterpart in the reference)."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_FP8_LINEAR", "Native FP8 linear")
+    if fp8_weight.ndim != 2:
+        raise ValueError("fp8_weight must have shape [out_rows, in_cols]")
+    dev = _target_device(fp8_weight)
+    w = _fp8_bytes(fp8_weight, dev)
+    rows, cols = int(w.shape[0]), int(w.shape[1])
+    nbytes = int(lib.fp8_e4m3_tiles8_bytes(rows, cols))
+    if nbytes < 0:
+        _check("fp8_e4m3_tiles8_bytes", nbytes)
+    tiles = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+    with _launch(lib, dev):
+        code = lib.fp8_e4m3_pack_tiles8(_p(w), _p(tiles), rows, cols)
+    _check("fp8_e4m3_pack_tiles8", code)
+    return Fp8Tiles8(tiles, rows, cols)
+
+
+def fp8_e4m3_block_linear_tiles8_f32(packed: Fp8Tiles8, scale_inv: torch.Tensor, hidden: torch.Tensor) -> torch.Tensor:
+    """fp8_e4m3_block_linear_f32 on a weight packed by pack_fp8_tiles8: the
+    same values, bit for bit (no counterpart in the reference)."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_FP8_LINEAR", "Native FP8 linear")
+    if scale_inv.ndim != 2:
+        raise ValueError("scale_inv must have shape [scale_rows, scale_cols]")
+    dev = _target_device(packed.tiles, scale_inv, hidden)
+    x, bf16 = _hidden_in(hidden, dev)
+    s = _on(scale_inv, dev, torch.float32)
+    out_rows, in_cols = packed.rows, packed.cols
+    if int(x.shape[1]) != in_cols:
+        raise ValueError("hidden input size does not match FP8 weight columns")
+    if int(s.shape[0]) != (out_rows + 127) // 128 or int(s.shape[1]) != (in_cols + 127) // 128:
+        raise ValueError("scale_inv shape does not match FP8 128x128 block layout")
+    out = torch.empty((int(x.shape[0]), out_rows), dtype=torch.float32, device=dev)
+    with _launch(lib, dev):
+        code = getattr(lib, _twin("fp8_e4m3_block_linear_tiles8_f32", bf16))(
+            _p(packed.tiles), _p(s), _p(x), _p(out), int(x.shape[0]), out_rows, in_cols, (in_cols + 127) // 128)
+    _check("fp8_e4m3_block_linear_tiles8_f32", code)
     return _home(out, hidden)
 
 
