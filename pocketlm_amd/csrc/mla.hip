@@ -76,15 +76,39 @@ __global__ __launch_bounds__(kThreads) void mla_qabs_kernel(const float* __restr
 // NW waves; lane l of every wave takes columns 4 l .. 4 l + 3 of the
 // workgroup's 256, wave w the rows d = w, w + NW, ... (8 in flight), and the
 // waves' sums are added in wave order.
+// RoPE on pairs (x0, x1) of each group of `dim` values (ds_forward.cpp:621-645).
+__device__ __forceinline__ void rope_pair(const float* in, float* out, int64_t pair, const float* cs, const float* sn) {
+    const float x0 = in[2 * pair], x1 = in[2 * pair + 1];
+    const float c = cs[pair], s = sn[pair];
+    out[2 * pair] = x0 * c - x1 * s;
+    out[2 * pair + 1] = x0 * s + x1 * c;
+}
+
+// With rope_in set (the attention block, whose q is [H][nope + rope] rows of
+// q_stride floats), workgroup (h, 0) also writes head h's q_pe with RoPE
+// (an odd rope width unrotated, ds_forward.cpp:628-630), the values of
+// mla_q_split_kernel.
 template <int NW>
-__global__ __launch_bounds__(NW * 64) void mla_qabs4_kernel(const float* __restrict__ q_nope,
+__global__ __launch_bounds__(NW * 64) void mla_qabs4_kernel(const float* __restrict__ q_nope, int64_t q_stride,
                                                            const float* __restrict__ wkv_b, float* __restrict__ q_abs,
-                                                           int64_t nope, int64_t R, int64_t v) {
+                                                           int64_t nope, int64_t R, int64_t v,
+                                                           const float* __restrict__ rope_in, float* __restrict__ q_pe,
+                                                           const float* __restrict__ cs, const float* __restrict__ sn,
+                                                           int64_t rope) {
     __shared__ float4 part[NW][64];
     const int64_t h = blockIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t c = static_cast<int64_t>(blockIdx.y) * 256 + 4 * lane;
-    const float* qh = q_nope + h * nope;
+    const float* qh = q_nope + h * q_stride;
+    if (rope_in != nullptr && blockIdx.y == 0) {
+        const float* in = rope_in + h * q_stride;
+        float* out = q_pe + h * rope;
+        if ((rope & 1) == 0) {
+            for (int64_t p = threadIdx.x; p < rope / 2; p += NW * 64) rope_pair(in, out, p, cs, sn);
+        } else {
+            for (int64_t d = threadIdx.x; d < rope; d += NW * 64) out[d] = in[d];
+        }
+    }
     const float* wh = wkv_b + h * (nope + v) * R;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (c < R) {
@@ -462,14 +486,6 @@ __device__ void rms_norm_block(const float* v, const float* w, float* out, int64
     __syncthreads();
 }
 
-// RoPE on pairs (x0, x1) of each group of `dim` values (ds_forward.cpp:621-645).
-__device__ __forceinline__ void rope_pair(const float* in, float* out, int64_t pair, const float* cs, const float* sn) {
-    const float x0 = in[2 * pair], x1 = in[2 * pair + 1];
-    const float c = cs[pair], s = sn[pair];
-    out[2 * pair] = x0 * c - x1 * s;
-    out[2 * pair + 1] = x0 * s + x1 * c;
-}
-
 
 // q [H][nope + rope] -> q_nope [H][nope], q_pe [H][rope] with RoPE.
 __global__ __launch_bounds__(kThreads) void mla_q_split_kernel(const float* __restrict__ q, float* __restrict__ q_nope,
@@ -579,9 +595,18 @@ int launch_split(dim3 grid, size_t lds, hipStream_t st, bool vec, const float* q
 }
 
 // The MLA launches; ws holds flash_workspace_bytes.
+// The absorbed-query kernel's 4-wide instance (the one that can also write
+// the RoPE'd q_pe).
+bool qabs4_ok(int64_t R, const float* wkv_b) { return R % 4 == 0 && plm::aligned16(wkv_b); }
+
+// With rope_in set, q_nope rows are q_stride floats apart and the q_abs
+// kernel writes q_pe (q_pe_out, which q_pe must name) from rope_in; only
+// when qabs4_ok.
 int flash(const float* q_nope, const float* q_pe, const float* kv, const float* pe, const float* wkv_b, float* out,
           int64_t H, int64_t L, int64_t nope, int64_t rope, int64_t R, int64_t v, float scale, float* ws,
-          hipStream_t st) {
+          hipStream_t st, int64_t q_stride = 0, const float* rope_in = nullptr, float* q_pe_out = nullptr,
+          const float* cs = nullptr, const float* sn = nullptr) {
+    if (rope_in != nullptr && (!qabs4_ok(R, wkv_b) || q_pe_out != q_pe)) return plm::fail(-2, "fused q split");
     const FlashLayout f = flash_layout(H, L, R);
     const int64_t per = f.per, nsplit = f.nsplit;
     const SplitShape sh = split_shape(R, rope);
@@ -589,10 +614,11 @@ int flash(const float* q_nope, const float* q_pe, const float* kv, const float* 
     float* part = ws + f.part;
     float* ml = ws + f.ml;
     float* lat = ws + f.lat;
-    if (R % 4 == 0 && plm::aligned16(wkv_b))
+    if (qabs4_ok(R, wkv_b))
         hipLaunchKernelGGL(mla_qabs4_kernel<kQabsWaves>,
                            dim3(static_cast<unsigned>(H), static_cast<unsigned>(plm::ceil_div(R, 256))),
-                           dim3(kQabsWaves * 64), 0, st, q_nope, wkv_b, q_abs, nope, R, v);
+                           dim3(kQabsWaves * 64), 0, st, q_nope, q_stride > 0 ? q_stride : nope, wkv_b, q_abs, nope,
+                           R, v, rope_in, q_pe_out, cs, sn, rope);
     else
         hipLaunchKernelGGL(mla_qabs_kernel, dim3(static_cast<unsigned>(H), static_cast<unsigned>(plm::ceil_div(R, 64))),
                            dim3(kThreads), 0, st, q_nope, wkv_b, q_abs, nope, R, v);
@@ -689,10 +715,16 @@ int attention_block(const BlockDims& d, ProjectA&& project_a, ProjectQb&& projec
                        rope, rms_eps);
     if ((code = plm::check_launch("mla norms")) != 0) return code;
     if ((code = project_qb(q_low, q)) != 0) return code;
-    const int64_t qn_threads = std::max(H * nope, H * rope);
-    hipLaunchKernelGGL(mla_q_split_kernel, dim3(static_cast<unsigned>(plm::ceil_div(std::max<int64_t>(qn_threads, 1), kThreads))),
-                       dim3(kThreads), 0, st, q, qn, qp, rope_cos, rope_sin, H, nope, rope);
-    if ((code = plm::check_launch("mla q split")) != 0) return code;
+    // q_nope and the RoPE'd q_pe: read and written by the q_abs kernel when
+    // its 4-wide instance runs, else split out here
+    const bool fused_q = qabs4_ok(R, kv_b_weight);
+    if (!fused_q) {
+        const int64_t qn_threads = std::max(H * nope, H * rope);
+        hipLaunchKernelGGL(mla_q_split_kernel,
+                           dim3(static_cast<unsigned>(plm::ceil_div(std::max<int64_t>(qn_threads, 1), kThreads))),
+                           dim3(kThreads), 0, st, q, qn, qp, rope_cos, rope_sin, H, nope, rope);
+        if ((code = plm::check_launch("mla q split")) != 0) return code;
+    }
     // the previous rows, then the new one (ds_forward.cpp:716-744)
     if (d.prev > 0) {
         hipError_t err = hipSuccess;
@@ -704,8 +736,10 @@ int attention_block(const BlockDims& d, ProjectA&& project_a, ProjectQb&& projec
                                  static_cast<size_t>(d.prev * rope) * sizeof(float), hipMemcpyDeviceToDevice, st);
         if (err != hipSuccess) return plm::hip_fail(err, "previous cache copy");
     }
-    code = flash(qn, qp, next_kv_cache, next_pe_cache, kv_b_weight, heads, H, L, nope, rope, R, v, softmax_scale, fws,
-                 st);
+    code = fused_q ? flash(q, qp, next_kv_cache, next_pe_cache, kv_b_weight, heads, H, L, nope, rope, R, v,
+                           softmax_scale, fws, st, qw, q + nope, qp, rope_cos, rope_sin)
+                   : flash(qn, qp, next_kv_cache, next_pe_cache, kv_b_weight, heads, H, L, nope, rope, R, v,
+                           softmax_scale, fws, st);
     if (code != 0) return code > 0 ? 100 + code : code;
     return project_o(heads);
 }
