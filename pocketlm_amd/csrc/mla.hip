@@ -10,6 +10,9 @@
 //
 //   mla_qabs_kernel       q_abs [H][R]: per head a (nope x R) product; waves
 //                         split nope, their partial sums added in wave order.
+//                         The 4-wide instance (mla_qabs4_kernel) can also
+//                         write the block's RoPE'd q_pe in place of
+//                         mla_q_split_kernel.
 //   mla_split_kernel      flash-decode partials: workgroup (split, 16 heads)
 //                         walks its tokens in tiles of 16 rows staged in LDS
 //                         (each latent row is read once for 16 heads); the
