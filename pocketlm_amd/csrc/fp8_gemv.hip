@@ -41,6 +41,13 @@
 #include "common.h"
 #include "route.h"
 
+// Loads of down-phase items (or lanes) that do not count read these zero
+// bytes instead, so no load sits behind a branch: the compiler can then wait
+// for each pipeline slot alone rather than for every load in flight.  The
+// kernel gets the address as an argument (looked up per device), so the
+// loads cannot be folded away as reads of a never-written array.
+static __device__ __align__(256) unsigned char down_zero_page[256];
+
 namespace {
 
 constexpr int kMaxGroups = 64;  // experts per launch (pointer tables travel as kernel arguments)
@@ -132,7 +139,9 @@ struct CombineArgs {
     const MoePlan* plan;  // as in RowsArgs (tab rows 4-5 for the down matrices)
     int ndev;
     int fused;            // split_last computed inside the routed tiles (fp8_combine_kernel FUSED)
-    uint16_t* out_bf16;   // fused only: bf16(bf16(out) + bf16(out_last)), or null
+    uint16_t* out_bf16;   // summed mode: bf16(bf16(out) + bf16(out_last)) (no split-off group: bf16(out)), or null
+    int rows_per_wg;      // fp8_down_kernel: output rows per workgroup (at most kDownMaxRows)
+    const unsigned char* zero;  // fp8_down_kernel: 256 zero bytes in device memory
 };
 
 static_assert(kMaxGroups == 64, "the plan maps one lane of the first wave to each group");
@@ -843,7 +852,9 @@ __device__ __forceinline__ void stage_groups(const CombineArgs& a, GroupInfo* gi
                 gi[g].s = a.s[g - a.ndev];
             }
         }
-        gi[g].rw[m] = (a.route != nullptr && m < a.mc) ? a.route[static_cast<int64_t>(a.g_base + g) * a.route_sg +
+        // (a split-off last group is unweighted and has no route entry)
+        const bool routed = !(a.split_last && g == a.ngroups - 1);
+        gi[g].rw[m] = (a.route != nullptr && routed && m < a.mc) ? a.route[static_cast<int64_t>(a.g_base + g) * a.route_sg +
                                                                  static_cast<int64_t>(a.m0 + m) * a.route_sm]
                                                        : 1.0f;
     }
@@ -1009,6 +1020,340 @@ __global__ __launch_bounds__(64 * kCombineWaves) void fp8_combine_kernel(const C
             if (a.per_group_out) o += static_cast<int64_t>(a.g_base + g_lo) * a.m_total * a.rows;
             float* dst = last ? a.out_last : a.out;
             dst[o] = a.accumulate ? dst[o] + v : v;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ down phase, one workgroup per CU
+//
+// fp8_down_kernel computes what fp8_combine_kernel computes, laid out for the
+// 256 compute units of the part:
+//   * a workgroup of up to 16 waves owns rows_per_wg output rows (28 at
+//     7168 rows: 256 workgroups, each streaming the same bytes) in up to 4
+//     tiles of 8 rows.  Such a range may cross a 128-row scale block, so a
+//     lane takes the scale of its own accumulator rows (at most two scale
+//     rows per workgroup);
+//   * items (group, block) go to waves round robin, nw = min(16, items), and
+//     the wave sums are added in wave order: a row's arithmetic depends on
+//     the items alone, never on the batch, the row range or the grid;
+//   * each wave keeps P items in flight (a ring of P register slots; every
+//     load is unconditional, slots past the wave's last item read a zero
+//     page), so the compiler waits for one slot at a time;
+//   * FUSED: the split-off last group (the shared expert) is computed by the
+//     same workgroup, its items on the last waves when it has fewer items
+//     than waves (the wave sums then equal those of a launch of that group
+//     alone), and its first item is loaded before the plan of a
+//     device-routed call is known.
+// STAGE (one activation row): every wave reads the groups' addresses and
+// route weights itself (lane g holds group g's) and copies the activations of
+// its own items into its own LDS region, so no workgroup barrier stands
+// before the weight stream.  Otherwise the workgroup stages the groups in
+// LDS behind one barrier and each item also loads its activation pieces.
+constexpr int kDownWaves = 16;
+constexpr int kDownMaxRows = 32;
+constexpr int kDownItemBytes = 512;    // one item's activations at one row: hi and lo planes of 128 columns
+constexpr int kDownStageItems = 12;    // STAGE: items per wave at most (6 KB of LDS per wave)
+constexpr int kDownStageLoads = kDownStageItems / 2;  // a wave load (1 KB) carries two items
+
+// The address as a value the compiler cannot see through, so a load from
+// "real or zero page" stays one unconditional load (it would otherwise
+// split it into branches, which make it wait for every load in flight).
+__device__ __forceinline__ const void* opaque_addr(bool use, const void* p, const void* alt) {
+    uint64_t v = reinterpret_cast<uint64_t>(use ? p : alt);
+    asm volatile("" : "+v"(v));
+    return reinterpret_cast<const void*>(v);
+}
+
+template <class T>
+__device__ __forceinline__ T* lane_ptr(T* p, int lane) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(v), lane);
+    const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(v >> 32), lane);
+    return reinterpret_cast<T*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+template <int TT, int P, bool STAGE, bool FUSED>
+__global__ __launch_bounds__(64 * kDownWaves) void fp8_down_kernel(const CombineArgs a) {
+    extern __shared__ plm_u32x4 stage4[];  // STAGE: per wave, its items' activations [item][hi, lo][128] bf16
+    __shared__ float red[(FUSED ? 2 : 1) * kDownWaves * TT * 64];
+    __shared__ GroupInfo gi[STAGE ? 1 : kMaxGroups + 1];
+    __shared__ int plan_count;
+    const int nw = blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int lane = threadIdx.x & 63;
+    const int li = lane & 15;
+    const int64_t lane_col = 64 * (li >> 3) + 16 * (lane >> 4);
+    const int xm = li & 7;  // activation row of the lane's B column
+    const bool xlive = xm < a.mc;
+    const unsigned char* zero = a.zero;
+
+    int g_lo = 0, g_hi = a.ngroups, tile = blockIdx.x;
+    if (a.per_group_out) {
+        g_lo = tile / a.tiles_per_group;
+        g_hi = g_lo + 1;
+        tile -= g_lo * a.tiles_per_group;
+    } else if (FUSED) {
+        g_hi = a.ngroups - 1;
+    }
+    const int64_t row0 = static_cast<int64_t>(tile) * a.rows_per_wg;
+    const int64_t rend = min(row0 + a.rows_per_wg, a.rows);
+    int64_t roff[TT];  // rows past the range re-read the last one; their results are dropped
+#pragma unroll
+    for (int t = 0; t < TT; ++t) roff[t] = min(row0 + 8 * t + (li & 7), rend - 1) * a.K + lane_col;
+    const int64_t srow_a = (row0 >> 7) * a.scale_cols;
+    const int64_t srow_b = ((rend - 1) >> 7) * a.scale_cols;
+    uint32_t sel_b = 0;  // bit 4t + j: accumulator j of tile t is a row of the second scale row
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (((row0 + 8 * t + 4 * ((lane >> 4) & 1) + j) >> 7) != (row0 >> 7)) sel_b |= 1u << (4 * t + j);
+
+    // The shared group's items (FUSED): blocks s_first, s_first + nw, ...
+    int s_first = 0, ns = 0;
+    const uint8_t* s_w = nullptr;
+    const float* s_s = nullptr;
+    if constexpr (FUSED) {
+        const int shift = nw > a.nbe ? nw - a.nbe : 0;
+        s_first = wave - shift;
+        ns = s_first >= 0 ? (a.nbe - 1 - s_first) / nw + 1 : 0;
+        s_w = a.w[a.ngroups - 1 - a.ndev];
+        s_s = a.s[a.ngroups - 1 - a.ndev];
+    }
+    int nr = 0;  // routed items of this wave (blocks wave, wave + nw, ... of the summed groups), once the plan is read
+
+    // STAGE: lane g holds group g's down matrix, scales and route weight.
+    const uint8_t* lw = nullptr;
+    const float* lsc = nullptr;
+    float lrw = 1.0f;
+    unsigned char* region = reinterpret_cast<unsigned char*>(stage4) + static_cast<int64_t>(wave) * kDownStageItems * kDownItemBytes;
+
+    // One pipeline slot: an item's weight tiles, its scales, its route
+    // weight, whether it counts, and where its activations are.
+    struct Slot {
+        plm_u32x4 q[TT];
+        float sv;  // lane 0: the scale of the first scale row, lane 1: of the second
+        float rw;  // the lane's route weight
+        bool keep;
+        int g;
+        int64_t blk;
+        int item;  // STAGE: the item's place in the wave's LDS region
+        XPiece<true> xh, xl;
+    };
+    auto issue_item = [&](Slot& sl, bool exists, int g, int64_t blk, int item, const uint8_t* W, const float* S,
+                          float rw) {
+        const bool keep_l = !(a.zero_skip && rw == 0.0f);
+        // the whole wave skips a missing item, one no live row keeps, or a group without weights
+        const bool live = exists && W != nullptr && S != nullptr && __any(xlive && keep_l);
+        const bool in = live && blk * 128 + lane_col < a.K;
+        const int64_t col = blk * 128;
+#pragma unroll
+        for (int t = 0; t < TT; ++t) sl.q[t] = wload16(opaque_addr(in, W + roff[t] + col, zero + lane_col));
+        // lane 0 reads the scale of the first scale row, the others that of the
+        // second (a vector load, counted in order with the weights)
+        sl.sv = plm_gload_f32(opaque_addr(live, S + ((lane & 1) ? srow_b : srow_a) + blk, zero));
+        sl.rw = rw;
+        sl.keep = keep_l && live;
+        sl.g = g;
+        sl.blk = blk;
+        sl.item = item;
+        if constexpr (!STAGE) {
+            const int64_t xo =
+                (static_cast<int64_t>(a.g_base + g) * a.m_total + a.m0 + (xlive ? xm : 0)) * a.K + col + lane_col;
+            const bool xin = xlive && in;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                sl.xh.v[i] = xload16(opaque_addr(xin, a.act_hi + xo + 8 * i, zero + 16 * i));
+                sl.xl.v[i] = xload16(opaque_addr(xin, a.act_lo + xo + 8 * i, zero + 16 * i));
+            }
+        }
+    };
+    auto issue_s = [&](Slot& sl, int k) {
+        const bool e = k < ns;
+        issue_item(sl, e, a.ngroups - 1, e ? s_first + static_cast<int64_t>(k) * nw : 0, k, e ? s_w : nullptr,
+                   e ? s_s : nullptr, 1.0f);
+    };
+    auto issue_r = [&](Slot& sl, int k) {
+        const bool e = k < nr;
+        const int c = e ? wave + k * nw : 0;
+        const int gl = c / a.nbe;
+        const int g = g_lo + gl;
+        if constexpr (STAGE) {
+            issue_item(sl, e, g, c - gl * a.nbe, ns + k, e ? lane_ptr(lw, g) : nullptr, e ? lane_ptr(lsc, g) : nullptr,
+                       e ? lane_value(lrw, g) : 1.0f);
+        } else {
+            issue_item(sl, e, g, c - gl * a.nbe, ns + k, e ? gi[g].w : nullptr, e ? gi[g].s : nullptr,
+                       e ? gi[g].rw[xm] : 1.0f);
+        }
+    };
+    auto accumulate = [&](Slot& sl, plm_f32x4 (&acc)[TT], auto san) {
+        constexpr bool SAN = decltype(san)::value;
+        if constexpr (STAGE) {
+            const bool rd = xlive && sl.blk * 128 + lane_col < a.K;
+            const unsigned char* hs = region + sl.item * kDownItemBytes + 2 * lane_col;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                sl.xh.v[i] = rd ? *reinterpret_cast<const plm_u32x4*>(hs + 16 * i) : plm_u32x4{0, 0, 0, 0};
+                sl.xl.v[i] = rd ? *reinterpret_cast<const plm_u32x4*>(hs + 256 + 16 * i) : plm_u32x4{0, 0, 0, 0};
+            }
+        }
+        const BOperands<true, SAN> bh(sl.xh), bl(sl.xl);
+        const float fa = lane_value(sl.sv, 0) * sl.rw;
+        const float fb = lane_value(sl.sv, 1) * sl.rw;
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            plm_bf16x8 a0, a1;
+            weights_to_bf16(SAN ? zero_nan_bytes(sl.q[t]) : sl.q[t], a0, a1);
+            plm_f32x4 d = mfma_bf16(a0, bh.h0, plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+            d = mfma_bf16(a1, bh.h1, d);
+            d = mfma_bf16(a0, bl.h0, d);
+            d = mfma_bf16(a1, bl.h1, d);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float f = ((sel_b >> (4 * t + j)) & 1u) ? fb : fa;
+                acc[t][j] = sl.keep ? fmaf(d[j], f, acc[t][j]) : acc[t][j];
+            }
+        }
+    };
+
+    Slot ss, rs[P];  // the shared items' slot, the routed items' ring
+    plm_f32x4 acc[TT], acc_s[TT];
+    auto rings = [&](auto san) {
+        // the shared items: the first was issued before the routed ring, so
+        // waiting for it leaves the ring's loads in flight
+        if (ns > 0) accumulate(ss, acc_s, san);
+        for (int k = 1; k < ns; ++k) {
+            issue_s(ss, k);
+            accumulate(ss, acc_s, san);
+        }
+        for (int k0 = 0; k0 < nr; k0 += P) {
+#pragma unroll
+            for (int u = 0; u < P; ++u) {
+                if (k0 + u < nr) accumulate(rs[u], acc, san);
+                issue_r(rs[u], k0 + u + P);
+            }
+        }
+    };
+#pragma unroll
+    for (int t = 0; t < TT; ++t) acc[t] = acc_s[t] = plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    if constexpr (STAGE) {
+        // Loads in the order they are waited for: the groups' addresses and
+        // route weights and the plan's count, the shared group's first item,
+        // the activations of the wave's items.
+        int count_v = kMaxGroups + 1;
+        if (lane < a.ngroups) {
+            if (lane < a.ndev) {
+                lw = reinterpret_cast<const uint8_t*>(a.plan->tab[4][lane]);
+                lsc = reinterpret_cast<const float*>(a.plan->tab[5][lane]);
+            } else {
+                lw = a.w[lane - a.ndev];
+                lsc = a.s[lane - a.ndev];
+            }
+            // one activation row, m0 (a split-off last group is unweighted and has no route entry)
+            const bool routed = !(a.split_last && lane == a.ngroups - 1);
+            lrw = (a.route != nullptr && routed)
+                      ? a.route[static_cast<int64_t>(a.g_base + lane) * a.route_sg + static_cast<int64_t>(a.m0) * a.route_sm]
+                      : 1.0f;
+        }
+        if (lane == 0 && a.ndev > 0) count_v = a.plan->count;
+        issue_s(ss, 0);
+        const int nr_all = wave < (g_hi - g_lo) * a.nbe ? ((g_hi - g_lo) * a.nbe - 1 - wave) / nw + 1 : 0;
+        const int items = ns + nr_all;  // at most kDownStageItems (the host checks)
+        plm_u32x4 xv[kDownStageLoads];
+        const int half = lane >> 5, plane = (lane >> 4) & 1, piece = lane & 15;
+#pragma unroll
+        for (int i = 0; i < kDownStageLoads; ++i) {
+            const int it = 2 * i + half;
+            int g, blk;
+            if (it < ns) {
+                g = a.ngroups - 1;
+                blk = s_first + it * nw;
+            } else {
+                const int c = wave + (it - ns) * nw;
+                g = g_lo + c / a.nbe;
+                blk = c - (c / a.nbe) * a.nbe;
+            }
+            const bool ok = it < items && blk * 128 + piece * 8 < a.K;
+            const uint16_t* src = (plane ? a.act_lo : a.act_hi) +
+                                  (static_cast<int64_t>(a.g_base + g) * a.m_total + a.m0) * a.K + blk * 128 + piece * 8;
+            xv[i] = xload16(opaque_addr(ok, src, zero));
+        }
+        const int cnt = __builtin_amdgcn_readfirstlane(count_v);
+        if (a.ndev > 0) g_hi = min(g_hi, cnt);
+        const int nr_items = (g_hi - g_lo) * a.nbe;
+        nr = wave < nr_items ? (nr_items - 1 - wave) / nw + 1 : 0;
+#pragma unroll
+        for (int u = 0; u < P; ++u) issue_r(rs[u], u);
+#pragma unroll
+        for (int i = 0; i < kDownStageLoads; ++i)
+            if (2 * i < items)
+                *reinterpret_cast<plm_u32x4*>(region + (2 * i + half) * kDownItemBytes + plane * 256 + piece * 16) = xv[i];
+        plm_wave_sync();
+    } else {
+        // The workgroup stages the groups' addresses and route weights.
+        issue_s(ss, 0);
+        for (int t = threadIdx.x; t < a.ngroups * kMaxM; t += blockDim.x) {
+            const int g = t / kMaxM, m = t - g * kMaxM;
+            if (m == 0) {
+                if (g < a.ndev) {
+                    gi[g].w = reinterpret_cast<const uint8_t*>(a.plan->tab[4][g]);
+                    gi[g].s = reinterpret_cast<const float*>(a.plan->tab[5][g]);
+                } else {
+                    gi[g].w = a.w[g - a.ndev];
+                    gi[g].s = a.s[g - a.ndev];
+                }
+            }
+            const bool routed = !(a.split_last && g == a.ngroups - 1);
+            gi[g].rw[m] = (a.route != nullptr && routed && m < a.mc)
+                              ? a.route[static_cast<int64_t>(a.g_base + g) * a.route_sg +
+                                        static_cast<int64_t>(a.m0 + m) * a.route_sm]
+                              : 1.0f;
+        }
+        if (threadIdx.x == 0) plan_count = a.ndev > 0 ? a.plan->count : kMaxGroups + 1;
+        __syncthreads();
+        if (a.ndev > 0) g_hi = min(g_hi, plan_count);
+        const int nr_items = (g_hi - g_lo) * a.nbe;
+        nr = wave < nr_items ? (nr_items - 1 - wave) / nw + 1 : 0;
+#pragma unroll
+        for (int u = 0; u < P; ++u) issue_r(rs[u], u);
+    }
+    rings(std::false_type{});
+    bool bad = false;
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bad = bad || acc[t][j] != acc[t][j] || acc_s[t][j] != acc_s[t][j];
+    if (__any(bad)) {
+        // NaN weight bytes count as 0: the wave's items again, NaN bytes zeroed
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[t] = acc_s[t] = plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        issue_s(ss, 0);
+#pragma unroll
+        for (int u = 0; u < P; ++u) issue_r(rs[u], u);
+        rings(std::true_type{});
+    }
+    halves_to_lds(acc, red, wave, lane);
+    if constexpr (FUSED) halves_to_lds(acc_s, red, kDownWaves + wave, lane);
+    __syncthreads();
+
+    for (int t = threadIdx.x; t < TT * 64; t += blockDim.x) {
+        const int tt = t >> 6, r = (t >> 3) & 7, m = t & 7;
+        const int64_t row = row0 + 8 * tt + r;
+        if (m >= a.mc || row >= rend) continue;
+        float v = 0.0f;
+        for (int w = 0; w < nw; ++w) v += red[w * TT * 64 + t];
+        int64_t o = static_cast<int64_t>(a.m0 + m) * a.rows + row;
+        if constexpr (FUSED) {
+            float v2 = 0.0f;
+            for (int w = 0; w < nw; ++w) v2 += red[(kDownWaves + w) * TT * 64 + t];
+            a.out_last[o] = v2;
+            a.out[o] = v;
+            if (a.out_bf16 != nullptr) a.out_bf16[o] = moe_bf16_tail(v, v2, true);
+        } else {
+            if (a.per_group_out) o += static_cast<int64_t>(a.g_base + g_lo) * a.m_total * a.rows;
+            a.out[o] = a.accumulate ? a.out[o] + v : v;
+            if (a.out_bf16 != nullptr) a.out_bf16[o] = moe_bf16_tail(v, 0.0f, false);
         }
     }
 }
@@ -1305,12 +1650,110 @@ void launch_combine_cfg(const CombineArgs& a, hipStream_t st) {
     }
 }
 
-// The down phase: 2 tiles per wave, 1 block in flight (the 9-expert
-// DeepSeek-V3 down phase: 30.5 us against 42.0 with 1 tile at one row).
-void launch_combine(const CombineArgs& a, int mcount, hipStream_t st) {
+// The down phase as fp8_combine_kernel lays it out: 2 tiles per wave, 1 block
+// in flight.
+void launch_combine_tiles(const CombineArgs& a, int mcount, hipStream_t st) {
     CombineArgs b = a;
     b.mc = mcount;
     launch_combine_cfg<2, 1>(b, st);
+}
+
+// The device address of down_zero_page on the current device (looked up the
+// first time a device asks, with that device current, and kept).
+int zero_page_address(const unsigned char** out) {
+    static std::mutex mu;
+    static std::vector<std::pair<int, const unsigned char*>> known;
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return plm::hip_fail(err, "hipGetDevice");
+    std::lock_guard<std::mutex> lock(mu);
+    for (const auto& k : known)
+        if (k.first == dev) {
+            *out = k.second;
+            return 0;
+        }
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(down_zero_page));
+    if (err != hipSuccess) return plm::hip_fail(err, "hipGetSymbolAddress(down_zero_page)");
+    known.emplace_back(dev, static_cast<const unsigned char*>(p));
+    *out = static_cast<const unsigned char*>(p);
+    return 0;
+}
+
+// Kernels whose LDS passes 64 KiB must say so once per device: bytes is the
+// most dynamic LDS a launch of fn asks for (its static LDS comes on top).
+int allow_large_lds(const void* fn, int bytes) {
+    static std::mutex mu;
+    static std::vector<std::pair<const void*, int>> done;
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return plm::hip_fail(err, "hipGetDevice");
+    std::lock_guard<std::mutex> lock(mu);
+    for (const auto& d : done)
+        if (d.first == fn && d.second == dev) return 0;
+    err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (err != hipSuccess) return plm::hip_fail(err, "LDS attribute");
+    done.emplace_back(fn, dev);
+    return 0;
+}
+
+template <int TT, int P, bool STAGE, bool FUSED>
+int launch_down_cfg(const CombineArgs& b, unsigned grid, int nw, size_t shmem, hipStream_t st) {
+    const void* fn = reinterpret_cast<const void*>(&fp8_down_kernel<TT, P, STAGE, FUSED>);
+    if (shmem > 0) {
+        const int code = allow_large_lds(fn, kDownWaves * kDownStageItems * kDownItemBytes);
+        if (code != 0) return code;
+    }
+    hipLaunchKernelGGL((fp8_down_kernel<TT, P, STAGE, FUSED>), dim3(grid), dim3(nw * plm::kWave), shmem, st, b);
+    return 0;
+}
+
+template <int TT, int P, bool STAGE>
+int launch_down_tt(const CombineArgs& b, unsigned grid, int nw, size_t shmem, hipStream_t st) {
+    return b.fused ? launch_down_cfg<TT, P, STAGE, true>(b, grid, nw, shmem, st)
+                   : launch_down_cfg<TT, P, STAGE, false>(b, grid, nw, shmem, st);
+}
+
+// The down phase (fp8_down_kernel): rows per workgroup so that the grid
+// fills the compute units once (7168 rows: 28 each, 256 workgroups), up to
+// 32; the split-off last group always in the routed workgroups (FUSED); the
+// activation planes in LDS at one row when they fit.
+int launch_combine(const CombineArgs& a, int mcount, hipStream_t st) {
+    CombineArgs b = a;
+    b.mc = mcount;
+    b.fused = b.split_last ? 1 : 0;  // FUSED is the layout of a split-off last group, nothing else
+    const int zc = zero_page_address(&b.zero);
+    if (zc != 0) return zc;
+    const int outs = b.per_group_out ? b.ngroups : 1;
+    int64_t per = plm::ceil_div(b.rows * outs, plm::cu_count());
+    per = std::min<int64_t>(kDownMaxRows, std::max<int64_t>(4, plm::ceil_div(per, 4) * 4));
+    b.rows_per_wg = static_cast<int>(per);
+    b.tiles_per_group = static_cast<int>(plm::ceil_div(b.rows, per));
+    const int nw = static_cast<int>(
+        std::max<int64_t>(1, std::min<int64_t>(static_cast<int64_t>(combine_segments(b)) * b.nbe, kDownWaves)));
+    const unsigned grid = static_cast<unsigned>(static_cast<int64_t>(b.tiles_per_group) * outs);
+    // One activation row: each wave copies its own items' activations into
+    // its LDS region (a wave's items: its shared-group blocks, then its
+    // blocks of the summed groups).
+    const int64_t ns_max = b.fused ? plm::ceil_div(b.nbe, nw) : 0;
+    const int64_t nr_max = plm::ceil_div(static_cast<int64_t>(combine_segments(b)) * b.nbe, nw);
+    const bool stage = mcount == 1 && !b.per_group_out && ns_max + nr_max <= kDownStageItems && b.K % 8 == 0 &&
+                       plm::aligned16(b.act_hi) && plm::aligned16(b.act_lo);
+    const size_t shmem = stage ? static_cast<size_t>(nw) * kDownStageItems * kDownItemBytes : 0;
+    // Items in flight per wave within 128 VGPRs (16 waves): the activations
+    // read from memory (several rows) take the registers of one slot.  At
+    // 28 rows one item per wave is in flight: 16 waves of 3.5 KB items keep
+    // the memory system busy, and deeper rings were slower (the 9-expert
+    // DeepSeek-V3 down phase 27.0 us with 1, 33.9 with 2).
+    const int tt = static_cast<int>(plm::ceil_div(per, 8));
+    if (stage) {
+        if (tt == 1) return launch_down_tt<1, 3, true>(b, grid, nw, shmem, st);
+        if (tt == 2) return launch_down_tt<2, 3, true>(b, grid, nw, shmem, st);
+        return launch_down_tt<4, 1, true>(b, grid, nw, shmem, st);
+    }
+    if (tt == 1) return launch_down_tt<1, 3, false>(b, grid, nw, shmem, st);
+    if (tt == 2) return launch_down_tt<2, 2, false>(b, grid, nw, shmem, st);
+    return launch_down_tt<4, 1, false>(b, grid, nw, shmem, st);
 }
 
 // A GEMV problem over groups that share the activations.
@@ -1474,7 +1917,8 @@ int run_combine(const CombineProblem& p, hipStream_t st) {
             a.m0 = static_cast<int>(m0);
             a.mc = mc;
             if (fast) {
-                launch_combine(a, mc, st);
+                const int lc = launch_combine(a, mc, st);
+                if (lc != 0) return lc;
             } else {
                 const int64_t total = static_cast<int64_t>(combine_outputs(a)) * mc * p.rows;
                 const unsigned blocks = static_cast<unsigned>(plm::ceil_div(total, 256));
@@ -1900,8 +2344,9 @@ int device_routed_impl(const uint64_t* table, int64_t num_experts, const int64_t
     c.ndev = ndev;
     c.fused = 1;
     c.out_bf16 = out_bf16;
-    launch_combine(c, static_cast<int>(batch), st);
-    return plm::check_launch("fp8 combine kernel");
+    code = launch_combine(c, static_cast<int>(batch), st);
+    if (code != 0) return code;
+    return plm::check_launch("fp8 down kernel");
 }
 
 // Several weights of different row counts sharing the activations, in one
