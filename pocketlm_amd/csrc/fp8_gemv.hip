@@ -3,33 +3,25 @@
 //
 // Design.  The path is HBM-bound (2 flop per weight byte at one activation
 // row), so every kernel streams each weight byte once per call, for all
-// activation rows, with 16-byte loads:
-//
-//   * A "chunk" is 1024 columns of one weight row: lane l of a wave reads
-//     bytes [16l, 16l+16) with one global_load_dwordx4, decodes them with
-//     v_cvt_pk_f32_fp8 (4 instructions per 16 bytes) and dots them with the
-//     matching 16 activations.  The 16-byte span never crosses a 128-column
-//     scale block, so the partial is scaled once.
-//   * A workgroup owns a tile of TR rows and splits the row's chunks across
-//     its waves (wave w takes chunks w, w+nw, ...); nw depends only on the
-//     number of chunks per row, so the per-row arithmetic - lane partials,
-//     the fixed xor-butterfly lane sum, the in-order sum over waves - is the
-//     same for every batch size and tile shape.  That is what makes batched
-//     calls bit-exact to per-row calls, as the reference's tests require.
-//   * NaN weight bytes must contribute 0 (fp8_linear.cpp:31-33).  The fast
-//     path decodes with the hardware converter (NaN stays NaN) and only when
-//     a 16-byte partial comes out NaN re-decodes that span with NaN -> 0.
+// activation rows, with 16-byte nontemporal loads, and does the dot products
+// on the matrix cores (v_mfma_f32_16x16x32_bf16; e4m3 -> bf16 is exact).
+// Activation rows are MFMA columns and a column's result depends on that
+// column alone, so a batched call returns, row for row, the bits of per-row
+// calls (the reference's batch-reuse tests).  NaN weight bytes contribute 0
+// (fp8_linear.cpp:31-33): a wave whose sums come out NaN runs its blocks
+// again with NaN bytes zeroed.
 //
 // fp8_rows_kernel  : rows of one or more experts sharing the activations
 //                    (linear, dual, gate/up phase with the SiLU epilogue, and
 //                    several weights of different row counts in one grid);
-//                    the activations are fp32, or bf16 widened in the kernel
-//                    (the *_bf16x_f32 entry points; widening is exact).
-// fp8_combine_kernel: rows whose K range is the concatenation of several
+//                    the activations are fp32 (split into bf16 hi + lo) or
+//                    bf16 (the *_bf16x_f32 entry points).
+// fp8_down_kernel  : rows whose K range is the concatenation of several
 //                    experts' down matrices, each with its own activations
-//                    and route weight (down phase + routed combine); a last
-//                    group can be split off into its own output (the shared
-//                    expert beside the routed sum).
+//                    (the SiLU intermediate as bf16 hi / lo planes) and route
+//                    weight (down phase + routed combine); a last group can
+//                    be split off into its own output (the shared expert
+//                    beside the routed sum).
 #include <algorithm>
 #include <cstddef>
 #include <cstdint>
@@ -52,7 +44,6 @@ namespace {
 
 constexpr int kMaxGroups = 64;  // experts per launch (pointer tables travel as kernel arguments)
 constexpr int kMaxWaves = 8;
-constexpr int kCombineWaves = 8;  // waves of a down-phase workgroup (at most)
 constexpr int kMaxM = 8;        // activation rows per launch; larger batches are split
 constexpr int kMaxVar = 8;      // matrices of different row counts per many-linear launch
 
@@ -138,7 +129,7 @@ struct CombineArgs {
     int mc;               // activation rows of this launch
     const MoePlan* plan;  // as in RowsArgs (tab rows 4-5 for the down matrices)
     int ndev;
-    int fused;            // split_last computed inside the routed tiles (fp8_combine_kernel FUSED)
+    int fused;            // the split-off last group computed by the routed workgroups (fp8_down_kernel FUSED)
     uint16_t* out_bf16;   // summed mode: bf16(bf16(out) + bf16(out_last)) (no split-off group: bf16(out)), or null
     int rows_per_wg;      // fp8_down_kernel: output rows per workgroup (at most kDownMaxRows)
     const unsigned char* zero;  // fp8_down_kernel: 256 zero bytes in device memory
@@ -828,211 +819,24 @@ __device__ __forceinline__ uint16_t moe_bf16_tail(float routed, float shared, bo
     return static_cast<uint16_t>(v != v ? 0x7FC0u : bf16_rne_bits(v));
 }
 
-// What every item of a group needs, staged in LDS by the whole workgroup
-// before its waves start: the down matrix, its scales and the route weight
-// of each activation row.  (Read per item from global memory, the route and
-// a plan's pointers were two dependent round trips before every item's
-// weight loads.)
+// What every item of a group needs (several activation rows: staged in LDS
+// by the whole workgroup before its waves start): the down matrix, its
+// scales and the route weight of each activation row.
 struct GroupInfo {
     const uint8_t* w;
     const float* s;
     float rw[kMaxM];
 };
 
-// Every thread calls it (it synchronises the workgroup).
-__device__ __forceinline__ void stage_groups(const CombineArgs& a, GroupInfo* gi) {
-    for (int t = threadIdx.x; t < a.ngroups * kMaxM; t += blockDim.x) {
-        const int g = t / kMaxM, m = t - g * kMaxM;
-        if (m == 0) {
-            if (g < a.ndev) {
-                gi[g].w = reinterpret_cast<const uint8_t*>(a.plan->tab[4][g]);
-                gi[g].s = reinterpret_cast<const float*>(a.plan->tab[5][g]);
-            } else {
-                gi[g].w = a.w[g - a.ndev];
-                gi[g].s = a.s[g - a.ndev];
-            }
-        }
-        // (a split-off last group is unweighted and has no route entry)
-        const bool routed = !(a.split_last && g == a.ngroups - 1);
-        gi[g].rw[m] = (a.route != nullptr && routed && m < a.mc) ? a.route[static_cast<int64_t>(a.g_base + g) * a.route_sg +
-                                                                 static_cast<int64_t>(a.m0 + m) * a.route_sm]
-                                                       : 1.0f;
-    }
-    __syncthreads();
-}
-
-// One pass of a combine-kernel wave over items [first, end) of the groups
-// from g_lo (item c: group g_lo + c / nbe, block c % nbe), items first,
-// first + nw, ..., U items' loads issued together.  acc += route(g, m) *
-// scale * D_g(block) . act_g,m; with zero_skip, an (item, activation row)
-// whose route is exactly 0 adds nothing (fp8_linear.cpp:630-747), and an
-// item no live row keeps is not loaded.
-template <int TT, int U, bool SAN, class Groups>
-__device__ __forceinline__ void combine_pass(const CombineArgs& a, const Groups& gi, int g_lo, int first, int end,
-                                             bool weighted, int64_t row0, int lane, int nw, plm_f32x4 (&acc)[TT]) {
-    const int li = lane & 15;
-    const int64_t lane_col = 64 * (li >> 3) + 16 * (lane >> 4);
-    const int xm = li & 7;
-    const bool xlive = xm < a.mc;
-    int64_t roff[TT];
-#pragma unroll
-    for (int t = 0; t < TT; ++t) roff[t] = min(row0 + 8 * t + (li & 7), a.rows - 1) * a.K + lane_col;
-    const int64_t srow = (row0 >> 7) * a.scale_cols;
-    for (int c0 = first; c0 < end; c0 += U * nw) {
-        plm_u32x4 q[U][TT];
-        XPiece<true> xh[U], xl[U];
-        float f[U];
-        bool keep[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int c = c0 + u * nw;
-            const int gl = c < end ? c / a.nbe : 0;
-            const int g = g_lo + gl;
-            const int64_t blk = c - gl * a.nbe;
-            const int64_t col = blk * 128;
-            const uint8_t* W = gi[g].w;
-            const float* S = gi[g].s;
-            const float rw = weighted ? gi[g].rw[xm] : 1.0f;
-            keep[u] = !(a.zero_skip && rw == 0.0f);
-            // the whole wave skips an item no live row keeps, or a group without weights
-            const bool item = c < end && W != nullptr && S != nullptr && __any(xlive && keep[u]);
-            const bool in = item && col + lane_col < a.K;
-#pragma unroll
-            for (int t = 0; t < TT; ++t) q[u][t] = in ? wload16(W + roff[t] + col) : plm_u32x4{0, 0, 0, 0};
-            const int64_t xo = (static_cast<int64_t>(a.g_base + g) * a.m_total + a.m0 + (xlive ? xm : 0)) * a.K +
-                               col + lane_col;
-            xh[u] = load_xpiece<true>(a.act_hi + xo, xlive && in);
-            xl[u] = load_xpiece<true>(a.act_lo + xo, xlive && in);
-            f[u] = item ? plm_gload_f32(S + srow + blk) * rw : 0.0f;
-            keep[u] = keep[u] && item;
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const BOperands<true, SAN> bh(xh[u]), bl(xl[u]);
-#pragma unroll
-            for (int t = 0; t < TT; ++t) {
-                plm_bf16x8 a0, a1;
-                weights_to_bf16(SAN ? zero_nan_bytes(q[u][t]) : q[u][t], a0, a1);
-                plm_f32x4 d = mfma_bf16(a0, bh.h0, plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-                d = mfma_bf16(a1, bh.h1, d);
-                d = mfma_bf16(a0, bl.h0, d);
-                d = mfma_bf16(a1, bl.h1, d);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[t][j] = keep[u] ? fmaf(d[j], f[u], acc[t][j]) : acc[t][j];
-            }
-        }
-    }
-}
-
-// A combine pass with its NaN redo.
-template <int TT, int U, class Groups>
-__device__ __forceinline__ void combine_items(const CombineArgs& a, const Groups& gi, int g_lo, int first, int end,
-                                              bool weighted, int64_t row0, int lane, int nw, plm_f32x4 (&acc)[TT]) {
-#pragma unroll
-    for (int t = 0; t < TT; ++t) acc[t] = plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    combine_pass<TT, U, false>(a, gi, g_lo, first, end, weighted, row0, lane, nw, acc);
-    if (any_nan(acc)) {
-#pragma unroll
-        for (int t = 0; t < TT; ++t) acc[t] = plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        combine_pass<TT, U, true>(a, gi, g_lo, first, end, weighted, row0, lane, nw, acc);
-    }
-}
-
-// Down phase of every MLP / MoE entry point: rows whose K range is the
-// concatenation of several groups' down matrices, each with its own
-// activations (the bf16 hi / lo planes of the SiLU intermediate) and route
-// weight.  Items (group, block) go to waves round robin; nw depends only on
-// the number of items.  FUSED (the device-routed MoE): one workgroup
-// computes both the routed sum and the split-off last group (the shared
-// expert) of its rows, each with the item-to-wave assignment of the split
-// tiles, and also writes the bf16 tail of the two when out_bf16 is set.
-template <int TT, int U, bool FUSED>
-__global__ __launch_bounds__(64 * kCombineWaves) void fp8_combine_kernel(const CombineArgs a) {
-    __shared__ float red[(FUSED ? 2 : 1) * kCombineWaves * TT * 64];
-    __shared__ GroupInfo gi[kMaxGroups + 1];  // the device-routed MoE: up to 64 chosen + the shared expert
-    const int nw = blockDim.x >> 6;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-    const int lane = threadIdx.x & 63;
-    int g_lo = 0;
-    int g_hi = a.ngroups;
-    int tile = blockIdx.x;
-    bool last = false;  // this workgroup computes the split-off last group
-    if (a.per_group_out) {
-        g_lo = tile / a.tiles_per_group;
-        g_hi = g_lo + 1;
-        tile -= g_lo * a.tiles_per_group;
-    } else if (a.split_last) {
-        g_hi = a.ngroups - 1;
-        if (!FUSED && tile >= a.tiles_per_group) {
-            tile -= a.tiles_per_group;
-            g_lo = g_hi;
-            g_hi = a.ngroups;
-            last = true;
-        }
-    }
-    const int64_t row0 = static_cast<int64_t>(tile) * 8 * TT;
-    // Device-chosen groups past the router's count are left out.  The items
-    // before them keep their wave assignment (item c goes to wave c % nw), so
-    // the sums are those of a call given just the chosen groups.
-    if (a.ndev > 0 && !last) g_hi = min(g_hi, a.plan->count);
-    stage_groups(a, gi);
-
-    plm_f32x4 acc[TT];
-    combine_items<TT, U>(a, gi, g_lo, wave, (g_hi - g_lo) * a.nbe, !last, row0, lane, nw, acc);
-    halves_to_lds(acc, red, wave, lane);
-    if constexpr (FUSED) {
-        // The split-off group in the same registers.  With fewer items than
-        // waves its items go, in order, to the last waves (those with the
-        // fewest routed items), one each: the wave sums then add the same
-        // values in the same order as a tile of its own (whose item c sits
-        // on wave c), the other waves adding exact zeros.
-        if (a.split_last) {
-            const int shift = nw > a.nbe ? nw - a.nbe : 0;
-            const int first = wave - shift;
-            if (first >= 0) {
-                combine_items<TT, U>(a, gi, a.ngroups - 1, first, a.nbe, false, row0, lane, nw, acc);
-            } else {
-#pragma unroll
-                for (int t = 0; t < TT; ++t) acc[t] = plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            }
-            halves_to_lds(acc, red, kCombineWaves + wave, lane);
-        }
-    }
-    __syncthreads();
-
-    for (int t = threadIdx.x; t < TT * 64; t += blockDim.x) {
-        const int tt = t >> 6, r = (t >> 3) & 7, m = t & 7;
-        const int64_t row = row0 + 8 * tt + r;
-        if (m >= a.mc || row >= a.rows) continue;
-        const int cell = tt * 64 + r * 8 + m;
-        float v = 0.0f;
-        for (int w = 0; w < nw; ++w) v += red[w * TT * 64 + cell];
-        int64_t o = static_cast<int64_t>(a.m0 + m) * a.rows + row;
-        if constexpr (FUSED) {
-            float v2 = 0.0f;
-            if (a.split_last) {
-                for (int w = 0; w < nw; ++w) v2 += red[(kCombineWaves + w) * TT * 64 + cell];
-                a.out_last[o] = v2;
-            }
-            a.out[o] = v;
-            if (a.out_bf16 != nullptr) a.out_bf16[o] = moe_bf16_tail(v, v2, a.split_last != 0);
-        } else {
-            if (a.per_group_out) o += static_cast<int64_t>(a.g_base + g_lo) * a.m_total * a.rows;
-            float* dst = last ? a.out_last : a.out;
-            dst[o] = a.accumulate ? dst[o] + v : v;
-        }
-    }
-}
-
 // ------------------------------------------------------------------ down phase, one workgroup per CU
 //
-// fp8_down_kernel computes what fp8_combine_kernel computes, laid out for the
-// 256 compute units of the part:
+// fp8_down_kernel, laid out for the 256 compute units of the part:
 //   * a workgroup of up to 16 waves owns rows_per_wg output rows (28 at
 //     7168 rows: 256 workgroups, each streaming the same bytes) in up to 4
-//     tiles of 8 rows.  Such a range may cross a 128-row scale block, so a
-//     lane takes the scale of its own accumulator rows (at most two scale
-//     rows per workgroup);
+//     tiles of 8 rows.  Tiles start at multiples of 8 (the first and last
+//     may be partial: rows outside the range are read again from its edge
+//     and dropped), so a tile never crosses a 128-row scale block and its
+//     scale is the same for the whole wave;
 //   * items (group, block) go to waves round robin, nw = min(16, items), and
 //     the wave sums are added in wave order: a row's arithmetic depends on
 //     the items alone, never on the batch, the row range or the grid;
@@ -1055,15 +859,6 @@ constexpr int kDownItemBytes = 512;    // one item's activations at one row: hi 
 constexpr int kDownStageItems = 12;    // STAGE: items per wave at most (6 KB of LDS per wave)
 constexpr int kDownStageLoads = kDownStageItems / 2;  // a wave load (1 KB) carries two items
 
-// The address as a value the compiler cannot see through, so a load from
-// "real or zero page" stays one unconditional load (it would otherwise
-// split it into branches, which make it wait for every load in flight).
-__device__ __forceinline__ const void* opaque_addr(bool use, const void* p, const void* alt) {
-    uint64_t v = reinterpret_cast<uint64_t>(use ? p : alt);
-    asm volatile("" : "+v"(v));
-    return reinterpret_cast<const void*>(v);
-}
-
 template <class T>
 __device__ __forceinline__ T* lane_ptr(T* p, int lane) {
     const uint64_t v = reinterpret_cast<uint64_t>(p);
@@ -1072,7 +867,40 @@ __device__ __forceinline__ T* lane_ptr(T* p, int lane) {
     return reinterpret_cast<T*>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-template <int TT, int P, bool STAGE, bool FUSED>
+// The address as a value the compiler cannot see through, so a load from
+// "real or zero page" stays one unconditional load (it would otherwise
+// split it into branches, which make it wait for every load in flight).
+__device__ __forceinline__ const void* opaque_addr(bool use, const void* p, const void* alt) {
+    uint64_t v = reinterpret_cast<uint64_t>(use ? p : alt);
+    asm("" : "+v"(v));  // touches no memory (not volatile), so uniform loads around it stay scalar
+    return reinterpret_cast<const void*>(v);
+}
+
+// The B operand of the down phase's matrix-core tiles.  Its 16 columns are
+// (plane p, half h', activation row m) = (n >> 3, (n >> 2) & 1, n & 3): the
+// hi and lo bf16 planes of the SiLU intermediate sit in columns of their own,
+// so one MFMA pair per tile covers both (the dot over plane p of weight row r
+// and row m, half h, is D[(r, h)][(p, h, m)]).  Four activation rows per
+// pass; rows 4-7 take a second pass with the same arithmetic.  Lane l reads
+// the 16 values at columns 64 h' + 16 (l >> 4) of plane p, row m.
+// Adds the four parts of each (weight row, activation row) of the lanes' D
+// tiles in one fixed order, ((hi, h 0) + (hi, h 1)) + ((lo, h 0) + (lo, h 1)),
+// and leaves tile t's sums in LDS: red[(slot * NT + t) * 64 + r * 8 + m].
+template <int NT>
+__device__ __forceinline__ void planes_to_lds(const plm_f32x4 (&acc)[NT], float* red, int slot, int lane, int mbase) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float v = acc[t][j];
+            const float hi = v + __shfl(v, (lane + 36) & 63);
+            const float lo = __shfl(v, (lane + 8) & 63) + __shfl(v, (lane + 44) & 63);
+            if (lane < 32 && (lane & 15) < 4)
+                red[(slot * NT + t) * 64 + (4 * (lane >> 4) + j) * 8 + mbase + (lane & 3)] = hi + lo;
+        }
+}
+
+template <int TT, int P, bool STAGE, bool FUSED, int MP>
 __global__ __launch_bounds__(64 * kDownWaves) void fp8_down_kernel(const CombineArgs a) {
     extern __shared__ plm_u32x4 stage4[];  // STAGE: per wave, its items' activations [item][hi, lo][128] bf16
     __shared__ float red[(FUSED ? 2 : 1) * kDownWaves * TT * 64];
@@ -1082,9 +910,11 @@ __global__ __launch_bounds__(64 * kDownWaves) void fp8_down_kernel(const Combine
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63;
     const int li = lane & 15;
+    // A: the lane's weight row (li & 7) and 16 bytes at column 64 (li >> 3) + 16 (lane >> 4) of the block
     const int64_t lane_col = 64 * (li >> 3) + 16 * (lane >> 4);
-    const int xm = li & 7;  // activation row of the lane's B column
-    const bool xlive = xm < a.mc;
+    // B: column li = (plane, half, activation row); the lane's 16 values at b_col of that plane and row
+    const int bplane = li >> 3, bm = li & 3;
+    const int64_t b_col = 64 * ((li >> 2) & 1) + 16 * (lane >> 4);
     const unsigned char* zero = a.zero;
 
     int g_lo = 0, g_hi = a.ngroups, tile = blockIdx.x;
@@ -1097,17 +927,16 @@ __global__ __launch_bounds__(64 * kDownWaves) void fp8_down_kernel(const Combine
     }
     const int64_t row0 = static_cast<int64_t>(tile) * a.rows_per_wg;
     const int64_t rend = min(row0 + a.rows_per_wg, a.rows);
-    int64_t roff[TT];  // rows past the range re-read the last one; their results are dropped
+    const int64_t base = row0 & ~int64_t(7);  // tile t holds rows base + 8t .. base + 8t + 7
+    int64_t roff[TT];  // rows outside [row0, rend) re-read its edge; their results are dropped
 #pragma unroll
-    for (int t = 0; t < TT; ++t) roff[t] = min(row0 + 8 * t + (li & 7), rend - 1) * a.K + lane_col;
+    for (int t = 0; t < TT; ++t) roff[t] = max(row0, min(base + 8 * t + (li & 7), rend - 1)) * a.K + lane_col;
+    // the range spans at most two 128-row scale blocks; tile t takes the second when its rows lie there
     const int64_t srow_a = (row0 >> 7) * a.scale_cols;
     const int64_t srow_b = ((rend - 1) >> 7) * a.scale_cols;
-    uint32_t sel_b = 0;  // bit 4t + j: accumulator j of tile t is a row of the second scale row
+    bool tile_b[TT];
 #pragma unroll
-    for (int t = 0; t < TT; ++t)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (((row0 + 8 * t + 4 * ((lane >> 4) & 1) + j) >> 7) != (row0 >> 7)) sel_b |= 1u << (4 * t + j);
+    for (int t = 0; t < TT; ++t) tile_b[t] = ((base + 8 * t) >> 7) != (row0 >> 7);
 
     // The shared group's items (FUSED): blocks s_first, s_first + nw, ...
     int s_first = 0, ns = 0;
@@ -1122,29 +951,35 @@ __global__ __launch_bounds__(64 * kDownWaves) void fp8_down_kernel(const Combine
     }
     int nr = 0;  // routed items of this wave (blocks wave, wave + nw, ... of the summed groups), once the plan is read
 
-    // STAGE: lane g holds group g's down matrix, scales and route weight.
+    // STAGE: lane g holds group g's down matrix, scales and route weight
+    // (read once by every wave at the start; items take them by readlane).
     const uint8_t* lw = nullptr;
     const float* lsc = nullptr;
     float lrw = 1.0f;
     unsigned char* region = reinterpret_cast<unsigned char*>(stage4) + static_cast<int64_t>(wave) * kDownStageItems * kDownItemBytes;
 
     // One pipeline slot: an item's weight tiles, its scales, its route
-    // weight, whether it counts, and where its activations are.
+    // weights, whether it counts, and where its activations are.
     struct Slot {
         plm_u32x4 q[TT];
-        float sv;  // lane 0: the scale of the first scale row, lane 1: of the second
-        float rw;  // the lane's route weight
-        bool keep;
-        int g;
-        int64_t blk;
-        int item;  // STAGE: the item's place in the wave's LDS region
-        XPiece<true> xh, xl;
+        float sv;      // lane 0: the scale of the first scale row, lane 1: of the second
+        float rw[MP];  // the route weight of the lane's activation row, per pass
+        bool keep[MP];
+        int item;      // STAGE: the item's place in the wave's LDS region
+        XPiece<true> x[MP];
     };
+    auto row_live = [&](int pass) { return bm + 4 * pass < a.mc; };
     auto issue_item = [&](Slot& sl, bool exists, int g, int64_t blk, int item, const uint8_t* W, const float* S,
-                          float rw) {
-        const bool keep_l = !(a.zero_skip && rw == 0.0f);
+                          const float (&rw)[MP]) {
+        bool any_keep = false;
+        bool keep_l[MP];
+#pragma unroll
+        for (int ps = 0; ps < MP; ++ps) {
+            keep_l[ps] = !(a.zero_skip && rw[ps] == 0.0f);
+            any_keep = any_keep || (row_live(ps) && keep_l[ps]);
+        }
         // the whole wave skips a missing item, one no live row keeps, or a group without weights
-        const bool live = exists && W != nullptr && S != nullptr && __any(xlive && keep_l);
+        const bool live = exists && W != nullptr && S != nullptr && __any(any_keep);
         const bool in = live && blk * 128 + lane_col < a.K;
         const int64_t col = blk * 128;
 #pragma unroll
@@ -1152,72 +987,96 @@ __global__ __launch_bounds__(64 * kDownWaves) void fp8_down_kernel(const Combine
         // lane 0 reads the scale of the first scale row, the others that of the
         // second (a vector load, counted in order with the weights)
         sl.sv = plm_gload_f32(opaque_addr(live, S + ((lane & 1) ? srow_b : srow_a) + blk, zero));
-        sl.rw = rw;
-        sl.keep = keep_l && live;
-        sl.g = g;
-        sl.blk = blk;
+#pragma unroll
+        for (int ps = 0; ps < MP; ++ps) {
+            sl.rw[ps] = rw[ps];
+            // at one activation row the route weight, hence keep, is the whole wave's
+            sl.keep[ps] = STAGE ? __builtin_amdgcn_readfirstlane(keep_l[ps] && live) != 0 : keep_l[ps] && live;
+        }
         sl.item = item;
         if constexpr (!STAGE) {
-            const int64_t xo =
-                (static_cast<int64_t>(a.g_base + g) * a.m_total + a.m0 + (xlive ? xm : 0)) * a.K + col + lane_col;
-            const bool xin = xlive && in;
+            const bool xin = live && blk * 128 + b_col < a.K;
+            const uint16_t* plane = bplane ? a.act_lo : a.act_hi;
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                sl.xh.v[i] = xload16(opaque_addr(xin, a.act_hi + xo + 8 * i, zero + 16 * i));
-                sl.xl.v[i] = xload16(opaque_addr(xin, a.act_lo + xo + 8 * i, zero + 16 * i));
+            for (int ps = 0; ps < MP; ++ps) {
+                const int m = bm + 4 * ps;
+                const int64_t xo =
+                    (static_cast<int64_t>(a.g_base + g) * a.m_total + a.m0 + (m < a.mc ? m : 0)) * a.K + col + b_col;
+                const bool ok = xin && m < a.mc;
+#pragma unroll
+                for (int i = 0; i < 2; ++i) sl.x[ps].v[i] = xload16(opaque_addr(ok, plane + xo + 8 * i, zero + 16 * i));
             }
         }
     };
     auto issue_s = [&](Slot& sl, int k) {
         const bool e = k < ns;
+        float rw[MP];
+#pragma unroll
+        for (int ps = 0; ps < MP; ++ps) rw[ps] = 1.0f;
         issue_item(sl, e, a.ngroups - 1, e ? s_first + static_cast<int64_t>(k) * nw : 0, k, e ? s_w : nullptr,
-                   e ? s_s : nullptr, 1.0f);
+                   e ? s_s : nullptr, rw);
     };
     auto issue_r = [&](Slot& sl, int k) {
         const bool e = k < nr;
         const int c = e ? wave + k * nw : 0;
         const int gl = c / a.nbe;
         const int g = g_lo + gl;
+        float rw[MP];
         if constexpr (STAGE) {
+            rw[0] = e ? lane_value(lrw, g) : 1.0f;
             issue_item(sl, e, g, c - gl * a.nbe, ns + k, e ? lane_ptr(lw, g) : nullptr, e ? lane_ptr(lsc, g) : nullptr,
-                       e ? lane_value(lrw, g) : 1.0f);
+                       rw);
         } else {
-            issue_item(sl, e, g, c - gl * a.nbe, ns + k, e ? gi[g].w : nullptr, e ? gi[g].s : nullptr,
-                       e ? gi[g].rw[xm] : 1.0f);
+#pragma unroll
+            for (int ps = 0; ps < MP; ++ps) rw[ps] = e ? gi[g].rw[bm + 4 * ps] : 1.0f;
+            issue_item(sl, e, g, c - gl * a.nbe, ns + k, e ? gi[g].w : nullptr, e ? gi[g].s : nullptr, rw);
         }
     };
-    auto accumulate = [&](Slot& sl, plm_f32x4 (&acc)[TT], auto san) {
+    auto accumulate = [&](Slot& sl, plm_f32x4 (&acc)[MP][TT], auto san) {
         constexpr bool SAN = decltype(san)::value;
         if constexpr (STAGE) {
-            const bool rd = xlive && sl.blk * 128 + lane_col < a.K;
-            const unsigned char* hs = region + sl.item * kDownItemBytes + 2 * lane_col;
+            if (!sl.keep[0]) return;
+            // every lane reads (the item's region is written in full; lanes of
+            // other activation rows feed B columns whose results are dropped)
+            const unsigned char* xs = region + sl.item * kDownItemBytes + bplane * 256 + 2 * b_col;
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                sl.xh.v[i] = rd ? *reinterpret_cast<const plm_u32x4*>(hs + 16 * i) : plm_u32x4{0, 0, 0, 0};
-                sl.xl.v[i] = rd ? *reinterpret_cast<const plm_u32x4*>(hs + 256 + 16 * i) : plm_u32x4{0, 0, 0, 0};
-            }
+            for (int i = 0; i < 2; ++i) sl.x[0].v[i] = *reinterpret_cast<const plm_u32x4*>(xs + 16 * i);
         }
-        const BOperands<true, SAN> bh(sl.xh), bl(sl.xl);
-        const float fa = lane_value(sl.sv, 0) * sl.rw;
-        const float fb = lane_value(sl.sv, 1) * sl.rw;
+        const float fa = lane_value(sl.sv, 0);
+        const float fb = lane_value(sl.sv, 1);
+        plm_bf16x8 a0[TT], a1[TT];
 #pragma unroll
-        for (int t = 0; t < TT; ++t) {
-            plm_bf16x8 a0, a1;
-            weights_to_bf16(SAN ? zero_nan_bytes(sl.q[t]) : sl.q[t], a0, a1);
-            plm_f32x4 d = mfma_bf16(a0, bh.h0, plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-            d = mfma_bf16(a1, bh.h1, d);
-            d = mfma_bf16(a0, bl.h0, d);
-            d = mfma_bf16(a1, bl.h1, d);
+        for (int t = 0; t < TT; ++t) weights_to_bf16(SAN ? zero_nan_bytes(sl.q[t]) : sl.q[t], a0[t], a1[t]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float f = ((sel_b >> (4 * t + j)) & 1u) ? fb : fa;
-                acc[t][j] = sl.keep ? fmaf(d[j], f, acc[t][j]) : acc[t][j];
+        for (int ps = 0; ps < MP; ++ps) {
+            plm_bf16x8 b0, b1;
+            if constexpr (SAN) {
+                // infinite or NaN activations as they are (the planes carry them in hi, lo = 0)
+                b0 = __builtin_bit_cast(plm_bf16x8, sl.x[ps].v[0]);
+                b1 = __builtin_bit_cast(plm_bf16x8, sl.x[ps].v[1]);
+            } else {
+                b0 = __builtin_bit_cast(plm_bf16x8, sl.x[ps].v[0]);
+                b1 = __builtin_bit_cast(plm_bf16x8, sl.x[ps].v[1]);
+            }
+            const float rwv = sl.rw[ps];
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                plm_f32x4 d = mfma_bf16(a0[t], b0, plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+                d = mfma_bf16(a1[t], b1, d);
+                const float f = (tile_b[t] ? fb : fa) * rwv;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if constexpr (STAGE)
+                        acc[ps][t][j] = fmaf(d[j], f, acc[ps][t][j]);
+                    else
+                        acc[ps][t][j] = sl.keep[ps] ? fmaf(d[j], f, acc[ps][t][j]) : acc[ps][t][j];
+                }
             }
         }
     };
 
     Slot ss, rs[P];  // the shared items' slot, the routed items' ring
-    plm_f32x4 acc[TT], acc_s[TT];
+    plm_f32x4 acc[MP][TT], acc_s[MP][TT];
     auto rings = [&](auto san) {
         // the shared items: the first was issued before the routed ring, so
         // waiting for it leaves the ring's loads in flight
@@ -1234,13 +1093,18 @@ __global__ __launch_bounds__(64 * kDownWaves) void fp8_down_kernel(const Combine
             }
         }
     };
+    auto zero_acc = [&]() {
 #pragma unroll
-    for (int t = 0; t < TT; ++t) acc[t] = acc_s[t] = plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int ps = 0; ps < MP; ++ps)
+#pragma unroll
+            for (int t = 0; t < TT; ++t) acc[ps][t] = acc_s[ps][t] = plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    };
+    zero_acc();
 
     if constexpr (STAGE) {
         // Loads in the order they are waited for: the groups' addresses and
         // route weights and the plan's count, the shared group's first item,
-        // the activations of the wave's items.
+        // the activations of the wave's items; then the routed ring.
         int count_v = kMaxGroups + 1;
         if (lane < a.ngroups) {
             if (lane < a.ndev) {
@@ -1258,6 +1122,8 @@ __global__ __launch_bounds__(64 * kDownWaves) void fp8_down_kernel(const Combine
         }
         if (lane == 0 && a.ndev > 0) count_v = a.plan->count;
         issue_s(ss, 0);
+        // the staging covers every item the groups could give this wave; the
+        // plan's count is known only once the loads above are back
         const int nr_all = wave < (g_hi - g_lo) * a.nbe ? ((g_hi - g_lo) * a.nbe - 1 - wave) / nw + 1 : 0;
         const int items = ns + nr_all;  // at most kDownStageItems (the host checks)
         plm_u32x4 xv[kDownStageLoads];
@@ -1321,26 +1187,30 @@ __global__ __launch_bounds__(64 * kDownWaves) void fp8_down_kernel(const Combine
     rings(std::false_type{});
     bool bad = false;
 #pragma unroll
-    for (int t = 0; t < TT; ++t)
+    for (int ps = 0; ps < MP; ++ps)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bad = bad || acc[t][j] != acc[t][j] || acc_s[t][j] != acc_s[t][j];
+        for (int t = 0; t < TT; ++t)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bad = bad || acc[ps][t][j] != acc[ps][t][j] || acc_s[ps][t][j] != acc_s[ps][t][j];
     if (__any(bad)) {
         // NaN weight bytes count as 0: the wave's items again, NaN bytes zeroed
-#pragma unroll
-        for (int t = 0; t < TT; ++t) acc[t] = acc_s[t] = plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        zero_acc();
         issue_s(ss, 0);
 #pragma unroll
         for (int u = 0; u < P; ++u) issue_r(rs[u], u);
         rings(std::true_type{});
     }
-    halves_to_lds(acc, red, wave, lane);
-    if constexpr (FUSED) halves_to_lds(acc_s, red, kDownWaves + wave, lane);
+#pragma unroll
+    for (int ps = 0; ps < MP; ++ps) {
+        planes_to_lds(acc[ps], red, wave, lane, 4 * ps);
+        if constexpr (FUSED) planes_to_lds(acc_s[ps], red, kDownWaves + wave, lane, 4 * ps);
+    }
     __syncthreads();
 
     for (int t = threadIdx.x; t < TT * 64; t += blockDim.x) {
         const int tt = t >> 6, r = (t >> 3) & 7, m = t & 7;
-        const int64_t row = row0 + 8 * tt + r;
-        if (m >= a.mc || row >= rend) continue;
+        const int64_t row = base + 8 * tt + r;
+        if (m >= a.mc || row < row0 || row >= rend) continue;
         float v = 0.0f;
         for (int w = 0; w < nw; ++w) v += red[w * TT * 64 + t];
         int64_t o = static_cast<int64_t>(a.m0 + m) * a.rows + row;
@@ -1633,31 +1503,6 @@ int combine_outputs(const CombineArgs& a) {
     return a.per_group_out ? a.ngroups : (a.split_last && !a.fused ? 2 : 1);
 }
 
-template <int TT, int U>
-void launch_combine_cfg(const CombineArgs& a, hipStream_t st) {
-    CombineArgs b = a;
-    const int tiles = static_cast<int>(plm::ceil_div(a.rows, 8 * TT));
-    b.tiles_per_group = tiles;
-    const int nw = static_cast<int>(
-        std::max<int64_t>(1, std::min<int64_t>(static_cast<int64_t>(combine_segments(a)) * a.nbe, kCombineWaves)));
-    const int64_t grid = static_cast<int64_t>(tiles) * combine_outputs(a);
-    if (a.fused) {
-        hipLaunchKernelGGL((fp8_combine_kernel<TT, U, true>), dim3(static_cast<unsigned>(grid)),
-                           dim3(nw * plm::kWave), 0, st, b);
-    } else {
-        hipLaunchKernelGGL((fp8_combine_kernel<TT, U, false>), dim3(static_cast<unsigned>(grid)),
-                           dim3(nw * plm::kWave), 0, st, b);
-    }
-}
-
-// The down phase as fp8_combine_kernel lays it out: 2 tiles per wave, 1 block
-// in flight.
-void launch_combine_tiles(const CombineArgs& a, int mcount, hipStream_t st) {
-    CombineArgs b = a;
-    b.mc = mcount;
-    launch_combine_cfg<2, 1>(b, st);
-}
-
 // The device address of down_zero_page on the current device (looked up the
 // first time a device asks, with that device current, and kept).
 int zero_page_address(const unsigned char** out) {
@@ -1697,21 +1542,21 @@ int allow_large_lds(const void* fn, int bytes) {
     return 0;
 }
 
-template <int TT, int P, bool STAGE, bool FUSED>
+template <int TT, int P, bool STAGE, bool FUSED, int MP>
 int launch_down_cfg(const CombineArgs& b, unsigned grid, int nw, size_t shmem, hipStream_t st) {
-    const void* fn = reinterpret_cast<const void*>(&fp8_down_kernel<TT, P, STAGE, FUSED>);
+    const void* fn = reinterpret_cast<const void*>(&fp8_down_kernel<TT, P, STAGE, FUSED, MP>);
     if (shmem > 0) {
         const int code = allow_large_lds(fn, kDownWaves * kDownStageItems * kDownItemBytes);
         if (code != 0) return code;
     }
-    hipLaunchKernelGGL((fp8_down_kernel<TT, P, STAGE, FUSED>), dim3(grid), dim3(nw * plm::kWave), shmem, st, b);
+    hipLaunchKernelGGL((fp8_down_kernel<TT, P, STAGE, FUSED, MP>), dim3(grid), dim3(nw * plm::kWave), shmem, st, b);
     return 0;
 }
 
-template <int TT, int P, bool STAGE>
+template <int TT, int P, bool STAGE, int MP>
 int launch_down_tt(const CombineArgs& b, unsigned grid, int nw, size_t shmem, hipStream_t st) {
-    return b.fused ? launch_down_cfg<TT, P, STAGE, true>(b, grid, nw, shmem, st)
-                   : launch_down_cfg<TT, P, STAGE, false>(b, grid, nw, shmem, st);
+    return b.fused ? launch_down_cfg<TT, P, STAGE, true, MP>(b, grid, nw, shmem, st)
+                   : launch_down_cfg<TT, P, STAGE, false, MP>(b, grid, nw, shmem, st);
 }
 
 // The down phase (fp8_down_kernel): rows per workgroup so that the grid
@@ -1725,8 +1570,11 @@ int launch_combine(const CombineArgs& a, int mcount, hipStream_t st) {
     const int zc = zero_page_address(&b.zero);
     if (zc != 0) return zc;
     const int outs = b.per_group_out ? b.ngroups : 1;
+    // activation rows 5-8 take a second pass of B columns (the same arithmetic
+    // per row) and hold twice the accumulators: at most 16 rows per workgroup
+    const int mp = mcount > 4 ? 2 : 1;
     int64_t per = plm::ceil_div(b.rows * outs, plm::cu_count());
-    per = std::min<int64_t>(kDownMaxRows, std::max<int64_t>(4, plm::ceil_div(per, 4) * 4));
+    per = std::min<int64_t>(mp == 2 ? 16 : kDownMaxRows, std::max<int64_t>(4, plm::ceil_div(per, 4) * 4));
     b.rows_per_wg = static_cast<int>(per);
     b.tiles_per_group = static_cast<int>(plm::ceil_div(b.rows, per));
     const int nw = static_cast<int>(
@@ -1745,15 +1593,20 @@ int launch_combine(const CombineArgs& a, int mcount, hipStream_t st) {
     // 28 rows one item per wave is in flight: 16 waves of 3.5 KB items keep
     // the memory system busy, and deeper rings were slower (the 9-expert
     // DeepSeek-V3 down phase 27.0 us with 1, 33.9 with 2).
-    const int tt = static_cast<int>(plm::ceil_div(per, 8));
+    // tiles start at multiples of 8: a range starting at 4 mod 8 takes one tile more
+    const int tt = static_cast<int>(plm::ceil_div(per + (per % 8), 8));
     if (stage) {
-        if (tt == 1) return launch_down_tt<1, 3, true>(b, grid, nw, shmem, st);
-        if (tt == 2) return launch_down_tt<2, 3, true>(b, grid, nw, shmem, st);
-        return launch_down_tt<4, 1, true>(b, grid, nw, shmem, st);
+        if (tt == 1) return launch_down_tt<1, 3, true, 1>(b, grid, nw, shmem, st);
+        if (tt == 2) return launch_down_tt<2, 3, true, 1>(b, grid, nw, shmem, st);
+        return launch_down_tt<4, 1, true, 1>(b, grid, nw, shmem, st);
     }
-    if (tt == 1) return launch_down_tt<1, 3, false>(b, grid, nw, shmem, st);
-    if (tt == 2) return launch_down_tt<2, 2, false>(b, grid, nw, shmem, st);
-    return launch_down_tt<4, 1, false>(b, grid, nw, shmem, st);
+    if (mp == 2) {
+        if (tt == 1) return launch_down_tt<1, 2, false, 2>(b, grid, nw, shmem, st);
+        return launch_down_tt<2, 1, false, 2>(b, grid, nw, shmem, st);
+    }
+    if (tt == 1) return launch_down_tt<1, 3, false, 1>(b, grid, nw, shmem, st);
+    if (tt == 2) return launch_down_tt<2, 2, false, 1>(b, grid, nw, shmem, st);
+    return launch_down_tt<4, 1, false, 1>(b, grid, nw, shmem, st);
 }
 
 // A GEMV problem over groups that share the activations.
