@@ -737,6 +737,30 @@ def table(args):
         del sets
         torch.cuda.empty_cache()
 
+    # ---- the o projection through the reference-ABI entry point, whose
+    # activations are fp32 (bf16 values widened, as the reference's wrapper
+    # passes them: src/pcketlm/native/__init__.py:3442-3476)
+    if want("fp8 o 7168x16384 (fp32 activations)"):
+        rows, cols = 7168, 16384
+        count = max(2, math.ceil(MALL_BYTES / (rows * cols)))
+        sets = fp8_sets(rows, cols, count)
+        host_w, host_s = sets[0][0].cpu().numpy(), sets[0][1].cpu().numpy()
+        for m in (1, 8):
+            x = torch.randn((m, cols), generator=gen, device="cuda").to(torch.bfloat16).float()
+            y = torch.empty((m, rows), device="cuda")
+            lib.pocketlm_set_stream(_stream_ptr(torch))
+
+            def make(sets=sets, x=x, y=y, m=m):
+                return [lambda w=w, s=s: lib.fp8_e4m3_block_linear_f32(
+                    ctypes.c_void_p(w.data_ptr()), ctypes.c_void_p(s.data_ptr()), ctypes.c_void_p(x.data_ptr()),
+                    ctypes.c_void_p(y.data_ptr()), m, rows, cols, cols // 128) for w, s in sets]
+
+            xh = x.cpu().numpy()
+            measure("fp8 o 7168x16384 (fp32 activations)", m, make, fp8_bytes(rows, cols, m) + 2 * m * cols,
+                    lambda w=host_w, s=host_s, xh=xh: oracle.fp8_linear(w, s, xh, batch_reuse=True))
+        del sets
+        torch.cuda.empty_cache()
+
     # ---- the o projection with its weight in 8-row tiles (packed once; the
     # same values as the row-major linear)
     if want("fp8 o 7168x16384 (8-row tiles)"):

@@ -528,6 +528,14 @@ int ds_route_topk_f32(const float* logits, const float* bias, int64_t batch, int
 int native_lm_head_topk_u16(const uint16_t* hidden, const uint16_t* weight, int64_t* out_ids, float* out_logits,
                             int64_t rows, int64_t hidden_size, int64_t top_k, int dtype_code, int64_t token_offset);
 
+/* fp16_matmul.cpp:344-396 (native_fp16_matmul): c = a @ b for fp16 (u16
+ * storage) a [m][k], b [k][n], c [m][n] (all device, row-major), fp32
+ * accumulation, c rounded to fp16 to nearest even.  The reference widens to
+ * fp32 and calls sgemm; the sums here run in another order (within 1 fp16
+ * ulp of the fp32 product rounded).  m or n = 0 writes nothing, k = 0 writes
+ * zeros.  Codes 1 null, 2 negative dims. */
+int native_fp16_matmul(const uint16_t* a, const uint16_t* b, uint16_t* c, int64_t m, int64_t n, int64_t k);
+
 /* ---------------------------------------------------------------- weight files to HBM */
 
 /* New export: byte ranges of a file copied into device memory (current

@@ -70,6 +70,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "fp8_e4m3_block_mlp_many_weighted_bf16x_f32": (_i32, [_vp] * 9 + [_i64] * 6),
     "fp8_e4m3_block_mlp_many_weighted_shared_bf16x_f32": (_i32, [_vp] * 10 + [_i64] * 6),
     "native_lm_head_topk_u16": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i64]),
+    "native_fp16_matmul": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64]),
     "pocketlm_file_spans_to_device": (_i32, [ctypes.c_char_p, _vp, _vp, _vp, _i64]),
     "row8_artifact_load_tensor": (_vp, [ctypes.c_char_p, ctypes.c_ulonglong, ctypes.c_ulonglong]),
     "row8_artifact_free_tensor": (None, [_vp]),

@@ -1,6 +1,7 @@
 // lm_head top-k (src/pcketlm/native/fp16_matmul.cpp:136-204): the logits of
 // one fp16/bf16 hidden vector against every row of a [rows, hidden] u16
-// weight, and the top_k of them with their row ids (+ token_offset).
+// weight, and the top_k of them with their row ids (+ token_offset); and the
+// same file's fp16 matmul (native_fp16_matmul, 344-396).
 //
 // The weight is the largest single read of a decode step (vocab x hidden, a
 // GB or two), so the GEMV streams it once at HBM rate:
@@ -197,9 +198,63 @@ __global__ __launch_bounds__(kTopkThreads) void topk_level_kernel(const float* _
     }
 }
 
+// C = A @ B in fp16 with fp32 accumulation (fp16_matmul.cpp:344-396: the
+// fp16 operands widened to fp32, an sgemm, the product rounded to fp16 to
+// nearest even).  One wave per 16 x 16 tile of C on the matrix cores: fp16
+// products are exact in fp32, so the result differs from the fp32 product
+// only in the order of the fp32 sums.  An operand of the rarely used
+// unquantized path, kept simple: elementwise bounds-checked loads.
+typedef _Float16 plm_f16x8 __attribute__((ext_vector_type(8)));
+typedef float plm_f32x4_mm __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void fp16_matmul_kernel(const uint16_t* __restrict__ a,
+                                                          const uint16_t* __restrict__ b, uint16_t* __restrict__ c,
+                                                          int64_t m, int64_t n, int64_t k, int64_t tiles_n,
+                                                          int64_t tiles) {
+    const int64_t tile = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (tile >= tiles) return;  // whole waves; no barrier below
+    const int lane = threadIdx.x & 63;
+    const int i = lane & 15, q = lane >> 4;
+    const int64_t tm = tile / tiles_n, tn = tile - tm * tiles_n;
+    const int64_t row = tm * 16 + i;  // A operand: row i, k = 8q .. 8q + 7 of each step
+    const int64_t col = tn * 16 + i;  // B operand: column i, the same k
+    plm_f32x4_mm acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int64_t k0 = 0; k0 < k; k0 += 32) {
+        plm_f16x8 av, bv;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int64_t kk = k0 + 8 * q + e;
+            const uint16_t x = row < m && kk < k ? a[row * k + kk] : uint16_t{0};
+            const uint16_t y = col < n && kk < k ? b[kk * n + col] : uint16_t{0};
+            av[e] = __builtin_bit_cast(_Float16, x);
+            bv[e] = __builtin_bit_cast(_Float16, y);
+        }
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
+    }
+    // D: column i, rows 4q .. 4q + 3
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t r = tm * 16 + 4 * q + j;
+        if (r < m && col < n) c[r * n + col] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(acc[j]));
+    }
+}
+
 }  // namespace
 
 // ====================================================================== C ABI
+
+PLM_EXPORT int native_fp16_matmul(const uint16_t* a, const uint16_t* b, uint16_t* c, int64_t m, int64_t n,
+                                  int64_t k) {
+    if (!a || !b || !c) return plm::fail(1, "null pointer");
+    if (m < 0 || n < 0 || k < 0) return plm::fail(2, "bad dimensions");
+    if (m == 0 || n == 0) return 0;
+    const int64_t tiles_n = plm::ceil_div(n, 16);
+    const int64_t tiles = plm::ceil_div(m, 16) * tiles_n;
+    if (plm::ceil_div(tiles, 4) > INT32_MAX) return plm::fail(2, "too many tiles");
+    hipLaunchKernelGGL(fp16_matmul_kernel, dim3(static_cast<unsigned>(plm::ceil_div(tiles, 4))), dim3(256), 0,
+                       plm::current_stream(), a, b, c, m, n, k, tiles_n, tiles);
+    return plm::check_launch("fp16 matmul kernel");
+}
 
 PLM_EXPORT int native_lm_head_topk_u16(const uint16_t* hidden, const uint16_t* weight, int64_t* out_ids,
                                        float* out_logits, int64_t rows, int64_t hidden_size, int64_t top_k,

@@ -1448,6 +1448,29 @@ def native_lm_head_topk_available() -> bool:
     return _available("PCKETLM_DISABLE_NATIVE_MATMUL")
 
 
+native_fp16_matmul_available = native_lm_head_topk_available
+
+
+def fp16_matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """src/pcketlm/native/__init__.py:2226-2249 -> fp16_matmul.cpp:344-396:
+    a [m, k] @ b [k, n] in fp16 with fp32 accumulation, rounded to fp16."""
+    lib = _require("PCKETLM_DISABLE_NATIVE_MATMUL", "Native fp16 matmul")
+    if a.dtype != torch.float16 or b.dtype != torch.float16:
+        raise TypeError("fp16_matmul requires torch.float16 inputs")
+    if a.ndim != 2 or b.ndim != 2:
+        raise ValueError("fp16_matmul requires 2D matrices")
+    if int(a.shape[1]) != int(b.shape[0]):
+        raise ValueError("fp16_matmul input shapes are incompatible")
+    dev = _target_device(a, b)
+    ad, bd = _on(a, dev), _on(b, dev)
+    m, k, n = int(ad.shape[0]), int(ad.shape[1]), int(bd.shape[1])
+    out = torch.empty((m, n), dtype=torch.float16, device=dev)
+    with _launch(lib, dev):
+        code = lib.native_fp16_matmul(_p(ad), _p(bd), _p(out), m, n, k)
+    _check("native_fp16_matmul", code)
+    return _home(out, a)
+
+
 def lm_head_topk_u16(hidden: torch.Tensor, weight: torch.Tensor, *, top_k: int,
                      token_offset: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
     """src/pcketlm/native/__init__.py:2283-2323 -> fp16_matmul.cpp:155-204:

@@ -123,6 +123,11 @@ def test_kill_switches(monkeypatch):
     monkeypatch.setenv("PCKETLM_DISABLE_NATIVE_FP8_DEQUANT", "on")
     with pytest.raises(RuntimeError, match="unavailable: disabled"):
         native.fp8_e4m3_dequant_to_fp16(torch.zeros((4, 4), dtype=torch.uint8), torch.ones((1, 1)))
+    # tests/test_native_fp16_matmul.py:30-39
+    monkeypatch.setenv("PCKETLM_DISABLE_NATIVE_MATMUL", "1")
+    assert native.native_fp16_matmul_available() is False
+    with pytest.raises(RuntimeError, match="unavailable"):
+        native.fp16_matmul(torch.ones((1, 1), dtype=torch.float16), torch.ones((1, 1), dtype=torch.float16))
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the behaviour without a device")

@@ -61,6 +61,9 @@ REFERENCE_LOADERS = {
         ("ds_forward_verify_f32", 6, 663),
         ("ds_moe_layer_forward_fp8_f32", 16, 719),
     ],
+    "_load_fp16_matmul_lib (1573-1581)": [
+        ("native_fp16_matmul", 6, 1573),
+    ],
     "_load_fp16_packed_gemv_lib (1634-1649)": [
         ("native_pack_u16_rows8", 4, 1634),
         ("native_packed_gemv_rows8", 6, 1641),
@@ -235,6 +238,7 @@ def test_ds_callback_bridges_argument_and_callback_codes(lib):
     lib.ds_session_destroy(h)
 
 
+@pytest.mark.gpu
 def test_rowmajor_kv_entry_points_are_documented_not_implemented(lib):
     """kv_attention_decode_* / kv_dense_layer_decode_{fp16,u16_ext}: the
     reference's argument codes, then 90 with the reason."""
