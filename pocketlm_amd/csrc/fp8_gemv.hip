@@ -265,12 +265,14 @@ __device__ __forceinline__ void route_plan_body(const float* __restrict__ logits
         __shared__ uint64_t picked[kMaxM][64];       // [row][lane]: bits of the lane's picked experts
         uint64_t tab[kPlanRoles][4];
         if (wave == 0) {
+            // unconditional loads (rows past the table read its last entry)
 #pragma unroll
             for (int r = 0; r < kPlanRoles; ++r)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int e = 4 * lane + j;
-                    tab[r][j] = e < experts ? table[static_cast<int64_t>(r) * experts + e] : 0;
+                    const uint64_t v = table[static_cast<int64_t>(r) * experts + min(e, experts - 1)];
+                    tab[r][j] = e < experts ? v : 0;
                 }
         }
         for (int m = wave; m < batch; m += waves)

@@ -159,10 +159,11 @@ __host__ __device__ constexpr int plm_route_j(int experts) { return experts <= 2
 // taken, the lowest id among equals; without NaNs that is the order of the
 // choices, larger first, lower id first among equals.
 template <int J>
-__device__ void plm_route_wave(const float* __restrict__ lrow, const float* __restrict__ bias, int experts,
-                               int top_k, int n_groups, int topk_groups, int scoring, float route_scale, float* score,
-                               float* choice, RouteWave& rw, int64_t* idx, float* w, uint64_t* taken_out = nullptr,
-                               float* wdense = nullptr) {
+__device__ __forceinline__ void plm_route_wave_generic(const float* __restrict__ lrow, const float* __restrict__ bias,
+                                                       int experts, int top_k, int n_groups, int topk_groups,
+                                                       int scoring, float route_scale, float* score, float* choice,
+                                                       RouteWave& rw, int64_t* idx, float* w, uint64_t* taken_out,
+                                                       float* wdense) {
     static_assert(J % 4 == 0 && J <= 64, "J experts per lane, a multiple of 4, at most 64");
     const int lane = static_cast<int>(threadIdx.x & 63);
     const int e0 = lane * J;
@@ -436,4 +437,157 @@ __device__ void plm_route_wave(const float* __restrict__ lrow, const float* __re
             w[i] = plm_bf16_round(v * route_scale);
         }
     plm_wave_sync();
+}
+
+// The same routing for the common case, in registers and without LDS:
+// 4 experts per lane (at most 256), a multiple of 4 of them, 16-byte aligned
+// logits and bias, sigmoid scores, and either no groups or groups of whole
+// lanes.  Returns false, having written nothing, when the row falls outside
+// that case or holds a NaN choice or group score; the caller then runs the
+// general version.  The arithmetic is the general version's, step for step
+// (the same scores, group ranks, pick rounds, sum order and weight rounding),
+// so the two agree bit for bit wherever this one applies.
+__device__ __forceinline__ bool plm_route_wave4_fast(const float* __restrict__ lrow, const float* __restrict__ bias,
+                                                     int experts, int top_k, int n_groups, int topk_groups,
+                                                     int scoring, float route_scale, int64_t* idx, float* w,
+                                                     uint64_t* taken_out, float* wdense) {
+    constexpr int J = 4;
+    const int lane = static_cast<int>(threadIdx.x & 63);
+    const int e0 = lane * J;
+    const float ninf = -__builtin_inff();
+    if (scoring != 0 || experts > 64 * J || (experts & 3) != 0 || top_k > 64 || (reinterpret_cast<uintptr_t>(lrow) & 15) != 0 ||
+        (bias != nullptr && (reinterpret_cast<uintptr_t>(bias) & 15) != 0))
+        return false;
+    const int gsz = n_groups > 1 ? experts / n_groups : experts;
+    const int lg = gsz / J;
+    if (n_groups > 1 && !(gsz % J == 0 && (lg == 1 || lg == 2 || lg == 4 || lg == 8 || lg == 16))) return false;
+    const bool own = e0 < experts;
+    const float4 xv = *reinterpret_cast<const float4*>(lrow + (own ? e0 : 0));
+    const float4 bv = bias != nullptr ? *reinterpret_cast<const float4*>(bias + (own ? e0 : 0))
+                                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float x[4] = {own ? xv.x : 0.0f, own ? xv.y : 0.0f, own ? xv.z : 0.0f, own ? xv.w : 0.0f};
+    const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
+    float sv[J], cv[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        sv[j] = 1.0f / (1.0f + expf(-x[j]));
+        cv[j] = sv[j];
+    }
+    if (bias != nullptr && own) {
+#pragma unroll
+        for (int j = 0; j < J; ++j) cv[j] += bb[j];
+    }
+    bool nan = false;
+#pragma unroll
+    for (int j = 0; j < J; ++j) nan = nan || (own && cv[j] != cv[j]);
+    if (__ballot(nan) != 0) return false;
+    if (n_groups > 1) {
+        float b1 = ninf, b2 = ninf;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const float v = cv[j];
+            const bool gt1 = v > b1, gt2 = v > b2;
+            b2 = gt1 ? b1 : (gt2 ? v : b2);
+            b1 = gt1 ? v : b1;
+        }
+        if (lg >= 2) plm_top2_step<0xB1>(b1, b2);
+        if (lg >= 4) plm_top2_step<0x4E>(b1, b2);
+        if (lg >= 8) plm_top2_step<0x141>(b1, b2);
+        if (lg >= 16) plm_top2_step<0x140>(b1, b2);
+        const float mine = bias != nullptr ? b1 + b2 : b1;
+        const float gs = __shfl(mine, (lane * lg) & 63);
+        if (__ballot(lane < n_groups && gs != gs) != 0) return false;
+        const int kg = topk_groups < 1 ? 1 : (topk_groups > n_groups ? n_groups : topk_groups);
+        int r = 0;
+        for (int h = 0; h < n_groups; ++h) {
+            const float o = __uint_as_float(plm_readlane(__float_as_uint(mine), h * lg));
+            r += o > gs || (o == gs && h < lane);
+        }
+        const uint64_t keep = __ballot(lane < n_groups && r < kg);
+        const int g = lane / lg;
+        if (!(g < n_groups && ((keep >> g) & 1ull))) {
+#pragma unroll
+            for (int j = 0; j < J; ++j) cv[j] = ninf;
+        }
+    }
+    const int k = top_k < 1 ? 1 : (top_k > experts ? experts : top_k);
+    uint32_t key[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) key[j] = own ? plm_order_key(cv[j]) : 0u;
+    uint64_t taken = 0;
+    int my_pick = 0;
+    float my_s = 0.0f, sum = 0.0f;
+    for (int i = 0; i < k; ++i) {
+        uint32_t bo = key[0];
+        int bj = 0;
+        float bs = sv[0];
+#pragma unroll
+        for (int j = 1; j < J; ++j) {
+            const bool better = key[j] > bo;
+            bo = better ? key[j] : bo;
+            bj = better ? j : bj;
+            bs = better ? sv[j] : bs;
+        }
+        const uint32_t top = plm_wave_max_u32(bo);
+        const uint64_t hit = __ballot(top != 0 && bo == top);
+        const int owner = hit != 0 ? static_cast<int>(__builtin_ctzll(hit)) : 0;
+        const int pick = static_cast<int>(plm_readlane(static_cast<uint32_t>(e0 + bj), owner));
+        const float s = __uint_as_float(plm_readlane(__float_as_uint(bs), owner));
+        if (lane == owner) {
+            taken |= 1ull << bj;
+#pragma unroll
+            for (int j = 0; j < J; ++j) key[j] = j == bj ? 0u : key[j];
+        }
+        my_pick = lane == i ? pick : my_pick;
+        my_s = lane == i ? s : my_s;
+        sum += s;
+    }
+    const float denom = sum > 1e-12f ? sum : 1e-12f;
+    if (taken_out != nullptr) {
+        taken_out[lane] = taken;
+        if (own) {
+            float4 v;
+            float* vp = reinterpret_cast<float*>(&v);
+#pragma unroll
+            for (int j = 0; j < J; ++j) vp[j] = ((taken >> j) & 1ull) ? plm_bf16_round((sv[j] / denom) * route_scale) : 0.0f;
+            *reinterpret_cast<float4*>(wdense + e0) = v;
+        }
+    }
+    if (idx != nullptr && lane < k) {
+        idx[lane] = my_pick;
+        w[lane] = plm_bf16_round((my_s / denom) * route_scale);
+    }
+    plm_wave_sync();
+    return true;
+}
+
+// The general version out of line: the common case stays a short stretch
+// of straight-line code.
+template <int J>
+__device__ __noinline__ void plm_route_wave_cold(const float* __restrict__ lrow, const float* __restrict__ bias,
+                                                 int experts, int top_k, int n_groups, int topk_groups, int scoring,
+                                                 float route_scale, float* score, float* choice, RouteWave& rw,
+                                                 int64_t* idx, float* w, uint64_t* taken_out, float* wdense) {
+    plm_route_wave_generic<J>(lrow, bias, experts, top_k, n_groups, topk_groups, scoring, route_scale, score, choice,
+                              rw, idx, w, taken_out, wdense);
+}
+
+// Routes one row: the register version where it applies (4 experts per
+// lane), else the general one.  Arguments as plm_route_wave_generic's.
+template <int J>
+__device__ __forceinline__ void plm_route_wave(const float* __restrict__ lrow, const float* __restrict__ bias,
+                                               int experts, int top_k, int n_groups, int topk_groups, int scoring,
+                                               float route_scale, float* score, float* choice, RouteWave& rw,
+                                               int64_t* idx, float* w, uint64_t* taken_out = nullptr,
+                                               float* wdense = nullptr) {
+    if constexpr (J == 4) {
+        if (plm_route_wave4_fast(lrow, bias, experts, top_k, n_groups, topk_groups, scoring, route_scale, idx, w,
+                                 taken_out, wdense))
+            return;
+        plm_route_wave_cold<4>(lrow, bias, experts, top_k, n_groups, topk_groups, scoring, route_scale, score, choice,
+                               rw, idx, w, taken_out, wdense);
+    } else {
+        plm_route_wave_generic<J>(lrow, bias, experts, top_k, n_groups, topk_groups, scoring, route_scale, score,
+                                  choice, rw, idx, w, taken_out, wdense);
+    }
 }

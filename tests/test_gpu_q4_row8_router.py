@@ -310,6 +310,35 @@ def test_deepseek_route_widths_against_oracle(nat, oracle_mod, experts, groups, 
                 assert np.allclose(host(w.float()), ow, rtol=8e-3), (rows, b is None, scoring)
 
 
+@pytest.mark.parametrize("experts,groups,kept,top_k", [
+    (256, 8, 4, 8), (256, 4, 2, 8), (256, 1, 1, 8), (64, 8, 2, 6), (64, 16, 5, 7), (32, 2, 1, 4),
+])
+def test_register_router_equals_general_router(nat, experts, groups, kept, top_k):
+    """The register version of the 4-experts-per-lane router (16-byte
+    aligned logits) and the general version (the same logits one float off
+    that alignment) give the same indices and weight bits, with ties,
+    infinite logits, a bias and batches."""
+    rng = np.random.default_rng(experts * 100 + groups)
+    for rows in (1, 7):
+        logits = (rng.standard_normal((rows, experts)) * 3).astype(np.float32)
+        logits[:, 5::9] = logits[:, 2:3]  # ties
+        logits[0, 3] = np.inf
+        logits[-1, 7] = -np.inf
+        bias = (rng.standard_normal(experts) * 0.1).astype(np.float32)
+        for b in (None, bias):
+            aligned = dev(logits)
+            buf = torch.zeros(rows * experts + 1, device="cuda")
+            buf[1:] = aligned.reshape(-1)
+            shifted = buf[1:].view(rows, experts)
+            assert aligned.data_ptr() % 16 == 0 and shifted.data_ptr() % 16 != 0
+            kw = dict(top_k=top_k, n_groups=groups, topk_groups=kept, bias=None if b is None else dev(b),
+                      weights_dtype=torch.float32)
+            ia, wa = nat.route_deepseek(aligned, **kw)
+            ib, wb = nat.route_deepseek(shifted, **kw)
+            assert torch.equal(ia, ib), (rows, b is None)
+            assert torch.equal(wa.view(torch.int32), wb.view(torch.int32)), (rows, b is None)
+
+
 def _route_in_order(logits, top_k, n_groups, topk_groups, bias, scale):
     """The routing as one in-order scan per step (strict > keeps the first
     of equal values; a NaN is kept only when it is where a scan starts)."""
