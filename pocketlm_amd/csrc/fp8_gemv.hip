@@ -680,6 +680,22 @@ __device__ __forceinline__ void rows_pass(const RowsArgs& a, const uint8_t* cons
     }
 }
 
+// Makes uniform values opaque to the compiler (touches no memory): the
+// loads that produce them are issued together where they are pinned, one
+// round trip, where a branch on each loaded value would cost one each.
+__device__ __forceinline__ void pin_one(int& v) { asm("" : "+s"(v)); }
+__device__ __forceinline__ void pin_one(int64_t& v) { asm("" : "+s"(v)); }
+template <class T>
+__device__ __forceinline__ void pin_one(T*& p) {
+    uint64_t v = reinterpret_cast<uint64_t>(p);
+    asm("" : "+s"(v));
+    p = reinterpret_cast<T*>(v);
+}
+template <class... T>
+__device__ __forceinline__ void pin_scalar(T&... v) {
+    (pin_one(v), ...);
+}
+
 // Rows of one or more weights sharing the activations (linear, dual, the
 // gate/up phase with its SiLU epilogue, weights of different row counts in
 // one grid).  A workgroup owns TT tiles (8 TT rows) of each of its NWT
@@ -690,20 +706,33 @@ template <int TT, int U, bool BURST, int NWT, bool SILU, bool XB>
 __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int block) {
     constexpr int NT = NWT * TT;
     __shared__ float red[kMaxWaves * NT * 64];
-    const int nw = blockDim.x >> 6;
+    // the arguments of the prologue and of the loop, read at once
+    int nw = blockDim.x >> 6, tpg = a.tiles_per_group, nvar = a.nvar, mc = a.mc, m0 = a.m0, nb = a.nblocks;
+    int tiled = a.tiled;
+    int64_t rows = a.rows, K = a.K, scale_cols = a.scale_cols, x_stride = a.x_stride;
+    const char* xbase = XB ? reinterpret_cast<const char*>(a.xb) : reinterpret_cast<const char*>(a.x);
+    const uint8_t* w0[NWT];
+    const float* s0[NWT];
+#pragma unroll
+    for (int i = 0; i < NWT; ++i) {
+        w0[i] = a.w[i][0];
+        s0[i] = a.s[i][0];
+        pin_scalar(w0[i], s0[i]);
+    }
+    pin_scalar(nw, tpg, nvar, mc, m0, nb, tiled, rows, K, scale_cols, x_stride, xbase);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63;
     int g;
-    int64_t row0, rows = a.rows;
-    if (a.nvar > 0) {
+    int64_t row0;
+    if (nvar > 0) {
         g = 0;
         for (int i = 1; i < a.nvar; ++i)
             if (block >= a.vtile[i]) g = i;
         row0 = static_cast<int64_t>(block - a.vtile[g]) * 8 * TT;
         rows = a.vrows[g];
     } else {
-        g = block / a.tiles_per_group;
-        row0 = static_cast<int64_t>(block - g * a.tiles_per_group) * 8 * TT;
+        g = block / tpg;
+        row0 = static_cast<int64_t>(block - g * tpg) * 8 * TT;
     }
 
     const uint8_t* W[NWT];
@@ -721,7 +750,14 @@ __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int block) {
         }
         ga = g - a.ndev;
     }
-    if (ga >= 0) {
+    if (ga == 0) {
+        // the first argument slot came with the other arguments
+#pragma unroll
+        for (int i = 0; i < NWT; ++i) {
+            W[i] = w0[i];
+            S[i] = s0[i];
+        }
+    } else if (ga > 0) {
 #pragma unroll
         for (int i = 0; i < NWT; ++i) {
             W[i] = a.w[i][ga];
@@ -735,7 +771,7 @@ __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int block) {
     const int li = lane & 15;
     const int64_t lane_col = 64 * (li >> 3) + 16 * (lane >> 4);
     const int xm = li & 7;  // activation row of this lane's B column
-    const bool xlive = xm < a.mc;
+    const bool xlive = xm < mc;
     plm_f32x4 acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = plm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -745,16 +781,16 @@ __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int block) {
         const float* sp[NWT];
 #pragma unroll
         for (int i = 0; i < NWT; ++i) {
-            sp[i] = S[i] + (row0 >> 7) * a.scale_cols;
+            sp[i] = S[i] + (row0 >> 7) * scale_cols;
 #pragma unroll
             for (int t = 0; t < TT; ++t) {
                 // rows past the end read the last row; their results are dropped
                 const int64_t r = min(row0 + 8 * t + (li & 7), rows - 1);
-                wrow[i * TT + t] = a.tiled ? W[i] + ((r >> 3) * a.nblocks * 1024 + (r & 7) * 128) : W[i] + r * a.K;
+                wrow[i * TT + t] = tiled ? W[i] + ((r >> 3) * nb * 1024 + (r & 7) * 128) : W[i] + r * K;
             }
         }
-        const int64_t xo = static_cast<int64_t>(a.m0 + (xlive ? xm : 0)) * a.x_stride;
-        const char* xrow = XB ? reinterpret_cast<const char*>(a.xb + xo) : reinterpret_cast<const char*>(a.x + xo);
+        const int64_t xo = static_cast<int64_t>(m0 + (xlive ? xm : 0)) * x_stride;
+        const char* xrow = xbase + xo * (XB ? 2 : 4);
         auto pass = [&](auto san) {
             constexpr bool SAN = decltype(san)::value;
             if constexpr (BURST)
