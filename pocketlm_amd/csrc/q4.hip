@@ -498,17 +498,36 @@ __global__ __launch_bounds__(NWS * 64) void q4_down_kernel(const Q4CombineArgs a
             }
             ch = cl = plm_f4{0.0f, 0.0f, 0.0f, 0.0f};
         };
+        // Two items in flight: the next item's weights and B values are read
+        // before the current one is computed (an item past the last re-reads
+        // the current one's addresses; its values are not used).
         const uint4* pg = a.planes + static_cast<int64_t>(gl) * a.planes_stride;
-        bool first = true;
-        while (g < ng) {
-            if (!first) load_w(s);
-            first = false;
-            const bool ok = static_cast<int64_t>(s) * kStepBytes + piece * 16 < row_bytes;
-            const uint4* bp = pg + static_cast<int64_t>(s) * 128 + piece;
-            uint4 bv[8];
+        uint4 bv[8];
+        auto load_b = [&](const uint4* pgx, int step, uint4 (&dst)[8]) {
+            const uint4* bp = pgx + static_cast<int64_t>(step) * 128 + piece;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) bv[k] = bp[k * 16];
-            pin_w();
+            for (int k = 0; k < 8; ++k) dst[k] = bp[k * 16];
+        };
+        load_b(pg, g < ng ? s : steps - 1, bv);
+        while (g < ng) {
+            int gn = g, sn = s;
+            sn += NWS;
+            while (sn >= steps) {
+                sn -= steps;
+                ++gn;
+            }
+            const int gq = gn < ng ? gn : g, sq = gn < ng ? sn : s;
+            const uint8_t* wn = a.w[gq];
+            const uint4* pn = a.planes + static_cast<int64_t>(gq) * a.planes_stride;
+            uint4 qn[TR], bn[8];
+            {
+                const int64_t byte = static_cast<int64_t>(sq) * kStepBytes + piece * 16;
+                const int64_t bc = byte < row_bytes ? byte : row_bytes - 16;
+#pragma unroll
+                for (int t = 0; t < TR; ++t) qn[t] = *reinterpret_cast<const uint4*>(wn + roff[t] + bc);
+            }
+            load_b(pn, sq, bn);
+            const bool ok = static_cast<int64_t>(s) * kStepBytes + piece * 16 < row_bytes;
             if (!ok) {
 #pragma unroll
                 for (int k = 0; k < 8; ++k) bv[k] = make_uint4(0u, 0u, 0u, 0u);
@@ -527,15 +546,13 @@ __global__ __launch_bounds__(NWS * 64) void q4_down_kernel(const Q4CombineArgs a
                     al[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bl, al[t], 0, 0, 0);
                 }
             }
-            const int gprev = g;
-            advance();
-            if (g != gprev) {
-                fold(gprev);
-                if (g < ng) {
-                    wg = a.w[g];
-                    pg = a.planes + static_cast<int64_t>(g) * a.planes_stride;
-                }
-            }
+            if (gn != g) fold(g);
+            g = gn;
+            s = sn;
+#pragma unroll
+            for (int t = 0; t < TR; ++t) q[t] = qn[t];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) bv[k] = bn[k];
         }
         // the diagonal elements of row group c sit in the quad 20c .. 20c + 3
 #pragma unroll
