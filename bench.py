@@ -363,6 +363,18 @@ def _ref_lib():
     return lib
 
 
+def _ref_row8_lib():
+    """The reference's fp16_packed_gemv.cpp built from its source (oracle/_ref), or None."""
+    path = REPO / "oracle" / "_ref" / "libref_fp16_packed_gemv.so"
+    if not path.exists():
+        return None
+    lib = ctypes.CDLL(str(path))
+    vp, i64 = ctypes.c_void_p, ctypes.c_longlong
+    lib.native_packed_gemv_rows8.argtypes = [vp, vp, vp, i64, i64, ctypes.c_int]
+    lib.native_packed_gemv_rows8.restype = ctypes.c_int
+    return lib
+
+
 def _omp():
     """The OpenMP runtime the reference build links (to set its thread count)."""
     gomp = ctypes.CDLL("libgomp.so.1")
@@ -485,16 +497,18 @@ def cpu_verifier_baseline(seconds_each=2.0):
 
 def _traffic(workload):
     """HBM bytes per step from the committed counter runs (FETCH_SIZE and
-    WRITE_SIZE scaled by a plain copy's reading; profiles/traffic.json), or
-    None when they are absent."""
+    WRITE_SIZE scaled by a plain copy's reading; profiles/traffic.json) and
+    where they come from, or (None, None) when they are absent.  The counters
+    are not read live: they need runs of their own under rocprofv3."""
     f = REPO / "profiles" / "traffic.json"
     if not f.exists():
-        return None
+        return None, None
     try:
         entry = json.loads(f.read_text()).get(workload) or {}
-        return entry.get("bytes_per_step")
+        src = f"profiles/traffic.json[{workload!r}]: " + (entry.get("source") or "?")
+        return entry.get("bytes_per_step"), src
     except (OSError, ValueError, AttributeError):
-        return None
+        return None, None
 
 
 def main_line(args):
@@ -512,17 +526,19 @@ def main_line(args):
     value = moe_step_bytes(1) / (ms / 1e3) / 1e9
     moe_ms = r["ms_per_moe"]
     achieved = moe_layer_bytes(1) / (moe_ms / 1e3) / 1e9
+    traffic, traffic_src = _traffic("moe_layer")
     roof = {
         "bound": "hbm",
         "kernel": "the MoE layer's launches of fp8_e4m3_block_moe_device_routed_bf16x_f32: moe_plan_kernel, "
-                  "fp8_rows_kernel (gate/up + SiLU, 8 chosen + shared expert), fp8_combine_kernel (down, "
+                  "fp8_rows_kernel (gate/up + SiLU, 8 chosen + shared expert), fp8_down_kernel (down, "
                   "route-weighted sum, shared expert, bf16 output)",
         "achieved": round(achieved, 2),
         "peak": PEAK_HBM_GBS,
         "unit": "GB/s",
         "frac": round(achieved / PEAK_HBM_GBS, 4),
-        "traffic": _traffic("moe_layer"),
+        "traffic": traffic,
         "traffic_unit": "HBM bytes per MoE layer call (all its launches)",
+        "traffic_source": traffic_src,
         "us_per_launch_group": round(1e3 * moe_ms, 3),
         "bytes_per_launch_group": moe_layer_bytes(1),
     }
@@ -666,7 +682,26 @@ def table(args):
     def want(*names):
         return not only or any(t in n for n in names for t in only)
 
-    def measure(name, m, make_calls, nbytes, cpu_fn=None, cpu_kind="port"):
+    ref8, refr8 = _ref_lib(), _ref_row8_lib()
+    omp = _omp()
+    all_threads = omp.omp_get_max_threads()
+    os.environ.pop("PCKETLM_NATIVE_THREADS", None)
+    os.environ["PCKETLM_ENABLE_NATIVE_FP8_BATCH_REUSE"] = "1"  # the reference's one-pass batch mode
+
+    def cpu_time(fn):
+        t0 = time.perf_counter()
+        n = 0
+        while True:
+            fn()
+            n += 1
+            if time.perf_counter() - t0 > 1.5:
+                break
+        return (time.perf_counter() - t0) / n * 1e6
+
+    def measure(name, m, make_calls, nbytes, cpu_fn=None, cpu_kind="port", ref_fn=None):
+        """ref_fn: the reference's own compiled code (oracle/_ref) for this
+        row, timed with all threads and with one; cpu_fn (the oracle's
+        restatement) only where the reference build has no such entry."""
         if not want(name):
             return
         calls = make_calls()
@@ -679,20 +714,22 @@ def table(args):
         launches = [calls[i % len(calls)] for i in range(reps)]
         med = timer.run(launches, hold_ms=max(30.0, 0.05 * len(launches))) / reps
         gbs = nbytes / (med / 1e3) / 1e9
-        cpu_us = cpu_gbs = None
-        if cpu_fn is not None and not args.no_cpu:
-            t0 = time.perf_counter()
-            n = 0
-            while True:
-                cpu_fn()
-                n += 1
-                if time.perf_counter() - t0 > 1.5:
-                    break
-            cpu_us = (time.perf_counter() - t0) / n * 1e6
+        cpu_us = cpu_gbs = cpu1_us = None
+        if ref_fn is not None and not args.no_cpu:
+            cpu_kind = "reference"
+            omp.omp_set_num_threads(all_threads)
+            cpu_us = cpu_time(ref_fn)
+            omp.omp_set_num_threads(1)
+            cpu1_us = cpu_time(ref_fn)
+            omp.omp_set_num_threads(all_threads)
             cpu_gbs = nbytes / (cpu_us / 1e6) / 1e9
-        rows_out.append((name, m, 1e3 * med, gbs, 100 * gbs / PEAK_HBM_GBS, cpu_us, cpu_gbs, cpu_kind))
+        elif cpu_fn is not None and not args.no_cpu:
+            cpu_us = cpu_time(cpu_fn)
+            cpu_gbs = nbytes / (cpu_us / 1e6) / 1e9
+        rows_out.append((name, m, 1e3 * med, gbs, 100 * gbs / PEAK_HBM_GBS, cpu_us, cpu_gbs, cpu_kind, cpu1_us))
         print(f"{name:40s} M={m}  {1e3 * med:9.2f} us  {gbs:8.1f} GB/s  {100 * gbs / PEAK_HBM_GBS:5.1f}%"
-              + (f"   cpu {cpu_us:10.1f} us {cpu_gbs:7.2f} GB/s" if cpu_us else ""), flush=True)
+              + (f"   cpu {cpu_us:10.1f} us {cpu_gbs:7.2f} GB/s {cpu_kind}" if cpu_us else "")
+              + (f" (1 thread {cpu1_us:10.1f} us)" if cpu1_us else ""), flush=True)
 
     import oracle
     from oracle import mla as oracle_mla
@@ -732,8 +769,12 @@ def table(args):
                     ctypes.c_void_p(y.data_ptr()), m, rows, cols, math.ceil(cols / 128)) for w, s in sets]
 
             xh = x.float().cpu().numpy()
+            yh = np.empty((m, rows), dtype=np.float32)
             measure(name, m, make, fp8_bytes(rows, cols, m),
-                    lambda w=host_w, s=host_s, xh=xh: oracle.fp8_linear(w, s, xh, batch_reuse=True))
+                    lambda w=host_w, s=host_s, xh=xh: oracle.fp8_linear(w, s, xh, batch_reuse=True),
+                    ref_fn=None if ref8 is None else
+                    lambda w=host_w, s=host_s, xh=xh, yh=yh, m=m, rows=rows, cols=cols: ref8.fp8_e4m3_block_linear_f32(
+                        w.ctypes.data, s.ctypes.data, xh.ctypes.data, yh.ctypes.data, m, rows, cols, s.shape[1]))
         del sets
         torch.cuda.empty_cache()
 
@@ -756,8 +797,12 @@ def table(args):
                     ctypes.c_void_p(y.data_ptr()), m, rows, cols, cols // 128) for w, s in sets]
 
             xh = x.cpu().numpy()
+            yh = np.empty((m, rows), dtype=np.float32)
             measure("fp8 o 7168x16384 (fp32 activations)", m, make, fp8_bytes(rows, cols, m) + 2 * m * cols,
-                    lambda w=host_w, s=host_s, xh=xh: oracle.fp8_linear(w, s, xh, batch_reuse=True))
+                    lambda w=host_w, s=host_s, xh=xh: oracle.fp8_linear(w, s, xh, batch_reuse=True),
+                    ref_fn=None if ref8 is None else
+                    lambda w=host_w, s=host_s, xh=xh, yh=yh, m=m: ref8.fp8_e4m3_block_linear_f32(
+                        w.ctypes.data, s.ctypes.data, xh.ctypes.data, yh.ctypes.data, m, rows, cols, s.shape[1]))
         del sets
         torch.cuda.empty_cache()
 
@@ -786,8 +831,12 @@ def table(args):
                     ctypes.c_void_p(y.data_ptr()), m, rows, cols, cols // 128) for t, s in packed]
 
             xh = x.float().cpu().numpy()
+            yh = np.empty((m, rows), dtype=np.float32)
             measure("fp8 o 7168x16384 (8-row tiles)", m, make, fp8_bytes(rows, cols, m),
-                    lambda w=host_w, s=host_s, xh=xh: oracle.fp8_linear(w, s, xh, batch_reuse=True))
+                    lambda w=host_w, s=host_s, xh=xh: oracle.fp8_linear(w, s, xh, batch_reuse=True),
+                    ref_fn=None if ref8 is None else
+                    lambda w=host_w, s=host_s, xh=xh, yh=yh, m=m: ref8.fp8_e4m3_block_linear_f32(
+                        w.ctypes.data, s.ctypes.data, xh.ctypes.data, yh.ctypes.data, m, rows, cols, s.shape[1]))
         del packed
         torch.cuda.empty_cache()
 
@@ -813,10 +862,17 @@ def table(args):
                     for t in tabs]
 
             xh = x.float().cpu().numpy()
+            yq_h, yk_h = np.empty((m, 1536), dtype=np.float32), np.empty((m, 576), dtype=np.float32)
             measure("fp8 q_a + kv_a (one launch)", m, make,
                     fp8_bytes(1536, 7168, m) + fp8_bytes(576, 7168, m) - 2 * m * 7168,
                     lambda xh=xh: (oracle.fp8_linear(hq[0], hq[1], xh, batch_reuse=True),
-                                   oracle.fp8_linear(hq[2], hq[3], xh, batch_reuse=True)))
+                                   oracle.fp8_linear(hq[2], hq[3], xh, batch_reuse=True)),
+                    ref_fn=None if ref8 is None else
+                    lambda xh=xh, m=m: (
+                        ref8.fp8_e4m3_block_linear_f32(hq[0].ctypes.data, hq[1].ctypes.data, xh.ctypes.data,
+                                                       yq_h.ctypes.data, m, 1536, 7168, 56),
+                        ref8.fp8_e4m3_block_linear_f32(hq[2].ctypes.data, hq[3].ctypes.data, xh.ctypes.data,
+                                                       yk_h.ctypes.data, m, 576, 7168, 56)))
         del qa, kva
         torch.cuda.empty_cache()
 
@@ -901,11 +957,17 @@ def table(args):
         lib.pocketlm_set_stream(_stream_ptr(torch))
         hp = packs[0].cpu().view(torch.int16).numpy().view(np.uint16)
         hh = h.cpu().view(torch.int16).numpy().view(np.uint16)
+        yh = np.empty((rows,), dtype=np.float32)
+        # the reference's packed GEMV takes u16 activations: its wrapper casts fp32 ones to fp16
+        ref_row8 = None if refr8 is None else (
+            lambda hp=hp, hh=hh, yh=yh, rows=rows, cols=cols: refr8.native_packed_gemv_rows8(
+                hh.ctypes.data, hp.ctypes.data, yh.ctypes.data, rows, cols, 0))
         measure(name, 1, lambda packs=packs, h=h, y=y, rows=rows, cols=cols: [
             lambda p=p: lib.native_packed_gemv_rows8(ctypes.c_void_p(h.data_ptr()), ctypes.c_void_p(p.data_ptr()),
                                                      ctypes.c_void_p(y.data_ptr()), rows, cols, 0) for p in packs],
             2 * math.ceil(rows / 8) * 8 * cols + 2 * cols + 4 * rows,
-            lambda hp=hp, hh=hh, rows=rows, cols=cols: oracle.packed_gemv_rows8(hh, hp, rows, cols, 0))
+            lambda hp=hp, hh=hh, rows=rows, cols=cols: oracle.packed_gemv_rows8(hh, hp, rows, cols, 0),
+            ref_fn=ref_row8)
         if rows == 3584:  # o-proj and down-proj also run on fp32 activations
             hf = h.float()
             hhf = hf.cpu().numpy()
@@ -915,7 +977,10 @@ def table(args):
                                                                     ctypes.c_void_p(y.data_ptr()), rows, cols, 0)
                 for p in packs],
                 2 * math.ceil(rows / 8) * 8 * cols + 4 * cols + 4 * rows,
-                lambda hp=hp, hhf=hhf, rows=rows, cols=cols: oracle.packed_gemv_rows8_f32_hidden(hhf, hp, rows, cols, 0))
+                lambda hp=hp, hhf=hhf, rows=rows, cols=cols: oracle.packed_gemv_rows8_f32_hidden(hhf, hp, rows, cols, 0),
+                ref_fn=None if refr8 is None else
+                lambda hp=hp, hhf=hhf, yh=yh, rows=rows, cols=cols: refr8.native_packed_gemv_rows8(
+                    hhf.astype(np.float16).view(np.uint16).ctypes.data, hp.ctypes.data, yh.ctypes.data, rows, cols, 0))
         del packs
         torch.cuda.empty_cache()
 
@@ -965,10 +1030,21 @@ def table(args):
         def cpu_many(names):
             return lambda: [oracle.packed_gemv_rows8(hh16, host[n], shapes[n][0], shapes[n][1], 0) for n in names]
 
+        hout = {k: np.empty((v[0],), dtype=np.float32) for k, v in shapes.items()}
+        hattn16, hact16 = hattn.astype(np.float16).view(np.uint16), hact.astype(np.float16).view(np.uint16)
+
+        def ref_gemv(name, x16):
+            rows, cols = shapes[name]
+            return refr8.native_packed_gemv_rows8(x16.ctypes.data, host[name].ctypes.data, hout[name].ctypes.data,
+                                                  rows, cols, 0)
+
+        def ref_many(names):
+            return None if refr8 is None else (lambda: [ref_gemv(n, hh16) for n in names])
+
         measure("row8 q/k/v (one launch)", 1, lambda: [many(l, ["q", "k", "v"]) for l in dense],
-                wbytes(["q", "k", "v"]) + 2 * H, cpu_many(["q", "k", "v"]))
+                wbytes(["q", "k", "v"]) + 2 * H, cpu_many(["q", "k", "v"]), ref_fn=ref_many(["q", "k", "v"]))
         measure("row8 gate/up (one launch)", 1, lambda: [many(l, ["gate", "up"]) for l in dense],
-                wbytes(["gate", "up"]) + 2 * H, cpu_many(["gate", "up"]))
+                wbytes(["gate", "up"]) + 2 * H, cpu_many(["gate", "up"]), ref_fn=ref_many(["gate", "up"]))
 
         def layer_calls():
             out = []
@@ -990,21 +1066,30 @@ def table(args):
         launches = [calls[i % len(calls)] for i in range(4 * 30)]
         med = timer.run(launches) / 30
         gbs = layer_bytes / (med / 1e3) / 1e9
-        cpu_us = cpu_gbs = None
+        def ref_layer():
+            for n in ("q", "k", "v"):
+                ref_gemv(n, hh16)
+            ref_gemv("o", hattn16)
+            for n in ("gate", "up"):
+                ref_gemv(n, hh16)
+            ref_gemv("down", hact16)
+
+        cpu_us = cpu_gbs = cpu1_us = None
+        kind = "port"
         if not args.no_cpu:
-            t0 = time.perf_counter()
-            n = 0
-            while True:
-                cpu_layer()
-                n += 1
-                if time.perf_counter() - t0 > 1.5:
-                    break
-            cpu_us = (time.perf_counter() - t0) / n * 1e6
+            if refr8 is not None:
+                kind = "reference"
+                cpu_us = cpu_time(ref_layer)
+                omp.omp_set_num_threads(1)
+                cpu1_us = cpu_time(ref_layer)
+                omp.omp_set_num_threads(all_threads)
+            else:
+                cpu_us = cpu_time(cpu_layer)
             cpu_gbs = layer_bytes / (cpu_us / 1e6) / 1e9
         print(f"{'row8 dense layer (4 launches)':40s} M=1  {1e3 * med:9.2f} us  {gbs:8.1f} GB/s  "
               f"{100 * gbs / PEAK_HBM_GBS:5.1f}%", flush=True)
         rows_out.append(("row8 dense layer (4 launches)", 1, 1e3 * med, gbs, 100 * gbs / PEAK_HBM_GBS, cpu_us, cpu_gbs,
-                         "port"))
+                         kind, cpu1_us))
         del dense, host
         torch.cuda.empty_cache()
 
@@ -1076,29 +1161,40 @@ def table(args):
         dev_name = "ds-v3 MoE layer, device-routed (2 launches, bf16 output)"
         print(f"{dev_name:40s} M=1  {1e3 * dev_med:9.2f} us  {dev_gbs:8.1f} GB/s  {100 * dev_gbs / PEAK_HBM_GBS:5.1f}%",
               flush=True)
-        cpu_us = cpu_gbs = None
+        cpu_us = cpu_gbs = cpu1_us = None
+        moe_kind = "port"
         if not args.no_cpu:
-            # the oracle's weighted many-expert MLP plus the shared expert's MLP on one layer
+            # the weighted many-expert MLP plus the shared expert's MLP on one layer:
+            # the reference's build (fp8_linear.cpp:212, 475), else the oracle's restatement
             routed = [tuple(t.cpu().numpy() for t in e) for e in layers[0][:8]]
             shared = tuple(t.cpu().numpy() for t in layers[0][8])
             hx, hr = x.float().cpu().numpy(), rw.cpu().numpy()
-            t0 = time.perf_counter()
-            n = 0
-            while True:
-                oracle.fp8_mlp_many_weighted(routed, hx, hr)
-                oracle.fp8_mlp(*shared, hx)
-                n += 1
-                if time.perf_counter() - t0 > 1.5:
-                    break
-            cpu_us = (time.perf_counter() - t0) / n * 1e6
+            if ref8 is not None:
+                moe_kind = "reference"
+                tabs = [np.array([e[k].ctypes.data for e in routed], dtype=np.uint64) for k in range(6)]
+                out_r, out_s = np.empty((1, 7168), dtype=np.float32), np.empty((1, 7168), dtype=np.float32)
+
+                def ref_moe():
+                    ref8.fp8_e4m3_block_mlp_many_weighted_f32(*[t.ctypes.data for t in tabs], hx.ctypes.data,
+                                                              hr.ctypes.data, out_r.ctypes.data, 8, 1, 2048, 7168, 56, 16)
+                    ref8.fp8_e4m3_block_mlp_f32(*[t.ctypes.data for t in shared], hx.ctypes.data, out_s.ctypes.data,
+                                                1, 2048, 7168, 56, 16)
+
+                cpu_us = cpu_time(ref_moe)
+                omp.omp_set_num_threads(1)
+                cpu1_us = cpu_time(ref_moe)
+                omp.omp_set_num_threads(all_threads)
+            else:
+                cpu_us = cpu_time(lambda: (oracle.fp8_mlp_many_weighted(routed, hx, hr), oracle.fp8_mlp(*shared, hx)))
             cpu_gbs = nbytes / (cpu_us / 1e6) / 1e9
             del routed, shared
         rows_out.append(("ds-v3 MoE layer (8 routed + shared, 2 launches)", 1, 1e3 * med, gbs, 100 * gbs / PEAK_HBM_GBS,
-                         cpu_us, cpu_gbs, "port"))
-        rows_out.append((dev_name, 1, 1e3 * dev_med, dev_gbs, 100 * dev_gbs / PEAK_HBM_GBS, cpu_us, cpu_gbs, "port"))
+                         cpu_us, cpu_gbs, moe_kind, cpu1_us))
+        rows_out.append((dev_name, 1, 1e3 * dev_med, dev_gbs, 100 * dev_gbs / PEAK_HBM_GBS, cpu_us, cpu_gbs, moe_kind,
+                         cpu1_us))
         for name, us in decode_steps(layers, dev_tables, logits, x):
             gbs_s = nbytes / (us / 1e6) / 1e9
-            rows_out.append((name, 1, us, gbs_s, 100 * gbs_s / PEAK_HBM_GBS, None, None, "port"))
+            rows_out.append((name, 1, us, gbs_s, 100 * gbs_s / PEAK_HBM_GBS, None, None, "port", None))
         del layers, dev_tables
         torch.cuda.empty_cache()
 
@@ -1344,13 +1440,16 @@ def table(args):
     if want("fp8 pack -> HBM"):
         transfers.append(pack_transfer(torch))
 
-    lines = [f"CPU: the oracle's restatement (kind \"port\"), {oracle.num_threads()} OpenMP threads, "
-             "weights warm in host RAM; about 1.5 s of calls per row.", "",
-             "| workload | M | GPU µs (mean) | GPU GB/s | % of 8 TB/s | CPU µs | CPU GB/s | CPU kind |",
-             "|---|---|---|---|---|---|---|---|"]
-    for name, m, us, gbs, pct, cus, cgbs, kind in rows_out:
+    lines = [f"CPU: the reference's own fp8_linear.cpp / fp16_packed_gemv.cpp built from its sources "
+             f"(oracle/_ref, kind \"reference\"; FP8 batches in its one-pass batch mode) with {all_threads} "
+             "OpenMP threads and with one, else the oracle's restatement (kind \"port\"); weights warm in "
+             "host RAM; about 1.5 s of calls per figure.", "",
+             "| workload | M | GPU µs (mean) | GPU GB/s | % of 8 TB/s | CPU µs | CPU GB/s | CPU kind | CPU 1-thread µs |",
+             "|---|---|---|---|---|---|---|---|---|"]
+    for name, m, us, gbs, pct, cus, cgbs, kind, c1 in rows_out:
         lines.append(f"| {name} | {m} | {us:.2f} | {gbs:.0f} | {pct:.1f} | "
-                     + (f"{cus:.0f} | {cgbs:.2f} | {kind} |" if cus else "— | — | — |"))
+                     + (f"{cus:.0f} | {cgbs:.2f} | {kind} | " if cus else "— | — | — | ")
+                     + (f"{c1:.0f} |" if c1 else "— |"))
     if transfers:
         lines += ["", "Weight files to HBM (file in the page cache, median of 5 loads; PCIe 5.0 x16 = 64 GB/s "
                   "per direction):", "",
