@@ -686,7 +686,7 @@ def table(args):
     omp = _omp()
     all_threads = omp.omp_get_max_threads()
     os.environ.pop("PCKETLM_NATIVE_THREADS", None)
-    os.environ["PCKETLM_ENABLE_NATIVE_FP8_BATCH_REUSE"] = "1"  # the reference's one-pass batch mode
+    os.environ.pop("PCKETLM_ENABLE_NATIVE_FP8_BATCH_REUSE", None)  # the reference's default mode
 
     def cpu_time(fn):
         t0 = time.perf_counter()
@@ -1268,6 +1268,17 @@ def table(args):
                 dev_step(i)
             graphs.append(g)
         out.append(("ds-v3 router + MoE step, device-routed, one HIP graph", wall(lambda i: graphs[i % len(graphs)].replay())))
+        # four steps per graph: the runtime's gap between back-to-back graph
+        # launches (about 9 us in a kernel trace) is paid once per four steps
+        graphs4 = []
+        for j in range(2):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                for i in range(4):
+                    dev_step(4 * j + i)
+            graphs4.append(g)
+        out.append(("ds-v3 router + MoE step, device-routed, 4 steps per HIP graph",
+                    wall(lambda i: graphs4[i % 2].replay(), n=10) / 4))
         lib.pocketlm_set_stream(_stream_ptr(torch))
         for name, us in out:
             print(f"{name:40s} M=1  {us:9.2f} us (wall clock per step)", flush=True)
@@ -1441,7 +1452,8 @@ def table(args):
         transfers.append(pack_transfer(torch))
 
     lines = [f"CPU: the reference's own fp8_linear.cpp / fp16_packed_gemv.cpp built from its sources "
-             f"(oracle/_ref, kind \"reference\"; FP8 batches in its one-pass batch mode) with {all_threads} "
+             f"(oracle/_ref, kind \"reference\"; FP8 batches in its default mode, one weight pass per row, "
+             f"which outran its one-pass batch mode here) with {all_threads} "
              "OpenMP threads and with one, else the oracle's restatement (kind \"port\"); weights warm in "
              "host RAM; about 1.5 s of calls per figure.", "",
              "| workload | M | GPU µs (mean) | GPU GB/s | % of 8 TB/s | CPU µs | CPU GB/s | CPU kind | CPU 1-thread µs |",
