@@ -44,6 +44,18 @@ int pocketlm_set_stream(void* hip_stream);
 /* New: human-readable text of the last failure on this thread ("" if none). */
 const char* pocketlm_last_error(void);
 
+/* New, no counterpart in the reference (whose CPU kernels need no device
+ * scratch).  Each host thread keeps device scratch per (device, stream) it
+ * calls on: an arena at its high-water size (growth at least doubles it and
+ * keeps the block it replaced, for work still queued or graphs captured
+ * earlier) and 64 stream words.  pocketlm_scratch_bytes: the calling
+ * thread's bytes held.  pocketlm_release_scratch: waits for the calling
+ * thread's streams and frees its scratch; graphs it captured must not be
+ * replayed afterwards.  Returns 0, or a negative code with nothing freed when
+ * a stream wait fails. */
+int64_t pocketlm_scratch_bytes(void);
+int pocketlm_release_scratch(void);
+
 /* New: 1 when a HIP device of architecture gfx950 is visible, else 0. */
 int pocketlm_device_available(void);
 

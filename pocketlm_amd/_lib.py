@@ -43,6 +43,8 @@ DS_VERIFY_CALLBACK = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_lo
 _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pocketlm_set_stream": (_i32, [_vp]),
     "pocketlm_last_error": (ctypes.c_char_p, []),
+    "pocketlm_scratch_bytes": (_i64, []),
+    "pocketlm_release_scratch": (_i32, []),
     "pocketlm_device_available": (_i32, []),
     "fp8_dequant_cpu_has_avx2_f16c": (_i32, []),
     "fp8_linear_avx512_cpu_has_avx512": (_i32, []),

@@ -18,26 +18,41 @@ thread_local hipStream_t t_stream = nullptr;
 thread_local char t_error[512] = {0};
 
 // Scratch of one (device, stream) for the calling host thread.  Blocks are
-// never freed while the process runs: a launch already queued, or a HIP
-// graph captured earlier, may still read a block that a larger request has
-// since replaced, so growth allocates a new block and keeps the old one.
-// Capacity grows at least twofold, which bounds the retired blocks to the
-// size of the current one.  Per thread: two host threads enqueueing on one
-// stream interleave their launches, and must not share intermediates.
+// kept until the thread calls pocketlm_release_scratch (or the process
+// ends): a launch already queued, or a HIP graph captured earlier, may still
+// read a block that a larger request has since replaced, so growth allocates
+// a new block and keeps the old one.  Capacity grows at least twofold, which
+// bounds the retired blocks to the size of the current one.  Per thread: two
+// host threads enqueueing on one stream interleave their launches, and must
+// not share intermediates.
 struct Arena {
     void* ptr = nullptr;
     size_t size = 0;
 };
 
+struct Words {
+    unsigned* ptr = nullptr;
+    bool owned = false;  // allocated (a slot of the zeroed pool otherwise)
+};
+
 struct ThreadScratch {
     std::map<std::pair<int, hipStream_t>, Arena> arenas;
-    std::map<std::pair<int, hipStream_t>, unsigned*> words;
+    std::map<std::pair<int, hipStream_t>, Words> words;
+    std::vector<std::pair<int, void*>> retired;  // (device, block) replaced by growth
+    size_t bytes = 0;                            // device bytes held (arenas and retired)
 };
 
 thread_local ThreadScratch t_scratch;
 
-std::mutex g_retired_mu;
-std::vector<void*> g_retired;  // replaced blocks, kept until the process ends
+// Stream words come from a pool that is zero when the module loads, one
+// slot per (device, stream, host thread), never handed out twice: no
+// zeroing launch is needed, so a first call under stream capture finds its
+// words zero both in the graph and outside it.  Past the pool, words are
+// allocated and zeroed by a kernel on the stream.
+constexpr int kWordSlots = 1024;
+__device__ unsigned g_word_pool[kWordSlots * kStreamWords];
+std::mutex g_pool_mu;
+std::map<int, std::pair<unsigned*, int>> g_pool_next;  // device -> (pool address, next free slot)
 
 // hipMalloc with the calling thread's stream-capture mode relaxed for the
 // call: under a capture in the global mode the runtime refuses allocations
@@ -101,12 +116,10 @@ void* workspace(size_t bytes) {
         hip_fail(err, "hipMalloc(workspace)");
         return nullptr;
     }
-    if (a.ptr != nullptr) {
-        std::lock_guard<std::mutex> lock(g_retired_mu);
-        g_retired.push_back(a.ptr);
-    }
+    if (a.ptr != nullptr) t_scratch.retired.emplace_back(dev, a.ptr);
     a.ptr = p;
     a.size = want;
+    t_scratch.bytes += want;
     return a.ptr;
 }
 
@@ -117,7 +130,25 @@ unsigned* stream_words() {
         hip_fail(err, "hipGetDevice");
         return nullptr;
     }
-    unsigned*& w = t_scratch.words[{dev, t_stream}];
+    Words& slot = t_scratch.words[{dev, t_stream}];
+    if (slot.ptr == nullptr) {
+        std::lock_guard<std::mutex> lock(g_pool_mu);
+        auto it = g_pool_next.find(dev);
+        if (it == g_pool_next.end()) {
+            void* base = nullptr;
+            err = hipGetSymbolAddress(&base, HIP_SYMBOL(g_word_pool));
+            if (err != hipSuccess) {
+                hip_fail(err, "hipGetSymbolAddress(g_word_pool)");
+                return nullptr;
+            }
+            it = g_pool_next.emplace(dev, std::make_pair(static_cast<unsigned*>(base), 0)).first;
+        }
+        if (it->second.second < kWordSlots) {
+            slot.ptr = it->second.first + static_cast<size_t>(it->second.second) * kStreamWords;
+            ++it->second.second;
+        }
+    }
+    unsigned*& w = slot.ptr;
     if (w == nullptr) {
         void* p = nullptr;
         err = malloc_relaxed(&p, kStreamWords * sizeof(unsigned));
@@ -136,6 +167,7 @@ unsigned* stream_words() {
             return nullptr;
         }
         w = static_cast<unsigned*>(p);
+        slot.owned = true;
     }
     return w;
 }
@@ -163,6 +195,51 @@ PLM_EXPORT int pocketlm_set_stream(void* hip_stream) {
 }
 
 PLM_EXPORT const char* pocketlm_last_error(void) { return plm::t_error; }
+
+// Device bytes of scratch the calling host thread holds (its arenas and the
+// blocks they replaced).
+PLM_EXPORT int64_t pocketlm_scratch_bytes(void) { return static_cast<int64_t>(plm::t_scratch.bytes); }
+
+// Waits for the calling thread's streams, then frees its scratch: arenas,
+// the blocks they replaced and allocated stream words (pool slots are not
+// handed out again).  Graphs captured by this thread must not be replayed
+// afterwards.  The next call on the thread starts a new arena.
+PLM_EXPORT int pocketlm_release_scratch(void) {
+    int prev = 0;
+    if (hipGetDevice(&prev) != hipSuccess) return plm::fail(-1, "hipGetDevice failed");
+    int code = 0;
+    auto on_device = [&](int dev) {
+        const hipError_t err = hipSetDevice(dev);
+        if (err != hipSuccess && code == 0) code = plm::hip_fail(err, "hipSetDevice");
+        return err == hipSuccess;
+    };
+    for (auto& kv : plm::t_scratch.arenas)
+        if (on_device(kv.first.first)) {
+            const hipError_t err = hipStreamSynchronize(kv.first.second);
+            if (err != hipSuccess && code == 0) code = plm::hip_fail(err, "hipStreamSynchronize");
+        }
+    for (auto& kv : plm::t_scratch.words)
+        if (on_device(kv.first.first)) {
+            const hipError_t err = hipStreamSynchronize(kv.first.second);
+            if (err != hipSuccess && code == 0) code = plm::hip_fail(err, "hipStreamSynchronize");
+        }
+    if (code != 0) {
+        hipSetDevice(prev);
+        return code;  // nothing freed: the streams' work may still read it
+    }
+    for (auto& kv : plm::t_scratch.arenas)
+        if (kv.second.ptr != nullptr && on_device(kv.first.first)) hipFree(kv.second.ptr);
+    for (auto& r : plm::t_scratch.retired)
+        if (on_device(r.first)) hipFree(r.second);
+    for (auto& kv : plm::t_scratch.words)
+        if (kv.second.owned && on_device(kv.first.first)) hipFree(kv.second.ptr);
+    plm::t_scratch.arenas.clear();
+    plm::t_scratch.retired.clear();
+    plm::t_scratch.words.clear();
+    plm::t_scratch.bytes = 0;
+    hipSetDevice(prev);
+    return code;
+}
 
 PLM_EXPORT int pocketlm_device_available(void) {
     int count = 0;

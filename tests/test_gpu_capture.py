@@ -93,6 +93,94 @@ def test_q4_moe_captured_cold_replays_with_and_without_fp16_overflow(nat, oracle
     assert seen_overflow
 
 
+def test_q4_moe_captured_warm_replays_with_and_without_fp16_overflow(nat, oracle_mod):
+    """The capturing thread calls the Q4 MoE eagerly on its stream first, so
+    its stream words exist before the capture (no zeroing inside the graph)
+    and the replays rely on the epoch that the down phase advances on the
+    device.  Eager calls on the same thread and stream follow the capture;
+    replays alternate inputs whose intermediate fits fp16 with inputs that
+    overflow it, each equal to the eager call bit for bit."""
+    H, I, S = 512, 1024, 2
+    normal = [_q4_expert(oracle_mod, H, I, 500 + 3 * e, 0.02, 0.02) for e in range(S)]
+    big = [_q4_expert(oracle_mod, H, I, 600 + 3 * e, 50.0, 1e-5) for e in range(S)]
+    weights = [[t.clone() for t in e] for e in normal]
+    x = torch.from_numpy(np.random.default_rng(7).standard_normal(H).astype(np.float16)).cuda()
+    route = torch.tensor([0.6, 0.5], device="cuda")
+
+    def call():
+        return nat.q4_moe_selected_forward_u16(x, [tuple(e) for e in weights], route, hidden_size=H,
+                                               intermediate_size=I)
+
+    side = torch.cuda.Stream()
+
+    def capture():
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            first = call()  # words and arena of this (thread, stream) exist from here on
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            out = call()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(side):
+            again = call()  # an eager call on the same pair before the first replay
+        torch.cuda.synchronize()
+        assert torch.equal(first.view(torch.int16), again.view(torch.int16))
+        return graph, out
+
+    graph, captured = _in_fresh_thread(capture)
+    seen = set()
+    for trial, src in enumerate([big, normal, big, big, normal, normal, big]):
+        for dst, s in zip(weights, src):
+            for d, t in zip(dst, s):
+                d.copy_(t)
+        x.copy_(torch.from_numpy(np.random.default_rng(70 + trial).standard_normal(H).astype(np.float16)))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = call()
+        torch.cuda.synchronize()
+        assert torch.equal(captured.view(torch.int16), eager.view(torch.int16)), trial
+        seen.add(src is big)
+    assert seen == {True, False}
+
+
+def test_scratch_release_across_thread_churn(nat):
+    """Each host thread keeps its own scratch arena; pocketlm_release_scratch
+    frees it.  Six short-lived threads that call an entry point and release
+    leave the device's free memory where it was; a thread that does not
+    release keeps its arena (counted by pocketlm_scratch_bytes)."""
+    from pocketlm_amd import _lib
+
+    lib = _lib.load()
+    rows, hid = 1 << 22, 16  # the top-k's logits alone take 16 MiB of scratch
+    weight = (torch.randn((rows, hid), device="cuda") * 0.1).to(torch.float16)
+    hidden = torch.randn((hid,), device="cuda").to(torch.float16)
+
+    def work(release):
+        def run():
+            torch.cuda.set_device(0)
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                nat.lm_head_topk_u16(hidden, weight, top_k=8)
+                torch.cuda.synchronize()
+                held = int(lib.pocketlm_scratch_bytes())
+                code = lib.pocketlm_release_scratch() if release else 0
+                return held, code, int(lib.pocketlm_scratch_bytes())
+        return _in_fresh_thread(run)
+
+    work(True)  # first use: module and symbol set-up
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    for _ in range(6):
+        held, code, after = work(True)
+        assert held >= 16 << 20 and code == 0 and after == 0
+    torch.cuda.synchronize()
+    free1 = torch.cuda.mem_get_info()[0]
+    assert free1 >= free0 - (24 << 20), (free0, free1)
+    held, code, after = work(False)
+    assert held >= 16 << 20 and after == held
+
+
 def _fp8(rows, cols, seed):
     g = torch.Generator().manual_seed(seed)
     w = (torch.randn((rows, cols), generator=g) * 0.02).to(torch.float8_e4m3fn).view(torch.uint8)

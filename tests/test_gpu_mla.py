@@ -132,7 +132,8 @@ def test_error_codes(nat):
         lib.ds_session_destroy(handle)
 
 
-@pytest.mark.parametrize("dims", [(16, 6, 5, 4, 3, 4, 2, 3), (64, 16, 16, 4, 8, 8, 8, 32), (48, 8, 12, 2, 4, 6, 4, 0)])
+@pytest.mark.parametrize("dims", [(16, 6, 5, 4, 3, 4, 2, 3), (64, 16, 16, 4, 8, 8, 8, 32), (48, 8, 12, 2, 4, 6, 4, 0),
+                                  (32, 8, 16, 3, 4, 5, 4, 7)])  # odd rope width: the pe part stays unrotated
 def test_block_matches_the_oracle(nat, dims):
     hidden_dim, q_rank, kv_rank, heads, nope, rope, v, prev = dims
     t = block_inputs(*dims)
@@ -204,7 +205,8 @@ def test_block_deepseek_like_dimensions_in_place_cache(nat):
     assert rel(host(kv_buf)[prev], want_kv[prev]) < 1e-6 and rel(host(pe_buf)[prev], want_pe[prev]) < 1e-6
 
 
-@pytest.mark.parametrize("dims", [FP8_DIMS, (7168, 1536, 512, 16, 128, 64, 128, 300)])
+@pytest.mark.parametrize("dims", [FP8_DIMS, (7168, 1536, 512, 16, 128, 64, 128, 300),
+                                  (256, 128, 64, 3, 16, 5, 16, 7)])  # odd rope width: pe unrotated
 def test_fp8_attention_block_matches_the_oracle(nat, dims):
     """The FP8 model's one-token attention (fp8_source.py:6337-6454) through
     ds_fp8_attention_block_bf16x_f32 against the oracle's restatement (C

@@ -123,3 +123,63 @@ def test_noalloc_rejects_a_call_beyond_its_scratch(lib):
     b = _call(lib, "fp8_e4m3_block_moe_device_routed_bf16x_f32", layer, idx, w, x)
     assert b[0] == 0
     _same(lib, layer, *_inputs(rng, 2, 8, 64, 256, 24))
+
+
+def test_noalloc_allocates_nothing_in_a_fresh_thread(lib):
+    """After a warm-up in the main thread, a host thread that has no scratch
+    yet makes several no-alloc calls through the C ABI into buffers made
+    beforehand: its scratch stays at 0 bytes (a call through the workspace
+    would have created an arena) and the device's free memory does not move;
+    the workspace entry point then does create one, which the thread frees."""
+    import threading
+
+    layer = _Layer(16, 2048, 7168, 710)
+    rng = np.random.default_rng(6)
+    inputs = [_inputs(rng, m, 8, 16, 7168, 30 + m) for m in (4, 1, 2)]
+    _same(lib, layer, *inputs[0])  # warm-up: module, symbols, the main thread's arena
+    stream = torch.cuda.Stream()
+    outs = [(torch.empty((4, 7168), device="cuda"), torch.empty((4, 7168), device="cuda"),
+             torch.empty((4, 7168), dtype=torch.int16, device="cuda"), torch.empty((1,), dtype=torch.int32, device="cuda"))
+            for _ in inputs]
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+
+    def call(fn, idx, w, x, o):
+        m, k = idx.shape
+        return getattr(lib, fn)(P(layer.table), layer.n, P(idx), P(w), k, ctypes.cast(layer.shared_arr, ctypes.c_void_p),
+                                P(x), P(o[0]), P(o[1]), P(o[2]), P(o[3]), m, layer.inter, layer.hid,
+                                (layer.hid + 127) // 128, (layer.inter + 127) // 128)
+
+    # the stream's first launches set up the runtime's own per-stream memory
+    lib.pocketlm_set_stream(ctypes.c_void_p(stream.cuda_stream))
+    assert call("fp8_e4m3_block_moe_device_routed_bf16x_f32_noalloc", *inputs[0], outs[0]) == 0
+    lib.pocketlm_set_stream(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    box = {}
+
+    def run():
+        try:
+            lib.pocketlm_set_stream(ctypes.c_void_p(stream.cuda_stream))
+            free0 = torch.cuda.mem_get_info()[0]
+            codes = [call("fp8_e4m3_block_moe_device_routed_bf16x_f32_noalloc", *inp, o)
+                     for _ in range(3) for inp, o in zip(inputs, outs)]
+            stream.synchronize()
+            box["codes"] = codes
+            box["free"] = (free0, torch.cuda.mem_get_info()[0])
+            box["noalloc_bytes"] = int(lib.pocketlm_scratch_bytes())
+            box["ws_code"] = call("fp8_e4m3_block_moe_device_routed_bf16x_f32", *inputs[0], outs[0])
+            stream.synchronize()
+            box["workspace_bytes"] = int(lib.pocketlm_scratch_bytes())
+            box["release"] = lib.pocketlm_release_scratch()
+            box["released_bytes"] = int(lib.pocketlm_scratch_bytes())
+        except BaseException as exc:
+            box["error"] = exc
+
+    t = threading.Thread(target=run)
+    t.start()
+    t.join()
+    if "error" in box:
+        raise box["error"]
+    assert box["codes"] == [0] * 9 and box["ws_code"] == 0
+    assert box["noalloc_bytes"] == 0
+    assert box["free"][0] == box["free"][1]
+    assert box["workspace_bytes"] > 0 and box["release"] == 0 and box["released_bytes"] == 0
