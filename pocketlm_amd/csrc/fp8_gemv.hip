@@ -1509,7 +1509,9 @@ void launch_rows(const RowsArgs& a, int mcount, int ngroups, hipStream_t st) {
             launch_rows_cfg<2, 2, false, NWT, SILU>(b, ngroups, st);
         else if (few)
             launch_rows_cfg<1, 2, false, NWT, SILU>(b, ngroups, st);
-        else if (per_wave <= 8)
+        else if (per_wave <= 8 && rows_tiles(b, ngroups, 1) <= plm::cu_count())
+            // 8 deep holds 146 VGPRs: one workgroup per CU, so only while the grid fits the CUs
+            // (q_a + kv_a, 264 tiles: 9.7 us at 8 deep)
             launch_rows_cfg<1, 8, false, NWT, SILU>(b, ngroups, st);
         else
             launch_rows_cfg<1, 4, false, NWT, SILU>(b, ngroups, st);
