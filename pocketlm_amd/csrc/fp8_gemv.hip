@@ -265,15 +265,13 @@ __device__ __forceinline__ void route_plan_body(const float* __restrict__ logits
         __shared__ uint64_t picked[kMaxM][64];       // [row][lane]: bits of the lane's picked experts
         uint64_t tab[kPlanRoles][4];
         if (wave == 0) {
-            // unconditional loads (rows past the table read its last entry)
+            // unconditional loads (rows past the table read its last entry;
+            // the router never picks them), first used after the routing
 #pragma unroll
             for (int r = 0; r < kPlanRoles; ++r)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int e = 4 * lane + j;
-                    const uint64_t v = table[static_cast<int64_t>(r) * experts + min(e, experts - 1)];
-                    tab[r][j] = e < experts ? v : 0;
-                }
+                for (int j = 0; j < 4; ++j)
+                    tab[r][j] = table[static_cast<int64_t>(r) * experts + min(4 * lane + j, experts - 1)];
         }
         for (int m = wave; m < batch; m += waves)
             plm_route_wave<4>(logits + static_cast<int64_t>(m) * experts, bias, experts, top_k, n_groups, topk_groups,

@@ -277,7 +277,8 @@ def test_moe_from_logits_equals_router_then_device_routed(nat, m):
 
 def test_moe_from_logits_deepseek_shapes_and_nan_logits(nat):
     """DeepSeek-V3 experts over 16 resident slots (2 per group); a NaN logit
-    sends that row through the rounds path of the router."""
+    sends that row through the rounds path of the router; the batch of two
+    and each of its rows alone."""
     experts = {e: _expert(2048, 7168, 4000 + 3 * e) for e in range(16)}
     shared = _expert(2048, 7168, 3990)
     table = nat.FP8ExpertTable(experts, 16)
@@ -286,6 +287,52 @@ def test_moe_from_logits_deepseek_shapes_and_nan_logits(nat):
     logits[1, 5] = float("nan")
     x = _x(2, 7168, 78, torch.bfloat16)
     _from_logits_case(nat, table, experts, shared, logits.cuda(), x=x)
+    _from_logits_case(nat, table, experts, shared, logits[1:].cuda(), x=x[1:].contiguous())
+    _from_logits_case(nat, table, experts, shared, logits[:1].cuda(), x=x[:1].contiguous())
+
+
+def test_moe_from_logits_one_row_deepseek_shapes_and_graph_replays(nat):
+    """The decode step's case: one row, 256 experts (ids over 8 weight sets
+    of the DeepSeek-V3 shapes, 2048 x 7168), the shared expert and a
+    correction bias.  Eager calls with new logits each time, then a HIP
+    graph replayed with new logits and eager work in between: every result
+    equals route_deepseek followed by the device-routed call, bit for bit."""
+    sets = [_expert(2048, 7168, 6000 + 3 * i) for i in range(8)]
+    experts = {e: sets[e % 8] for e in range(256)}
+    shared = _expert(2048, 7168, 5990)
+    table = nat.FP8ExpertTable(experts, 256)
+    g = torch.Generator().manual_seed(91)
+    bias = (torch.randn((256,), generator=g) * 0.1).cuda()
+    x = _x(1, 7168, 92, torch.bfloat16)
+    for _ in range(3):
+        _from_logits_case(nat, table, experts, shared, torch.randn((1, 256), generator=g).cuda(), x=x, bias=bias)
+    _from_logits_case(nat, table, experts, None, torch.randn((1, 256), generator=g).cuda(), x=x)
+
+    logits = torch.randn((1, 256), generator=g).cuda()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            nat.fp8_e4m3_block_moe_from_logits(table, x, logits, shared, bias=bias)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        captured = nat.fp8_e4m3_block_moe_from_logits(table, x, logits, shared, bias=bias)
+    busy = torch.randn((256, 256), device="cuda")
+    for trial in range(4):
+        logits.copy_(torch.randn((1, 256), generator=g).cuda())
+        graph.replay()
+        torch.cuda.synchronize()
+        idx, w = nat.route_deepseek(logits, weights_dtype=torch.float32, bias=bias)
+        want = nat.fp8_e4m3_block_moe_device_routed_f32(table, x, idx, w, shared)
+        busy = busy @ busy.T / 256.0  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(captured.indices, idx), trial
+        assert torch.equal(captured.weights, w), trial
+        assert torch.equal(captured.routed, want.routed), trial
+        assert torch.equal(captured.shared, want.shared), trial
+        assert torch.equal(captured.output.view(torch.int16), want.output.view(torch.int16)), trial
 
 
 @pytest.mark.parametrize("n,resident", [(384, 48), (2048, 16)])
