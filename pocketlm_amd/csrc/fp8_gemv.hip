@@ -1428,18 +1428,23 @@ int waves_for_blocks(int64_t nb) {
 // Waves of a rows launch.  Each family of entry points keeps one rule for
 // every batch size (it fixes the per-row arithmetic): the linear family
 // (linear, dual, many) spreads K evenly for the pipelined loop, the SiLU
-// gate/up phase of the MLP / MoE family takes min(8, blocks).
+// gate/up phase of the MLP / MoE family takes min(4, blocks): four
+// workgroups of four waves per CU instead of two of eight, so a slow wave
+// holds back a smaller share of the CU (DeepSeek-V3 layer, device-routed:
+// 76.9-77.8 us against 78.3-79.7 with 8 waves, same box).
+constexpr int kSiluWaves = 4;
 template <bool SILU>
 int rows_waves(int64_t nb) {
-    return SILU ? waves_for(nb) : waves_for_blocks(nb);
+    return SILU ? static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(nb, kSiluWaves))) : waves_for_blocks(nb);
 }
 
 // Tiles per wave (TT, 8 rows each) and blocks in flight per wave (U) only
 // shape the grid and the schedule, so they are chosen per launch.  Measured
 // on the DeepSeek-V3 shapes (us, one MI355X): at one activation row 1 tile
 // with 2 blocks in flight (o 7168x16384 25.5, 2048x7168 6.3), and 1 tile
-// with 4 blocks for the gate/up pair (9 experts' gate/up 41.5 against 43.9
-// with 2 tiles and 1 block); with several rows, wider tiles share each
+// in bursts for the gate/up pair (with 8 waves: bursts of 4 blocks, 9
+// experts' gate/up 41.5 against 43.9 with 2 tiles and 1 block; with the 4
+// waves of rows_waves, bursts of 2); with several rows, wider tiles share each
 // activation load among more weight rows while the grid keeps enough
 // workgroups (o at 8 rows: 4 tiles 29.5, 2 tiles 32.9, 1 tile 45.0).
 constexpr int64_t kMinTiles = 192;
@@ -1485,9 +1490,10 @@ void launch_rows(const RowsArgs& a, int mcount, int ngroups, hipStream_t st) {
     RowsArgs b = a;
     b.mc = mcount;
     if constexpr (SILU) {
-        // the MoE's gate/up: bursts of blocks
+        // the MoE's gate/up: bursts of 2 blocks (of a wave's 14 at 7168
+        // columns; bursts of 3, 4, 5 and 7 were slower)
         if (mcount == 1 || rows_tiles(b, ngroups, 2) < kMinTiles)
-            launch_rows_cfg<1, 4, true, NWT, SILU>(b, ngroups, st);
+            launch_rows_cfg<1, 2, true, NWT, SILU>(b, ngroups, st);
         else
             launch_rows_cfg<2, 1, true, NWT, SILU>(b, ngroups, st);
         return;
