@@ -529,9 +529,9 @@ def main_line(args):
     traffic, traffic_src = _traffic("moe_layer")
     roof = {
         "bound": "hbm",
-        "kernel": "the MoE layer's launches of fp8_e4m3_block_moe_device_routed_bf16x_f32: moe_plan_kernel, "
-                  "fp8_rows_kernel (gate/up + SiLU, 8 chosen + shared expert), fp8_down_kernel (down, "
-                  "route-weighted sum, shared expert, bf16 output)",
+        "kernel": "the MoE layer's launches of fp8_e4m3_block_moe_device_routed_bf16x_f32: fp8_rows_kernel "
+                  "(the plan from the router's choices, gate/up + SiLU, 8 chosen + shared expert), fp8_down_kernel "
+                  "(down, route-weighted sum, shared expert, bf16 output)",
         "achieved": round(achieved, 2),
         "peak": PEAK_HBM_GBS,
         "unit": "GB/s",

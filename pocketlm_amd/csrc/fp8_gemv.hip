@@ -47,8 +47,8 @@ constexpr int kMaxWaves = 8;
 constexpr int kMaxM = 8;        // activation rows per launch; larger batches are split
 constexpr int kMaxVar = 8;      // matrices of different row counts per many-linear launch
 
-// Experts chosen on the device (the device-routed MoE).  moe_plan_kernel
-// writes, for the sorted distinct experts of the router's [batch][top_k]
+// Experts chosen on the device (the device-routed MoE).  The plan holds,
+// for the sorted distinct experts of the router's [batch][top_k]
 // indices, their six addresses (gate w/s, up w/s, down w/s; one row of tab
 // per role) and the dense route matrix [group][batch].
 constexpr int kPlanRoles = 6;
@@ -91,10 +91,25 @@ struct RowsArgs {
     // g - ndev.  ndev = 0: all groups from the arguments.
     const MoePlan* plan;
     int ndev;
+    int nw;  // waves per workgroup (the block size over 64)
     // Weights in 8-row tiles (fp8_e4m3_pack_tiles8): the byte of row r,
     // column c sits at ((r / 8) * nblocks + c / 128) * 1024 + (r % 8) * 128
     // + c % 128.  Only the weight addresses change.
     int tiled;
+    // The plan made in the gate/up launch (the device-routed MoE, inplan =
+    // 1): the grid's first workgroup writes the plan for the down phase from
+    // the router's choices pidx / pwts [pbatch][ptop_k] and the device table
+    // ptable [6][pexperts], and each device-chosen group finds its expert
+    // from the choices itself instead of reading the plan.
+    int inplan;
+    int pbatch;
+    int ptop_k;
+    int64_t pexperts;
+    const uint64_t* ptable;
+    const int64_t* pidx;
+    const float* pwts;
+    MoePlan* pout;
+    int* prejected;
 };
 
 // Byte offset of column offset off (a multiple of 16) from a weight row's
@@ -143,8 +158,17 @@ struct PlanShared {
     int64_t sel[kMaxGroups];
 };
 
-// Run by a whole workgroup (every thread calls it: it synchronises the
-// workgroup); the first wave does the work.
+// The plan of the router's n = batch * top_k choices (n <= 64) as
+// run_fp8_moe builds it on the host (fp8_source.py:1600, 1653-1716): the
+// distinct in-range experts in ascending order, their addresses from the
+// device table [6][num_experts], and the route matrix [group][batch] (a
+// row's weight for the expert, 0 when the row did not choose it; a repeated
+// index within a row keeps its first weight).  An index outside
+// [0, num_experts) is left out; an expert whose weight addresses are not
+// 16-byte aligned (scales: 4) keeps its group but gets null addresses, so it
+// contributes nothing.  Both are counted in *rejected.  Run by a whole
+// workgroup (every thread calls it: it synchronises the workgroup); the
+// first wave does the work.
 __device__ void plan_from_choices(const uint64_t* __restrict__ table, int64_t num_experts, const int64_t* idx,
                                   const float* wts, int batch, int top_k, MoePlan* __restrict__ plan,
                                   int* __restrict__ rejected, PlanShared& ps) {
@@ -216,22 +240,36 @@ __device__ void plan_from_choices(const uint64_t* __restrict__ table, int64_t nu
     }
 }
 
-// One wave (the whole workgroup) writes the plan of the router's
-// n = batch * top_k choices (n <= 64) as run_fp8_moe builds it on the host
-// (fp8_source.py:1600, 1653-1716): the distinct in-range experts in
-// ascending order, their addresses from the device table [6][num_experts],
-// and the route matrix [group][batch] (a row's weight for the expert, 0 when
-// the row did not choose it; a repeated index within a row keeps its first
-// weight).  An index outside [0, num_experts) is left out; an expert whose
-// weight addresses are not 16-byte aligned (scales: 4) keeps its group but
-// gets null addresses, so it contributes nothing.  Both are counted in
-// *rejected.
-__global__ __launch_bounds__(64) void moe_plan_kernel(const uint64_t* __restrict__ table, int64_t num_experts,
-                                                      const int64_t* __restrict__ idx,
-                                                      const float* __restrict__ wts, int batch, int top_k,
-                                                      MoePlan* __restrict__ plan, int* __restrict__ rejected) {
-    __shared__ PlanShared ps;
-    plan_from_choices(table, num_experts, idx, wts, batch, top_k, plan, rejected, ps);
+// The expert of device-chosen group g as plan_from_choices numbers the
+// groups (the distinct in-range choices of the n = batch * top_k, in
+// ascending order) and its six table addresses, all null when any of them is
+// misaligned; returns the number of groups.  One wave does it alone, in two
+// memory round trips (the choices, then the expert's table entries).
+__device__ __forceinline__ int group_expert(const uint64_t* __restrict__ table, int64_t num_experts,
+                                            const int64_t* __restrict__ idx, int n, int g, int lane,
+                                            uint64_t (&ad)[kPlanRoles]) {
+    const int64_t v = lane < n ? idx[lane] : -1;
+    const int e = v >= 0 && v < num_experts ? static_cast<int>(v) : -1;
+    bool first = e >= 0;  // no earlier choice names the same expert
+    for (int i = 0; i < n; ++i) first = first && !(i < lane && __builtin_amdgcn_readlane(e, i) == e);
+    const uint64_t fm = __ballot(first);
+    const int count = __popcll(fm);
+    if (g >= count) return count;
+    int rank = 0;
+    for (int i = 0; i < n; ++i) rank += static_cast<int>((fm >> i) & 1) & (__builtin_amdgcn_readlane(e, i) < e);
+    const int eg = __builtin_amdgcn_readlane(e, __builtin_ctzll(__ballot(first && rank == g)));
+#pragma unroll
+    for (int r = 0; r < kPlanRoles; ++r) ad[r] = table[static_cast<int64_t>(r) * num_experts + eg];
+    bool aligned = true;
+#pragma unroll
+    for (int r = 0; r < kPlanRoles; ++r) aligned = aligned && (ad[r] & ((r & 1) ? 3u : 15u)) == 0;
+#pragma unroll
+    for (int r = 0; r < kPlanRoles; ++r) {
+        const uint64_t v = aligned ? ad[r] : 0;
+        ad[r] = (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v >> 32)))) << 32) |
+                static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+    }
+    return count;
 }
 
 // The router and the plan in one launch: DeepSeek-V3 routing of every row's
@@ -700,12 +738,13 @@ __device__ __forceinline__ void pin_scalar(T&... v) {
 // weights; its nw waves split the K blocks (block b on wave b % nw), and nw
 // depends only on K.  TT and U (blocks in flight per wave) change the grid
 // and the schedule, never a row's arithmetic.
-template <int TT, int U, bool BURST, int NWT, bool SILU, bool XB>
+template <int TT, int U, bool BURST, int NWT, bool SILU, bool XB, bool INPLAN>
 __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int block) {
+    static_assert(!INPLAN || (NWT == 2 && SILU), "the in-launch plan is the MoE gate/up phase's");
     constexpr int NT = NWT * TT;
     __shared__ float red[kMaxWaves * NT * 64];
     // the arguments of the prologue and of the loop, read at once
-    int nw = blockDim.x >> 6, tpg = a.tiles_per_group, nvar = a.nvar, mc = a.mc, m0 = a.m0, nb = a.nblocks;
+    int nw = a.nw, tpg = a.tiles_per_group, nvar = a.nvar, mc = a.mc, m0 = a.m0, nb = a.nblocks;
     int tiled = a.tiled;
     int64_t rows = a.rows, K = a.K, scale_cols = a.scale_cols, x_stride = a.x_stride;
     const char* xbase = XB ? reinterpret_cast<const char*>(a.xb) : reinterpret_cast<const char*>(a.x);
@@ -720,17 +759,27 @@ __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int block) {
     pin_scalar(nw, tpg, nvar, mc, m0, nb, tiled, rows, K, scale_cols, x_stride, xbase);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63;
+    // In-launch plan: the first workgroup writes the plan, after a pass
+    // through the body as a tile with no weights (the plan's stores come
+    // after every weight and scale load in program order, so the compiler
+    // keeps those loads scalar where they are uniform).
+    int tile = block;
+    bool writer = false;
+    if constexpr (INPLAN) {
+        writer = block == 0;
+        tile = max(block - 1, 0);
+    }
     int g;
     int64_t row0;
     if (nvar > 0) {
         g = 0;
         for (int i = 1; i < a.nvar; ++i)
-            if (block >= a.vtile[i]) g = i;
-        row0 = static_cast<int64_t>(block - a.vtile[g]) * 8 * TT;
+            if (tile >= a.vtile[i]) g = i;
+        row0 = static_cast<int64_t>(tile - a.vtile[g]) * 8 * TT;
         rows = a.vrows[g];
     } else {
-        g = block / tpg;
-        row0 = static_cast<int64_t>(block - g * tpg) * 8 * TT;
+        g = tile / tpg;
+        row0 = static_cast<int64_t>(tile - g * tpg) * 8 * TT;
     }
 
     const uint8_t* W[NWT];
@@ -738,15 +787,31 @@ __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int block) {
     int ga = g;  // argument slot
     if constexpr (NWT == 2 && SILU) {
         // (device-chosen groups exist only for the gate/up phase of the MoE)
-        if (g < a.ndev) {
-            if (g >= a.plan->count) return;  // the router chose fewer experts (uniform: before any barrier)
+        if (writer) {
 #pragma unroll
             for (int i = 0; i < NWT; ++i) {
-                W[i] = reinterpret_cast<const uint8_t*>(a.plan->tab[2 * i][g]);
-                S[i] = reinterpret_cast<const float*>(a.plan->tab[2 * i + 1][g]);
+                W[i] = nullptr;
+                S[i] = nullptr;
+            }
+        } else if (g < a.ndev) {
+            if constexpr (INPLAN) {
+                uint64_t ad[kPlanRoles];
+                if (g >= group_expert(a.ptable, a.pexperts, a.pidx, a.pbatch * a.ptop_k, g, lane, ad)) return;
+#pragma unroll
+                for (int i = 0; i < NWT; ++i) {
+                    W[i] = reinterpret_cast<const uint8_t*>(ad[2 * i]);
+                    S[i] = reinterpret_cast<const float*>(ad[2 * i + 1]);
+                }
+            } else {
+                if (g >= a.plan->count) return;  // the router chose fewer experts (uniform: before any barrier)
+#pragma unroll
+                for (int i = 0; i < NWT; ++i) {
+                    W[i] = reinterpret_cast<const uint8_t*>(a.plan->tab[2 * i][g]);
+                    S[i] = reinterpret_cast<const float*>(a.plan->tab[2 * i + 1][g]);
+                }
             }
         }
-        ga = g - a.ndev;
+        ga = writer ? -1 : g - a.ndev;
     }
     if (ga == 0) {
         // the first argument slot came with the other arguments
@@ -806,10 +871,10 @@ __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int block) {
     halves_to_lds(acc, red, wave, lane);
     __syncthreads();
 
-    for (int t = threadIdx.x; t < TT * 64; t += blockDim.x) {
+    for (int t = threadIdx.x; t < TT * 64; t += nw * 64) {
         const int tt = t >> 6, r = (t >> 3) & 7, m = t & 7;
         const int64_t row = row0 + 8 * tt + r;
-        if (m >= a.mc || row >= rows) continue;
+        if (m >= a.mc || row >= rows || writer) continue;
         float v[NWT];
 #pragma unroll
         for (int i = 0; i < NWT; ++i) {
@@ -829,11 +894,17 @@ __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int block) {
             for (int i = 0; i < NWT; ++i) a.out[i][o] = v[i];
         }
     }
+    if constexpr (INPLAN) {
+        if (writer) {
+            __shared__ PlanShared ps;
+            plan_from_choices(a.ptable, a.pexperts, a.pidx, a.pwts, a.pbatch, a.ptop_k, a.pout, a.prejected, ps);
+        }
+    }
 }
 
-template <int TT, int U, bool BURST, int NWT, bool SILU, bool XB>
+template <int TT, int U, bool BURST, int NWT, bool SILU, bool XB, bool INPLAN = false>
 __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
-    rows_tile<TT, U, BURST, NWT, SILU, XB>(a, static_cast<int>(blockIdx.x));
+    rows_tile<TT, U, BURST, NWT, SILU, XB, INPLAN>(a, static_cast<int>(blockIdx.x));
 }
 
 
@@ -1455,12 +1526,24 @@ void launch_rows_cfg(const RowsArgs& a, int ngroups, hipStream_t st) {
     RowsArgs b = a;
     b.tiles_per_group = static_cast<int>(plm::ceil_div(a.rows, 8 * TT));
     const int nw = rows_waves<SILU>(a.nblocks);
-    int64_t grid = static_cast<int64_t>(b.tiles_per_group) * ngroups;
+    b.nw = nw;
+    int64_t grid = static_cast<int64_t>(b.tiles_per_group) * ngroups + (a.inplan ? 1 : 0);
     if (a.nvar > 0) {
         b.vtile[0] = 0;
         for (int i = 0; i < a.nvar; ++i)
             b.vtile[i + 1] = b.vtile[i] + static_cast<int>(plm::ceil_div(a.vrows[i], 8 * TT));
         grid = b.vtile[a.nvar];
+    }
+    if constexpr (NWT == 2 && SILU) {
+        if (a.inplan) {
+            if (a.xb != nullptr)
+                hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, true, true>),
+                                   dim3(static_cast<unsigned>(grid)), dim3(nw * plm::kWave), 0, st, b);
+            else
+                hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, false, true>),
+                                   dim3(static_cast<unsigned>(grid)), dim3(nw * plm::kWave), 0, st, b);
+            return;
+        }
     }
     if (a.xb != nullptr) {
         hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, true>), dim3(static_cast<unsigned>(grid)),
@@ -1485,6 +1568,9 @@ int64_t rows_blocks_per_wave(const RowsArgs& a) {
     return plm::ceil_div(a.nblocks, rows_waves<SILU>(a.nblocks));
 }
 
+template <int NWT>
+void launch_rows_linear(const RowsArgs& b, int mcount, int ngroups, hipStream_t st);
+
 template <int NWT, bool SILU>
 void launch_rows(const RowsArgs& a, int mcount, int ngroups, hipStream_t st) {
     RowsArgs b = a;
@@ -1496,8 +1582,15 @@ void launch_rows(const RowsArgs& a, int mcount, int ngroups, hipStream_t st) {
             launch_rows_cfg<1, 2, true, NWT, SILU>(b, ngroups, st);
         else
             launch_rows_cfg<2, 1, true, NWT, SILU>(b, ngroups, st);
-        return;
+    } else {
+        launch_rows_linear<NWT>(b, mcount, ngroups, st);
     }
+}
+
+// The linear family's launches.
+template <int NWT>
+void launch_rows_linear(const RowsArgs& b, int mcount, int ngroups, hipStream_t st) {
+    constexpr bool SILU = false;
     // Pipeline depth at one row: every block of a wave in flight up to 8
     // (7168 columns: q_a 1536 rows 6.0 us, 576 rows 5.8, 2048 rows 6.1),
     // 4 deep beyond (16384 columns: 28.0 us against 32.2 at 8 deep).
@@ -2198,9 +2291,17 @@ int device_routed_impl(const uint64_t* table, int64_t num_experts, const int64_t
                            const_cast<int64_t*>(idx), const_cast<float*>(wts), plan, rejected);
         code = plm::check_launch("moe route + plan kernel");
     } else {
-        hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(64), 0, st, table, num_experts, idx, wts,
-                           static_cast<int>(batch), static_cast<int>(top_k), plan, rejected);
-        code = plm::check_launch("moe plan kernel");
+        // the plan is made in the gate/up launch (its first workgroup writes
+        // it; the routed workgroups find their experts from the choices)
+        a.inplan = 1;
+        a.pbatch = static_cast<int>(batch);
+        a.ptop_k = static_cast<int>(top_k);
+        a.pexperts = num_experts;
+        a.ptable = table;
+        a.pidx = idx;
+        a.pwts = wts;
+        a.pout = plan;
+        a.prejected = rejected;
     }
     if (code != 0) return code;
 
