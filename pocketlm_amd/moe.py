@@ -21,8 +21,8 @@ is a bf16 add.  Expert selection (sorted unique ids of the router's
 indices) needs the indices on the host, as in the reference.
 
 run_fp8_moe_device keeps the router's outputs on the device instead: the
-experts are chosen by a plan kernel from a device table of every expert
-(native.FP8ExpertTable), and the bf16 tail is done by the library, so the
+experts are chosen on the device, in the gate/up launch, from a device
+table of every expert (native.FP8ExpertTable), and the bf16 tail is done by the library, so the
 layer issues no host read-back.  Its values are those of the weighted path
 at M == 1 and of the row-weighted path at M > 1.
 """
