@@ -619,6 +619,40 @@ __device__ __forceinline__ void run_pipelined(int nk, Issue& issue, Compute& com
 // the loads of U blocks b = b0, b0 + nw, ... are issued together, then the
 // U blocks are consumed.  Activations are loaded by the lanes of live rows
 // only and scales per block.
+// v of lane K of the lane's quad (lanes 4j .. 4j + 3).
+template <int K>
+__device__ __forceinline__ plm_u32x4 quad_part(plm_u32x4 v) {
+    plm_u32x4 r;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        r[c] = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v[c]), K * 0x55, 0xF, 0xF, false));
+    return r;
+}
+
+// One activation row (X1, the linear family's loop, where every lane reads
+// a piece: lanes of B columns past the batch read row 0's): the lanes of a
+// quad (activation rows m = 0-3 of one B column half and quarter) hold the
+// same piece, so each loads one 16-byte part of it and the parts are
+// exchanged across the quad, one load instruction per block instead of two
+// (bf16) or four (fp32).  o 7168x16384 at one row: 26.2 -> 23.0 us (bf16),
+// 36.2 -> 28.9 us (fp32).  The gate/up burst loop loads on the live lanes
+// only and gains nothing from it.
+template <bool XB>
+__device__ __forceinline__ plm_u32x4 load_xpart(const char* piece, int lane) {
+    return xload16(piece + 16 * ((lane & 3) % (XB ? 2 : 4)));
+}
+template <bool XB>
+__device__ __forceinline__ XPiece<XB> quad_piece(plm_u32x4 part) {
+    XPiece<XB> x;
+    x.v[0] = quad_part<0>(part);
+    x.v[1] = quad_part<1>(part);
+    if constexpr (!XB) {
+        x.v[2] = quad_part<2>(part);
+        x.v[3] = quad_part<3>(part);
+    }
+    return x;
+}
+
 template <int TT, int U, int NWT, bool XB, bool SAN>
 __device__ __forceinline__ void rows_pass_burst(const RowsArgs& a, const uint8_t* const (&wrow)[NWT * TT],
                                                 const float* const (&sp)[NWT], const char* xrow, bool xlive,
@@ -664,7 +698,7 @@ __device__ __forceinline__ void rows_pass_burst(const RowsArgs& a, const uint8_t
 // 0 into B columns whose results are dropped, and the blocks beyond a
 // multiple of P run first, unpipelined.  The wave's scales come first, one
 // load for up to 64 blocks (lane k holds block k's), read with v_readlane.
-template <int TT, int P, int NWT, bool XB, bool SAN>
+template <int TT, int P, int NWT, bool XB, bool SAN, bool X1>
 __device__ __forceinline__ void rows_pass(const RowsArgs& a, const uint8_t* const (&wrow)[NWT * TT],
                                           const float* const (&sp)[NWT], const char* xrow, int64_t lane_col,
                                           int wave, int nw, int lane, plm_f32x4 (&acc)[NWT * TT]) {
@@ -686,13 +720,21 @@ __device__ __forceinline__ void rows_pass(const RowsArgs& a, const uint8_t* cons
             const int64_t off = min((wave + static_cast<int64_t>(kb + k) * nw) * 128 + lane_col, K - 16);
 #pragma unroll
             for (int t = 0; t < NT; ++t) q[slot][t] = wload16(wrow[t] + tile_col(off, a.tiled));
-            x[slot] = load_xpiece<XB>(xrow + off * XE, true);
+            if constexpr (X1)
+                x[slot].v[0] = load_xpart<XB>(xrow + off * XE, lane);
+            else
+                x[slot] = load_xpiece<XB>(xrow + off * XE, true);
         };
         auto compute = [&](int slot, int k) {
             float sc[NWT];
 #pragma unroll
             for (int n = 0; n < NWT; ++n) sc[n] = lane_value(sv[n], k);
-            XPiece<XB> xv = x[slot];
+            XPiece<XB> xv;
+            if constexpr (X1) {
+                xv = quad_piece<XB>(x[slot].v[0]);
+            } else {
+                xv = x[slot];
+            }
             plm_u32x4 qv[NT];
 #pragma unroll
             for (int t = 0; t < NT; ++t) qv[t] = q[slot][t];
@@ -738,9 +780,10 @@ __device__ __forceinline__ void pin_scalar(T&... v) {
 // weights; its nw waves split the K blocks (block b on wave b % nw), and nw
 // depends only on K.  TT and U (blocks in flight per wave) change the grid
 // and the schedule, never a row's arithmetic.
-template <int TT, int U, bool BURST, int NWT, bool SILU, bool XB, bool INPLAN>
+template <int TT, int U, bool BURST, int NWT, bool SILU, bool XB, bool INPLAN, bool X1>
 __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int block) {
     static_assert(!INPLAN || (NWT == 2 && SILU), "the in-launch plan is the MoE gate/up phase's");
+    static_assert(!X1 || !BURST, "the quad-shared activation loads are the pipelined loop's");
     constexpr int NT = NWT * TT;
     __shared__ float red[kMaxWaves * NT * 64];
     // the arguments of the prologue and of the loop, read at once
@@ -859,7 +902,7 @@ __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int block) {
             if constexpr (BURST)
                 rows_pass_burst<TT, U, NWT, XB, SAN>(a, wrow, sp, xrow, xlive, lane_col, wave, nw, acc);
             else
-                rows_pass<TT, U, NWT, XB, SAN>(a, wrow, sp, xrow, lane_col, wave, nw, lane, acc);
+                rows_pass<TT, U, NWT, XB, SAN, X1>(a, wrow, sp, xrow, lane_col, wave, nw, lane, acc);
         };
         pass(std::false_type{});
         if (any_nan(acc)) {
@@ -902,9 +945,9 @@ __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int block) {
     }
 }
 
-template <int TT, int U, bool BURST, int NWT, bool SILU, bool XB, bool INPLAN = false>
+template <int TT, int U, bool BURST, int NWT, bool SILU, bool XB, bool INPLAN = false, bool X1 = false>
 __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
-    rows_tile<TT, U, BURST, NWT, SILU, XB, INPLAN>(a, static_cast<int>(blockIdx.x));
+    rows_tile<TT, U, BURST, NWT, SILU, XB, INPLAN, X1>(a, static_cast<int>(blockIdx.x));
 }
 
 
@@ -1521,7 +1564,8 @@ int rows_waves(int64_t nb) {
 constexpr int64_t kMinTiles = 192;
 constexpr int64_t kCUs = 256;  // MI355X compute units
 
-template <int TT, int P, bool BURST, int NWT, bool SILU>
+// X1: the launch has one activation row (mc == 1).
+template <int TT, int P, bool BURST, int NWT, bool SILU, bool X1 = false>
 void launch_rows_cfg(const RowsArgs& a, int ngroups, hipStream_t st) {
     RowsArgs b = a;
     b.tiles_per_group = static_cast<int>(plm::ceil_div(a.rows, 8 * TT));
@@ -1537,19 +1581,19 @@ void launch_rows_cfg(const RowsArgs& a, int ngroups, hipStream_t st) {
     if constexpr (NWT == 2 && SILU) {
         if (a.inplan) {
             if (a.xb != nullptr)
-                hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, true, true>),
+                hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, true, true, X1>),
                                    dim3(static_cast<unsigned>(grid)), dim3(nw * plm::kWave), 0, st, b);
             else
-                hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, false, true>),
+                hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, false, true, X1>),
                                    dim3(static_cast<unsigned>(grid)), dim3(nw * plm::kWave), 0, st, b);
             return;
         }
     }
     if (a.xb != nullptr) {
-        hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, true>), dim3(static_cast<unsigned>(grid)),
+        hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, true, false, X1>), dim3(static_cast<unsigned>(grid)),
                            dim3(nw * plm::kWave), 0, st, b);
     } else {
-        hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, false>), dim3(static_cast<unsigned>(grid)),
+        hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, false, false, X1>), dim3(static_cast<unsigned>(grid)),
                            dim3(nw * plm::kWave), 0, st, b);
     }
 }
@@ -1601,17 +1645,17 @@ void launch_rows_linear(const RowsArgs& b, int mcount, int ngroups, hipStream_t 
         // in the FP8 attention block 24.2 -> about 13 us with 4 tiles; the
         // expert down 7168x2048 6.32 -> 6.23 with 2, 6.78 with 4)
         if (few && rows_tiles(b, ngroups, 4) >= 2 * kCUs)
-            launch_rows_cfg<4, 2, false, NWT, SILU>(b, ngroups, st);
+            launch_rows_cfg<4, 2, false, NWT, SILU, true>(b, ngroups, st);
         else if (few && rows_tiles(b, ngroups, 2) >= kMinTiles)
-            launch_rows_cfg<2, 2, false, NWT, SILU>(b, ngroups, st);
+            launch_rows_cfg<2, 2, false, NWT, SILU, true>(b, ngroups, st);
         else if (few)
-            launch_rows_cfg<1, 2, false, NWT, SILU>(b, ngroups, st);
+            launch_rows_cfg<1, 2, false, NWT, SILU, true>(b, ngroups, st);
         else if (per_wave <= 8 && rows_tiles(b, ngroups, 1) <= plm::cu_count())
             // 8 deep holds 146 VGPRs: one workgroup per CU, so only while the grid fits the CUs
             // (q_a + kv_a, 264 tiles: 9.7 us at 8 deep)
-            launch_rows_cfg<1, 8, false, NWT, SILU>(b, ngroups, st);
+            launch_rows_cfg<1, 8, false, NWT, SILU, true>(b, ngroups, st);
         else
-            launch_rows_cfg<1, 4, false, NWT, SILU>(b, ngroups, st);
+            launch_rows_cfg<1, 4, false, NWT, SILU, true>(b, ngroups, st);
         return;
     }
     if constexpr (NWT == 1) {
