@@ -9,13 +9,13 @@
 //     pieces of a row (8 values), eight pieces in flight per lane, and fma
 //     them in fp32 against the hidden vector staged once per workgroup in
 //     LDS; a DPP wave sum ends each row.
-//   * topk_level_kernel: blocks of 1024 entries keep their top_k (a larger
-//     value first, equal values by the lower row), found by a bisection on
-//     order-preserving keys; levels repeat on the survivors until one block
-//     writes the top_k in descending order (top_k <= 64).  NaN logits rank
-//     as -inf.  With fewer rows than
-//     top_k the remaining slots are id -1, logit -inf, the reference's
-//     initial values.
+//   * topk_level_kernel: slices of 1024 entries, one wave each, keep their
+//     top_k (a larger value first, equal values by the lower row), found by
+//     a bisection on order-preserving keys counted with ballots; levels
+//     repeat on the survivors until one slice writes the top_k in
+//     descending order (top_k <= 64).  NaN logits rank as -inf.  With fewer
+//     rows than top_k the remaining slots are id -1, logit -inf, the
+//     reference's initial values.
 #include <algorithm>
 
 #include "common.h"
@@ -25,8 +25,9 @@ namespace {
 constexpr int kLmRowsPerWave = 4;
 constexpr int kLmWaves = 4;              // 256 threads: 16 rows per workgroup
 constexpr int kLmUnroll = 8;             // 16-byte pieces in flight per lane
-constexpr int kTopkSlice = 1024;         // entries per block of a selection level (one per thread)
-constexpr int kTopkThreads = 1024;
+constexpr int kTopkJ = 16;               // entries per lane of a selection slice (1024 per slice)
+constexpr int kTopkWaves = 4;            // slices per workgroup of a reducing level
+constexpr int kTopkFinalWaves = 8;       // slices of the last two levels (one workgroup)
 constexpr int kMaxTopK = 64;
 
 __device__ __forceinline__ float u16f(uint32_t v, bool bf16) {
@@ -106,95 +107,196 @@ __device__ __forceinline__ uint32_t order_key(float v) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// Entries of the block whose key is at least t (block-wide, every thread
-// gets the count).
-__device__ __forceinline__ int count_at_least(uint32_t key, uint32_t t, int* wave_cnt) {
-    const int wave = threadIdx.x >> 6;
-    const unsigned long long m = __ballot(key != 0u && key >= t);
-    if ((threadIdx.x & 63) == 0) wave_cnt[wave] = __popcll(m);
-    __syncthreads();
-    int c = 0;
-    for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) c += wave_cnt[w];
-    __syncthreads();
-    return c;
+// LDS writes of a wave made visible to its other lanes.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Exclusive count of set flags at lower positions (block-wide prefix).
-__device__ __forceinline__ int prefix_count(bool flag, int* wave_cnt) {
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const unsigned long long m = __ballot(flag);
-    if (lane == 0) wave_cnt[wave] = __popcll(m);
-    __syncthreads();
-    int c = __popcll(m & ((1ull << lane) - 1ull));
-    for (int w = 0; w < wave; ++w) c += wave_cnt[w];
-    __syncthreads();
-    return c;
+// Set lanes of m below this lane.
+__device__ __forceinline__ int lanes_below(unsigned long long m) {
+    return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
 }
 
-// One selection level: block b takes entries [b * kTopkSlice, ...) of
-// (value, row) pairs (first level: the logits, row = index), one per
-// thread, and keeps its top_k in rank order at out[b * top_k + rank];
-// missing ranks get (-inf, -1).  With final set (one block), writes ids +
-// token_offset and logits instead, -1 / -inf past the available entries.
-//
-// Rank order: a larger value first, equal values by position in the block.
-// The first level's rows rise with the position, and every later level
-// stores a block's survivors in rank order, blocks in row order, so the
-// lower position is the lower row.  The block finds the top_k without
-// comparing all pairs: a 32-step bisection on the order-preserving keys
-// finds the top_k-th largest key T; entries above T and the lowest-placed
-// entries equal to T make exactly top_k survivors, ranked among themselves.
-template <bool FIRST>
-__global__ __launch_bounds__(kTopkThreads) void topk_level_kernel(const float* __restrict__ in_v,
-                                                                  const int64_t* __restrict__ in_r, int64_t n_in,
-                                                                  int top_k, float* __restrict__ out_v,
-                                                                  int64_t* __restrict__ out_r, int final,
-                                                                  int64_t token_offset) {
-    static_assert(kTopkSlice == kTopkThreads, "one entry per thread");
-    __shared__ int wave_cnt[kTopkThreads / 64];
-    __shared__ float sv[kMaxTopK];
-    __shared__ int sp[kMaxTopK];
-    const int i = threadIdx.x;
-    const int64_t base = static_cast<int64_t>(blockIdx.x) * kTopkSlice;
-    const int64_t gi = base + i;
-    float val = 0.0f;
-    uint32_t key = 0u;
-    if (gi < n_in && (FIRST || in_r[gi] >= 0)) {
-        val = FIRST ? key_of(in_v[gi]) : in_v[gi];
-        key = order_key(val);
+// Top-k selection.  A slice of 64 J entries (J per lane of one wave, entry j
+// of lane l at position 64 j + l) keeps its top_k in rank order: a larger
+// value first, equal values by position.  The first level's rows rise with
+// the position, and every later level stores a slice's survivors in rank
+// order, slices in row order, so the lower position is the lower row.  No
+// barrier: a 32-step bisection on the order-preserving keys, counted with
+// ballots, finds the top_k-th largest key T; entries above T and the
+// lowest-placed entries equal to T make exactly top_k survivors (fewer when
+// the slice holds fewer), ranked among themselves.  Missing ranks of a level
+// that is not the last are (NaN, -1), which the next level reads as absent
+// (no kept value is NaN: NaN logits rank as -inf); the last level writes ids
+// + token_offset and logits, (-1, -inf) past the available entries.
+
+// Keys of one slice's entries (0: absent).  FIRST: the values are logits.
+template <bool FIRST, int J>
+__device__ __forceinline__ void slice_keys(float (&val)[J], uint32_t (&key)[J], int64_t avail, int lane) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const bool ok = j * 64 + lane < avail && (FIRST || val[j] == val[j]);
+        val[j] = ok ? (FIRST ? key_of(val[j]) : val[j]) : 0.0f;
+        key[j] = ok ? order_key(val[j]) : 0u;
     }
-    const int64_t o = final ? 0 : static_cast<int64_t>(blockIdx.x) * top_k;
-    for (int t = i; t < top_k; t += blockDim.x) {
-        out_v[o + t] = -__builtin_inff();
-        out_r[o + t] = -1;
-    }
+}
+
+// The slice's survivors, unranked, in sv / sp [0, kept) (value, position),
+// and entries after them in [kept, 64) that rank after every survivor;
+// returns kept.  Every lane of the wave calls it.
+template <int J>
+__device__ __forceinline__ int slice_survivors(const float (&val)[J], const uint32_t (&key)[J], int top_k, float* sv,
+                                               int* sp, int lane) {
+    auto count_at_least = [&](uint32_t t) {
+        int c = 0;
+#pragma unroll
+        for (int j = 0; j < J; ++j) c += __popcll(__ballot(key[j] >= t));
+        return c;
+    };
     // T: the largest t with at least top_k entries at or above it (0 when
-    // the block holds fewer than top_k entries: all of them survive)
+    // the slice holds fewer than top_k entries: all of them survive)
     uint32_t T = 0u;
     for (int bit = 31; bit >= 0; --bit) {
         const uint32_t cand = T | (1u << bit);
-        if (count_at_least(key, cand, wave_cnt) >= top_k) T = cand;
+        if (count_at_least(cand) >= top_k) T = cand;
     }
-    const int above = T == 0u ? 0 : count_at_least(key, T + 1u, wave_cnt);
-    const bool tie = key != 0u && key == T;
-    const int tie_pos = prefix_count(tie, wave_cnt);
-    const bool keep = key != 0u && (key > T || (tie && tie_pos < top_k - above));
-    const int slot = prefix_count(keep, wave_cnt);
-    if (keep) {
-        sv[slot] = val;
-        sp[slot] = i;
+    const int need = top_k - (T == 0u ? 0 : count_at_least(T + 1u));  // ties kept, lowest positions first
+    int ties = 0, kept = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const bool tie = key[j] != 0u && key[j] == T;
+        const unsigned long long tm = __ballot(tie);
+        const bool keep = key[j] != 0u && (key[j] > T || (tie && ties + lanes_below(tm) < need));
+        ties += __popcll(tm);
+        const unsigned long long km = __ballot(keep);
+        if (keep) {
+            const int slot = kept + lanes_below(km);
+            sv[slot] = val[j];
+            sp[slot] = j * 64 + lane;
+        }
+        kept += __popcll(km);  // at most top_k
     }
-    const int kept = count_at_least(keep ? 1u : 0u, 1u, wave_cnt);  // survivors (<= top_k)
-    __syncthreads();
-    if (i < kept) {
-        const float c = sv[i];
-        const int pi = sp[i];
-        int rank = 0;
-        for (int j = 0; j < kept; ++j) rank += (sv[j] > c) || (sv[j] == c && sp[j] < pi);
-        const int64_t row = FIRST ? base + pi : in_r[base + pi];
+    if (lane >= kept) {
+        sv[lane] = -__builtin_inff();
+        sp[lane] = 0x7FFFFFFF;
+    }
+    wave_sync();
+    return kept;
+}
+
+// Rank of survivor (c, pi) among the 64 slots.
+__device__ __forceinline__ int survivor_rank(const float* sv, const int* sp, float c, int pi) {
+    int rank = 0;
+#pragma unroll 4
+    for (int j = 0; j < kMaxTopK; j += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(sv + j);
+        const int4 q = *reinterpret_cast<const int4*>(sp + j);
+        rank += (v.x > c) || (v.x == c && q.x < pi);
+        rank += (v.y > c) || (v.y == c && q.y < pi);
+        rank += (v.z > c) || (v.z == c && q.z < pi);
+        rank += (v.w > c) || (v.w == c && q.w < pi);
+    }
+    return rank;
+}
+
+// One reducing level: slice b of in keeps its top_k at out[b * top_k + rank].
+template <bool FIRST>
+__global__ __launch_bounds__(kTopkWaves * 64) void topk_level_kernel(const float* __restrict__ in_v,
+                                                                     const int64_t* __restrict__ in_r, int64_t n_in,
+                                                                     int top_k, float* __restrict__ out_v,
+                                                                     int64_t* __restrict__ out_r) {
+    constexpr int J = kTopkJ;
+    __shared__ __align__(16) float sv[kTopkWaves][kMaxTopK];
+    __shared__ __align__(16) int sp[kTopkWaves][kMaxTopK];
+    const int wave = static_cast<int>(threadIdx.x >> 6);
+    const int lane = static_cast<int>(threadIdx.x & 63);
+    const int64_t slice = static_cast<int64_t>(blockIdx.x) * kTopkWaves + wave;
+    const int64_t base = slice * (64 * J);
+    if (base >= n_in) return;  // a whole wave; no barrier below
+    // every load issued before the first use (entries past the end read the
+    // last one and are dropped)
+    float val[J];
+    uint32_t key[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) val[j] = in_v[min(base + j * 64 + lane, n_in - 1)];
+    __builtin_amdgcn_sched_barrier(0);  // keep the loads together
+    slice_keys<FIRST, J>(val, key, n_in - base, lane);
+    const int kept = slice_survivors<J>(val, key, top_k, sv[wave], sp[wave], lane);
+    const int64_t o = slice * top_k;
+    if (lane < kept) {
+        const float c = sv[wave][lane];
+        const int pi = sp[wave][lane];
+        const int rank = survivor_rank(sv[wave], sp[wave], c, pi);
         out_v[o + rank] = c;
-        out_r[o + rank] = final ? row + token_offset : row;
+        out_r[o + rank] = FIRST ? base + pi : in_r[base + pi];
+    } else if (lane < top_k) {
+        out_v[o + lane] = __builtin_nanf("");
+        out_r[o + lane] = -1;
+    }
+}
+
+// The last two levels in one workgroup: wave w takes slice w of in (at most
+// kTopkFinalWaves slices) and leaves its survivors in rank order in LDS;
+// then wave 0 selects the top_k of those and writes ids + token_offset and
+// logits.
+template <bool FIRST>
+__global__ __launch_bounds__(kTopkFinalWaves * 64) void topk_final_kernel(const float* __restrict__ in_v,
+                                                                          const int64_t* __restrict__ in_r,
+                                                                          int64_t n_in, int top_k,
+                                                                          float* __restrict__ out_v,
+                                                                          int64_t* __restrict__ out_r,
+                                                                          int64_t token_offset) {
+    constexpr int J = kTopkJ;
+    static_assert(kTopkFinalWaves * kMaxTopK <= 64 * J, "the survivors of every slice fit one slice");
+    __shared__ __align__(16) float sv[kTopkFinalWaves][kMaxTopK];
+    __shared__ __align__(16) int sp[kTopkFinalWaves][kMaxTopK];
+    __shared__ float cv[kTopkFinalWaves * kMaxTopK];
+    __shared__ int64_t cr[kTopkFinalWaves * kMaxTopK];
+    const int wave = static_cast<int>(threadIdx.x >> 6);
+    const int lane = static_cast<int>(threadIdx.x & 63);
+    const int64_t base = static_cast<int64_t>(wave) * (64 * J);
+    const int nslices = static_cast<int>((n_in + 64 * J - 1) / (64 * J));
+    if (base < n_in) {  // whole waves
+        float val[J];
+        uint32_t key[J];
+#pragma unroll
+        for (int j = 0; j < J; ++j) val[j] = in_v[min(base + j * 64 + lane, n_in - 1)];
+        __builtin_amdgcn_sched_barrier(0);
+        slice_keys<FIRST, J>(val, key, n_in - base, lane);
+        const int kept = slice_survivors<J>(val, key, top_k, sv[wave], sp[wave], lane);
+        const int o = wave * top_k;
+        if (lane < kept) {
+            const float c = sv[wave][lane];
+            const int pi = sp[wave][lane];
+            const int rank = survivor_rank(sv[wave], sp[wave], c, pi);
+            cv[o + rank] = c;
+            cr[o + rank] = FIRST ? base + pi : in_r[base + pi];
+        } else if (lane < top_k) {
+            cv[o + lane] = __builtin_nanf("");
+            cr[o + lane] = -1;
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    const int n2 = nslices * top_k;
+    float val[J];
+    uint32_t key[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) val[j] = cv[min(j * 64 + lane, n2 - 1)];
+    slice_keys<false, J>(val, key, n2, lane);
+    const int kept = slice_survivors<J>(val, key, top_k, sv[0], sp[0], lane);
+    if (lane < kept) {
+        const float c = sv[0][lane];
+        const int pi = sp[0][lane];
+        const int rank = survivor_rank(sv[0], sp[0], c, pi);
+        out_v[rank] = c;
+        out_r[rank] = cr[pi] + token_offset;
+    } else if (lane < top_k) {
+        out_v[lane] = -__builtin_inff();
+        out_r[lane] = -1;
     }
 }
 
@@ -265,8 +367,8 @@ PLM_EXPORT int native_lm_head_topk_u16(const uint16_t* hidden, const uint16_t* w
     if (top_k > kMaxTopK) return plm::fail(2, "top_k above %d", kMaxTopK);
     if (rows > (int64_t{1} << 40)) return plm::fail(2, "too many rows");
     hipStream_t st = plm::current_stream();
-    // candidates of the first level; later levels are smaller (top_k <= kTopkSlice / 16)
-    const int64_t cand_half = plm::ceil_div(plm::ceil_div(rows, kTopkSlice) * top_k, 64) * 64;
+    // candidates of the first level; later levels are smaller (top_k <= 64 * kTopkJ / 32)
+    const int64_t cand_half = plm::ceil_div(plm::ceil_div(rows, 64 * kTopkJ) * top_k, 64) * 64;
     const size_t logit_bytes = static_cast<size_t>(plm::ceil_div(rows * 4, 256) * 256);
     const size_t candv_bytes = static_cast<size_t>(2 * cand_half * 4);
     char* ws = static_cast<char*>(plm::workspace(logit_bytes + candv_bytes + static_cast<size_t>(2 * cand_half) * 8));
@@ -293,7 +395,7 @@ PLM_EXPORT int native_lm_head_topk_u16(const uint16_t* hidden, const uint16_t* w
     }
     int code = plm::check_launch("lm_head logits kernel");
     if (code != 0) return code;
-    // levels of 1024-entry blocks keeping their top_k, until one block is left
+    // levels of slices keeping their top_k, until one slice is left
     const float* in_v = logits;
     const int64_t* in_r = nullptr;
     int64_t n = rows;
@@ -301,19 +403,20 @@ PLM_EXPORT int native_lm_head_topk_u16(const uint16_t* hidden, const uint16_t* w
     float* bufs_v[2] = {cand_v, cand_v + cand_half};
     int64_t* bufs_r[2] = {cand_r, cand_r + cand_half};
     for (int level = 0;; ++level) {
-        const int64_t blocks = plm::ceil_div(n, kTopkSlice);
-        const int final = blocks == 1 ? 1 : 0;
-        float* ov = final ? out_logits : bufs_v[level & 1];
-        int64_t* orow = final ? out_ids : bufs_r[level & 1];
-        if (first) {
-            hipLaunchKernelGGL(topk_level_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kTopkThreads), 0,
-                               st, in_v, in_r, n, static_cast<int>(top_k), ov, orow, final, token_offset);
-        } else {
-            hipLaunchKernelGGL(topk_level_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(kTopkThreads), 0,
-                               st, in_v, in_r, n, static_cast<int>(top_k), ov, orow, final, token_offset);
+        const int64_t blocks = plm::ceil_div(n, 64 * kTopkJ);  // slices
+        if (blocks <= kTopkFinalWaves) {
+            auto kern = first ? topk_final_kernel<true> : topk_final_kernel<false>;
+            hipLaunchKernelGGL(kern, dim3(1), dim3(kTopkFinalWaves * 64), 0, st, in_v, in_r, n, static_cast<int>(top_k),
+                               out_logits, out_ids, token_offset);
+            return plm::check_launch("top-k final kernel");
         }
+        float* ov = bufs_v[level & 1];
+        int64_t* orow = bufs_r[level & 1];
+        auto kern = first ? topk_level_kernel<true> : topk_level_kernel<false>;
+        hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(plm::ceil_div(blocks, kTopkWaves))), dim3(kTopkWaves * 64),
+                           0, st, in_v, in_r, n, static_cast<int>(top_k), ov, orow);
         code = plm::check_launch("top-k level kernel");
-        if (code != 0 || final) return code;
+        if (code != 0) return code;
         in_v = ov;
         in_r = orow;
         n = blocks * top_k;
