@@ -448,8 +448,7 @@ __global__ __launch_bounds__(kThreads) void mla_value_kernel(const float* __rest
 }
 
 // ------------------------------------------------------------------ block helpers
-// y[n] = W[n] . x: one wave per row; VEC: float4 loads (K % 4 == 0, aligned).
-template <bool VEC>
+// y[n] = W[n] . x, one wave per row (any K and alignment).
 __global__ __launch_bounds__(kThreads) void f32_gemv_kernel(const float* __restrict__ W, const float* __restrict__ x,
                                                            float* __restrict__ y, int64_t N, int64_t K) {
     const int lane = threadIdx.x & 63;
@@ -457,21 +456,67 @@ __global__ __launch_bounds__(kThreads) void f32_gemv_kernel(const float* __restr
     if (n >= N) return;
     const float* row = W + n * K;
     float acc = 0.0f;
-    if constexpr (VEC) {
-        const float4* r4 = reinterpret_cast<const float4*>(row);
-        const float4* x4 = reinterpret_cast<const float4*>(x);
-        for (int64_t k = lane; k < K / 4; k += 64) {
-            const float4 a = r4[k], b = x4[k];
-            acc = fmaf(a.x, b.x, acc);
-            acc = fmaf(a.y, b.y, acc);
-            acc = fmaf(a.z, b.z, acc);
-            acc = fmaf(a.w, b.w, acc);
-        }
-    } else {
-        for (int64_t k = lane; k < K; k += 64) acc = fmaf(row[k], x[k], acc);
-    }
+    for (int64_t k = lane; k < K; k += 64) acc = fmaf(row[k], x[k], acc);
     acc = plm_wave_sum(acc);
     if (lane == kSumLane) y[n] = acc;
+}
+
+// y[n] = W[n] . x for K % 4 == 0 and 16-byte aligned W and x: a workgroup
+// owns kGemvRows rows and its waves split K (float4 k on wave (k / 64) % 4),
+// so each activation load serves kGemvRows weight loads; kGemvU steps of
+// loads are issued before their fmas.  The wave sums are added in wave
+// order.
+constexpr int kGemvRows = 4;
+constexpr int kGemvU = 4;
+__global__ __launch_bounds__(kThreads) void f32_gemv_rows_kernel(const float* __restrict__ W,
+                                                                const float* __restrict__ x, float* __restrict__ y,
+                                                                int64_t N, int64_t K) {
+    __shared__ float red[kThreads / 64][kGemvRows];
+    const int wave = static_cast<int>(threadIdx.x >> 6);
+    const int lane = static_cast<int>(threadIdx.x & 63);
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kGemvRows;
+    const int64_t K4 = K / 4;
+    const float4* r4[kGemvRows];
+#pragma unroll
+    for (int i = 0; i < kGemvRows; ++i)
+        r4[i] = reinterpret_cast<const float4*>(W + min(n0 + i, N - 1) * K);  // rows past N re-read the last
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    float acc[kGemvRows];
+#pragma unroll
+    for (int i = 0; i < kGemvRows; ++i) acc[i] = 0.0f;
+    for (int64_t k0 = threadIdx.x; k0 < K4; k0 += static_cast<int64_t>(kThreads) * kGemvU) {
+        float4 xv[kGemvU], wv[kGemvU][kGemvRows];
+#pragma unroll
+        for (int u = 0; u < kGemvU; ++u) {
+            const int64_t k = min(k0 + static_cast<int64_t>(u) * kThreads, K4 - 1);  // in range; dropped below
+            xv[u] = x4[k];
+#pragma unroll
+            for (int i = 0; i < kGemvRows; ++i) wv[u][i] = r4[i][k];
+        }
+        __builtin_amdgcn_sched_barrier(0);  // every load of the steps before the first fma
+#pragma unroll
+        for (int u = 0; u < kGemvU; ++u) {
+            if (k0 + static_cast<int64_t>(u) * kThreads >= K4) xv[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+            for (int i = 0; i < kGemvRows; ++i) {
+                if (k0 + static_cast<int64_t>(u) * kThreads >= K4) wv[u][i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                acc[i] = fmaf(wv[u][i].x, xv[u].x, acc[i]);
+                acc[i] = fmaf(wv[u][i].y, xv[u].y, acc[i]);
+                acc[i] = fmaf(wv[u][i].z, xv[u].z, acc[i]);
+                acc[i] = fmaf(wv[u][i].w, xv[u].w, acc[i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kGemvRows; ++i) {
+        const float t = plm_wave_sum(acc[i]);
+        if (lane == kSumLane) red[wave][i] = t;
+    }
+    __syncthreads();
+    if (threadIdx.x < kGemvRows && n0 + threadIdx.x < N) {
+        const int i = static_cast<int>(threadIdx.x);
+        y[n0 + i] = ((red[0][i] + red[1][i]) + red[2][i]) + red[3][i];
+    }
 }
 
 // v = v * (1 / sqrt(mean(v^2) + eps)) * w (ds_forward.cpp:610-619), one workgroup.
@@ -534,12 +579,14 @@ __global__ __launch_bounds__(kThreads) void mla_norms_kernel(float* __restrict__
 }
 
 int gemv(const float* W, const float* x, float* y, int64_t N, int64_t K, hipStream_t st) {
-    const bool vec = K % 4 == 0 && plm::aligned16(W) && plm::aligned16(x);
-    const dim3 grid(static_cast<unsigned>(plm::ceil_div(N, kThreads / 64)));
-    if (vec)
-        hipLaunchKernelGGL(f32_gemv_kernel<true>, grid, dim3(kThreads), 0, st, W, x, y, N, K);
-    else
-        hipLaunchKernelGGL(f32_gemv_kernel<false>, grid, dim3(kThreads), 0, st, W, x, y, N, K);
+    static_assert(kThreads == 256, "four waves add their sums in f32_gemv_rows_kernel");
+    if (K % 4 == 0 && plm::aligned16(W) && plm::aligned16(x)) {
+        hipLaunchKernelGGL(f32_gemv_rows_kernel, dim3(static_cast<unsigned>(plm::ceil_div(N, kGemvRows))),
+                           dim3(kThreads), 0, st, W, x, y, N, K);
+    } else {
+        hipLaunchKernelGGL(f32_gemv_kernel, dim3(static_cast<unsigned>(plm::ceil_div(N, kThreads / 64))),
+                           dim3(kThreads), 0, st, W, x, y, N, K);
+    }
     return plm::check_launch("f32 gemv");
 }
 
