@@ -641,6 +641,43 @@ template <bool XB>
 __device__ __forceinline__ plm_u32x4 load_xpart(const char* piece, int lane) {
     return xload16(piece + 16 * ((lane & 3) % (XB ? 2 : 4)));
 }
+// Two to four activation rows (XS == 2): the lanes of B columns of rows
+// 4-7 are past the batch, so lane m + 4 (the next quad of its row of 16)
+// loads the second half of row m's piece and the halves are swapped between
+// the two lanes with DPP row shifts: one load instruction per block instead
+// of two (bf16), two instead of four (fp32).
+template <bool XB>
+__device__ __forceinline__ const char* pair_half(const char* piece, int lane) {
+    return piece + ((lane >> 2) & 1) * (XB ? 16 : 32);
+}
+__device__ __forceinline__ plm_u32x4 pair_swap(plm_u32x4 v, bool upper) {
+    plm_u32x4 r;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int from_up = __builtin_amdgcn_mov_dpp(static_cast<int>(v[c]), 0x104, 0xF, 0xF, false);  // row_shl:4
+        const int from_lo = __builtin_amdgcn_mov_dpp(static_cast<int>(v[c]), 0x114, 0xF, 0xF, false);  // row_shr:4
+        r[c] = static_cast<uint32_t>(upper ? from_lo : from_up);
+    }
+    return r;
+}
+template <bool XB>
+__device__ __forceinline__ XPiece<XB> pair_piece(const XPiece<XB>& own, int lane) {
+    const bool upper = ((lane >> 2) & 1) != 0;  // holds the second half
+    XPiece<XB> x;
+    if constexpr (XB) {
+        const plm_u32x4 other = pair_swap(own.v[0], upper);
+        x.v[0] = upper ? other : own.v[0];
+        x.v[1] = upper ? own.v[0] : other;
+    } else {
+        const plm_u32x4 o0 = pair_swap(own.v[0], upper), o1 = pair_swap(own.v[1], upper);
+        x.v[0] = upper ? o0 : own.v[0];
+        x.v[1] = upper ? o1 : own.v[1];
+        x.v[2] = upper ? own.v[0] : o0;
+        x.v[3] = upper ? own.v[1] : o1;
+    }
+    return x;
+}
+
 template <bool XB>
 __device__ __forceinline__ XPiece<XB> quad_piece(plm_u32x4 part) {
     XPiece<XB> x;
@@ -698,7 +735,9 @@ __device__ __forceinline__ void rows_pass_burst(const RowsArgs& a, const uint8_t
 // 0 into B columns whose results are dropped, and the blocks beyond a
 // multiple of P run first, unpipelined.  The wave's scales come first, one
 // load for up to 64 blocks (lane k holds block k's), read with v_readlane.
-template <int TT, int P, int NWT, bool XB, bool SAN, bool X1>
+// XS: how the activation pieces are loaded: 0 every lane its own, 1 one
+// activation row (quad-shared parts), 2 two to four rows (pair-shared halves).
+template <int TT, int P, int NWT, bool XB, bool SAN, int XS>
 __device__ __forceinline__ void rows_pass(const RowsArgs& a, const uint8_t* const (&wrow)[NWT * TT],
                                           const float* const (&sp)[NWT], const char* xrow, int64_t lane_col,
                                           int wave, int nw, int lane, plm_f32x4 (&acc)[NWT * TT]) {
@@ -720,18 +759,25 @@ __device__ __forceinline__ void rows_pass(const RowsArgs& a, const uint8_t* cons
             const int64_t off = min((wave + static_cast<int64_t>(kb + k) * nw) * 128 + lane_col, K - 16);
 #pragma unroll
             for (int t = 0; t < NT; ++t) q[slot][t] = wload16(wrow[t] + tile_col(off, a.tiled));
-            if constexpr (X1)
+            if constexpr (XS == 1) {
                 x[slot].v[0] = load_xpart<XB>(xrow + off * XE, lane);
-            else
+            } else if constexpr (XS == 2) {
+                const char* h = pair_half<XB>(xrow + off * XE, lane);
+                x[slot].v[0] = xload16(h);
+                if constexpr (!XB) x[slot].v[1] = xload16(h + 16);
+            } else {
                 x[slot] = load_xpiece<XB>(xrow + off * XE, true);
+            }
         };
         auto compute = [&](int slot, int k) {
             float sc[NWT];
 #pragma unroll
             for (int n = 0; n < NWT; ++n) sc[n] = lane_value(sv[n], k);
             XPiece<XB> xv;
-            if constexpr (X1) {
+            if constexpr (XS == 1) {
                 xv = quad_piece<XB>(x[slot].v[0]);
+            } else if constexpr (XS == 2) {
+                xv = pair_piece<XB>(x[slot], lane);
             } else {
                 xv = x[slot];
             }
@@ -780,10 +826,10 @@ __device__ __forceinline__ void pin_scalar(T&... v) {
 // weights; its nw waves split the K blocks (block b on wave b % nw), and nw
 // depends only on K.  TT and U (blocks in flight per wave) change the grid
 // and the schedule, never a row's arithmetic.
-template <int TT, int U, bool BURST, int NWT, bool SILU, bool XB, bool INPLAN, bool X1>
+template <int TT, int U, bool BURST, int NWT, bool SILU, bool XB, bool INPLAN, int XS>
 __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int block) {
     static_assert(!INPLAN || (NWT == 2 && SILU), "the in-launch plan is the MoE gate/up phase's");
-    static_assert(!X1 || !BURST, "the quad-shared activation loads are the pipelined loop's");
+    static_assert(XS == 0 || !BURST, "the shared activation loads are the pipelined loop's");
     constexpr int NT = NWT * TT;
     __shared__ float red[kMaxWaves * NT * 64];
     // the arguments of the prologue and of the loop, read at once
@@ -895,14 +941,16 @@ __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int block) {
                 wrow[i * TT + t] = tiled ? W[i] + ((r >> 3) * nb * 1024 + (r & 7) * 128) : W[i] + r * K;
             }
         }
-        const int64_t xo = static_cast<int64_t>(m0 + (xlive ? xm : 0)) * x_stride;
+        // XS == 2: lane m + 4 reads row m (rows 4-7 are past the batch)
+        const int xr = XS == 2 ? (xm & 3) : xm;
+        const int64_t xo = static_cast<int64_t>(m0 + (xr < mc ? xr : 0)) * x_stride;
         const char* xrow = xbase + xo * (XB ? 2 : 4);
         auto pass = [&](auto san) {
             constexpr bool SAN = decltype(san)::value;
             if constexpr (BURST)
                 rows_pass_burst<TT, U, NWT, XB, SAN>(a, wrow, sp, xrow, xlive, lane_col, wave, nw, acc);
             else
-                rows_pass<TT, U, NWT, XB, SAN, X1>(a, wrow, sp, xrow, lane_col, wave, nw, lane, acc);
+                rows_pass<TT, U, NWT, XB, SAN, XS>(a, wrow, sp, xrow, lane_col, wave, nw, lane, acc);
         };
         pass(std::false_type{});
         if (any_nan(acc)) {
@@ -945,9 +993,9 @@ __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int block) {
     }
 }
 
-template <int TT, int U, bool BURST, int NWT, bool SILU, bool XB, bool INPLAN = false, bool X1 = false>
+template <int TT, int U, bool BURST, int NWT, bool SILU, bool XB, bool INPLAN = false, int XS = 0>
 __global__ __launch_bounds__(512) void fp8_rows_kernel(const RowsArgs a) {
-    rows_tile<TT, U, BURST, NWT, SILU, XB, INPLAN, X1>(a, static_cast<int>(blockIdx.x));
+    rows_tile<TT, U, BURST, NWT, SILU, XB, INPLAN, XS>(a, static_cast<int>(blockIdx.x));
 }
 
 
@@ -1564,8 +1612,8 @@ int rows_waves(int64_t nb) {
 constexpr int64_t kMinTiles = 192;
 constexpr int64_t kCUs = 256;  // MI355X compute units
 
-// X1: the launch has one activation row (mc == 1).
-template <int TT, int P, bool BURST, int NWT, bool SILU, bool X1 = false>
+// XS: 1 when the launch has one activation row, 2 for two to four.
+template <int TT, int P, bool BURST, int NWT, bool SILU, int XS = 0>
 void launch_rows_cfg(const RowsArgs& a, int ngroups, hipStream_t st) {
     RowsArgs b = a;
     b.tiles_per_group = static_cast<int>(plm::ceil_div(a.rows, 8 * TT));
@@ -1581,19 +1629,19 @@ void launch_rows_cfg(const RowsArgs& a, int ngroups, hipStream_t st) {
     if constexpr (NWT == 2 && SILU) {
         if (a.inplan) {
             if (a.xb != nullptr)
-                hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, true, true, X1>),
+                hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, true, true, XS>),
                                    dim3(static_cast<unsigned>(grid)), dim3(nw * plm::kWave), 0, st, b);
             else
-                hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, false, true, X1>),
+                hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, false, true, XS>),
                                    dim3(static_cast<unsigned>(grid)), dim3(nw * plm::kWave), 0, st, b);
             return;
         }
     }
     if (a.xb != nullptr) {
-        hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, true, false, X1>), dim3(static_cast<unsigned>(grid)),
+        hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, true, false, XS>), dim3(static_cast<unsigned>(grid)),
                            dim3(nw * plm::kWave), 0, st, b);
     } else {
-        hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, false, false, X1>), dim3(static_cast<unsigned>(grid)),
+        hipLaunchKernelGGL((fp8_rows_kernel<TT, P, BURST, NWT, SILU, false, false, XS>), dim3(static_cast<unsigned>(grid)),
                            dim3(nw * plm::kWave), 0, st, b);
     }
 }
@@ -1631,6 +1679,28 @@ void launch_rows(const RowsArgs& a, int mcount, int ngroups, hipStream_t st) {
     }
 }
 
+// The linear family's launches of several activation rows (XS 2: at most
+// four; the 4-tile instance keeps its own loads: o 7168x16384 at 2 and 4
+// rows was 0.4-0.6 us slower with the pair-shared halves, the 1- and 2-tile
+// shapes 0.25-0.65 us faster).
+template <int NWT, int XS>
+void launch_rows_batch(const RowsArgs& b, int ngroups, bool few, hipStream_t st) {
+    constexpr bool SILU = false;
+    if constexpr (NWT == 1) {
+        if (rows_tiles(b, ngroups, 4) >= kMinTiles) {
+            launch_rows_cfg<4, 2, false, NWT, SILU>(b, ngroups, st);
+            return;
+        }
+    }
+    if (rows_tiles(b, ngroups, 2) >= kMinTiles) {
+        launch_rows_cfg<2, 2, false, NWT, SILU, XS>(b, ngroups, st);
+    } else if (few) {
+        launch_rows_cfg<1, 2, false, NWT, SILU, XS>(b, ngroups, st);
+    } else {
+        launch_rows_cfg<1, 4, false, NWT, SILU, XS>(b, ngroups, st);
+    }
+}
+
 // The linear family's launches.
 template <int NWT>
 void launch_rows_linear(const RowsArgs& b, int mcount, int ngroups, hipStream_t st) {
@@ -1645,32 +1715,23 @@ void launch_rows_linear(const RowsArgs& b, int mcount, int ngroups, hipStream_t 
         // in the FP8 attention block 24.2 -> about 13 us with 4 tiles; the
         // expert down 7168x2048 6.32 -> 6.23 with 2, 6.78 with 4)
         if (few && rows_tiles(b, ngroups, 4) >= 2 * kCUs)
-            launch_rows_cfg<4, 2, false, NWT, SILU, true>(b, ngroups, st);
+            launch_rows_cfg<4, 2, false, NWT, SILU, 1>(b, ngroups, st);
         else if (few && rows_tiles(b, ngroups, 2) >= kMinTiles)
-            launch_rows_cfg<2, 2, false, NWT, SILU, true>(b, ngroups, st);
+            launch_rows_cfg<2, 2, false, NWT, SILU, 1>(b, ngroups, st);
         else if (few)
-            launch_rows_cfg<1, 2, false, NWT, SILU, true>(b, ngroups, st);
+            launch_rows_cfg<1, 2, false, NWT, SILU, 1>(b, ngroups, st);
         else if (per_wave <= 8 && rows_tiles(b, ngroups, 1) <= plm::cu_count())
             // 8 deep holds 146 VGPRs: one workgroup per CU, so only while the grid fits the CUs
             // (q_a + kv_a, 264 tiles: 9.7 us at 8 deep)
-            launch_rows_cfg<1, 8, false, NWT, SILU, true>(b, ngroups, st);
+            launch_rows_cfg<1, 8, false, NWT, SILU, 1>(b, ngroups, st);
         else
-            launch_rows_cfg<1, 4, false, NWT, SILU, true>(b, ngroups, st);
+            launch_rows_cfg<1, 4, false, NWT, SILU, 1>(b, ngroups, st);
         return;
     }
-    if constexpr (NWT == 1) {
-        if (rows_tiles(b, ngroups, 4) >= kMinTiles) {
-            launch_rows_cfg<4, 2, false, NWT, SILU>(b, ngroups, st);
-            return;
-        }
-    }
-    if (rows_tiles(b, ngroups, 2) >= kMinTiles) {
-        launch_rows_cfg<2, 2, false, NWT, SILU>(b, ngroups, st);
-    } else if (few) {
-        launch_rows_cfg<1, 2, false, NWT, SILU>(b, ngroups, st);
-    } else {
-        launch_rows_cfg<1, 4, false, NWT, SILU>(b, ngroups, st);
-    }
+    if (mcount <= 4)
+        launch_rows_batch<NWT, 2>(b, ngroups, few, st);
+    else
+        launch_rows_batch<NWT, 0>(b, ngroups, few, st);
 }
 
 // Groups summed by one output tile: every group in summed mode, except a
