@@ -15,7 +15,11 @@
 //                    (linear, dual, gate/up phase with the SiLU epilogue, and
 //                    several weights of different row counts in one grid);
 //                    the activations are fp32 (split into bf16 hi + lo) or
-//                    bf16 (the *_bf16x_f32 entry points).
+//                    bf16 (the *_bf16x_f32 entry points); at one to four
+//                    activation rows the lanes of B columns past the batch
+//                    share the activation loads; for the device-routed MoE
+//                    its first workgroup writes the plan of the router's
+//                    choices.
 // fp8_down_kernel  : rows whose K range is the concatenation of several
 //                    experts' down matrices, each with its own activations
 //                    (the SiLU intermediate as bf16 hi / lo planes) and route
