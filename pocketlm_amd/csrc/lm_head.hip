@@ -24,7 +24,6 @@ namespace {
 
 constexpr int kLmRowsPerWave = 4;
 constexpr int kLmWaves = 4;              // 256 threads: 16 rows per workgroup
-constexpr int kLmUnroll = 8;             // 16-byte pieces in flight per lane
 constexpr int kTopkJ = 16;               // entries per lane of a selection slice (1024 per slice)
 constexpr int kTopkWaves = 4;            // slices per workgroup of a reducing level
 constexpr int kTopkFinalWaves = 8;       // slices of the last two levels (one workgroup)
@@ -47,7 +46,9 @@ __device__ __forceinline__ float dot8(const uint4& w, const uint4& x, float acc)
 }
 
 // K % 8 == 0, x and w 16-byte aligned.  Dynamic LDS: K u16 values.
-template <bool BF16>
+// U: 16-byte pieces in flight per lane (a row of up to 64 U pieces in one
+// round of loads).
+template <bool BF16, int U>
 __global__ __launch_bounds__(kLmWaves * 64) void lm_head_logits_kernel(const uint16_t* __restrict__ x,
                                                                        const uint16_t* __restrict__ w,
                                                                        float* __restrict__ logits, int64_t rows,
@@ -64,15 +65,15 @@ __global__ __launch_bounds__(kLmWaves * 64) void lm_head_logits_kernel(const uin
         if (row >= rows) break;  // wave-uniform
         const uint4* wr = reinterpret_cast<const uint4*>(w + row * K);
         float acc = 0.0f;
-        for (int c0 = lane; c0 < nx; c0 += 64 * kLmUnroll) {
-            uint4 q[kLmUnroll];
+        for (int c0 = lane; c0 < nx; c0 += 64 * U) {
+            uint4 q[U];
 #pragma unroll
-            for (int u = 0; u < kLmUnroll; ++u) {
+            for (int u = 0; u < U; ++u) {
                 const int c = c0 + u * 64;
                 q[u] = wr[c < nx ? c : nx - 1];  // in range; an out-of-range piece is not used
             }
 #pragma unroll
-            for (int u = 0; u < kLmUnroll; ++u) {
+            for (int u = 0; u < U; ++u) {
                 const int c = c0 + u * 64;
                 if (c < nx) acc = dot8<BF16>(q[u], xs[c], acc);
             }
@@ -382,13 +383,12 @@ PLM_EXPORT int native_lm_head_topk_u16(const uint16_t* hidden, const uint16_t* w
         const int64_t per_block = kLmWaves * kLmRowsPerWave;
         const dim3 grid(static_cast<unsigned>(plm::ceil_div(rows, per_block)));
         const size_t shmem = static_cast<size_t>(hidden_size) * 2;
-        if (dtype_code == 1) {
-            hipLaunchKernelGGL(lm_head_logits_kernel<true>, grid, dim3(kLmWaves * 64), shmem, st, hidden, weight,
-                               logits, rows, hidden_size);
-        } else {
-            hipLaunchKernelGGL(lm_head_logits_kernel<false>, grid, dim3(kLmWaves * 64), shmem, st, hidden, weight,
-                               logits, rows, hidden_size);
-        }
+        // rows of more than 512 pieces in one round of 16 loads per lane (DeepSeek-V3's
+        // 7168 columns), shorter rows in rounds of 8
+        const bool wide = hidden_size / 8 > 64 * 8;
+        auto kern = dtype_code == 1 ? (wide ? lm_head_logits_kernel<true, 16> : lm_head_logits_kernel<true, 8>)
+                                    : (wide ? lm_head_logits_kernel<false, 16> : lm_head_logits_kernel<false, 8>);
+        hipLaunchKernelGGL(kern, grid, dim3(kLmWaves * 64), shmem, st, hidden, weight, logits, rows, hidden_size);
     } else {
         hipLaunchKernelGGL(lm_head_logits_scalar_kernel, dim3(static_cast<unsigned>(plm::ceil_div(rows, 256))),
                            dim3(256), 0, st, hidden, weight, logits, rows, hidden_size, dtype_code);
