@@ -448,7 +448,8 @@ __global__ __launch_bounds__(kThreads) void mla_value_kernel(const float* __rest
 }
 
 // ------------------------------------------------------------------ block helpers
-// y[n] = W[n] . x, one wave per row (any K and alignment).
+// y[n] = W[n] . x, one wave per row; VEC: float4 loads (K % 4 == 0, aligned).
+template <bool VEC>
 __global__ __launch_bounds__(kThreads) void f32_gemv_kernel(const float* __restrict__ W, const float* __restrict__ x,
                                                            float* __restrict__ y, int64_t N, int64_t K) {
     const int lane = threadIdx.x & 63;
@@ -456,7 +457,19 @@ __global__ __launch_bounds__(kThreads) void f32_gemv_kernel(const float* __restr
     if (n >= N) return;
     const float* row = W + n * K;
     float acc = 0.0f;
-    for (int64_t k = lane; k < K; k += 64) acc = fmaf(row[k], x[k], acc);
+    if constexpr (VEC) {
+        const float4* r4 = reinterpret_cast<const float4*>(row);
+        const float4* x4 = reinterpret_cast<const float4*>(x);
+        for (int64_t k = lane; k < K / 4; k += 64) {
+            const float4 a = r4[k], b = x4[k];
+            acc = fmaf(a.x, b.x, acc);
+            acc = fmaf(a.y, b.y, acc);
+            acc = fmaf(a.z, b.z, acc);
+            acc = fmaf(a.w, b.w, acc);
+        }
+    } else {
+        for (int64_t k = lane; k < K; k += 64) acc = fmaf(row[k], x[k], acc);
+    }
     acc = plm_wave_sum(acc);
     if (lane == kSumLane) y[n] = acc;
 }
@@ -580,11 +593,17 @@ __global__ __launch_bounds__(kThreads) void mla_norms_kernel(float* __restrict__
 
 int gemv(const float* W, const float* x, float* y, int64_t N, int64_t K, hipStream_t st) {
     static_assert(kThreads == 256, "four waves add their sums in f32_gemv_rows_kernel");
-    if (K % 4 == 0 && plm::aligned16(W) && plm::aligned16(x)) {
+    const bool vec = K % 4 == 0 && plm::aligned16(W) && plm::aligned16(x);
+    if (vec && K / 4 >= static_cast<int64_t>(kThreads) * kGemvU) {
+        // rows of at least 4096 values: the row groups (q_b 24576x1536 was
+        // 1.7 us faster one wave per row)
         hipLaunchKernelGGL(f32_gemv_rows_kernel, dim3(static_cast<unsigned>(plm::ceil_div(N, kGemvRows))),
                            dim3(kThreads), 0, st, W, x, y, N, K);
+    } else if (vec) {
+        hipLaunchKernelGGL(f32_gemv_kernel<true>, dim3(static_cast<unsigned>(plm::ceil_div(N, kThreads / 64))),
+                           dim3(kThreads), 0, st, W, x, y, N, K);
     } else {
-        hipLaunchKernelGGL(f32_gemv_kernel, dim3(static_cast<unsigned>(plm::ceil_div(N, kThreads / 64))),
+        hipLaunchKernelGGL(f32_gemv_kernel<false>, dim3(static_cast<unsigned>(plm::ceil_div(N, kThreads / 64))),
                            dim3(kThreads), 0, st, W, x, y, N, K);
     }
     return plm::check_launch("f32 gemv");
