@@ -133,7 +133,10 @@ def test_error_codes(nat):
 
 
 @pytest.mark.parametrize("dims", [(16, 6, 5, 4, 3, 4, 2, 3), (64, 16, 16, 4, 8, 8, 8, 32), (48, 8, 12, 2, 4, 6, 4, 0),
-                                  (32, 8, 16, 3, 4, 5, 4, 7)])  # odd rope width: the pe part stays unrotated
+                                  (32, 8, 16, 3, 4, 5, 4, 7),  # odd rope width: the pe part stays unrotated
+                                  # rows of 4104 values (q_a, kv_a: the row-group GEMV) with row
+                                  # counts that are not multiples of 4, and unaligned q_b rows
+                                  (4104, 386, 64, 4, 16, 14, 16, 5)])
 def test_block_matches_the_oracle(nat, dims):
     hidden_dim, q_rank, kv_rank, heads, nope, rope, v, prev = dims
     t = block_inputs(*dims)
